@@ -1,0 +1,109 @@
+/* C ABI of the PTO-WSP HIP backend (libptowsp_hip.so) for one MI355X GPU.
+ *
+ * It is the drop-in for the reference's codegen plugin boundary: a loader
+ * that today calls compile_codegen() and then dlopens the artifact and
+ * calls `<module>_main(RuntimeContext*, CSPTContext*)` calls these entry
+ * points instead.  Plain pointers and sizes only; the structures come from
+ * ptowsp_abi.h (layouts identical to the reference artifact ABI).
+ *
+ * Threading: one program may be used by one thread at a time; different
+ * programs are independent.  Errors: functions returning int give 0 on
+ * success and -1 on failure, with the message in ptowsp_hip_last_error().
+ */
+#ifndef PTOWSP_HIP_H
+#define PTOWSP_HIP_H
+
+#include <stddef.h>
+#include <stdint.h>
+
+#include "ptowsp_abi.h"
+
+#ifdef __cplusplus
+extern "C" {
+#endif
+
+typedef struct ptowsp_program ptowsp_program;
+typedef struct ptowsp_runtime ptowsp_runtime;
+
+typedef struct ptowsp_run_info {
+    uint64_t total_cycles; /* cpu_sim cycle-model makespan (ProgramStats.total_cycles) */
+    uint64_t task_count;   /* tasks executed */
+    uint32_t launches;     /* kernel launches enqueued */
+    uint32_t reserved;
+} ptowsp_run_info;
+
+typedef struct ptowsp_timing {
+    double device_ms; /* first launch start .. last launch end (HIP events on the stream) */
+    double h2d_ms;    /* staging of host-resident tensors into HBM */
+    double d2h_ms;    /* copy-back of written host-resident tensors */
+} ptowsp_timing;
+
+/* Replaces compile_codegen(module, CompileOptions{target}) for the target
+ * "hip_gfx950" (reference src/python/pto_codegen.cpp:3352-3434; called from
+ * python/pto_wsp/program.py:437-454).  `module_text` is the serialized
+ * module written by pto_wsp.ir_bridge.workload_to_codegen_ir (the reference
+ * passes the pybind ir::Module built by python/pto_wsp/ir_bridge.py:112-139).
+ * Parses, validates and plans the workload; kernels are emitted and built
+ * with hiprtc for gfx950 on first use (cached on disk). */
+int ptowsp_hip_compile(const char* module_text, ptowsp_program** out);
+
+/* Replaces the artifact entry `uint64_t <module>_main(RuntimeContext*, CSPTContext*)`
+ * (reference include/pto/wsp/codegen/abi/workload_abi.hpp:71, driven by
+ * CodegenExecutable::run_with_symbols, src/python/pto_codegen.cpp:3542-3566).
+ * Synchronous: runs every launch on the null stream and returns after all
+ * outputs (including host-resident ones) are written.  Returns the cycle-model
+ * makespan, or 0 on failure (see ptowsp_hip_last_error).  `cspt` is unused,
+ * as in the reference's cpu_sim path. */
+uint64_t ptowsp_hip_workload_main(ptowsp_program* prog, RuntimeContext* ctx, CSPTContext* cspt);
+
+/* Non-blocking run behind Program.execute() (reference python/pto_wsp/program.py:670-733):
+ * stages host-resident tensors, enqueues every launch on `hip_stream`
+ * (a hipStream_t, may be NULL) and returns. */
+int ptowsp_hip_launch(ptowsp_program* prog, RuntimeContext* ctx, void* hip_stream, ptowsp_run_info* info);
+
+/* Program.synchronize() (reference python/pto_wsp/program.py:735-743): waits
+ * for the last launch, copies written host-resident tensors back, and
+ * reports device errors (which the reference has no channel for). */
+int ptowsp_hip_synchronize(ptowsp_program* prog, ptowsp_timing* timing);
+
+/* Error message of the last failing call on this thread (new: the
+ * reference's run path has no error channel). */
+const char* ptowsp_hip_last_error(void);
+
+/* Frees the program and its staging buffers. */
+void ptowsp_hip_release(ptowsp_program* prog);
+
+/* Introspection. */
+int ptowsp_hip_num_launches(const ptowsp_program* prog);
+/* cpu_sim cycles of one task of `kernel` (reference
+ * include/pto/wsp/codegen/abi/ptoisa_bridge.hpp:54-303), or UINT64_MAX. */
+uint64_t ptowsp_hip_kernel_cycles(const ptowsp_program* prog, const char* kernel);
+/* Family chosen for `kernel`: 0 row program, 1 tile program, 2 gemm; -1 unknown. */
+int ptowsp_hip_kernel_family(const ptowsp_program* prog, const char* kernel);
+/* Emits and builds every launch for contiguous row-major tensors without
+ * touching a GPU (hiprtc only); returns the source of launch `index` through
+ * `source`, valid until the next call. */
+int ptowsp_hip_precompile(ptowsp_program* prog, int index, const char** source);
+
+/* Evaluates only the cpu_sim cycle model (total_cycles, task_count) for the
+ * bindings in `ctx`, on the host, without launching anything. */
+int ptowsp_hip_cycle_model(ptowsp_program* prog, RuntimeContext* ctx, ptowsp_run_info* info);
+
+/* Runtime tables that back a RuntimeContext, the equivalent of the
+ * reference's CodegenRuntime (src/python/pto_codegen.cpp:3453-3508):
+ * tensors (pointer + element strides), DenseDyn axis sizes by name, u64 and
+ * pointer symbols by FNV-1a-64 id, and 256 zeroed u64 slots. */
+ptowsp_runtime* ptowsp_rt_create(void);
+void ptowsp_rt_destroy(ptowsp_runtime* rt);
+int ptowsp_rt_set_tensor(ptowsp_runtime* rt, uint32_t tensor_id, void* ptr, uint32_t ndim, const int64_t* strides);
+int ptowsp_rt_set_axis_size(ptowsp_runtime* rt, const char* name, int64_t size);
+int ptowsp_rt_set_symbol_u64(ptowsp_runtime* rt, uint64_t symbol_id, uint64_t value);
+int ptowsp_rt_set_symbol_ptr(ptowsp_runtime* rt, uint64_t symbol_id, void* ptr);
+void ptowsp_rt_clear(ptowsp_runtime* rt);
+RuntimeContext* ptowsp_rt_context(ptowsp_runtime* rt);
+
+#ifdef __cplusplus
+}
+#endif
+
+#endif /* PTOWSP_HIP_H */

@@ -1,0 +1,46 @@
+/* CPU oracle for the PTO-WSP data-parallel tile path.  TEST INFRASTRUCTURE:
+ * only tests/, __graft_entry__.smoke() and bench.py's cpu_baseline leg may
+ * load it, as the checker.  It is never part of the product path.
+ *
+ * pto_cpusim_run() executes a serialized workload module (the text that the
+ * Python bridge pto_wsp.ir_bridge writes, format "PTOWSP-MODULE 1") the way
+ * the reference's generated cpu_sim artifact does:
+ *   - loop nest, task argument packing and tile view addressing:
+ *       src/python/pto_codegen.cpp:2222-2709
+ *   - per-op tile semantics of the generated kernels:
+ *       src/python/pto_codegen.cpp:471-1241
+ *   - cpu_sim cycle counting (valid_rows*valid_cols per tile op, m*k*n per
+ *     TMATMUL): include/pto/wsp/codegen/abi/ptoisa_bridge.hpp:54-303
+ *   - in-order, window-stall scheduler giving total_cycles (the makespan):
+ *       src/python/pto_codegen.cpp:1561-1607
+ * The pto-isa submodule that implements the tile instructions is absent
+ * from the reference checkout, so reductions are restated as sequential
+ * fp32 sums, TEXP as expf, TRSQRT as 1/sqrtf and TMATMUL as a sequential
+ * fp32 dot product; their exact rounding order is "parity unpinned" beyond
+ * the tolerances of the reference's own examples.
+ */
+#ifndef PTOWSP_CPU_SIM_H
+#define PTOWSP_CPU_SIM_H
+
+#include <stdint.h>
+
+#include "ptowsp_abi.h"
+
+#ifdef __cplusplus
+extern "C" {
+#endif
+
+/* Runs the module.  Returns 0 on success and stores the model makespan in
+ * *total_cycles; returns -1 on error (message in pto_cpusim_last_error()). */
+int pto_cpusim_run(const char* module_text, RuntimeContext* ctx, uint64_t* total_cycles);
+
+/* Number of tasks executed by the last successful run. */
+uint64_t pto_cpusim_last_task_count(void);
+
+const char* pto_cpusim_last_error(void);
+
+#ifdef __cplusplus
+}
+#endif
+
+#endif

@@ -1,0 +1,319 @@
+// Kernel analysis.  The validation rules and the cycle cost restate the
+// reference's kernel emitter (src/python/pto_codegen.cpp:350-1241) and the
+// cpu_sim cycle wrappers (include/pto/wsp/codegen/abi/ptoisa_bridge.hpp:54-303):
+// every tile op costs valid_rows*valid_cols of its destination, TMATMUL costs
+// m*k*n, TROWSUM/TROWMAX cost the rows of the [rows,1] result and RowMean adds
+// a TDIVS of the same size.  Valid dims always equal the static tile shapes,
+// because the workload emitter passes the static shapes as tail arguments
+// (src/python/pto_codegen.cpp:2507-2545).
+#include "analysis.hpp"
+
+#include <algorithm>
+
+namespace ptowsp {
+
+namespace {
+
+[[noreturn]] void refuse(const KernelDef& k, const std::string& msg) {
+    throw CompileError("kernel " + k.name + ": " + msg);
+}
+
+uint64_t rc(const ValueInfo* v) { return static_cast<uint64_t>(v->rows) * static_cast<uint64_t>(v->cols); }
+
+bool is_binary(OpKind k) {
+    return k == OpKind::Add || k == OpKind::Sub || k == OpKind::Mul || k == OpKind::Div || k == OpKind::Max ||
+           k == OpKind::Min;
+}
+
+bool is_int(DType d) { return !dtype_is_float(d); }
+
+// Row-program classification (see analysis.hpp).  Returns false with a
+// reason when the kernel does not decompose into independent rows.
+bool classify_rows(const KernelDef& k, KernelAnalysis& a) {
+    auto no = [&](const std::string& why) {
+        a.not_row_reason = why;
+        return false;
+    };
+    for (const auto& op : k.ops)
+        if (op.kind == OpKind::Matmul) return no("matmul");
+    int R = 0, C = 0;
+    for (const auto& v : k.values) {
+        if (!v.tile) continue;
+        if (v.dtype != DType::F32) return no("non-f32 tile");
+        if (v.cols > C || (v.cols == C && v.rows > R)) {
+            C = v.cols;
+            R = v.rows;
+        }
+    }
+    if (C == 0) return no("no tiles");
+    a.rows = R;
+    a.cols = C;
+    a.row_class.assign(a.max_id + 1, RowClass::None);
+    auto shape_is = [](const ValueInfo* v, int r, int c) { return v->rows == r && v->cols == c; };
+
+    // Uses of each value as a broadcast operand, to tell [1,C] col vectors
+    // from other [1,*] tiles.
+    std::vector<int> bcast_row(a.max_id + 1, 0), bcast_col(a.max_id + 1, 0), other_use(a.max_id + 1, 0);
+    for (size_t i = 0; i < k.ops.size(); ++i) {
+        const auto& op = k.ops[i];
+        for (size_t j = 0; j < op.operands.size(); ++j) {
+            int id = op.operands[j];
+            if (is_binary(op.kind) && j == 1 && a.bin_mode[i] == BinMode::RowExpand) bcast_row[id]++;
+            else if (is_binary(op.kind) && j == 1 && a.bin_mode[i] == BinMode::ColExpand) bcast_col[id]++;
+            else if (!(op.kind == OpKind::Store && j == 0)) other_use[id]++;
+        }
+    }
+    auto base_class = [&](const ValueInfo* v) -> RowClass {
+        if (C > 1 && shape_is(v, R, C)) return RowClass::Full;
+        if (shape_is(v, R, 1)) return RowClass::RowVec;
+        if (R > 1 && v->rows == 1 && v->cols == R && bcast_row[v->id] && !other_use[v->id]) return RowClass::RowVecT;
+        if (R > 1 && v->rows == 1 && v->cols == C && bcast_col[v->id] && !other_use[v->id] && !bcast_row[v->id])
+            return RowClass::ColVec;
+        if (C > 1 && v->rows == C && v->cols == 1 && bcast_col[v->id] && !other_use[v->id] && !bcast_row[v->id])
+            return RowClass::ColVecT;
+        return RowClass::None;
+    };
+    for (const auto& v : k.values) {
+        if (!v.tile) {
+            a.row_class[v.id] = RowClass::Scalar;
+            continue;
+        }
+        RowClass c = base_class(&v);
+        if (c == RowClass::None)
+            return no("tile " + std::to_string(v.id) + " of shape " + std::to_string(v.rows) + "x" +
+                      std::to_string(v.cols) + " does not fit rows of " + std::to_string(R) + "x" + std::to_string(C));
+        bool from_param = a.param_of[v.id] >= 0;
+        bool from_load = false;
+        for (const auto& op : k.ops)
+            if (op.kind == OpKind::Load && op.result == v.id) from_load = true;
+        if ((c == RowClass::RowVecT || c == RowClass::ColVec || c == RowClass::ColVecT) && !from_param && !from_load)
+            return no("computed broadcast vector");
+        a.row_class[v.id] = c;
+    }
+    for (size_t i = 0; i < k.ops.size(); ++i) {
+        const auto& op = k.ops[i];
+        if (op.kind == OpKind::Store) {
+            RowClass s = a.row_class[op.operands[1]];
+            if (s != RowClass::Full && s != RowClass::RowVec) return no("store of a broadcast vector");
+        }
+        if (op.kind == OpKind::RowSum || op.kind == OpKind::RowMax || op.kind == OpKind::RowMean) {
+            RowClass s = a.row_class[op.operands[0]];
+            if (s != RowClass::Full && !(s == RowClass::RowVec && C == 1)) return no("row reduction of a vector");
+        }
+    }
+    return true;
+}
+
+}  // namespace
+
+KernelAnalysis analyze_kernel(const KernelDef& k) {
+    KernelAnalysis a;
+    a.def = &k;
+    if (k.custom) refuse(k, "custom C++ kernel bodies (cpp_src / cpp_tu_path) have no HIP lowering");
+    for (const auto& v : k.values) a.max_id = std::max(a.max_id, v.id);
+    for (const auto& op : k.ops) a.max_id = std::max(a.max_id, op.result);
+    const int n = a.max_id + 1;
+    a.by_id.assign(n, nullptr);
+    a.param_of.assign(n, -1);
+    a.preload.assign(n, false);
+    a.acc_vec.assign(n, false);
+    for (const auto& v : k.values) {
+        if (v.id <= 0) refuse(k, "bad value id");
+        a.by_id[v.id] = &v;
+    }
+    a.tensor_ordinal.assign(k.params.size(), -1);
+    a.scalar_ordinal.assign(k.params.size(), -1);
+    int nt = 0, ns = 0;
+    for (size_t i = 0; i < k.params.size(); ++i) {
+        int id = k.params[i].id;
+        if (id <= 0 || id >= n || !a.by_id[id]) refuse(k, "param " + k.params[i].name + " has no value");
+        a.param_of[id] = static_cast<int>(i);
+        if (a.by_id[id]->tile) {
+            a.tensor_ordinal[i] = nt++;
+            a.tensor_param_index.push_back(static_cast<int>(i));
+        } else {
+            a.scalar_ordinal[i] = ns++;
+        }
+    }
+    a.stored.assign(nt, false);
+    a.read.assign(nt, false);
+    a.bin_mode.assign(k.ops.size(), BinMode::Same);
+
+    auto val = [&](int id) -> const ValueInfo* {
+        if (id <= 0 || id >= n || !a.by_id[id]) refuse(k, "op references undefined value " + std::to_string(id));
+        return a.by_id[id];
+    };
+    // Scalars that have a value: scalar params and Constant() results (:605-655).
+    std::vector<bool> scalar_known(n, false);
+    for (size_t i = 0; i < k.params.size(); ++i)
+        if (!a.by_id[k.params[i].id]->tile) {
+            DType d = a.by_id[k.params[i].id]->dtype;
+            if (d != DType::F32 && d != DType::I32 && d != DType::I64 && d != DType::Bool)
+                refuse(k, "unsupported scalar param dtype " + std::string(dtype_name(d)));
+            scalar_known[k.params[i].id] = true;
+        }
+    for (const auto& op : k.ops) {
+        if (op.kind != OpKind::Constant || op.result <= 0) continue;
+        const ValueInfo* r = val(op.result);
+        if (r->tile) refuse(k, "tile-shaped Constant ops have no compute in the reference lowering");
+        if (!op.has_value) continue;
+        if (dtype_is_float(r->dtype) && r->dtype != DType::F32) refuse(k, "unsupported constant dtype");
+        scalar_known[op.result] = true;
+    }
+
+    // Param tiles TLOADed at entry: used by any op except Matmul and Load,
+    // excluding a Store destination (:453-469).
+    for (const auto& op : k.ops) {
+        if (op.kind == OpKind::Matmul || op.kind == OpKind::Load) continue;
+        for (size_t j = 0; j < op.operands.size(); ++j) {
+            const ValueInfo* v = val(op.operands[j]);
+            if (!v->tile || a.param_of[v->id] < 0) continue;
+            if (op.kind == OpKind::Store && j == 0) continue;
+            a.preload[v->id] = true;
+        }
+    }
+    // Matmul results read by vector ops get a TMOV into a vector tile (:700-710).
+    for (const auto& op : k.ops) {
+        if (op.kind == OpKind::Matmul || op.kind == OpKind::Store) continue;
+        for (int id : op.operands) {
+            if (a.param_of[id] >= 0) continue;
+            for (const auto& q : k.ops)
+                if (q.kind == OpKind::Matmul && q.result == id) a.acc_vec[id] = true;
+        }
+    }
+
+    uint64_t cycles = 0;
+    for (size_t i = 0; i < k.params.size(); ++i) {
+        const ValueInfo* v = a.by_id[k.params[i].id];
+        if (v->tile && a.preload[v->id]) {
+            cycles += rc(v);
+            a.read[a.tensor_ordinal[i]] = true;
+        }
+    }
+    for (size_t oi = 0; oi < k.ops.size(); ++oi) {
+        const auto& op = k.ops[oi];
+        const ValueInfo* res = op.result > 0 ? val(op.result) : nullptr;
+        switch (op.kind) {
+            case OpKind::Constant: break;
+            case OpKind::Load: {
+                if (op.operands.empty()) refuse(k, "Load missing operand");
+                const ValueInfo* s = val(op.operands[0]);
+                if (a.param_of[s->id] < 0 || !s->tile) refuse(k, "Load src must be a kernel param tile");
+                if (!res || !res->tile) refuse(k, "Load without a tile result");
+                if (res->rows != s->rows || res->cols != s->cols || res->dtype != s->dtype) refuse(k, "Load shape mismatch");
+                a.read[a.tensor_ordinal[a.param_of[s->id]]] = true;
+                cycles += rc(s);
+                break;
+            }
+            case OpKind::Store: {
+                if (op.operands.size() < 2) refuse(k, "Store expects dst, src");
+                const ValueInfo* d = val(op.operands[0]);
+                const ValueInfo* s = val(op.operands[1]);
+                if (a.param_of[d->id] < 0 || !d->tile) refuse(k, "Store dst must be a kernel param tile");
+                if (!s->tile) refuse(k, "Store src must be a tile");
+                if (s->rows != d->rows || s->cols != d->cols)
+                    refuse(k, "Store of a " + std::to_string(s->rows) + "x" + std::to_string(s->cols) + " tile into a " +
+                                  std::to_string(d->rows) + "x" + std::to_string(d->cols) + " param");
+                const bool same = s->dtype == d->dtype;
+                const bool cast_ok = s->dtype == DType::F32 && (d->dtype == DType::F16 || d->dtype == DType::BF16);
+                if (!same && !cast_ok)
+                    refuse(k, std::string("Store dtype mismatch (unsupported cast ") + dtype_name(s->dtype) + " -> " +
+                                  dtype_name(d->dtype) + ")");
+                if (same && (d->dtype == DType::F64 || d->dtype == DType::Bool || d->dtype == DType::I8 ||
+                             d->dtype == DType::U8 || d->dtype == DType::I16 || d->dtype == DType::U16 ||
+                             d->dtype == DType::U32 || d->dtype == DType::U64))
+                    refuse(k, std::string("tiles of dtype ") + dtype_name(d->dtype) + " are not supported");
+                a.stored[a.tensor_ordinal[a.param_of[d->id]]] = true;
+                if (!same) cycles += rc(d);  // TCVT
+                cycles += rc(d);             // TSTORE
+                break;
+            }
+            case OpKind::Matmul: {
+                if (op.operands.size() < 2 || !res || !res->tile) refuse(k, "malformed Matmul");
+                const ValueInfo* av = val(op.operands[0]);
+                const ValueInfo* bv = val(op.operands[1]);
+                if (!av->tile || !bv->tile) refuse(k, "Matmul expects tile operands");
+                if (av->cols != bv->rows) refuse(k, "Matmul K mismatch");
+                const bool ok = (av->dtype == DType::F32 && bv->dtype == DType::F32) ||
+                                (av->dtype == DType::F16 && bv->dtype == DType::F16) ||
+                                (av->dtype == DType::BF16 && bv->dtype == DType::BF16);
+                if (!ok || res->dtype != DType::F32)
+                    refuse(k, std::string("Matmul: unsupported dtype combination ") + dtype_name(av->dtype) + " x " +
+                                  dtype_name(bv->dtype) + " -> " + dtype_name(res->dtype));
+                if (res->rows != av->rows || res->cols != bv->cols) refuse(k, "Matmul result shape mismatch");
+                for (int id : {av->id, bv->id})
+                    if (a.param_of[id] >= 0) a.read[a.tensor_ordinal[a.param_of[id]]] = true;
+                const uint64_t M = av->rows, K = av->cols, N = bv->cols;
+                cycles += M * K + K * N + M * K * N;
+                if (a.acc_vec[res->id]) cycles += M * N;
+                break;
+            }
+            case OpKind::Add: case OpKind::Sub: case OpKind::Mul: case OpKind::Div: case OpKind::Max: case OpKind::Min: {
+                if (op.operands.size() != 2 || !res) refuse(k, "binary op missing result/operands");
+                if (!res->tile) refuse(k, "binary op with a scalar result has no tile lowering");
+                const ValueInfo* av = val(op.operands[0]);
+                const ValueInfo* bv = val(op.operands[1]);
+                if (!av->tile && !scalar_known[av->id]) refuse(k, "scalar operand has no value");
+                if (!bv->tile && !scalar_known[bv->id]) refuse(k, "scalar operand has no value");
+                if (!av->tile && !bv->tile) refuse(k, "binary op on two scalars has no tile lowering");
+                if (dtype_is_float(res->dtype) && res->dtype != DType::F32)
+                    refuse(k, std::string("vector ops on ") + dtype_name(res->dtype) + " tiles are not supported");
+                if (!av->tile || !bv->tile) {
+                    const ValueInfo* tv = av->tile ? av : bv;
+                    const ValueInfo* sv = av->tile ? bv : av;
+                    if (!av->tile && op.kind == OpKind::Sub) refuse(k, "Sub: scalar - tile not supported");
+                    if (tv->rows != res->rows || tv->cols != res->cols) refuse(k, "scalar op shape mismatch");
+                    if (is_int(tv->dtype) != is_int(sv->dtype) || tv->dtype != res->dtype)
+                        refuse(k, "mixed int/float scalar op");
+                    a.bin_mode[oi] = av->tile ? BinMode::ScalarRight : BinMode::ScalarLeft;
+                } else {
+                    const int R = res->rows, C = res->cols;
+                    if (av->rows != R || av->cols != C) refuse(k, "Binary op broadcast pattern unsupported");
+                    if (av->dtype != res->dtype || bv->dtype != res->dtype) refuse(k, "mixed dtype tile op");
+                    if (bv->rows == R && bv->cols == C) a.bin_mode[oi] = BinMode::Same;
+                    else if ((bv->rows == R && bv->cols == 1) || (bv->rows == 1 && bv->cols == R))
+                        a.bin_mode[oi] = BinMode::RowExpand;
+                    else if ((op.kind == OpKind::Sub || op.kind == OpKind::Mul || op.kind == OpKind::Div) &&
+                             ((bv->rows == 1 && bv->cols == C) || (bv->rows == C && bv->cols == 1)))
+                        a.bin_mode[oi] = BinMode::ColExpand;
+                    else refuse(k, "Binary op broadcast pattern unsupported");
+                }
+                cycles += rc(res);
+                break;
+            }
+            case OpKind::Exp: case OpKind::Rsqrt: {
+                if (op.operands.size() != 1 || !res || !res->tile) refuse(k, "unary op expects a tile");
+                const ValueInfo* s = val(op.operands[0]);
+                if (!s->tile || s->dtype != DType::F32 || res->dtype != DType::F32) refuse(k, "Exp/Rsqrt need f32 tiles");
+                if (s->rows != res->rows || s->cols != res->cols) refuse(k, "unary op shape mismatch");
+                cycles += rc(res);
+                break;
+            }
+            case OpKind::RowSum: case OpKind::RowMax: case OpKind::RowMean: {
+                if (op.operands.size() != 1 || !res || !res->tile) refuse(k, "row reduce expects a tile");
+                const ValueInfo* s = val(op.operands[0]);
+                if (!s->tile) refuse(k, "row reduce expects a tile operand");
+                if (res->rows != s->rows || res->cols != 1) refuse(k, "row reduce result shape");
+                if (is_int(s->dtype) != is_int(res->dtype)) refuse(k, "row reduce dtype mismatch");
+                if (dtype_is_float(s->dtype) && s->dtype != DType::F32) refuse(k, "row reduce of non-f32 tiles");
+                cycles += static_cast<uint64_t>(res->rows) * (op.kind == OpKind::RowMean ? 2u : 1u);
+                break;
+            }
+            default:
+                // The reference emitter adds r*c cycles and computes nothing
+                // for these (:1223-1231); this backend refuses them.
+                refuse(k, "op '" + op.kind_name + "' has no compute in the reference cpu_sim lowering");
+        }
+    }
+    a.cycles = cycles;
+    for (size_t i = 0; i < a.tensor_param_index.size(); ++i) {
+        const ValueInfo* v = a.by_id[k.params[a.tensor_param_index[i]].id];
+        if (!dtype_is_float(v->dtype) && v->dtype != DType::I32 && v->dtype != DType::I64)
+            refuse(k, std::string("tensor params of dtype ") + dtype_name(v->dtype) + " are not supported");
+        if (v->dtype == DType::F64) refuse(k, "f64 tensor params are not supported");
+    }
+    a.family = classify_rows(k, a) ? Family::RowProgram : Family::TileProgram;
+    return a;
+}
+
+}  // namespace ptowsp

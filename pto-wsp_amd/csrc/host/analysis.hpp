@@ -1,0 +1,47 @@
+// Per-kernel analysis: validation against the reference lowering rules,
+// the static cpu_sim cycle cost of one task, and the choice of device
+// template family.
+#pragma once
+
+#include <cstdint>
+#include <string>
+#include <vector>
+
+#include "module.hpp"
+
+namespace ptowsp {
+
+// How a binary op combines its operands (src/python/pto_codegen.cpp:1078-1107).
+enum class BinMode { Same, RowExpand, ColExpand, ScalarRight, ScalarLeft };
+
+enum class Family { RowProgram, TileProgram, Gemm };
+
+// Role of a value inside a row program.
+enum class RowClass { None, Full, RowVec, RowVecT, ColVec, ColVecT, Scalar };
+
+struct KernelAnalysis {
+    const KernelDef* def = nullptr;
+    int max_id = 0;
+    std::vector<const ValueInfo*> by_id;   // value id -> info
+    std::vector<int> param_of;             // value id -> param index, -1
+    std::vector<int> tensor_ordinal;       // param index -> tensor-param ordinal, -1
+    std::vector<int> scalar_ordinal;       // param index -> scalar-param ordinal, -1
+    std::vector<int> tensor_param_index;   // tensor ordinal -> param index
+    std::vector<bool> preload;             // value id: param tile TLOADed at entry
+    std::vector<bool> acc_vec;             // value id: matmul result moved to a vector tile
+    std::vector<bool> stored;              // tensor ordinal: written by a Store
+    std::vector<bool> read;                // tensor ordinal: read (preload, Load, Matmul operand)
+    std::vector<BinMode> bin_mode;         // per op (binary ops only)
+    uint64_t cycles = 0;                   // cpu_sim cycles of one task
+
+    Family family = Family::TileProgram;
+    // Row-program shape: every Full value is [rows, cols].
+    int rows = 0, cols = 0;
+    std::vector<RowClass> row_class;       // value id -> class
+    std::string not_row_reason;
+};
+
+// Throws CompileError for kernels the reference lowering cannot compute.
+KernelAnalysis analyze_kernel(const KernelDef& k);
+
+}  // namespace ptowsp

@@ -1,0 +1,473 @@
+// Emits the HIP source of one launch.  The op-by-op lowering restates the
+// reference kernel emitter's semantics (src/python/pto_codegen.cpp:471-1241):
+// preloaded param tiles, TLOAD/TSTORE through strides s3/s4, the same
+// broadcast rules, RowMean as a sum divided by the column count, Rsqrt as
+// 1/sqrt, Matmul as an fp32 accumulation that ignores a third operand.
+#include "emit.hpp"
+
+#include <cstdio>
+#include <set>
+#include <sstream>
+
+#include "../device/ptowsp_launch.h"
+
+namespace ptowsp {
+
+namespace {
+
+std::string flt(double v) {
+    char buf[64];
+    std::snprintf(buf, sizeof buf, "%.17g", v);
+    return std::string("((float)(") + buf + "))";
+}
+
+const char* op_functor(OpKind k) {
+    switch (k) {
+        case OpKind::Add: return "OpAdd";
+        case OpKind::Sub: return "OpSub";
+        case OpKind::Mul: return "OpMul";
+        case OpKind::Div: return "OpDiv";
+        case OpKind::Max: return "OpMax";
+        case OpKind::Min: return "OpMin";
+        default: return "OpAdd";
+    }
+}
+
+int dt_code(DType d) { return static_cast<int>(d); }
+
+// Declarations of scalar params and Constant() values (:607-655).
+void emit_scalars(std::ostringstream& o, const KernelAnalysis& a, bool int_ok) {
+    const KernelDef& k = *a.def;
+    for (size_t i = 0; i < k.params.size(); ++i) {
+        const ValueInfo* v = a.by_id[k.params[i].id];
+        if (v->tile) continue;
+        const int so = a.scalar_ordinal[i];
+        if (so >= kMaxScalars) throw CompileError("kernel " + k.name + ": too many scalar params");
+        if (v->dtype == DType::F32)
+            o << "  const float s" << v->id << " = bits_f32(A.scal[" << so << "]);\n";
+        else if (!int_ok)
+            throw CompileError("kernel " + k.name + ": integer scalars need the tile-program lowering");
+        else if (v->dtype == DType::I32)
+            o << "  const i64 s" << v->id << " = (i64)(int)(u32)A.scal[" << so << "];\n";
+        else if (v->dtype == DType::I64)
+            o << "  const i64 s" << v->id << " = (i64)A.scal[" << so << "];\n";
+        else
+            o << "  const i64 s" << v->id << " = A.scal[" << so << "] != 0ull ? 1 : 0;\n";
+    }
+    for (const auto& op : k.ops) {
+        if (op.kind != OpKind::Constant || op.result <= 0) continue;
+        const ValueInfo* v = a.by_id[op.result];
+        if (v->tile || !op.has_value) continue;
+        if (v->dtype == DType::F32) {
+            o << "  const float s" << v->id << " = " << flt(op.value) << ";\n";
+        } else {
+            if (!int_ok) throw CompileError("kernel " + k.name + ": integer constants need the tile-program lowering");
+            o << "  const i64 s" << v->id << " = (i64)(" << static_cast<long long>(op.value) << "LL);\n";
+        }
+    }
+}
+
+// vars[0..ng) from the task index t (mixed radix, innermost grid loop fastest).
+void emit_decode(std::ostringstream& o, const std::string& ind, int ng, const std::string& t) {
+    if (ng == 0) return;
+    o << ind << "{ i64 q_ = " << t << ";\n";
+    for (int v = ng - 1; v >= 1; --v)
+        o << ind << "  vars[" << v << "] = q_ % A.ext[" << v << "]; q_ /= A.ext[" << v << "];\n";
+    o << ind << "  vars[0] = q_; }\n";
+}
+
+// Element offset expression of tensor ordinal p: affine part + indirect terms.
+std::string offset_expr(int p, int nvars, int first_term, int nterms) {
+    std::ostringstream e;
+    e << "(i64)0";
+    for (int v = 0; v < nvars; ++v) e << " + A.coef[" << p << "][" << v << "] * vars[" << v << "]";
+    for (int k = 0; k < nterms; ++k) e << " + indirect_index(A, " << (first_term + k) << ", vars, " << nvars << ")";
+    return e.str();
+}
+
+}  // namespace
+
+RowLayout row_layout(int cols, int vw) {
+    RowLayout l;
+    l.vw = vw;
+    const int n = cols / vw;
+    int g = 1;
+    while (g < 64 && n % (g * 2) == 0) g *= 2;
+    l.g = g;
+    l.nv = n / g;
+    int up = 32 / (l.nv * vw);
+    l.up = up < 1 ? 1 : (up > 8 ? 8 : up);
+    return l;
+}
+
+namespace {
+
+// ---------------------------------------------------------------------------
+// Row programs
+// ---------------------------------------------------------------------------
+EmittedKernel emit_row(const Module& m, const KernelAnalysis& a, const LaunchSpec& L, const EmitSpec& spec) {
+    (void)m;
+    const KernelDef& k = *a.def;
+    const RowLayout lay = row_layout(a.cols, spec.vec_width);
+    const int R = a.rows, C = a.cols, ng = static_cast<int>(L.grid.size());
+    const int rpw = 64 / lay.g, ch = rpw * lay.up;
+    const bool chunk_in_task = R % ch == 0;
+    const int ntens = static_cast<int>(a.tensor_param_index.size());
+    auto cls = [&](int id) { return a.row_class[id]; };
+    auto vname = [&](int id) { return (a.by_id[id]->tile ? "v" : "s") + std::to_string(id); };
+    auto tord = [&](int id) { return a.tensor_ordinal[a.param_of[id]]; };
+
+    // Values loaded up front: preloaded params and Load results.
+    std::vector<std::pair<int, int>> loads;  // value id, tensor ordinal
+    for (size_t i = 0; i < k.params.size(); ++i) {
+        const ValueInfo* v = a.by_id[k.params[i].id];
+        if (v->tile && a.preload[v->id]) loads.emplace_back(v->id, a.tensor_ordinal[i]);
+    }
+    for (const auto& op : k.ops)
+        if (op.kind == OpKind::Load) loads.emplace_back(op.result, tord(op.operands[0]));
+
+    // A stored tensor that is also read: wait for outstanding loads before stores.
+    std::set<int> read_t, stored_t;
+    for (const auto& [id, p] : loads) read_t.insert(L.targs[p]->tid);
+    for (int p = 0; p < ntens; ++p)
+        if (a.stored[p]) stored_t.insert(L.targs[p]->tid);
+    bool rw_alias = false;
+    for (int t : stored_t)
+        if (read_t.count(t)) rw_alias = true;
+
+    EmittedKernel ek;
+    ek.row_program = true;
+    ek.threads = 256;
+    ek.waves_per_block = 4;
+    ek.rows_per_chunk = ch;
+    std::ostringstream o;
+    o << "#include \"ptowsp_device.h\"\nusing namespace ptowsp;\n";
+    o << "// row program: kernel " << k.name << ", rows " << R << " x cols " << C << ", vw " << lay.vw << "\n";
+    o << "extern \"C\" __global__ void __launch_bounds__(256) ptowsp_entry(const LaunchArgs A) {\n";
+    o << "  constexpr int R = " << R << ", NV = " << lay.nv << ", VW = " << lay.vw << ", G = " << lay.g
+      << ", UP = " << lay.up << ";\n";
+    o << "  constexpr int RPW = 64 / G, CH = RPW * UP, WPB = 4;\n";
+    o << "  typedef RowSlice<NV, VW> RS;\n";
+    o << "  const int lane = threadIdx.x & 63, wave = threadIdx.x >> 6, team = lane / G, j = lane % G;\n";
+    o << "  (void)team; (void)j;\n";
+    emit_scalars(o, a, false);
+    o << "  const i64 total = A.ntasks * R;\n";
+    o << "  const i64 nch = (total + CH - 1) / CH;\n";
+    o << "  i64 vars[" << (ng > 0 ? ng : 1) << "];\n  (void)vars;\n";
+    o << "  for (i64 ch = (i64)blockIdx.x * WPB + wave; ch < nch; ch += (i64)gridDim.x * WPB) {\n";
+    o << "    int rr[UP]; bool ok[UP];\n";
+    for (int p = 0; p < ntens; ++p) o << "    char* tb" << p << "[UP];\n";
+    if (chunk_in_task) {
+        o << "    const i64 t = (ch * CH) / R;\n    const int r0 = (int)(ch * CH - t * R);\n";
+        emit_decode(o, "    ", ng, "t");
+        for (int p = 0; p < ntens; ++p) {
+            const int es = dtype_size(a.by_id[k.params[a.tensor_param_index[p]].id]->dtype);
+            o << "    char* b" << p << " = A.base[" << p << "] + (" << offset_expr(p, ng, 0, 0) << ") * " << es << ";\n";
+        }
+        o << "#pragma unroll\n    for (int u = 0; u < UP; ++u) {\n      rr[u] = r0 + u * RPW + team; ok[u] = true;\n";
+        for (int p = 0; p < ntens; ++p) o << "      tb" << p << "[u] = b" << p << ";\n";
+        o << "    }\n";
+    } else {
+        o << "#pragma unroll\n    for (int u = 0; u < UP; ++u) {\n";
+        o << "      i64 g = ch * CH + u * RPW + team; ok[u] = g < total; if (!ok[u]) g = 0;\n";
+        o << "      const i64 t = g / R; rr[u] = (int)(g - t * R);\n";
+        emit_decode(o, "      ", ng, "t");
+        for (int p = 0; p < ntens; ++p) {
+            const int es = dtype_size(a.by_id[k.params[a.tensor_param_index[p]].id]->dtype);
+            o << "      tb" << p << "[u] = A.base[" << p << "] + (" << offset_expr(p, ng, 0, 0) << ") * " << es << ";\n";
+        }
+        o << "    }\n";
+    }
+    // Phase 1: every load of the chunk, so UP*NV vector loads per value are in flight.
+    for (const auto& [id, p] : loads) {
+        switch (cls(id)) {
+            case RowClass::Full:
+                o << "    RS ld" << id << "[UP];\n#pragma unroll\n    for (int u = 0; u < UP; ++u) row_load<NV, VW, G>(ld" << id
+                  << "[u], (const float*)tb" << p << "[u] + (i64)rr[u] * A.s3[" << p << "], A.s4[" << p << "], j);\n";
+                break;
+            case RowClass::RowVec:
+                o << "    float ld" << id << "[UP];\n#pragma unroll\n    for (int u = 0; u < UP; ++u) ld" << id
+                  << "[u] = ((const float*)tb" << p << "[u])[(i64)rr[u] * A.s3[" << p << "]];\n";
+                break;
+            case RowClass::RowVecT:
+                o << "    float ld" << id << "[UP];\n#pragma unroll\n    for (int u = 0; u < UP; ++u) ld" << id
+                  << "[u] = ((const float*)tb" << p << "[u])[(i64)rr[u] * A.s4[" << p << "]];\n";
+                break;
+            case RowClass::ColVec:
+                o << "    RS ld" << id << "[UP];\n#pragma unroll\n    for (int u = 0; u < UP; ++u) row_load<NV, VW, G>(ld" << id
+                  << "[u], (const float*)tb" << p << "[u], A.s4[" << p << "], j);\n";
+                break;
+            case RowClass::ColVecT:
+                o << "    RS ld" << id << "[UP];\n#pragma unroll\n    for (int u = 0; u < UP; ++u) row_load_strided<NV, VW, G>(ld"
+                  << id << "[u], (const float*)tb" << p << "[u], A.s3[" << p << "], j);\n";
+                break;
+            default: throw CompileError("row program: bad load class");
+        }
+    }
+    // Phase 2: compute and store each pass.
+    o << "#pragma unroll\n    for (int u = 0; u < UP; ++u) {\n";
+    for (const auto& [id, p] : loads) {
+        const RowClass c = cls(id);
+        if (c == RowClass::RowVec || c == RowClass::RowVecT) o << "      const float v" << id << " = ld" << id << "[u];\n";
+        else o << "      const RS& v" << id << " = ld" << id << "[u];\n";
+    }
+    bool waited = false;
+    for (size_t oi = 0; oi < k.ops.size(); ++oi) {
+        const auto& op = k.ops[oi];
+        switch (op.kind) {
+            case OpKind::Constant:
+            case OpKind::Load:
+                break;
+            case OpKind::Store: {
+                const int d = op.operands[0], s = op.operands[1];
+                const int p = tord(d);
+                if (rw_alias && !waited) {
+                    o << "      __builtin_amdgcn_s_waitcnt(0);\n";
+                    waited = true;
+                }
+                if (cls(s) == RowClass::Full)
+                    o << "      if (ok[u]) row_store<NV, VW, G>((float*)tb" << p << "[u] + (i64)rr[u] * A.s3[" << p << "], "
+                      << vname(s) << ", A.s4[" << p << "], j);\n";
+                else
+                    o << "      if (ok[u] && j == 0) ((float*)tb" << p << "[u])[(i64)rr[u] * A.s3[" << p << "]] = " << vname(s)
+                      << ";\n";
+                break;
+            }
+            case OpKind::Add: case OpKind::Sub: case OpKind::Mul: case OpKind::Div: case OpKind::Max: case OpKind::Min: {
+                const int r = op.result, x = op.operands[0], y = op.operands[1];
+                const char* F = op_functor(op.kind);
+                const bool full = cls(r) == RowClass::Full;
+                const std::string ty = full ? "RS" : "float";
+                o << "      const " << ty << " v" << r << " = ";
+                switch (a.bin_mode[oi]) {
+                    case BinMode::Same:
+                        o << (full ? std::string("ew<") + F + ">(" : std::string(F) + "::f(") << vname(x) << ", " << vname(y) << ");\n";
+                        break;
+                    case BinMode::RowExpand:
+                        o << (full ? std::string("ew_rs<") + F + ">(" : std::string(F) + "::f(") << vname(x) << ", " << vname(y) << ");\n";
+                        break;
+                    case BinMode::ColExpand:
+                        o << "ew<" << F << ">(" << vname(x) << ", " << vname(y) << ");\n";
+                        break;
+                    case BinMode::ScalarRight:
+                        o << (full ? std::string("ew_rs<") + F + ">(" : std::string(F) + "::f(") << vname(x) << ", " << vname(y) << ");\n";
+                        break;
+                    case BinMode::ScalarLeft:
+                        if (op.kind == OpKind::Div)
+                            o << (full ? std::string("ew_sr<OpDiv>(") : std::string("OpDiv::f(")) << vname(x) << ", " << vname(y)
+                              << ");\n";
+                        else
+                            o << (full ? std::string("ew_rs<") + F + ">(" : std::string(F) + "::f(") << vname(y) << ", " << vname(x)
+                              << ");\n";
+                        break;
+                }
+                break;
+            }
+            case OpKind::Exp:
+            case OpKind::Rsqrt: {
+                const int r = op.result, x = op.operands[0];
+                const bool full = cls(r) == RowClass::Full;
+                if (full) o << "      const RS v" << r << " = " << (op.kind == OpKind::Exp ? "ew_exp(" : "ew_rsqrt(") << vname(x) << ");\n";
+                else o << "      const float v" << r << " = " << (op.kind == OpKind::Exp ? "expf(" : "rsqrt_cr(") << vname(x) << ");\n";
+                break;
+            }
+            case OpKind::RowSum:
+            case OpKind::RowMax:
+            case OpKind::RowMean: {
+                const int r = op.result, x = op.operands[0];
+                const int src_cols = a.by_id[x]->cols;
+                o << "      const float v" << r << " = ";
+                if (cls(x) == RowClass::Full) {
+                    if (op.kind == OpKind::RowMax) o << "team_max<G>(lane_max<NV * VW>(" << vname(x) << ".v))";
+                    else o << "team_sum<G>(lane_sum<NV * VW>(" << vname(x) << ".v))";
+                } else {
+                    o << vname(x);
+                }
+                if (op.kind == OpKind::RowMean) o << " / " << flt(static_cast<double>(src_cols));
+                o << ";\n";
+                break;
+            }
+            default: throw CompileError("row program: unexpected op " + op.kind_name);
+        }
+    }
+    o << "    }\n  }\n}\n";
+    ek.source = o.str();
+    ek.entry = "ptowsp_entry";
+    return ek;
+}
+
+// ---------------------------------------------------------------------------
+// Tile programs
+// ---------------------------------------------------------------------------
+EmittedKernel emit_tile(const Module& m, const KernelAnalysis& a, const LaunchSpec& L, const EmitSpec& spec) {
+    (void)m;
+    const KernelDef& k = *a.def;
+    const int ng = static_cast<int>(L.grid.size()), ni = static_cast<int>(L.inner.size());
+    const int nvars = ng + ni;
+    const int ntens = static_cast<int>(a.tensor_param_index.size());
+    auto is_int_v = [&](int id) { return !dtype_is_float(a.by_id[id]->dtype); };
+    auto tord = [&](int id) { return a.param_of[id] >= 0 ? a.tensor_ordinal[a.param_of[id]] : -1; };
+
+    // LDS tiles: op results, preloaded params.
+    std::set<int> lds_vals;
+    for (const auto& op : k.ops)
+        if (op.result > 0 && a.by_id[op.result]->tile) lds_vals.insert(op.result);
+    for (const auto& p : k.params)
+        if (a.by_id[p.id]->tile && a.preload[p.id]) lds_vals.insert(p.id);
+    size_t lds = 0;
+    for (int id : lds_vals) lds += static_cast<size_t>(a.by_id[id]->rows) * a.by_id[id]->cols * (is_int_v(id) ? 8 : 4);
+    if (lds > 160 * 1024)
+        throw CompileError("kernel " + k.name + ": tiles need " + std::to_string(lds) +
+                           " bytes of LDS, more than the 160 KiB of a gfx950 workgroup");
+
+    EmittedKernel ek;
+    ek.row_program = false;
+    ek.threads = spec.threads;
+    ek.lds_bytes = lds;
+    std::ostringstream o;
+    o << "#include \"ptowsp_device.h\"\nusing namespace ptowsp;\n";
+    o << "// tile program: kernel " << k.name << "\n";
+    o << "extern \"C\" __global__ void __launch_bounds__(" << spec.threads << ") ptowsp_entry(const LaunchArgs A) {\n";
+    o << "  constexpr int NT = " << spec.threads << ";\n";
+    for (int id : lds_vals) {
+        const ValueInfo* v = a.by_id[id];
+        o << "  __shared__ " << (is_int_v(id) ? "i64" : "float") << " L" << id << "[" << v->rows * v->cols << "];\n";
+    }
+    emit_scalars(o, a, true);
+    o << "  i64 vars[" << (nvars > 0 ? nvars : 1) << "];\n  (void)vars;\n";
+    o << "  for (i64 t = blockIdx.x; t < A.ntasks; t += gridDim.x) {\n";
+    emit_decode(o, "    ", ng, "t");
+    std::string ind = "    ";
+    for (int i = 0; i < ni; ++i) {
+        const int v = ng + i;
+        const int term = spec.inner_dyn_term.size() > static_cast<size_t>(i) ? spec.inner_dyn_term[i] : -1;
+        if (term >= 0) o << ind << "const i64 e" << i << " = indirect_index(A, " << term << ", vars, " << v << ");\n";
+        else o << ind << "const i64 e" << i << " = A.ext[" << v << "];\n";
+        o << ind << "for (vars[" << v << "] = 0; vars[" << v << "] < e" << i << "; ++vars[" << v << "]) {\n";
+        ind += "  ";
+    }
+    // Tile pointers with a per-task bounds check (indirect and run-time extents
+    // cannot all be checked on the host).
+    int term = 0;
+    for (int p = 0; p < ntens; ++p) {
+        const ValueInfo* v = a.by_id[k.params[a.tensor_param_index[p]].id];
+        const int nt = spec.indirect_count.size() > static_cast<size_t>(p) ? spec.indirect_count[p] : 0;
+        o << ind << "const i64 o" << p << " = " << offset_expr(p, nvars, term, nt) << ";\n";
+        term += nt;
+        o << ind << "if (o" << p << " < 0 || o" << p << " + (i64)" << (v->rows - 1) << " * A.s3[" << p << "] + (i64)" << (v->cols - 1)
+          << " * A.s4[" << p << "] >= A.span[" << p << "]) { if (threadIdx.x == 0) *A.err = 2; continue; }\n";
+        o << ind << "char* p" << p << " = A.base[" << p << "] + o" << p << " * " << dtype_size(v->dtype) << ";\n";
+    }
+    // Preloads (:764-779).
+    for (size_t i = 0; i < k.params.size(); ++i) {
+        const ValueInfo* v = a.by_id[k.params[i].id];
+        if (!v->tile || !a.preload[v->id]) continue;
+        const int p = a.tensor_ordinal[i];
+        o << ind << "tile_load_" << (is_int_v(v->id) ? "i" : "f") << "<" << dt_code(v->dtype) << ", " << v->rows << ", " << v->cols
+          << ", NT>(L" << v->id << ", p" << p << ", A.s3[" << p << "], A.s4[" << p << "]);\n";
+    }
+    o << ind << "__syncthreads();\n";
+    auto src = [&](int id, const std::string& e) {
+        return a.by_id[id]->tile ? "L" + std::to_string(id) + "[" + e + "]" : "s" + std::to_string(id);
+    };
+    for (size_t oi = 0; oi < k.ops.size(); ++oi) {
+        const auto& op = k.ops[oi];
+        const ValueInfo* res = op.result > 0 ? a.by_id[op.result] : nullptr;
+        switch (op.kind) {
+            case OpKind::Constant: continue;
+            case OpKind::Load: {
+                const ValueInfo* s = a.by_id[op.operands[0]];
+                const int p = tord(s->id);
+                o << ind << "tile_load_" << (is_int_v(s->id) ? "i" : "f") << "<" << dt_code(s->dtype) << ", " << s->rows << ", "
+                  << s->cols << ", NT>(L" << res->id << ", p" << p << ", A.s3[" << p << "], A.s4[" << p << "]);\n";
+                break;
+            }
+            case OpKind::Store: {
+                const ValueInfo* d = a.by_id[op.operands[0]];
+                const ValueInfo* s = a.by_id[op.operands[1]];
+                const int p = tord(d->id);
+                o << ind << "tile_store_" << (is_int_v(s->id) ? "i" : "f") << "<" << dt_code(d->dtype) << ", " << d->rows << ", "
+                  << d->cols << ", NT>(p" << p << ", L" << s->id << ", A.s3[" << p << "], A.s4[" << p << "]);\n";
+                break;
+            }
+            case OpKind::Matmul: {
+                const ValueInfo* av = a.by_id[op.operands[0]];
+                const ValueInfo* bv = a.by_id[op.operands[1]];
+                const int M = av->rows, K = av->cols, N = bv->cols;
+                auto elem = [&](const ValueInfo* v, const std::string& r, const std::string& c, int ld) {
+                    const int p = tord(v->id);
+                    if (p >= 0)
+                        return "gload_f<" + std::to_string(dt_code(v->dtype)) + ">(p" + std::to_string(p) + ", (i64)(" + r + ") * A.s3[" +
+                               std::to_string(p) + "] + (i64)(" + c + ") * A.s4[" + std::to_string(p) + "])";
+                    return "L" + std::to_string(v->id) + "[(" + r + ") * " + std::to_string(ld) + " + (" + c + ")]";
+                };
+                o << ind << "for (int e = threadIdx.x; e < " << M * N << "; e += NT) {\n";
+                o << ind << "  const int i = e / " << N << ", jj = e % " << N << ";\n";
+                o << ind << "  float acc = 0.0f;\n";
+                o << ind << "  for (int q = 0; q < " << K << "; ++q) acc = acc + " << elem(av, "i", "q", K) << " * "
+                  << elem(bv, "q", "jj", N) << ";\n";
+                o << ind << "  L" << res->id << "[e] = acc;\n" << ind << "}\n";
+                break;
+            }
+            case OpKind::Add: case OpKind::Sub: case OpKind::Mul: case OpKind::Div: case OpKind::Max: case OpKind::Min: {
+                const int x = op.operands[0], y = op.operands[1];
+                const int C = res->cols;
+                const char* F = op_functor(op.kind);
+                o << ind << "for (int e = threadIdx.x; e < " << res->rows * C << "; e += NT) L" << res->id << "[e] = ";
+                switch (a.bin_mode[oi]) {
+                    case BinMode::Same: o << F << "::f(" << src(x, "e") << ", " << src(y, "e") << ");\n"; break;
+                    case BinMode::RowExpand: o << F << "::f(" << src(x, "e") << ", " << src(y, "e / " + std::to_string(C)) << ");\n"; break;
+                    case BinMode::ColExpand: o << F << "::f(" << src(x, "e") << ", " << src(y, "e % " + std::to_string(C)) << ");\n"; break;
+                    case BinMode::ScalarRight: o << F << "::f(" << src(x, "e") << ", " << src(y, "e") << ");\n"; break;
+                    case BinMode::ScalarLeft:
+                        if (op.kind == OpKind::Div) o << "OpDiv::f(" << src(x, "e") << ", " << src(y, "e") << ");\n";
+                        else o << F << "::f(" << src(y, "e") << ", " << src(x, "e") << ");\n";
+                        break;
+                }
+                break;
+            }
+            case OpKind::Exp:
+            case OpKind::Rsqrt:
+                o << ind << "for (int e = threadIdx.x; e < " << res->rows * res->cols << "; e += NT) L" << res->id << "[e] = "
+                  << (op.kind == OpKind::Exp ? "expf(" : "rsqrt_cr(") << src(op.operands[0], "e") << ");\n";
+                break;
+            case OpKind::RowSum:
+            case OpKind::RowMax:
+            case OpKind::RowMean: {
+                const ValueInfo* s = a.by_id[op.operands[0]];
+                const std::string ty = is_int_v(s->id) ? "i64" : "float";
+                o << ind << "for (int r = threadIdx.x; r < " << s->rows << "; r += NT) {\n";
+                o << ind << "  " << ty << " acc = L" << s->id << "[r * " << s->cols << "];\n";
+                o << ind << "  for (int c = 1; c < " << s->cols << "; ++c) { const " << ty << " x = L" << s->id << "[r * " << s->cols
+                  << " + c]; acc = " << (op.kind == OpKind::RowMax ? "x > acc ? x : acc" : "acc + x") << "; }\n";
+                if (op.kind == OpKind::RowMean) {
+                    if (ty == "float") o << ind << "  acc = acc / " << flt(static_cast<double>(s->cols)) << ";\n";
+                    else o << ind << "  acc = acc / " << s->cols << ";\n";
+                }
+                o << ind << "  L" << res->id << "[r] = acc;\n" << ind << "}\n";
+                break;
+            }
+            default: throw CompileError("tile program: unexpected op " + op.kind_name);
+        }
+        o << ind << "__syncthreads();\n";
+    }
+    for (int i = ni - 1; i >= 0; --i) {
+        ind.resize(ind.size() - 2);
+        o << ind << "}\n";
+    }
+    o << "  }\n}\n";
+    ek.source = o.str();
+    ek.entry = "ptowsp_entry";
+    return ek;
+}
+
+}  // namespace
+
+EmittedKernel emit_launch(const Module& m, const KernelAnalysis& a, const LaunchSpec& L, const EmitSpec& spec) {
+    bool indirect = false;
+    for (int c : spec.indirect_count) indirect = indirect || c > 0;
+    if (a.family == Family::RowProgram && L.inner.empty() && !indirect) return emit_row(m, a, L, spec);
+    return emit_tile(m, a, L, spec);
+}
+
+}  // namespace ptowsp

@@ -1,0 +1,39 @@
+// HIP source emission for one launch of a traced kernel.
+#pragma once
+
+#include <string>
+#include <vector>
+
+#include "analysis.hpp"
+#include "plan.hpp"
+
+namespace ptowsp {
+
+// Launch-time facts a kernel is specialized on.
+struct EmitSpec {
+    int vec_width = 1;                 // row programs: 4, 2 or 1 floats per access
+    std::vector<int> indirect_count;   // per tensor ordinal: indirect index terms (in dim order)
+    std::vector<int> inner_dyn_term;   // per inner loop: indirect term index of its extent, or -1
+    int threads = 256;
+};
+
+struct EmittedKernel {
+    std::string source;
+    std::string entry;          // kernel symbol
+    int threads = 256;
+    int rows_per_chunk = 0;     // row programs: rows handled per wave iteration
+    int waves_per_block = 4;
+    bool row_program = false;
+    size_t lds_bytes = 0;
+};
+
+EmittedKernel emit_launch(const Module& m, const KernelAnalysis& a, const LaunchSpec& L, const EmitSpec& spec);
+
+// Parameters of the row-program layout for a row of `cols` floats with
+// accesses `vw` wide: lanes per row G, chunks per lane NV, unrolled passes UP.
+struct RowLayout {
+    int vw = 1, g = 1, nv = 1, up = 1;
+};
+RowLayout row_layout(int cols, int vw);
+
+}  // namespace ptowsp

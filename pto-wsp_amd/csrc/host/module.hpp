@@ -1,0 +1,138 @@
+// Codegen IR consumed by the HIP backend: tensors, kernel definitions and
+// the workload tree, parsed from the "PTOWSP-MODULE 1" text written by
+// pto_wsp/ir_bridge.py.
+//
+// Mirrors the reference's codegen attachments (include/pto/wsp/ir/codegen.hpp:22-77)
+// and the workload/axis/schedule nodes the cpu_sim emitter walks
+// (include/pto/wsp/ir/workload.hpp:15-54,92,119; axis.hpp:12-50;
+// schedule.hpp:13-36,211-231).  Extensions: affine and indirect index
+// expressions, and loop extents read from an int32 tensor element.
+#pragma once
+
+#include <cstdint>
+#include <map>
+#include <memory>
+#include <stdexcept>
+#include <string>
+#include <vector>
+
+namespace ptowsp {
+
+enum class DType : int { F16, BF16, F32, F64, I8, I16, I32, I64, U8, U16, U32, U64, Bool };
+
+const char* dtype_name(DType d);
+int dtype_size(DType d);
+bool dtype_is_float(DType d);
+
+struct CompileError : std::runtime_error {
+    using std::runtime_error::runtime_error;
+};
+
+struct TensorInfo {
+    DType dtype = DType::F32;
+    std::vector<int64_t> shape;
+};
+
+struct ValueInfo {
+    int id = 0;
+    DType dtype = DType::F32;
+    bool tile = false;
+    int rows = 0, cols = 0;
+};
+
+struct ParamInfo {
+    std::string name;
+    int id = 0;
+    std::string direction;
+};
+
+enum class OpKind { Load, Store, Add, Sub, Mul, Div, Max, Min, Exp, Rsqrt, RowSum, RowMax, RowMean, Matmul, Constant, Other };
+
+struct OpInfo {
+    OpKind kind = OpKind::Other;
+    std::string kind_name;
+    int result = -1;  // -1: no result
+    std::vector<int> operands;
+    bool has_value = false;
+    double value = 0.0;
+};
+
+struct KernelDef {
+    std::string name;
+    std::vector<ValueInfo> values;
+    std::vector<ParamInfo> params;
+    std::vector<OpInfo> ops;
+    bool custom = false;
+};
+
+struct IndexExpr {
+    char kind = 'c';  // v: loop var, c: constant, a: affine, t: element of an int32 tensor
+    std::string var;
+    int64_t c = 0;
+    std::vector<std::pair<std::string, int64_t>> terms;  // affine
+    int tid = -1, base_rank = 0;                          // indirect
+    std::vector<IndexExpr> idx;                           // indirect
+};
+
+struct ArgRef {
+    char kind = 'c';  // v: loop var, c: literal u64, s: runtime symbol
+    std::string var;
+    uint64_t u64 = 0;
+};
+
+struct TensorArg {
+    std::string param;
+    int tid = 0, base_rank = 0, view_rank = 0;
+    std::vector<IndexExpr> idx;
+};
+
+enum class AxisKind { Dense, Dyn, Ragged, DynTensor };
+
+struct Axis {
+    AxisKind kind = AxisKind::Dense;
+    int64_t size = 0;
+    std::string a, b;  // Dyn: runtime key; Ragged: outer / lengths symbol names
+    IndexExpr expr;    // DynTensor
+};
+
+enum class NodeKind { Empty, ParallelFor, ForEach, Combine, Sequential, Task, Select, Cond };
+
+struct Node {
+    NodeKind kind = NodeKind::Empty;
+    std::string var;
+    Axis axis;
+    std::unique_ptr<Node> body;
+    std::vector<std::unique_ptr<Node>> kids;
+    // task
+    std::string kernel;
+    int kernel_index = -1;
+    std::vector<ArgRef> axis_args, scalar_args;
+    std::vector<TensorArg> tensor_args;
+};
+
+struct Schedule {
+    bool has_dispatch = false;
+    std::string dispatch_policy;
+    int64_t num_targets = 0;
+    bool has_window = false;
+    int64_t window_size = 0;
+    std::string window_unit, window_overflow;
+    bool has_streams = false;
+    int64_t num_streams = 0;
+    bool stream_keyed = false;
+};
+
+struct Module {
+    std::string name;
+    std::vector<TensorInfo> tensors;
+    std::vector<KernelDef> kernels;
+    std::string workload_name;
+    std::unique_ptr<Node> root;
+    Schedule schedule;
+};
+
+Module parse_module(const std::string& text);
+
+uint64_t fnv1a_64(const std::string& s);
+
+}  // namespace ptowsp

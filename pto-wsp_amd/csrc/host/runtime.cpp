@@ -1,0 +1,825 @@
+// C ABI entry points of libptowsp_hip.so: compile, launch, synchronize and
+// the RuntimeContext tables.  See include/ptowsp_hip.h.
+#include <hip/hip_runtime_api.h>
+
+#include <algorithm>
+#include <chrono>
+#include <cstring>
+#include <map>
+#include <memory>
+#include <sstream>
+#include <string>
+#include <vector>
+
+#include "../device/ptowsp_launch.h"
+#include "analysis.hpp"
+#include "emit.hpp"
+#include "jit.hpp"
+#include "module.hpp"
+#include "plan.hpp"
+#include "ptowsp_hip.h"
+
+using namespace ptowsp;
+
+namespace {
+
+thread_local std::string g_last_error;
+
+void check(hipError_t e, const char* what) {
+    if (e != hipSuccess) throw std::runtime_error(std::string(what) + ": " + hipGetErrorString(e));
+}
+
+bool is_device_pointer(const void* p) {
+    hipPointerAttribute_t attr;
+    std::memset(&attr, 0, sizeof attr);
+    hipError_t e = hipPointerGetAttributes(&attr, p);
+    if (e != hipSuccess) {
+        (void)hipGetLastError();
+        return false;
+    }
+    return attr.type == hipMemoryTypeDevice || attr.type == hipMemoryTypeManaged;
+}
+
+struct TensorState {
+    char* host = nullptr;      // caller pointer when host-resident
+    char* dev = nullptr;       // device address used by kernels
+    std::vector<int64_t> stride;
+    int64_t span = 0;          // elements addressable from element 0
+    size_t bytes = 0;
+    bool staged = false;
+    bool written = false;
+};
+
+struct LaunchCache {
+    std::map<std::string, const JitKernel*> by_spec;
+    std::map<std::string, EmittedKernel> emitted;
+};
+
+}  // namespace
+
+struct ptowsp_program {
+    Module m;
+    std::vector<KernelAnalysis> ka;
+    Plan plan;
+    std::vector<LaunchCache> cache;
+    std::vector<bool> tensor_written;
+    std::vector<void*> stage_buf;
+    std::vector<size_t> stage_bytes;
+    struct CopyBack {
+        void* host;
+        const void* dev;
+        size_t bytes;
+    };
+    std::vector<CopyBack> copy_back;
+    hipStream_t stream = nullptr;
+    hipEvent_t ev0 = nullptr, ev1 = nullptr;
+    bool have_events = false;
+    bool pending = false;
+    int* d_err = nullptr;
+    double h2d_ms = 0.0;
+    std::string cycle_key;
+    CycleResult cycles;
+    bool cycles_valid = false;
+    std::string precompiled_source;
+
+    ~ptowsp_program() {
+        for (void* b : stage_buf)
+            if (b) (void)hipFree(b);
+        if (d_err) (void)hipFree(d_err);
+        if (ev0) (void)hipEventDestroy(ev0);
+        if (ev1) (void)hipEventDestroy(ev1);
+    }
+};
+
+struct ptowsp_runtime {
+    struct T {
+        void* ptr = nullptr;
+        std::vector<int64_t> strides;
+    };
+    std::map<uint32_t, T> tensors;
+    std::map<std::string, int64_t> axis;
+    std::map<uint64_t, uint64_t> sym;
+    std::map<uint64_t, void*> symp;
+    std::vector<uint64_t> slots = std::vector<uint64_t>(256, 0);
+    RuntimeContext ctx{};
+};
+
+namespace {
+
+int64_t rt_axis(void* c, const char* name) {
+    auto* rt = static_cast<ptowsp_runtime*>(c);
+    auto it = rt->axis.find(name ? name : "");
+    return it == rt->axis.end() ? 0 : it->second;
+}
+uint64_t rt_sym(void* c, uint64_t id) {
+    auto* rt = static_cast<ptowsp_runtime*>(c);
+    auto it = rt->sym.find(id);
+    return it == rt->sym.end() ? 0 : it->second;
+}
+void* rt_symp(void* c, uint64_t id) {
+    auto* rt = static_cast<ptowsp_runtime*>(c);
+    auto it = rt->symp.find(id);
+    return it == rt->symp.end() ? nullptr : it->second;
+}
+uint64_t rt_slot(void* c, uint32_t i) {
+    auto* rt = static_cast<ptowsp_runtime*>(c);
+    return i < rt->slots.size() ? rt->slots[i] : 0;
+}
+void rt_set_slot(void* c, uint32_t i, uint64_t v) {
+    auto* rt = static_cast<ptowsp_runtime*>(c);
+    if (i < rt->slots.size()) rt->slots[i] = v;
+}
+void* rt_tptr(void* c, uint32_t tid) {
+    auto* rt = static_cast<ptowsp_runtime*>(c);
+    auto it = rt->tensors.find(tid);
+    return it == rt->tensors.end() ? nullptr : it->second.ptr;
+}
+uint64_t rt_tstride(void* c, uint32_t tid, uint32_t dim) {
+    auto* rt = static_cast<ptowsp_runtime*>(c);
+    auto it = rt->tensors.find(tid);
+    if (it == rt->tensors.end() || dim >= it->second.strides.size()) return 0;
+    return static_cast<uint64_t>(it->second.strides[dim]);
+}
+KernelFn rt_kernel(void*, uint32_t) { return nullptr; }
+
+// ---------------------------------------------------------------------------
+// launch construction
+// ---------------------------------------------------------------------------
+
+struct RunEnv {
+    ptowsp_program* P;
+    RuntimeContext* ctx;
+    std::vector<TensorState> ts;
+    std::vector<std::pair<std::string, int64_t>> host_vars;
+};
+
+int64_t axis_extent(RunEnv& E, const Axis& a) {
+    switch (a.kind) {
+        case AxisKind::Dense: return a.size;
+        case AxisKind::Dyn: return E.ctx->get_axis_size(E.ctx->ctx, a.a.c_str());
+        case AxisKind::Ragged: {
+            const int64_t outer = static_cast<int64_t>(E.ctx->get_symbol_u64(E.ctx->ctx, fnv1a_64(a.a)));
+            const auto* len = static_cast<const int32_t*>(E.ctx->get_symbol_ptr(E.ctx->ctx, fnv1a_64(a.b)));
+            int64_t ub = 0;
+            if (len)
+                for (int64_t i = 0; i < outer; ++i) ub += len[i];
+            return ub;
+        }
+        case AxisKind::DynTensor: throw CompileError("internal: tensor-bound extent evaluated on the host");
+    }
+    return 0;
+}
+
+// Reads one int32 element of an index tensor (host or device resident).
+int64_t read_index_elem(RunEnv& E, int tid, int64_t off) {
+    const TensorState& t = E.ts[tid];
+    if (off < 0 || off >= t.span) throw std::runtime_error("index tensor element out of range");
+    int32_t v = 0;
+    if (t.host) std::memcpy(&v, t.host + off * 4, 4);
+    else check(hipMemcpy(&v, t.dev + off * 4, 4, hipMemcpyDeviceToHost), "hipMemcpy(index)");
+    return v;
+}
+
+int64_t eval_index_host(RunEnv& E, const IndexExpr& e, const std::vector<std::pair<std::string, int64_t>>& vars) {
+    auto lookup = [&](const std::string& n) -> int64_t {
+        for (auto it = vars.rbegin(); it != vars.rend(); ++it)
+            if (it->first == n) return it->second;
+        for (auto it = E.host_vars.rbegin(); it != E.host_vars.rend(); ++it)
+            if (it->first == n) return it->second;
+        throw std::runtime_error("unbound loop variable '" + n + "'");
+    };
+    switch (e.kind) {
+        case 'v': return lookup(e.var);
+        case 'c': return e.c;
+        case 'a': {
+            int64_t v = e.c;
+            for (const auto& [n, c] : e.terms) v += c * lookup(n);
+            return v;
+        }
+        case 't': {
+            if (E.P->m.tensors[e.tid].dtype != DType::I32) throw std::runtime_error("index tensors must be i32");
+            int64_t off = 0;
+            for (size_t d = 0; d < e.idx.size(); ++d) off += eval_index_host(E, e.idx[d], vars) * E.ts[e.tid].stride[d];
+            return read_index_elem(E, e.tid, off);
+        }
+    }
+    return 0;
+}
+
+// Affine decomposition: `scale * e` added into (constant, coef per loop var).
+struct Affine {
+    int64_t c = 0;
+    std::vector<int64_t> coef;
+};
+
+void add_affine(RunEnv& E, const IndexExpr& e, int64_t scale, const std::map<std::string, int>& loop_index, Affine& out) {
+    auto add_var = [&](const std::string& n, int64_t k) {
+        auto it = loop_index.find(n);
+        if (it != loop_index.end()) {
+            out.coef[it->second] += k;
+            return;
+        }
+        for (auto h = E.host_vars.rbegin(); h != E.host_vars.rend(); ++h)
+            if (h->first == n) {
+                out.c += k * h->second;
+                return;
+            }
+        throw std::runtime_error("unbound loop variable '" + n + "' in a tensor index");
+    };
+    switch (e.kind) {
+        case 'c': out.c += scale * e.c; break;
+        case 'v': add_var(e.var, scale); break;
+        case 'a':
+            out.c += scale * e.c;
+            for (const auto& [n, k] : e.terms) add_var(n, scale * k);
+            break;
+        default: throw std::runtime_error("internal: indirect index in an affine context");
+    }
+}
+
+struct BuiltLaunch {
+    LaunchArgs args{};
+    EmitSpec spec;
+    int64_t ntasks = 0;
+    bool host_checked = false;
+};
+
+// Row-program vector width allowed by the actual strides and alignment.
+int pick_vec_width(const KernelAnalysis& a, const LaunchArgs& A, int nvars) {
+    for (int vw : {4, 2}) {
+        if (a.cols % vw) continue;
+        bool ok = true;
+        for (size_t p = 0; p < a.tensor_param_index.size() && ok; ++p) {
+            const int id = a.def->params[a.tensor_param_index[p]].id;
+            const RowClass c = a.row_class[id];
+            if (c != RowClass::Full && c != RowClass::ColVec) continue;
+            if (A.s4[p] != 1) ok = false;
+            if (reinterpret_cast<uintptr_t>(A.base[p]) % (vw * 4)) ok = false;
+            if (c == RowClass::Full && A.s3[p] % vw) ok = false;
+            for (int v = 0; v < nvars; ++v)
+                if (A.coef[p][v] % vw) ok = false;
+        }
+        if (ok) return vw;
+    }
+    return 1;
+}
+
+BuiltLaunch build_launch(RunEnv& E, const LaunchSpec& L) {
+    ptowsp_program* P = E.P;
+    const KernelAnalysis& a = P->ka[L.kernel];
+    const KernelDef& k = P->m.kernels[L.kernel];
+    BuiltLaunch B;
+    LaunchArgs& A = B.args;
+    const int ng = static_cast<int>(L.grid.size()), ni = static_cast<int>(L.inner.size());
+    const int nvars = ng + ni;
+    std::map<std::string, int> loop_index;
+    for (int v = 0; v < nvars; ++v) loop_index[v < ng ? L.grid[v].var : L.inner[v - ng].var] = v;
+
+    B.ntasks = 1;
+    for (int v = 0; v < ng; ++v) {
+        A.ext[v] = axis_extent(E, *L.grid[v].axis);
+        if (A.ext[v] < 0) throw std::runtime_error("negative axis extent");
+        B.ntasks *= A.ext[v];
+    }
+    A.ntasks = B.ntasks;
+    int nterm = 0;
+    bool dyn_inner = false;
+    B.spec.inner_dyn_term.assign(ni, -1);
+    auto new_term = [&]() -> IndirectTerm& {
+        if (nterm >= kMaxIndirect) throw CompileError("kernel " + k.name + ": too many indirect index terms");
+        return A.ind[nterm++];
+    };
+    // Indirect terms for tensor params first (emitted in tensor order), then extents.
+    std::vector<Affine> aff(a.tensor_param_index.size());
+    B.spec.indirect_count.assign(a.tensor_param_index.size(), 0);
+    for (size_t p = 0; p < a.tensor_param_index.size(); ++p) {
+        const TensorArg& ta = *L.targs[p];
+        const TensorState& T = E.ts[ta.tid];
+        const TensorInfo& ti = P->m.tensors[ta.tid];
+        Affine& af = aff[p];
+        af.coef.assign(nvars, 0);
+        for (size_t d = 0; d < ta.idx.size(); ++d) {
+            const IndexExpr& e = ta.idx[d];
+            if (e.kind != 't') {
+                add_affine(E, e, T.stride[d], loop_index, af);
+                continue;
+            }
+            // Indirect: stride_d * index_tensor[affine(vars)].
+            IndirectTerm& it = new_term();
+            const TensorState& I = E.ts[e.tid];
+            if (P->m.tensors[e.tid].dtype != DType::I32) throw std::runtime_error("index tensors must be i32");
+            Affine ia;
+            ia.coef.assign(nvars, 0);
+            for (size_t q = 0; q < e.idx.size(); ++q) add_affine(E, e.idx[q], I.stride[q], loop_index, ia);
+            it.base = reinterpret_cast<const int*>(I.dev);
+            for (int v = 0; v < nvars; ++v) it.coef[v] = ia.coef[v];
+            it.c = ia.c;
+            it.span = I.span;
+            it.bound = ti.shape[d];
+            it.stride = T.stride[d];
+            B.spec.indirect_count[p]++;
+        }
+    }
+    for (int i = 0; i < ni; ++i) {
+        const Axis& ax = *L.inner[i].axis;
+        if (ax.kind != AxisKind::DynTensor) {
+            A.ext[ng + i] = axis_extent(E, ax);
+            continue;
+        }
+        dyn_inner = true;
+        if (ax.expr.kind != 't') throw CompileError("tensor-bound extent must be an element of an i32 tensor");
+        IndirectTerm& it = new_term();
+        const TensorState& I = E.ts[ax.expr.tid];
+        Affine ia;
+        ia.coef.assign(nvars, 0);
+        for (size_t q = 0; q < ax.expr.idx.size(); ++q) add_affine(E, ax.expr.idx[q], I.stride[q], loop_index, ia);
+        for (int v = ng + i; v < nvars; ++v)
+            if (ia.coef[v] != 0) throw CompileError("a loop extent may only depend on enclosing loops");
+        it.base = reinterpret_cast<const int*>(I.dev);
+        for (int v = 0; v < nvars; ++v) it.coef[v] = ia.coef[v];
+        it.c = ia.c;
+        it.span = I.span;
+        it.bound = int64_t(1) << 40;
+        it.stride = 1;
+        B.spec.inner_dyn_term[i] = nterm - 1;
+    }
+    bool any_indirect = nterm > 0;
+    for (size_t p = 0; p < a.tensor_param_index.size(); ++p) {
+        const TensorArg& ta = *L.targs[p];
+        const TensorState& T = E.ts[ta.tid];
+        const ValueInfo* v = a.by_id[k.params[a.tensor_param_index[p]].id];
+        const int es = dtype_size(v->dtype);
+        int64_t s3 = 0, s4 = 1;
+        if (ta.view_rank >= 2) {
+            const int d3 = ta.base_rank - ta.view_rank;
+            s3 = T.stride[d3];
+            s4 = T.stride[d3 + 1];
+        } else if (ta.view_rank == 1) {
+            s4 = T.stride[ta.base_rank - 1];
+        }
+        A.s3[p] = s3;
+        A.s4[p] = s4;
+        for (int q = 0; q < nvars; ++q) A.coef[p][q] = aff[p].coef[q];
+        A.base[p] = T.dev + aff[p].c * es;
+        A.span[p] = T.span - aff[p].c;
+        if (T.span == 0 && B.ntasks > 0)
+            throw std::runtime_error("kernel " + k.name + ": param " + k.params[a.tensor_param_index[p]].name +
+                                     " is bound to an empty tensor");
+        // Host-side bounds check over the whole launch box (affine part only).
+        if (!any_indirect && !dyn_inner && B.ntasks > 0) {
+            int64_t lo = aff[p].c, hi = aff[p].c + (v->rows - 1) * s3 + (v->cols - 1) * s4;
+            bool empty = false;
+            for (int q = 0; q < nvars; ++q) {
+                if (A.ext[q] <= 0) empty = true;
+                const int64_t span = A.coef[p][q] * (A.ext[q] - 1);
+                lo += std::min<int64_t>(0, span);
+                hi += std::max<int64_t>(0, span);
+            }
+            if (!empty && (lo < 0 || hi >= T.span)) {
+                std::ostringstream msg;
+                msg << "kernel " << k.name << ": tiles of param " << k.params[a.tensor_param_index[p]].name << " reach elements ["
+                    << lo << ", " << hi << "] of tensor " << ta.tid << ", which has " << T.span << " addressable elements";
+                throw std::runtime_error(msg.str());
+            }
+        }
+    }
+    B.host_checked = !any_indirect && !dyn_inner;
+    // Scalars.
+    const auto& sargs = L.task->scalar_args;
+    if (sargs.size() > static_cast<size_t>(kMaxScalars)) throw CompileError("too many scalar args");
+    for (size_t i = 0; i < sargs.size(); ++i) {
+        const ArgRef& s = sargs[i];
+        if (s.kind == 'c') A.scal[i] = s.u64;
+        else if (s.kind == 's') A.scal[i] = E.ctx->get_symbol_u64(E.ctx->ctx, s.u64);
+        else {
+            bool found = false;
+            for (auto h = E.host_vars.rbegin(); h != E.host_vars.rend(); ++h)
+                if (h->first == s.var) {
+                    A.scal[i] = static_cast<uint64_t>(h->second);
+                    found = true;
+                    break;
+                }
+            if (!found) throw CompileError("a scalar argument bound to a grid or in-kernel loop variable is not supported");
+        }
+    }
+    A.err = P->d_err;
+    B.spec.vec_width = a.family == Family::RowProgram ? pick_vec_width(a, A, nvars) : 1;
+    return B;
+}
+
+std::string spec_key(const EmitSpec& s) {
+    std::ostringstream o;
+    o << "vw" << s.vec_width << ";i";
+    for (int c : s.indirect_count) o << c << ",";
+    o << ";d";
+    for (int c : s.inner_dyn_term) o << c << ",";
+    return o.str();
+}
+
+const EmittedKernel& emitted_for(ptowsp_program* P, int li, const EmitSpec& spec) {
+    LaunchCache& c = P->cache[li];
+    const std::string key = spec_key(spec);
+    auto it = c.emitted.find(key);
+    if (it != c.emitted.end()) return it->second;
+    const LaunchSpec& L = P->plan.launches[li];
+    EmittedKernel ek = emit_launch(P->m, P->ka[L.kernel], L, spec);
+    return c.emitted.emplace(key, std::move(ek)).first->second;
+}
+
+void enqueue_launch(RunEnv& E, int li, hipStream_t stream, uint64_t& launches) {
+    ptowsp_program* P = E.P;
+    BuiltLaunch B = build_launch(E, P->plan.launches[li]);
+    if (B.ntasks <= 0) return;
+    const EmittedKernel& ek = emitted_for(P, li, B.spec);
+    LaunchCache& c = P->cache[li];
+    const std::string key = spec_key(B.spec);
+    const JitKernel* jk;
+    auto it = c.by_spec.find(key);
+    if (it == c.by_spec.end()) {
+        jk = &jit_kernel(ek.source, ek.entry);
+        c.by_spec[key] = jk;
+    } else {
+        jk = it->second;
+    }
+    int64_t blocks;
+    if (ek.row_program) {
+        const KernelAnalysis& a = P->ka[P->plan.launches[li].kernel];
+        const int64_t rows = B.ntasks * a.rows;
+        const int64_t chunks = (rows + ek.rows_per_chunk - 1) / ek.rows_per_chunk;
+        blocks = (chunks + ek.waves_per_block - 1) / ek.waves_per_block;
+    } else {
+        blocks = B.ntasks;
+    }
+    blocks = std::max<int64_t>(1, std::min<int64_t>(blocks, int64_t(1) << 20));
+    void* params[] = {&B.args};
+    check(hipModuleLaunchKernel(jk->function, static_cast<unsigned>(blocks), 1, 1, static_cast<unsigned>(ek.threads), 1, 1,
+                                0, stream, params, nullptr),
+          "hipModuleLaunchKernel");
+    ++launches;
+}
+
+void run_items(RunEnv& E, const std::vector<PlanItem>& items, hipStream_t stream, uint64_t& launches) {
+    for (const auto& it : items) {
+        if (!it.is_loop) {
+            enqueue_launch(E, it.launch, stream, launches);
+            continue;
+        }
+        const int64_t ub = axis_extent(E, *it.loop.axis);
+        E.host_vars.emplace_back(it.loop.var, 0);
+        for (int64_t i = 0; i < ub; ++i) {
+            E.host_vars.back().second = i;
+            run_items(E, it.body, stream, launches);
+        }
+        E.host_vars.pop_back();
+    }
+}
+
+double ms_since(std::chrono::steady_clock::time_point t0) {
+    return std::chrono::duration<double, std::milli>(std::chrono::steady_clock::now() - t0).count();
+}
+
+// Resolves every tensor, staging host-resident ones into HBM.
+void resolve_tensors(RunEnv& E, hipStream_t stream) {
+    ptowsp_program* P = E.P;
+    const size_t nt = P->m.tensors.size();
+    E.ts.assign(nt, TensorState{});
+    if (P->stage_buf.size() < nt) {
+        P->stage_buf.resize(nt, nullptr);
+        P->stage_bytes.resize(nt, 0);
+    }
+    P->copy_back.clear();
+    P->h2d_ms = 0.0;
+    for (size_t t = 0; t < nt; ++t) {
+        const TensorInfo& ti = P->m.tensors[t];
+        TensorState& T = E.ts[t];
+        char* ptr = static_cast<char*>(E.ctx->get_tensor_ptr(E.ctx->ctx, static_cast<uint32_t>(t)));
+        T.stride.resize(ti.shape.size());
+        int64_t span = 1;
+        for (size_t d = 0; d < ti.shape.size(); ++d) {
+            T.stride[d] = static_cast<int64_t>(E.ctx->get_tensor_stride(E.ctx->ctx, static_cast<uint32_t>(t), static_cast<uint32_t>(d)));
+            if (ti.shape[d] == 0) span = 0;
+        }
+        if (span) {
+            int64_t mx = 0;
+            for (size_t d = 0; d < ti.shape.size(); ++d) {
+                if (T.stride[d] < 0) throw std::runtime_error("tensor " + std::to_string(t) + ": negative strides are not supported");
+                mx += (ti.shape[d] - 1) * T.stride[d];
+            }
+            span = mx + 1;
+        }
+        T.span = span;
+        T.bytes = static_cast<size_t>(span) * dtype_size(ti.dtype);
+        T.written = P->tensor_written[t];
+        if (span == 0) continue;
+        if (!ptr) throw std::runtime_error("tensor " + std::to_string(t) + " has no data");
+        if (is_device_pointer(ptr)) {
+            T.dev = ptr;
+            continue;
+        }
+        T.host = ptr;
+        T.staged = true;
+        if (P->stage_bytes[t] < T.bytes) {
+            if (P->stage_buf[t]) check(hipFree(P->stage_buf[t]), "hipFree");
+            P->stage_buf[t] = nullptr;
+            check(hipMalloc(&P->stage_buf[t], T.bytes), "hipMalloc(staging)");
+            P->stage_bytes[t] = T.bytes;
+        }
+        T.dev = static_cast<char*>(P->stage_buf[t]);
+        const auto t0 = std::chrono::steady_clock::now();
+        check(hipMemcpyAsync(T.dev, T.host, T.bytes, hipMemcpyHostToDevice, stream), "hipMemcpyAsync(H2D)");
+        check(hipStreamSynchronize(stream), "hipStreamSynchronize(H2D)");
+        P->h2d_ms += ms_since(t0);
+        if (T.written) P->copy_back.push_back({T.host, T.dev, T.bytes});
+    }
+}
+
+CycleResult cycles_for(RunEnv& E) {
+    ptowsp_program* P = E.P;
+    CycleEnv env;
+    env.axis_size = [&](const std::string& n) { return E.ctx->get_axis_size(E.ctx->ctx, n.c_str()); };
+    env.symbol_u64 = [&](uint64_t id) { return E.ctx->get_symbol_u64(E.ctx->ctx, id); };
+    env.symbol_ptr = [&](uint64_t id) { return static_cast<const int32_t*>(E.ctx->get_symbol_ptr(E.ctx->ctx, id)); };
+    bool uses_tensor_extents = false;
+    std::ostringstream key;
+    std::function<void(const Node*)> walk = [&](const Node* n) {
+        if (!n) return;
+        if (n->kind == NodeKind::ParallelFor || n->kind == NodeKind::ForEach) {
+            const Axis& a = n->axis;
+            if (a.kind == AxisKind::Dyn) key << "d" << a.a << "=" << env.axis_size(a.a) << ";";
+            if (a.kind == AxisKind::Ragged) {
+                const int64_t outer = static_cast<int64_t>(env.symbol_u64(fnv1a_64(a.a)));
+                key << "r" << outer << ":";
+                if (const int32_t* len = env.symbol_ptr(fnv1a_64(a.b)))
+                    for (int64_t i = 0; i < outer; ++i) key << len[i] << ",";
+                key << ";";
+            }
+            if (a.kind == AxisKind::DynTensor) uses_tensor_extents = true;
+        }
+        walk(n->body.get());
+        for (const auto& c : n->kids) walk(c.get());
+    };
+    walk(P->m.root.get());
+    if (!uses_tensor_extents && P->cycles_valid && P->cycle_key == key.str()) return P->cycles;
+    env.index_value = [&](const IndexExpr& e, const std::vector<std::pair<std::string, int64_t>>& vars) {
+        return eval_index_host(E, e, vars);
+    };
+    CycleResult r = run_cycle_model(P->m, P->ka, env);
+    if (!uses_tensor_extents) {
+        P->cycle_key = key.str();
+        P->cycles = r;
+        P->cycles_valid = true;
+    }
+    return r;
+}
+
+int fail(const std::exception& e) {
+    g_last_error = e.what();
+    return -1;
+}
+
+}  // namespace
+
+extern "C" {
+
+const char* ptowsp_hip_last_error(void) { return g_last_error.c_str(); }
+
+int ptowsp_hip_compile(const char* module_text, ptowsp_program** out) {
+    try {
+        if (!module_text || !out) throw std::runtime_error("null argument");
+        auto P = std::make_unique<ptowsp_program>();
+        P->m = parse_module(module_text);
+        for (const auto& k : P->m.kernels) P->ka.push_back(analyze_kernel(k));
+        P->plan = build_plan(P->m, P->ka);
+        P->cache.resize(P->plan.launches.size());
+        P->tensor_written.assign(P->m.tensors.size(), false);
+        for (const auto& L : P->plan.launches) {
+            const KernelAnalysis& a = P->ka[L.kernel];
+            for (size_t p = 0; p < L.targs.size(); ++p)
+                if (a.stored[p]) P->tensor_written[L.targs[p]->tid] = true;
+        }
+        *out = P.release();
+        return 0;
+    } catch (const std::exception& e) {
+        return fail(e);
+    }
+}
+
+void ptowsp_hip_release(ptowsp_program* prog) { delete prog; }
+
+int ptowsp_hip_num_launches(const ptowsp_program* prog) { return prog ? static_cast<int>(prog->plan.launches.size()) : -1; }
+
+uint64_t ptowsp_hip_kernel_cycles(const ptowsp_program* prog, const char* kernel) {
+    if (!prog || !kernel) return UINT64_MAX;
+    for (size_t i = 0; i < prog->m.kernels.size(); ++i)
+        if (prog->m.kernels[i].name == kernel) return prog->ka[i].cycles;
+    return UINT64_MAX;
+}
+
+int ptowsp_hip_kernel_family(const ptowsp_program* prog, const char* kernel) {
+    if (!prog || !kernel) return -1;
+    for (size_t i = 0; i < prog->m.kernels.size(); ++i)
+        if (prog->m.kernels[i].name == kernel) return static_cast<int>(prog->ka[i].family);
+    return -1;
+}
+
+int ptowsp_hip_precompile(ptowsp_program* P, int index, const char** source) {
+    try {
+        if (!P) throw std::runtime_error("null program");
+        for (size_t li = 0; li < P->plan.launches.size(); ++li) {
+            const LaunchSpec& L = P->plan.launches[li];
+            const KernelAnalysis& a = P->ka[L.kernel];
+            EmitSpec spec;
+            spec.indirect_count.assign(L.targs.size(), 0);
+            for (size_t p = 0; p < L.targs.size(); ++p)
+                for (const auto& e : L.targs[p]->idx)
+                    if (e.kind == 't') spec.indirect_count[p]++;
+            spec.inner_dyn_term.assign(L.inner.size(), -1);
+            int term = 0;
+            for (int c : spec.indirect_count) term += c;
+            for (size_t i = 0; i < L.inner.size(); ++i)
+                if (L.inner[i].axis->kind == AxisKind::DynTensor) spec.inner_dyn_term[i] = term++;
+            if (a.family == Family::RowProgram) {
+                // Contiguous row-major views: vector width limited by the row length and row strides.
+                int vw = 4;
+                while (vw > 1 && a.cols % vw) vw /= 2;
+                for (size_t p = 0; p < L.targs.size(); ++p) {
+                    const auto& shape = P->m.tensors[L.targs[p]->tid].shape;
+                    if (L.targs[p]->view_rank >= 2 && !shape.empty())
+                        while (vw > 1 && shape.back() % vw) vw /= 2;
+                }
+                spec.vec_width = vw;
+            }
+            const EmittedKernel& ek = emitted_for(P, static_cast<int>(li), spec);
+            (void)jit_compile(ek.source);
+            if (static_cast<int>(li) == index) P->precompiled_source = ek.source;
+        }
+        if (source) *source = P->precompiled_source.c_str();
+        return 0;
+    } catch (const std::exception& e) {
+        return fail(e);
+    }
+}
+
+int ptowsp_hip_cycle_model(ptowsp_program* P, RuntimeContext* ctx, ptowsp_run_info* info) {
+    try {
+        if (!P || !ctx) throw std::runtime_error("null argument");
+        RunEnv E{P, ctx, {}, {}};
+        const size_t nt = P->m.tensors.size();
+        E.ts.assign(nt, TensorState{});
+        for (size_t t = 0; t < nt; ++t) {
+            const TensorInfo& ti = P->m.tensors[t];
+            TensorState& T = E.ts[t];
+            T.stride.resize(ti.shape.size());
+            int64_t span = 1;
+            bool empty = false;
+            for (size_t d = 0; d < ti.shape.size(); ++d) {
+                T.stride[d] = static_cast<int64_t>(ctx->get_tensor_stride(ctx->ctx, static_cast<uint32_t>(t), static_cast<uint32_t>(d)));
+                if (ti.shape[d] == 0) empty = true;
+                else span += (ti.shape[d] - 1) * T.stride[d];
+            }
+            T.span = empty ? 0 : span;
+            char* ptr = static_cast<char*>(ctx->get_tensor_ptr(ctx->ctx, static_cast<uint32_t>(t)));
+            if (ptr && is_device_pointer(ptr)) T.dev = ptr;
+            else T.host = ptr;
+        }
+        const CycleResult cyc = cycles_for(E);
+        if (info) {
+            info->total_cycles = cyc.total_cycles;
+            info->task_count = cyc.tasks;
+            info->launches = 0;
+            info->reserved = 0;
+        }
+        return 0;
+    } catch (const std::exception& e) {
+        return fail(e);
+    }
+}
+
+int ptowsp_hip_launch(ptowsp_program* P, RuntimeContext* ctx, void* hip_stream, ptowsp_run_info* info) {
+    try {
+        if (!P || !ctx) throw std::runtime_error("null argument");
+        if (P->pending) throw std::runtime_error("Program already started");
+        hipStream_t stream = static_cast<hipStream_t>(hip_stream);
+        if (!P->d_err) {
+            check(hipMalloc(reinterpret_cast<void**>(&P->d_err), sizeof(int)), "hipMalloc(err)");
+            check(hipMemset(P->d_err, 0, sizeof(int)), "hipMemset(err)");
+        }
+        if (!P->have_events) {
+            check(hipEventCreate(&P->ev0), "hipEventCreate");
+            check(hipEventCreate(&P->ev1), "hipEventCreate");
+            P->have_events = true;
+        }
+        RunEnv E{P, ctx, {}, {}};
+        resolve_tensors(E, stream);
+        const CycleResult cyc = cycles_for(E);
+        uint64_t launches = 0;
+        check(hipEventRecord(P->ev0, stream), "hipEventRecord");
+        run_items(E, P->plan.items, stream, launches);
+        check(hipEventRecord(P->ev1, stream), "hipEventRecord");
+        check(hipGetLastError(), "kernel launch");
+        P->stream = stream;
+        P->pending = true;
+        if (info) {
+            info->total_cycles = cyc.total_cycles;
+            info->task_count = cyc.tasks;
+            info->launches = static_cast<uint32_t>(launches);
+            info->reserved = 0;
+        }
+        return 0;
+    } catch (const std::exception& e) {
+        return fail(e);
+    }
+}
+
+int ptowsp_hip_synchronize(ptowsp_program* P, ptowsp_timing* timing) {
+    try {
+        if (!P) throw std::runtime_error("null program");
+        if (!P->pending) {
+            if (timing) *timing = ptowsp_timing{0.0, 0.0, 0.0};
+            return 0;
+        }
+        P->pending = false;
+        check(hipStreamSynchronize(P->stream), "hipStreamSynchronize");
+        float dev_ms = 0.0f;
+        check(hipEventElapsedTime(&dev_ms, P->ev0, P->ev1), "hipEventElapsedTime");
+        const auto t0 = std::chrono::steady_clock::now();
+        for (const auto& cb : P->copy_back) check(hipMemcpy(cb.host, cb.dev, cb.bytes, hipMemcpyDeviceToHost), "hipMemcpy(D2H)");
+        const double d2h = ms_since(t0);
+        P->copy_back.clear();
+        int err = 0;
+        check(hipMemcpy(&err, P->d_err, sizeof(int), hipMemcpyDeviceToHost), "hipMemcpy(err)");
+        if (err) {
+            const int zero = 0;
+            check(hipMemcpy(P->d_err, &zero, sizeof(int), hipMemcpyHostToDevice), "hipMemcpy(err reset)");
+            throw std::runtime_error(err == 1 ? "an indirect tensor index was out of range (tasks skipped)"
+                                              : "a task's tile fell outside its tensor (tasks skipped)");
+        }
+        if (timing) *timing = ptowsp_timing{static_cast<double>(dev_ms), P->h2d_ms, d2h};
+        return 0;
+    } catch (const std::exception& e) {
+        return fail(e);
+    }
+}
+
+uint64_t ptowsp_hip_workload_main(ptowsp_program* prog, RuntimeContext* ctx, CSPTContext* cspt) {
+    (void)cspt;
+    ptowsp_run_info info{};
+    if (ptowsp_hip_launch(prog, ctx, nullptr, &info) != 0) return 0;
+    if (ptowsp_hip_synchronize(prog, nullptr) != 0) return 0;
+    return info.total_cycles;
+}
+
+ptowsp_runtime* ptowsp_rt_create(void) {
+    auto* rt = new ptowsp_runtime();
+    rt->ctx.get_axis_size = rt_axis;
+    rt->ctx.get_symbol_u64 = rt_sym;
+    rt->ctx.get_symbol_ptr = rt_symp;
+    rt->ctx.get_slot_u64 = rt_slot;
+    rt->ctx.set_slot_u64 = rt_set_slot;
+    rt->ctx.get_tensor_ptr = rt_tptr;
+    rt->ctx.get_tensor_stride = rt_tstride;
+    rt->ctx.get_kernel = rt_kernel;
+    rt->ctx.ctx = rt;
+    return rt;
+}
+
+void ptowsp_rt_destroy(ptowsp_runtime* rt) { delete rt; }
+
+int ptowsp_rt_set_tensor(ptowsp_runtime* rt, uint32_t tid, void* ptr, uint32_t ndim, const int64_t* strides) {
+    if (!rt || (ndim && !strides)) return -1;
+    auto& t = rt->tensors[tid];
+    t.ptr = ptr;
+    t.strides.assign(strides, strides + ndim);
+    return 0;
+}
+
+int ptowsp_rt_set_axis_size(ptowsp_runtime* rt, const char* name, int64_t size) {
+    if (!rt || !name) return -1;
+    rt->axis[name] = size;
+    return 0;
+}
+
+int ptowsp_rt_set_symbol_u64(ptowsp_runtime* rt, uint64_t id, uint64_t value) {
+    if (!rt) return -1;
+    rt->sym[id] = value;
+    return 0;
+}
+
+int ptowsp_rt_set_symbol_ptr(ptowsp_runtime* rt, uint64_t id, void* ptr) {
+    if (!rt) return -1;
+    rt->symp[id] = ptr;
+    return 0;
+}
+
+void ptowsp_rt_clear(ptowsp_runtime* rt) {
+    if (!rt) return;
+    rt->tensors.clear();
+    rt->axis.clear();
+    rt->sym.clear();
+    rt->symp.clear();
+    std::fill(rt->slots.begin(), rt->slots.end(), 0);
+}
+
+RuntimeContext* ptowsp_rt_context(ptowsp_runtime* rt) { return rt ? &rt->ctx : nullptr; }
+
+}  // extern "C"

@@ -1,0 +1,218 @@
+"""GPU parity: the HIP target against the CPU oracle on identical inputs.
+
+Tolerances: fp32 elementwise/reduction work
+rtol 1e-5 (atol 1e-6 as in the reference's rmsnorm/decode examples); the
+tile-program family reproduces the oracle's operation order, so its results
+are compared bit-exactly where no exp() is involved.  Cycle counts must equal
+the oracle's (and the reference examples' recorded values).
+"""
+
+import math
+
+import numpy as np
+import pytest
+
+import workloads as W
+from oracle.runner import run_workload
+
+pytestmark = pytest.mark.gpu
+
+
+def run_hip(w, axis_sizes=None, symbols=None):
+    prog = w.compile(target="hip_gfx950")
+    if axis_sizes:
+        prog.set_axis_sizes(axis_sizes)
+    for k, v in (symbols or {}).items():
+        prog.set_symbol_f32(k, v)
+    prog.execute()
+    prog.synchronize()
+    return prog
+
+
+def test_rmsnorm_quickstart_host_arrays(gpu):
+    x = np.random.default_rng(0).standard_normal((1, 2, 16, 128), dtype=np.float32)
+    ga = {"x": x.copy(), "y": np.zeros_like(x)}
+    ca = {"x": x.copy(), "y": np.zeros_like(x)}
+    prog = run_hip(W.rr4(W.rmsnorm(ga)))
+    ref = run_workload(W.rr4(W.rmsnorm(ca)))
+    np.testing.assert_allclose(ga["y"], ca["y"], rtol=1e-5, atol=1e-6)
+    np.testing.assert_allclose(ga["y"], W.rmsnorm_ref(x), rtol=1e-5, atol=1e-6)
+    assert prog.stats.total_cycles == ref.total_cycles == 8240
+    assert prog.stats.task_count == 2
+    np.testing.assert_array_equal(ga["x"], x)
+
+
+def test_rmsnorm_device_tensors(gpu):
+    import torch
+
+    x = np.random.default_rng(3).standard_normal((4, 64, 16, 128), dtype=np.float32)
+    xd = torch.from_numpy(x).to(gpu)
+    yd = torch.zeros_like(xd)
+    prog = run_hip(W.rr4(W.rmsnorm({"x": xd, "y": yd})))
+    ca = {"x": x.copy(), "y": np.zeros_like(x)}
+    ref = run_workload(W.rr4(W.rmsnorm(ca)))
+    np.testing.assert_allclose(yd.cpu().numpy(), ca["y"], rtol=1e-5, atol=1e-6)
+    assert prog.stats.total_cycles == ref.total_cycles
+    assert prog.stats.device_time_ms > 0
+
+
+@pytest.mark.parametrize("shape", [(2, 5, 32, 512), (1, 3, 8, 64), (3, 2, 4, 16), (1, 1, 1, 8)])
+def test_softmax_tiles(gpu, shape):
+    x = (3.0 * np.random.default_rng(1).standard_normal(shape, dtype=np.float32)).astype(np.float32)
+    ga = {"x": x.copy(), "y": np.zeros_like(x)}
+    ca = {"x": x.copy(), "y": np.zeros_like(x)}
+    prog = run_hip(W.rr4(W.softmax(ga)))
+    ref = run_workload(W.rr4(W.softmax(ca)))
+    np.testing.assert_allclose(ga["y"], ca["y"], rtol=1e-5, atol=0)
+    assert prog.stats.total_cycles == ref.total_cycles
+
+
+def test_example_e2e_rmsnorm(gpu):
+    x = np.random.default_rng(0).standard_normal((1, 32, 16), dtype=np.float32)
+    ga = {"x": x.reshape(1, 2, 16, 16).copy(), "y": np.zeros((1, 2, 16, 16), np.float32)}
+    ca = {"x": x.reshape(1, 2, 16, 16).copy(), "y": np.zeros((1, 2, 16, 16), np.float32)}
+    prog = run_hip(W.rr4(W.rmsnorm(ga)))
+    run_workload(W.rr4(W.rmsnorm(ca)))
+    np.testing.assert_allclose(ga["y"], ca["y"], rtol=1e-5, atol=1e-6)
+    assert prog.stats.total_cycles == 1072
+
+
+def test_example_softmax_three_phase(gpu):
+    lg = (0.1 * np.random.default_rng(0).standard_normal((1, 32, 256), dtype=np.float32)).astype(np.float32)
+    ga, ca = W.softmax3_arrays(lg), W.softmax3_arrays(lg)
+    prog = run_hip(W.rr4(W.softmax3(ga)))
+    run_workload(W.rr4(W.softmax3(ca)))
+    for k in ("probs", "rmax", "rsum"):
+        np.testing.assert_allclose(ga[k], ca[k], rtol=1e-5, atol=1e-7)
+    assert prog.stats.total_cycles == 39848
+
+
+def test_example_bgemm_f16(gpu):
+    rng = np.random.default_rng(0)
+    a = rng.standard_normal((1, 64, 64), dtype=np.float32).astype(np.float16)
+    b = rng.standard_normal((1, 64, 64), dtype=np.float32).astype(np.float16)
+    ga = {"a": a.copy(), "b": b.copy(), "c": np.zeros((1, 64, 64), np.float32)}
+    ca = {"a": a.copy(), "b": b.copy(), "c": np.zeros((1, 64, 64), np.float32)}
+    prog = run_hip(W.rr4(W.bgemm(ga)))
+    run_workload(W.rr4(W.bgemm(ca)))
+    np.testing.assert_array_equal(ga["c"], ca["c"])
+    assert prog.stats.total_cycles == 275968
+
+
+def test_example_decode_attention(gpu):
+    rng = np.random.default_rng(0)
+    q = rng.standard_normal((1, 16), dtype=np.float32)
+    k = rng.standard_normal((64, 16), dtype=np.float32)
+    v = rng.standard_normal((64, 16), dtype=np.float32)
+
+    def arrs():
+        return {"q": q.copy(), "k_t": k.T.copy(), "v": v.copy(), "o": np.zeros((1, 16), np.float32)}
+
+    ga, ca = arrs(), arrs()
+    prog = run_hip(W.rr4(W.decode_attention(ga), 1024))
+    run_workload(W.rr4(W.decode_attention(ca), 1024))
+    np.testing.assert_allclose(ga["o"], ca["o"], rtol=1e-5, atol=1e-6)
+    s = (q @ k.T) / math.sqrt(16)
+    w = np.exp(s - s.max()) / np.exp(s - s.max()).sum()
+    np.testing.assert_allclose(ga["o"], w @ v, rtol=1e-5, atol=1e-6)
+    assert prog.stats.total_cycles == 4514
+
+
+def test_example_tiled_attention(gpu):
+    rng = np.random.default_rng(0)
+    q = rng.standard_normal((1, 2, 16, 8), dtype=np.float32)
+    k = rng.standard_normal((1, 2, 16, 8), dtype=np.float32)
+    v = rng.standard_normal((1, 2, 16, 8), dtype=np.float32)
+    ga, ca = W.attention_arrays(q, k, v, 8), W.attention_arrays(q, k, v, 8)
+    prog = run_hip(W.rr4(W.tiled_attention(ga, 8)))
+    ref = run_workload(W.rr4(W.tiled_attention(ca, 8)))
+    np.testing.assert_allclose(ga["o"], ca["o"], rtol=1e-5, atol=1e-6)
+    assert prog.stats.total_cycles == ref.total_cycles == 1680
+
+
+def test_validated_matmul_and_exact_2x2(gpu):
+    a = np.array([[[[1.0, 2.0], [3.0, 4.0]]]], np.float32)
+    b = np.array([[[[5.0, 6.0], [7.0, 8.0]]]], np.float32)
+    ga = {"a": a, "b": b, "c": np.zeros((1, 1, 2, 2), np.float32)}
+    run_hip(W.matmul_tile(ga, 2, 2, 2))
+    np.testing.assert_array_equal(ga["c"][0, 0], np.array([[19.0, 22.0], [43.0, 50.0]], np.float32))
+    rng = np.random.default_rng(0)
+    a = rng.standard_normal((2, 1, 16, 16), dtype=np.float32)
+    b = rng.standard_normal((2, 1, 16, 16), dtype=np.float32)
+    ga = {"a": a.copy(), "b": b.copy(), "c": np.zeros((2, 1, 16, 16), np.float32)}
+    ca = {"a": a.copy(), "b": b.copy(), "c": np.zeros((2, 1, 16, 16), np.float32)}
+    prog = run_hip(W.rr4(W.matmul_tile(ga, 16, 16, 16), 1024))
+    ref = run_workload(W.rr4(W.matmul_tile(ca, 16, 16, 16), 1024))
+    np.testing.assert_array_equal(ga["c"], ca["c"])
+    assert prog.stats.total_cycles == ref.total_cycles
+
+
+def test_dispatch_and_window_cycle_semantics(gpu):
+    from pto_wsp import DispatchPolicy, TaskWindow, WindowMode
+
+    a = np.arange(64, dtype=np.float32).reshape(4, 4, 4)
+    arrs = {"a": a, "b": np.zeros_like(a)}
+    p0 = run_hip(W.copy_tiles(arrs))
+    np.testing.assert_array_equal(arrs["b"], a)
+    serial = p0.stats.total_cycles
+    arrs["b"][:] = 0
+    p1 = run_hip(W.copy_tiles(arrs).dispatch(DispatchPolicy.round_robin(2)))
+    np.testing.assert_array_equal(arrs["b"], a)
+    assert p1.stats.total_cycles * 2 == serial
+    p2 = run_hip(W.copy_tiles(arrs).dispatch(DispatchPolicy.round_robin(2))
+                 .task_graph(window=TaskWindow(1, "tasks", WindowMode.STALL)))
+    assert p2.stats.total_cycles == serial
+
+
+def test_dense_dyn_rebinding_without_recompile(gpu):
+    rng = np.random.default_rng(0)
+    a = rng.standard_normal((4, 4, 4), dtype=np.float32)
+    b = rng.standard_normal((4, 4, 4), dtype=np.float32)
+    c = np.zeros((4, 4, 4), np.float32)
+    prog = W.dense_dyn_mm({"a": a, "b": b, "c": c}).named("dyn_axes").compile(target="hip_gfx950")
+    prog.set_axis_sizes({"b": 2})
+    prog.execute()
+    prog.synchronize()
+    np.testing.assert_allclose(c[:2], np.matmul(a[:2], b[:2]), rtol=0, atol=1e-5)
+    np.testing.assert_array_equal(c[2:], 0)
+    c2 = prog.stats.total_cycles
+    c[:] = 0
+    prog.set_axis_sizes({"b": 4})
+    prog.execute()
+    prog.synchronize()
+    np.testing.assert_allclose(c, np.matmul(a, b), rtol=0, atol=1e-5)
+    assert prog.stats.total_cycles / 4 == c2 / 2
+
+
+def test_scalar_symbol_rebinding(gpu):
+    x = np.arange(16, dtype=np.float32).reshape(4, 4)
+    y = np.zeros((4, 4), np.float32)
+    prog = W.scale_symbol({"x": x, "y": y}).named("dyn_scalar_symbol").compile(target="hip_gfx950")
+    prog.set_symbol_f32("scale_s", 2.0)
+    prog.execute()
+    prog.synchronize()
+    np.testing.assert_array_equal(y, x * 2.0)
+    c2 = prog.stats.total_cycles
+    prog.set_symbol_f32("scale_s", 3.0)
+    prog.execute()
+    prog.synchronize()
+    np.testing.assert_array_equal(y, x * 3.0)
+    assert prog.stats.total_cycles == c2
+
+
+def test_ragged_axis_rebinding(gpu):
+    from pto_wsp import Ragged
+
+    y = np.zeros((3, 1, 1), np.int32)
+    r = Ragged(outer_size=2, lengths=[1, 1])
+    prog = W.ragged_mark({"y": y}, r).named("dyn_ragged").compile(target="hip_gfx950")
+    prog.set_symbol_u64(f"outer_{id(r)}", 2)
+    prog.set_symbol_ptr(f"lengths_{id(r)}", np.asarray([1, 1], np.int32))
+    prog.execute()
+    prog.synchronize()
+    np.testing.assert_array_equal(y.reshape(3), [1, 1, 0])
+    y[:] = 0
+    prog.set_symbol_ptr(f"lengths_{id(r)}", np.asarray([1, 2], np.int32))
+    prog.execute()
+    prog.synchronize()
+    np.testing.assert_array_equal(y.reshape(3), [1, 1, 1])

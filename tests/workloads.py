@@ -1,0 +1,328 @@
+"""Workload factories shared by the tests.
+
+Each factory takes a dict of arrays (numpy, or torch tensors on the GPU)
+and returns an un-scheduled Workload over them, so the same workload can be
+built twice: once over the GPU-side buffers and once over the oracle's
+numpy copies.  The kernels restate the reference's README quickstart, its
+examples (examples/*/pto_wsp_impl.py) and its codegen tests
+(tests/test_codegen_*.py) in this repository's own words.
+"""
+
+import math
+
+import numpy as np
+
+from pto_wsp import (DType, Dense, DenseDyn, DispatchPolicy, In, InOut, Out, P, Ragged, Scalar, Symbol,
+                     TaskWindow, Tensor, Tile, WindowMode, kernel, pto, workload)
+
+F32, F16, BF16, I32 = DType.F32, DType.F16, DType.BF16, DType.I32
+
+
+def T(arr, dtype=F32) -> Tensor:
+    return Tensor(data=arr, shape=tuple(arr.shape), dtype=dtype)
+
+
+def rr4(w, window: int = 8192):
+    """The schedule every reference example uses: round_robin(4) + STALL window."""
+    return w.dispatch(DispatchPolicy.round_robin(num_aicpus=4)).task_graph(
+        window=TaskWindow(window, "tasks", WindowMode.STALL))
+
+
+# ---------------------------------------------------------------- rmsnorm
+def rmsnorm(arrs: dict):
+    """README quickstart kernel over X[B, T, R, C]: out = x * rsqrt(rowmean(x*x)), no eps."""
+    x = arrs["x"]
+    B, NT, R, C = x.shape
+    X, Y = T(arrs["x"]), T(arrs["y"])
+
+    @kernel
+    def rmsnorm_tile(x: In[Tile[R, C, F32]], out: Out[Tile[R, C, F32]]):
+        sq = pto.mul(x, x)
+        mean_sq = pto.rowmean(sq)
+        inv = pto.rsqrt(mean_sq)
+        pto.store(out, pto.mul(x, inv))
+
+    batch, tiles = Dense[B](), Dense[NT]()
+
+    @workload
+    def rmsnorm_wl():
+        for b in P(batch):
+            for t in P(tiles):
+                rmsnorm_tile[b, t](x=X[b][t], out=Y[b][t])
+
+    return rmsnorm_wl()
+
+
+# ---------------------------------------------------------------- row softmax
+def softmax(arrs: dict):
+    """Row softmax tile kernel over X[B, T, R, C]: e = exp(x - rowmax(x)); out = e / rowsum(e)."""
+    x = arrs["x"]
+    B, NT, R, C = x.shape
+    X, Y = T(arrs["x"]), T(arrs["y"])
+
+    @kernel
+    def softmax_tile(x: In[Tile[R, C, F32]], out: Out[Tile[R, C, F32]]):
+        m = pto.rowmax(x)
+        e = pto.exp(pto.sub(x, m))
+        s = pto.rowsum(e)
+        pto.store(out, pto.div(e, s))
+
+    batch, tiles = Dense[B](), Dense[NT]()
+
+    @workload
+    def softmax_wl():
+        for b in P(batch):
+            for t in P(tiles):
+                softmax_tile[b, t](x=X[b][t], out=Y[b][t])
+
+    return softmax_wl()
+
+
+# ---------------------------------------------------------------- 3-phase softmax (examples/softmax)
+def softmax3(arrs: dict):
+    """Three launches with P.seq accumulators: running max, exp + running sum, rescale."""
+    lg, pr = arrs["logits"], arrs["probs"]
+    B, S, V = lg.shape
+    tr, tc = 8, 64
+    st, vt = S // tr, V // tc
+    L = T(lg.reshape(B, st, tr, vt, tc))
+    PR = T(pr.reshape(B, st, tr, vt, tc))
+    RM, RS = T(arrs["rmax"]), T(arrs["rsum"])
+
+    @kernel
+    def update_rowmax(x_tile: In[Tile[tr, tc, F32]], m_acc: InOut[Tile[tr, 1, F32]]):
+        pto.store(m_acc, pto.max(m_acc, pto.rowmax(x_tile)))
+
+    @kernel
+    def exp_and_accumulate(x_tile: In[Tile[tr, tc, F32]], m_tile: In[Tile[tr, 1, F32]],
+                           y_tile: Out[Tile[tr, tc, F32]], l_acc: InOut[Tile[tr, 1, F32]]):
+        e = pto.exp(pto.sub(x_tile, m_tile))
+        pto.store(l_acc, pto.add(l_acc, pto.rowsum(e)))
+        pto.store(y_tile, e)
+
+    @kernel
+    def rescale(y_tile: InOut[Tile[tr, tc, F32]], l_tile: In[Tile[tr, 1, F32]]):
+        pto.store(y_tile, pto.div(y_tile, l_tile))
+
+    bb, ss, vv = Dense[B](), Dense[st](), Dense[vt]()
+
+    @workload
+    def softmax_workload():
+        for b in P(bb):
+            for s in P(ss):
+                for v in P.seq(vv):
+                    update_rowmax[b, s, v](x_tile=L[b][s][v], m_acc=RM[b][s])
+        for b in P(bb):
+            for s in P(ss):
+                for v in P.seq(vv):
+                    exp_and_accumulate[b, s, v](x_tile=L[b][s][v], m_tile=RM[b][s], y_tile=PR[b][s][v], l_acc=RS[b][s])
+        for b in P(bb):
+            for s in P(ss):
+                for v in P(vv):
+                    rescale[b, s, v](y_tile=PR[b][s][v], l_tile=RS[b][s])
+
+    return softmax_workload()
+
+
+def softmax3_arrays(logits: np.ndarray) -> dict:
+    B, S, V = logits.shape
+    return {"logits": logits.copy(), "probs": np.zeros_like(logits),
+            "rmax": np.full((B, S // 8, 8, 1), -np.inf, np.float32), "rsum": np.zeros((B, S // 8, 8, 1), np.float32)}
+
+
+# ---------------------------------------------------------------- bgemm (examples/bgemm pattern)
+def bgemm(arrs: dict, tm: int = 16, tn: int = 16, tk: int = 16, dtype=F16):
+    """C[b] += A[b] @ B[b] over tiles with a P.seq K loop and an InOut accumulator."""
+    a, b_, c = arrs["a"], arrs["b"], arrs["c"]
+    B, M, K = a.shape
+    N = b_.shape[2]
+    at = a.reshape(B, M // tm, tm, K // tk, tk).transpose(0, 1, 3, 2, 4)
+    bt = b_.reshape(B, K // tk, tk, N // tn, tn).transpose(0, 3, 1, 2, 4)
+    ct = c.reshape(B, M // tm, tm, N // tn, tn).transpose(0, 1, 3, 2, 4)
+    A, Bm, C = T(at, dtype), T(bt, dtype), T(ct)
+
+    @kernel
+    def gemm_tile(a_tile: In[Tile[tm, tk, dtype]], b_tile: In[Tile[tk, tn, dtype]], c_tile: InOut[Tile[tm, tn, F32]]):
+        acc = pto.matmul(a_tile, b_tile)
+        pto.store(c_tile, pto.add(c_tile, acc))
+
+    batch, mt, nt, kt = Dense[B](), Dense[M // tm](), Dense[N // tn](), Dense[K // tk]()
+
+    @workload
+    def bgemm_wl():
+        for b in P(batch):
+            for m in P(mt):
+                for n in P(nt):
+                    for k in P.seq(kt):
+                        gemm_tile[b, m, n, k](a_tile=A[b][m][k], b_tile=Bm[b][n][k], c_tile=C[b][m][n])
+
+    return bgemm_wl()
+
+
+# ---------------------------------------------------------------- decode / attention (f32 examples)
+def decode_attention(arrs: dict):
+    """examples/flashinfer_decode: one task, whole KV in one tile."""
+    q, kt, v, o = arrs["q"], arrs["k_t"], arrs["v"], arrs["o"]
+    d, kv = q.shape[1], kt.shape[1]
+    Q, KT, V, O = T(q), T(kt), T(v), T(o)
+
+    @kernel
+    def decode_attention_tile(q_tile: In[Tile[1, d, F32]], k_t_tile: In[Tile[d, kv, F32]],
+                              v_tile: In[Tile[kv, d, F32]], out_tile: Out[Tile[1, d, F32]]):
+        scores = pto.matmul(q_tile, k_t_tile)
+        scores = pto.mul(scores, pto.constant(1.0 / math.sqrt(d), F32))
+        scores = pto.sub(scores, pto.rowmax(scores))
+        e = pto.exp(scores)
+        w = pto.div(e, pto.rowsum(e))
+        pto.store(out_tile, pto.matmul(w, v_tile))
+
+    @workload
+    def decode():
+        decode_attention_tile[0](q_tile=Q, k_t_tile=KT, v_tile=V, out_tile=O)
+
+    return decode()
+
+
+def tiled_attention(arrs: dict, tile_seq: int):
+    """examples/attention: per (b, h, s-tile) softmax(q k^T / sqrt(d)) v."""
+    q, kt, v, o = arrs["q"], arrs["k_t"], arrs["v"], arrs["o"]
+    B, H, S, D = q.shape
+    st = S // tile_seq
+    Q = T(q.reshape(B, H, st, tile_seq, D))
+    KT = T(kt)
+    V = T(v.reshape(B, H, st, tile_seq, D))
+    O = T(o.reshape(B, H, st, tile_seq, D))
+
+    @kernel
+    def attention_tile(q: In[Tile[tile_seq, D, F32]], k_t: In[Tile[D, tile_seq, F32]],
+                       v: In[Tile[tile_seq, D, F32]], out: Out[Tile[tile_seq, D, F32]]):
+        s = pto.mul(pto.matmul(q, k_t), pto.constant(1.0 / math.sqrt(D), F32))
+        s = pto.sub(s, pto.rowmax(s))
+        e = pto.exp(s)
+        pto.store(out, pto.matmul(pto.div(e, pto.rowsum(e)), v))
+
+    bb, hh, ss = Dense[B](), Dense[H](), Dense[st]()
+
+    @workload
+    def attention():
+        for b, h in P(bb, hh):
+            for s in P(ss):
+                attention_tile[b, h, s](q=Q[b][h][s], k_t=KT[b][h][s], v=V[b][h][s], out=O[b][h][s])
+
+    return attention()
+
+
+def attention_arrays(q, k, v, tile_seq):
+    B, H, S, D = q.shape
+    kt = np.ascontiguousarray(k.reshape(B, H, S // tile_seq, tile_seq, D).transpose(0, 1, 2, 4, 3))
+    return {"q": q.copy(), "k_t": kt, "v": v.copy(), "o": np.zeros_like(q)}
+
+
+# ---------------------------------------------------------------- small reference tests
+def matmul_tile(arrs: dict, m: int, k: int, n: int, dtype=F32):
+    """tests/test_codegen_execute_basic.py / examples/validated_matmul: C[b][0] = A[b][0] @ B[b][0]."""
+    A, B, C = T(arrs["a"], dtype), T(arrs["b"], dtype), T(arrs["c"])
+    nb = arrs["a"].shape[0]
+
+    @kernel
+    def mm(a: In[Tile[m, k, dtype]], b: In[Tile[k, n, dtype]], out: Out[Tile[m, n, F32]]):
+        pto.store(out, pto.matmul(a, b))
+
+    batch = Dense[nb]()
+
+    @workload
+    def wl():
+        for b in P(batch):
+            mm[b](a=A[b][0], b=B[b][0], out=C[b][0])
+
+    return wl()
+
+
+def copy_tiles(arrs: dict, n: int = 4):
+    """tests/test_codegen_schedule_dispatch_window.py: copy 4x4 tiles."""
+    A, B = T(arrs["a"]), T(arrs["b"])
+    tiles = Dense[n]()
+
+    @kernel
+    def copy_tile(src: In[Tile[4, 4, F32]], dst: Out[Tile[4, 4, F32]]):
+        pto.store(dst, src)
+
+    @workload
+    def wl():
+        for t in P(tiles):
+            copy_tile[t](src=A[t], dst=B[t])
+
+    return wl()
+
+
+def scale_symbol(arrs: dict):
+    """tests/test_codegen_dynamic_symbols.py: y = x * s with s a runtime symbol."""
+    X, Y = T(arrs["x"]), T(arrs["y"])
+
+    @kernel
+    def scale(x_tile: In[Tile[4, 4, F32]], y_tile: Out[Tile[4, 4, F32]], s: Scalar[F32]):
+        pto.store(y_tile, pto.mul(x_tile, s))
+
+    @workload
+    def wl():
+        scale(x_tile=X, y_tile=Y, s=Symbol("scale_s"))
+
+    return wl()
+
+
+def dense_dyn_mm(arrs: dict):
+    """tests/test_codegen_dynamic_axes.py: DenseDyn batch bound at run time ("b")."""
+    a, b, c = T(arrs["a"]), T(arrs["b"]), T(arrs["c"])
+    batch = DenseDyn(0)
+
+    @kernel
+    def mm(a_tile: In[Tile[4, 4, F32]], b_tile: In[Tile[4, 4, F32]], c_tile: Out[Tile[4, 4, F32]]):
+        pto.store(c_tile, pto.matmul(a_tile, b_tile))
+
+    @workload
+    def wl():
+        for bidx in P(batch):
+            mm[bidx](a_tile=a[bidx], b_tile=b[bidx], c_tile=c[bidx])
+
+    return wl()
+
+
+def ragged_mark(arrs: dict, ragged: Ragged):
+    """tests/test_codegen_ragged_axis.py: y[t] += 1 over a flattened ragged axis."""
+    Y = T(arrs["y"], I32)
+
+    @kernel
+    def mark(y_tile: InOut[Tile[1, 1, I32]]):
+        v = pto.load(y_tile)
+        one = pto.constant(1.0, I32)
+        pto.store(y_tile, pto.add(v, one))
+
+    @workload
+    def wl():
+        for t in P.seq(ragged, name="t"):
+            mark[t](y_tile=Y[t])
+
+    return wl()
+
+
+# ---------------------------------------------------------------- numpy references (float64)
+def rmsnorm_ref(x):
+    x64 = x.astype(np.float64)
+    return x64 / np.sqrt(np.mean(x64 * x64, axis=-1, keepdims=True))
+
+
+def softmax_ref(x):
+    x64 = x.astype(np.float64)
+    e = np.exp(x64 - x64.max(axis=-1, keepdims=True))
+    return e / e.sum(axis=-1, keepdims=True)
+
+
+def bf16_round(x: np.ndarray) -> np.ndarray:
+    """float32 -> bf16 bit patterns (uint16), round to nearest even."""
+    u = np.ascontiguousarray(x, dtype=np.float32).view(np.uint32).astype(np.uint64)
+    r = ((u + 0x7FFF + ((u >> 16) & 1)) >> 16).astype(np.uint16)
+    return r
+
+
+def bf16_to_f32(b: np.ndarray) -> np.ndarray:
+    return (b.astype(np.uint32) << 16).view(np.float32)
