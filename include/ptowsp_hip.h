@@ -82,8 +82,10 @@ uint64_t ptowsp_hip_kernel_cycles(const ptowsp_program* prog, const char* kernel
 int ptowsp_hip_kernel_family(const ptowsp_program* prog, const char* kernel);
 /* Emits and builds every launch for contiguous row-major tensors without
  * touching a GPU (hiprtc only); returns the source of launch `index` through
- * `source`, valid until the next call. */
-int ptowsp_hip_precompile(ptowsp_program* prog, int index, const char** source);
+ * `source`, valid until the next call.  flags bit 0: build the variant that
+ * runs all tasks of a launch in program order (used when grid tasks write
+ * overlapping memory). */
+int ptowsp_hip_precompile(ptowsp_program* prog, int index, int flags, const char** source);
 
 /* Evaluates only the cpu_sim cycle model (total_cycles, task_count) for the
  * bindings in `ctx`, on the host, without launching anything. */

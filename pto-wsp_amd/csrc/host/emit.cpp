@@ -335,12 +335,18 @@ EmittedKernel emit_tile(const Module& m, const KernelAnalysis& a, const LaunchSp
     }
     emit_scalars(o, a, true);
     o << "  i64 vars[" << (nvars > 0 ? nvars : 1) << "];\n  (void)vars;\n";
-    o << "  for (i64 t = blockIdx.x; t < A.ntasks; t += gridDim.x) {\n";
-    emit_decode(o, "    ", ng, "t");
+    // Grid loops are decoded from the task index, or, for a serial launch,
+    // iterated in program order by a single workgroup.
+    const int decoded = spec.serial ? 0 : ng;
+    const int looped = nvars - decoded;
+    if (spec.serial) o << "  for (i64 t = blockIdx.x; t < 1; t += gridDim.x) {\n";
+    else o << "  for (i64 t = blockIdx.x; t < A.ntasks; t += gridDim.x) {\n";
+    emit_decode(o, "    ", decoded, "t");
     std::string ind = "    ";
-    for (int i = 0; i < ni; ++i) {
-        const int v = ng + i;
-        const int term = spec.inner_dyn_term.size() > static_cast<size_t>(i) ? spec.inner_dyn_term[i] : -1;
+    for (int i = 0; i < looped; ++i) {
+        const int v = decoded + i;
+        const int inner_i = v - ng;
+        const int term = inner_i >= 0 && spec.inner_dyn_term.size() > static_cast<size_t>(inner_i) ? spec.inner_dyn_term[inner_i] : -1;
         if (term >= 0) o << ind << "const i64 e" << i << " = indirect_index(A, " << term << ", vars, " << v << ");\n";
         else o << ind << "const i64 e" << i << " = A.ext[" << v << "];\n";
         o << ind << "for (vars[" << v << "] = 0; vars[" << v << "] < e" << i << "; ++vars[" << v << "]) {\n";
@@ -451,7 +457,7 @@ EmittedKernel emit_tile(const Module& m, const KernelAnalysis& a, const LaunchSp
         }
         o << ind << "__syncthreads();\n";
     }
-    for (int i = ni - 1; i >= 0; --i) {
+    for (int i = looped - 1; i >= 0; --i) {
         ind.resize(ind.size() - 2);
         o << ind << "}\n";
     }
@@ -466,7 +472,7 @@ EmittedKernel emit_tile(const Module& m, const KernelAnalysis& a, const LaunchSp
 EmittedKernel emit_launch(const Module& m, const KernelAnalysis& a, const LaunchSpec& L, const EmitSpec& spec) {
     bool indirect = false;
     for (int c : spec.indirect_count) indirect = indirect || c > 0;
-    if (a.family == Family::RowProgram && L.inner.empty() && !indirect) return emit_row(m, a, L, spec);
+    if (a.family == Family::RowProgram && L.inner.empty() && !indirect && !spec.serial) return emit_row(m, a, L, spec);
     return emit_tile(m, a, L, spec);
 }
 

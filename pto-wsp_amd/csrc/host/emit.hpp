@@ -15,6 +15,10 @@ struct EmitSpec {
     std::vector<int> indirect_count;   // per tensor ordinal: indirect index terms (in dim order)
     std::vector<int> inner_dyn_term;   // per inner loop: indirect term index of its extent, or -1
     int threads = 256;
+    // Run every task of the launch in program order in one workgroup: used
+    // when tasks of the grid write overlapping memory (the result then
+    // depends on the reference's sequential order).
+    bool serial = false;
 };
 
 struct EmittedKernel {

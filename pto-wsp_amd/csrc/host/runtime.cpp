@@ -264,6 +264,52 @@ int pick_vec_width(const KernelAnalysis& a, const LaunchArgs& A, int nvars) {
     return 1;
 }
 
+// True when two different tasks of the grid may touch the same element of a
+// tensor that the launch writes.  P() promises independent iterations; a
+// workload that breaks the promise (overlapping output views) still gets
+// the reference's result, by running the launch in program order.
+bool grid_write_hazard(const KernelAnalysis& a, const LaunchSpec& L, const LaunchArgs& A, const EmitSpec& spec, int ng,
+                       int nvars) {
+    if (A.ntasks <= 1) return false;
+    const KernelDef& k = *a.def;
+    const size_t np = a.tensor_param_index.size();
+    for (size_t p = 0; p < np; ++p) {
+        if (!a.stored[p]) continue;
+        const int tid = L.targs[p]->tid;
+        if (spec.indirect_count[p] > 0) return true;
+        const ValueInfo* vp = a.by_id[k.params[a.tensor_param_index[p]].id];
+        // Every other access to the written tensor must be the very same view.
+        for (size_t q = 0; q < np; ++q) {
+            if (q == p || L.targs[q]->tid != tid) continue;
+            const ValueInfo* vq = a.by_id[k.params[a.tensor_param_index[q]].id];
+            if (spec.indirect_count[q] > 0 || A.base[q] != A.base[p] || A.s3[q] != A.s3[p] || A.s4[q] != A.s4[p] ||
+                vq->rows != vp->rows || vq->cols != vp->cols)
+                return true;
+            for (int v = 0; v < nvars; ++v)
+                if (A.coef[q][v] != A.coef[p][v]) return true;
+        }
+        // Footprint of one task: its tile swept over the in-kernel loops.
+        int64_t width = (vp->rows - 1) * std::llabs(A.s3[p]) + (vp->cols - 1) * std::llabs(A.s4[p]) + 1;
+        for (size_t i = 0; i < L.inner.size(); ++i) {
+            const int v = ng + static_cast<int>(i);
+            if (A.coef[p][v] == 0) continue;
+            if (spec.inner_dyn_term[i] >= 0) return true;
+            width += std::llabs(A.coef[p][v]) * std::max<int64_t>(0, A.ext[v] - 1);
+        }
+        // Grid dimensions must nest without overlap, like the strides of an array.
+        std::vector<std::pair<int64_t, int64_t>> dims;
+        for (int v = 0; v < ng; ++v)
+            if (A.ext[v] > 1) dims.emplace_back(std::llabs(A.coef[p][v]), A.ext[v]);
+        std::sort(dims.begin(), dims.end());
+        int64_t span = width;
+        for (const auto& [c, e] : dims) {
+            if (c < span) return true;
+            span += c * (e - 1);
+        }
+    }
+    return false;
+}
+
 BuiltLaunch build_launch(RunEnv& E, const LaunchSpec& L) {
     ptowsp_program* P = E.P;
     const KernelAnalysis& a = P->ka[L.kernel];
@@ -403,13 +449,14 @@ BuiltLaunch build_launch(RunEnv& E, const LaunchSpec& L) {
         }
     }
     A.err = P->d_err;
+    B.spec.serial = grid_write_hazard(a, L, A, B.spec, ng, nvars);
     B.spec.vec_width = a.family == Family::RowProgram ? pick_vec_width(a, A, nvars) : 1;
     return B;
 }
 
 std::string spec_key(const EmitSpec& s) {
     std::ostringstream o;
-    o << "vw" << s.vec_width << ";i";
+    o << "vw" << s.vec_width << (s.serial ? ";serial" : "") << ";i";
     for (int c : s.indirect_count) o << c << ",";
     o << ";d";
     for (int c : s.inner_dyn_term) o << c << ",";
@@ -448,7 +495,7 @@ void enqueue_launch(RunEnv& E, int li, hipStream_t stream, uint64_t& launches) {
         const int64_t chunks = (rows + ek.rows_per_chunk - 1) / ek.rows_per_chunk;
         blocks = (chunks + ek.waves_per_block - 1) / ek.waves_per_block;
     } else {
-        blocks = B.ntasks;
+        blocks = B.spec.serial ? 1 : B.ntasks;
     }
     blocks = std::max<int64_t>(1, std::min<int64_t>(blocks, int64_t(1) << 20));
     void* params[] = {&B.args};
@@ -622,13 +669,14 @@ int ptowsp_hip_kernel_family(const ptowsp_program* prog, const char* kernel) {
     return -1;
 }
 
-int ptowsp_hip_precompile(ptowsp_program* P, int index, const char** source) {
+int ptowsp_hip_precompile(ptowsp_program* P, int index, int flags, const char** source) {
     try {
         if (!P) throw std::runtime_error("null program");
         for (size_t li = 0; li < P->plan.launches.size(); ++li) {
             const LaunchSpec& L = P->plan.launches[li];
             const KernelAnalysis& a = P->ka[L.kernel];
             EmitSpec spec;
+            spec.serial = (flags & 1) != 0;
             spec.indirect_count.assign(L.targs.size(), 0);
             for (size_t p = 0; p < L.targs.size(); ++p)
                 for (const auto& e : L.targs[p]->idx)

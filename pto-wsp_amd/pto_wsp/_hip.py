@@ -56,7 +56,7 @@ _lib.ptowsp_hip_num_launches.argtypes = [_vp]
 _lib.ptowsp_hip_kernel_cycles.argtypes = [_vp, ctypes.c_char_p]
 _lib.ptowsp_hip_kernel_cycles.restype = ctypes.c_uint64
 _lib.ptowsp_hip_kernel_family.argtypes = [_vp, ctypes.c_char_p]
-_lib.ptowsp_hip_precompile.argtypes = [_vp, ctypes.c_int, ctypes.POINTER(ctypes.c_char_p)]
+_lib.ptowsp_hip_precompile.argtypes = [_vp, ctypes.c_int, ctypes.c_int, ctypes.POINTER(ctypes.c_char_p)]
 _lib.ptowsp_hip_precompile.restype = ctypes.c_int
 _lib.ptowsp_hip_cycle_model.argtypes = [_vp, _vp, ctypes.POINTER(RunInfo)]
 _lib.ptowsp_hip_cycle_model.restype = ctypes.c_int
@@ -164,9 +164,9 @@ class NativeProgram:
     def kernel_family(self, name: str) -> str:
         return FAMILIES.get(int(_lib.ptowsp_hip_kernel_family(self._h, name.encode())), "unknown")
 
-    def precompile(self, index: int = 0) -> str:
+    def precompile(self, index: int = 0, serial: bool = False) -> str:
         src = ctypes.c_char_p()
-        if _lib.ptowsp_hip_precompile(self._h, int(index), ctypes.byref(src)) != 0:
+        if _lib.ptowsp_hip_precompile(self._h, int(index), 1 if serial else 0, ctypes.byref(src)) != 0:
             raise RuntimeError(_error())
         return src.value.decode() if src.value else ""
 

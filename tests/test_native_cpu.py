@@ -84,6 +84,16 @@ def test_emitted_kernels_build_for_gfx950(name):
     assert "ptowsp_entry" in src
 
 
+@pytest.mark.parametrize("name", ["rmsnorm", "softmax3", "bgemm_f16"])
+def test_serial_variants_build_for_gfx950(name):
+    from pto_wsp._hip import NativeProgram
+
+    make, _ = _cases()[name]
+    prog = NativeProgram(workload_to_codegen_ir(make(), name).module)
+    src = prog.precompile(0, serial=True)
+    assert "t < 1;" in src
+
+
 @pytest.mark.parametrize("name", list(_cases()))
 def test_cycle_model_matches_oracle(name):
     from pto_wsp._hip import NativeProgram
