@@ -1,18 +1,17 @@
 #!/usr/bin/env python3
 """Benchmark of the PTO-WSP data-parallel tile path on one MI355X.
 
-Default workload (the headline bandwidth config):
-the README rmsnorm tile kernel over X[16, 8192, 16, 128] fp32 ~ N(0,1)
-(1 GiB in, 1 GiB out), workload P(batch=16) x P(tiles=8192), schedule
-round_robin(4) + TaskWindow(8192, STALL), compiled with
-``compile(target="hip_gfx950")``.  A step is one ``execute()`` of the
-compiled program over resident device buffers; K steps are timed between
-``torch.cuda.synchronize()`` calls.
+Headline workload: the README rmsnorm tile kernel
+over X[16, 8192, 16, 128] fp32 ~ N(0,1) (1 GiB in, 1 GiB out), workload
+P(batch=16) x P(tiles=8192), schedule round_robin(4) + TaskWindow(8192,
+STALL), compiled with ``compile(target="hip_gfx950")``.  A step is one
+``execute()`` + ``synchronize()`` of the compiled program over device-resident
+buffers; K steps are timed between ``torch.cuda.synchronize()`` calls.
 
-Besides the headline line's fields, ``configs`` reports every BASELINE
-config this build runs (GB/s or TFLOP/s, fraction of the MI355X peak),
-and ``cpu_baseline`` times this repository's C restatement of the
-reference cpu_sim artifact (oracle/, 1 thread) on the same inputs.
+``configs`` reports every BASELINE config this build runs (GB/s or TFLOP/s
+and the fraction of the MI355X peak, from HIP-event kernel time), and
+``cpu_baseline`` times this repository's C restatement of the reference
+cpu_sim artifact (oracle/, 1 thread) on the same inputs.
 
     python bench.py [--gpus 1] [--steps K] [--warmup W] [--config NAME|all] [--no-cpu]
 """
@@ -31,19 +30,19 @@ for _p in (os.path.join(ROOT, "pto-wsp_amd"), ROOT):
 HBM_PEAK_GBS = 8000.0          # MI355X HBM3E
 BF16_PEAK_TFLOPS = 2500.0      # MI355X dense bf16 MFMA
 METRIC = "GB/s & TFLOP/s as % of MI355X roofline per config, 1 GPU, vs cpu_sim wall"
-
-CONFIGS = {
-    "rmsnorm_quickstart": {"kind": "rmsnorm", "shape": (1, 2, 16, 128), "sigma": 1.0, "seed": 0,
-                           "baseline_config": 0},
-    "rmsnorm_bw": {"kind": "rmsnorm", "shape": (16, 8192, 16, 128), "sigma": 1.0, "seed": 0, "baseline_config": 1},
-    "softmax": {"kind": "softmax", "shape": (8, 4096, 32, 512), "sigma": 3.0, "seed": 0, "baseline_config": 2},
-}
 HEADLINE = "rmsnorm_bw"
 
 
-def make_workload(kind, X, Y):
-    from pto_wsp import (DType, Dense, DispatchPolicy, In, Out, P, TaskWindow, Tensor, Tile, WindowMode,
-                         kernel, pto, workload)
+def rr4(w):
+    from pto_wsp import DispatchPolicy, TaskWindow, WindowMode
+
+    return (w.dispatch(DispatchPolicy.round_robin(num_aicpus=4))
+            .task_graph(window=TaskWindow(8192, "tasks", WindowMode.STALL)))
+
+
+def row_workload(kind, X, Y):
+    """rmsnorm / softmax / copy tile kernels over X[B, T, R, C] (rows of R x C tiles)."""
+    from pto_wsp import DType, Dense, In, Out, P, Tensor, Tile, kernel, pto, workload
 
     f32 = DType.F32
     B, NT, R, C = tuple(X.shape)
@@ -58,7 +57,7 @@ def make_workload(kind, X, Y):
             pto.store(out, pto.mul(x, inv))
 
         body = rmsnorm_tile
-    else:
+    elif kind == "softmax":
         @kernel
         def softmax_tile(x: In[Tile[R, C, f32]], out: Out[Tile[R, C, f32]]):
             m = pto.rowmax(x)
@@ -66,6 +65,12 @@ def make_workload(kind, X, Y):
             pto.store(out, pto.div(e, pto.rowsum(e)))
 
         body = softmax_tile
+    else:
+        @kernel
+        def copy_tile(x: In[Tile[R, C, f32]], out: Out[Tile[R, C, f32]]):
+            pto.store(out, x)
+
+        body = copy_tile
 
     batch, tiles = Dense[B](), Dense[NT]()
 
@@ -75,79 +80,192 @@ def make_workload(kind, X, Y):
             for t in P(tiles):
                 body[b, t](x=Xt[b][t], out=Yt[b][t])
 
-    return (wl().dispatch(DispatchPolicy.round_robin(num_aicpus=4))
-            .task_graph(window=TaskWindow(8192, "tasks", WindowMode.STALL)))
+    return rr4(wl())
+
+
+def bgemm_workload(A, Bm, C, tm=128, tn=128, tk=64):
+    """examples/bgemm pattern: C[b] += A[b] @ B[b] with a P.seq K loop and an InOut fp32 tile."""
+    from pto_wsp import DType, Dense, In, InOut, P, Tensor, Tile, kernel, pto, workload
+
+    bf16, f32 = DType.BF16, DType.F32
+    nb, M, K = tuple(A.shape)
+    N = Bm.shape[2]
+
+    def tiles(x, r, c, rt, ct):  # x[b, R, Cc] -> [b, R/rt, Cc/ct, rt, ct] view, either library
+        v = x.reshape(nb, r // rt, rt, c // ct, ct)
+        return v.permute(0, 1, 3, 2, 4) if hasattr(v, "permute") else v.transpose(0, 1, 3, 2, 4)
+
+    at = tiles(A, M, K, tm, tk)
+    bt = tiles(Bm, K, N, tk, tn)
+    bt = bt.permute(0, 2, 1, 3, 4) if hasattr(bt, "permute") else bt.transpose(0, 2, 1, 3, 4)
+    ct = tiles(C, M, N, tm, tn)
+    At = Tensor(data=at, shape=tuple(at.shape), dtype=bf16)
+    Bt = Tensor(data=bt, shape=tuple(bt.shape), dtype=bf16)
+    Ct = Tensor(data=ct, shape=tuple(ct.shape), dtype=f32)
+
+    @kernel
+    def gemm_tile(a_tile: In[Tile[tm, tk, bf16]], b_tile: In[Tile[tk, tn, bf16]], c_tile: InOut[Tile[tm, tn, f32]]):
+        acc = pto.matmul(a_tile, b_tile)
+        pto.store(c_tile, pto.add(c_tile, acc))
+
+    batch, mt, nt, kt = Dense[nb](), Dense[M // tm](), Dense[N // tn](), Dense[K // tk]()
+
+    @workload
+    def bgemm():
+        for b in P(batch):
+            for m in P(mt):
+                for n in P(nt):
+                    for k in P.seq(kt):
+                        gemm_tile[b, m, n, k](a_tile=At[b][m][k], b_tile=Bt[b][n][k], c_tile=Ct[b][m][n])
+
+    return rr4(bgemm())
+
+
+class RowCase:
+    unit, bound = "GB/s", "hbm"
+
+    def __init__(self, name, kind, shape, sigma, seed, baseline_config):
+        self.name, self.kind, self.shape, self.sigma, self.seed = name, kind, shape, sigma, seed
+        self.baseline_config = baseline_config
+
+    def setup(self, dev):
+        import torch
+
+        g = torch.Generator(device=dev)
+        g.manual_seed(self.seed)
+        self.x = torch.randn(self.shape, generator=g, device=dev, dtype=torch.float32) * self.sigma
+        self.y = torch.empty_like(self.x)
+        self.prog = row_workload(self.kind, self.x, self.y).compile(target="hip_gfx950")
+        self.work = 2 * self.x.numel() * 4  # bytes read + written
+
+    def peak(self):
+        return HBM_PEAK_GBS
+
+    def rate(self, seconds):
+        return self.work / seconds / 1e9
+
+    def describe(self):
+        return (f"{self.name}: {self.kind}_tile Tile[{self.shape[2]},{self.shape[3]},F32] over X{list(self.shape)}, "
+                f"P(batch={self.shape[0]}) x P(tiles={self.shape[1]}), round_robin(4), TaskWindow(8192, STALL)")
+
+    def cpu(self, budget_s):
+        """Oracle over the whole workload (repeated within the budget) + parity of the GPU output."""
+        import numpy as np
+
+        from oracle.runner import run_workload
+
+        xh = self.x.detach().cpu().numpy()
+        yh = np.zeros_like(xh)
+        times = []
+        t_start = time.perf_counter()
+        while len(times) < 8 and (time.perf_counter() - t_start) < budget_s:
+            t0 = time.perf_counter()
+            run_workload(row_workload(self.kind, xh, yh))
+            times.append(time.perf_counter() - t0)
+        sec = sum(times) / len(times)
+        same = bool(np.allclose(self.y.cpu().numpy(), yh, rtol=1e-5, atol=1e-6 if self.kind != "softmax" else 0.0))
+        sample = (f"the full {self.name} workload X{list(self.shape)}, {len(times)} run(s) of {sec:.2f} s each, "
+                  f"wall clock around the oracle call")
+        return self.work / sec / 1e9, sample, same
+
+
+class GemmCase:
+    unit, bound = "TFLOP/s", "mfma"
+
+    def __init__(self, name, nb, m, n, k, seed, baseline_config):
+        self.name, self.nb, self.m, self.n, self.k, self.seed = name, nb, m, n, k, seed
+        self.baseline_config = baseline_config
+        self.shape = (nb, m, k)
+
+    def setup(self, dev):
+        import torch
+
+        g = torch.Generator(device=dev)
+        g.manual_seed(self.seed)
+        self.a = (torch.rand((self.nb, self.m, self.k), generator=g, device=dev) * 2 - 1).to(torch.bfloat16)
+        self.b = (torch.rand((self.nb, self.k, self.n), generator=g, device=dev) * 2 - 1).to(torch.bfloat16)
+        self.c = torch.zeros((self.nb, self.m, self.n), device=dev, dtype=torch.float32)
+        self.prog = bgemm_workload(self.a, self.b, self.c).compile(target="hip_gfx950")
+        self.work = 2.0 * self.nb * self.m * self.n * self.k  # FLOP per step
+
+    def peak(self):
+        return BF16_PEAK_TFLOPS
+
+    def rate(self, seconds):
+        return self.work / seconds / 1e12
+
+    def describe(self):
+        return (f"{self.name}: C[b] += A[b] @ B[b], A,B[{self.nb},{self.m},{self.k}] bf16 U(-1,1), C fp32, "
+                "tiles 128x128 K-step 64, P(batch) x P(m_tiles) x P(n_tiles) x P.seq(k)")
+
+    def cpu(self, budget_s):
+        """Oracle on a bounded sample: batch 0, the first 2 m-tiles (all n, all k), from C = 0."""
+        import numpy as np
+
+        from oracle.runner import run_workload
+
+        del budget_s
+        import torch
+
+        a0 = self.a[:1, :256].contiguous().view(torch.int16).cpu().numpy().view(np.uint16)
+        b0 = self.b[:1].contiguous().view(torch.int16).cpu().numpy().view(np.uint16)
+        c0 = np.zeros((1, 256, self.n), np.float32)
+        t0 = time.perf_counter()
+        run_workload(bgemm_workload(a0, b0, c0))
+        sec = time.perf_counter() - t0
+        flop = 2.0 * 256 * self.n * self.k
+        # GPU result for the same tiles, from a fresh C = 0 run.
+        self.c.zero_()
+        self.prog.execute()
+        self.prog.synchronize()
+        got = self.c[0, :256].cpu().numpy()
+        rel = float(np.linalg.norm(got - c0) / np.linalg.norm(c0))
+        sample = f"batch 0, m-tiles 0-1 (256 x {self.n} outputs, K={self.k}), {flop / 1e9:.1f} GFLOP, one oracle run"
+        return flop / sec / 1e12, sample, rel <= 1e-2
+
+
+CASES = {
+    "rmsnorm_quickstart": lambda: RowCase("rmsnorm_quickstart", "rmsnorm", (1, 2, 16, 128), 1.0, 0, 0),
+    "rmsnorm_bw": lambda: RowCase("rmsnorm_bw", "rmsnorm", (16, 8192, 16, 128), 1.0, 0, 1),
+    "softmax": lambda: RowCase("softmax", "softmax", (8, 4096, 32, 512), 3.0, 0, 2),
+    "bgemm": lambda: GemmCase("bgemm", 64, 2048, 2048, 2048, 0, 3),
+    # Not a BASELINE config: a plain tile copy of known size (1 GiB in, 1 GiB
+    # out) through the same backend, used to calibrate rocprofv3 traffic
+    # counters and as the achievable-bandwidth reference.
+    "copy_calib": lambda: RowCase("copy_calib", "copy", (16, 8192, 16, 128), 1.0, 0, None),
+}
 
 
 def load_traffic(name):
-    """HBM bytes per launch measured with rocprofv3 --pmc (profiles/<name>_traffic.json), if committed."""
-    path = os.path.join(ROOT, "profiles", f"{name}_traffic.json")
+    """HBM bytes per launch from the committed rocprofv3 --pmc summary
+    (profiles/<name>_traffic.md, line 'traffic_bytes: N'), or None."""
+    path = os.path.join(ROOT, "profiles", f"{name}_traffic.md")
     if not os.path.exists(path):
         return None
     with open(path) as f:
-        return json.load(f).get("traffic_bytes")
+        for line in f:
+            if line.strip().startswith("traffic_bytes:"):
+                return int(line.split(":", 1)[1].strip())
+    return None
 
 
-def run_gpu(name, steps, warmup):
+def time_case(case, steps, warmup):
     import torch
 
-    cfg = CONFIGS[name]
-    dev = torch.device("cuda:0")
-    gen = torch.Generator(device=dev)
-    gen.manual_seed(cfg["seed"])
-    x = torch.randn(cfg["shape"], generator=gen, device=dev, dtype=torch.float32) * cfg["sigma"]
-    y = torch.empty_like(x)
-    prog = make_workload(cfg["kind"], x, y).compile(target="hip_gfx950")
     for _ in range(warmup):
-        prog.execute()
-        prog.synchronize()
+        case.prog.execute()
+        case.prog.synchronize()
     torch.cuda.synchronize()
     kernel_ms = []
     t0 = time.perf_counter()
     for _ in range(steps):
-        prog.execute()
-        prog.synchronize()
-        kernel_ms.append(prog.stats.device_time_ms)
+        case.prog.execute()
+        case.prog.synchronize()
+        kernel_ms.append(case.prog.stats.device_time_ms)
     torch.cuda.synchronize()
-    wall_ms = (time.perf_counter() - t0) * 1000.0
-    nbytes = 2 * x.numel() * 4
-    ms_step = wall_ms / steps
+    wall_s = time.perf_counter() - t0
     k_ms = sum(kernel_ms) / len(kernel_ms)
-    achieved = nbytes / (k_ms * 1e-3) / 1e9
-    return {
-        "x": x, "y": y, "prog": prog,
-        "ms_per_step": ms_step,
-        "kernel_ms": k_ms,
-        "gbps": nbytes / (ms_step * 1e-3) / 1e9,
-        "achieved_gbps": achieved,
-        "frac": achieved / HBM_PEAK_GBS,
-        "bytes": nbytes,
-        "tasks": prog.stats.task_count,
-        "total_cycles": prog.stats.total_cycles,
-    }
-
-
-def run_cpu(name, x, budget_s=12.0, max_reps=8):
-    """The oracle (C restatement of cpu_sim, 1 thread) on the same input."""
-    import numpy as np
-
-    from oracle.runner import run_workload
-
-    cfg = CONFIGS[name]
-    xh = x.detach().cpu().numpy()
-    yh = np.zeros_like(xh)
-    times = []
-    t_start = time.perf_counter()
-    while len(times) < max_reps and (time.perf_counter() - t_start) < budget_s:
-        t0 = time.perf_counter()
-        run_workload(make_workload(cfg["kind"], xh, yh))
-        times.append(time.perf_counter() - t0)
-    sec = sum(times) / len(times)
-    nbytes = 2 * xh.nbytes
-    return {"value": nbytes / sec / 1e9, "unit": "GB/s", "cores": 1, "kind": "port",
-            "sample": f"the full {name} workload X{list(cfg['shape'])}, {len(times)} run(s) of "
-                      f"{sec:.2f} s each, wall clock around the oracle call, 1 of {len(os.sched_getaffinity(0))} cores",
-            "y": yh}
+    return wall_s / steps * 1000.0, k_ms
 
 
 def main():
@@ -155,7 +273,7 @@ def main():
     ap.add_argument("--gpus", type=int, default=1)
     ap.add_argument("--steps", type=int, default=20)
     ap.add_argument("--warmup", type=int, default=3)
-    ap.add_argument("--config", default="all", help=f"one of {list(CONFIGS)} or 'all'")
+    ap.add_argument("--config", default="all", help=f"one of {list(CASES)} or 'all'")
     ap.add_argument("--no-cpu", action="store_true")
     args = ap.parse_args()
     if args.gpus != 1:
@@ -169,54 +287,57 @@ def main():
 
         __graft_entry__.build()
     assert torch.cuda.is_available(), "bench.py needs a GPU"
+    dev = torch.device("cuda:0")
 
-    names = list(CONFIGS) if args.config == "all" else [args.config]
+    if args.config == "all":
+        names = [n for n in CASES if n != "copy_calib"]
+    else:
+        names = [args.config]
     head = HEADLINE if HEADLINE in names else names[0]
-    per = {}
-    main_res = None
-    cpu = None
+    per, line_main, cpu = {}, None, None
     for name in names:
+        case = CASES[name]()
+        case.setup(dev)
         steps = args.steps if name == head else max(3, args.steps // 4)
-        r = run_gpu(name, steps, args.warmup)
-        entry = {"baseline_config": CONFIGS[name]["baseline_config"], "shape": list(CONFIGS[name]["shape"]),
-                 "kernel_ms": round(r["kernel_ms"], 5), "ms_per_step": round(r["ms_per_step"], 5),
-                 "achieved": round(r["achieved_gbps"], 1), "unit": "GB/s", "peak": HBM_PEAK_GBS,
-                 "frac": round(r["frac"], 4), "tasks": r["tasks"], "total_cycles": r["total_cycles"]}
-        if not args.no_cpu and name in (head, "softmax"):
-            c = run_cpu(name, r["x"], budget_s=12.0 if name == head else 6.0)
-            import numpy as np
-
-            same = bool(np.allclose(r["y"].cpu().numpy(), c.pop("y"), rtol=1e-5, atol=1e-6))
-            entry["cpu_sim_port_gbps"] = round(c["value"], 4)
+        ms_step, k_ms = time_case(case, steps, args.warmup)
+        achieved = case.rate(k_ms * 1e-3)
+        entry = {"baseline_config": case.baseline_config, "kernel_ms": round(k_ms, 5), "ms_per_step": round(ms_step, 5),
+                 "achieved": round(achieved, 2), "unit": case.unit, "peak": case.peak(),
+                 "frac": round(achieved / case.peak(), 4), "tasks": case.prog.stats.task_count,
+                 "total_cycles": case.prog.stats.total_cycles}
+        if not args.no_cpu and name != "rmsnorm_quickstart":
+            rate, sample, same = case.cpu(12.0 if name == head else 6.0)
+            entry["cpu_sim_port"] = round(rate, 6)
             entry["matches_cpu_sim"] = same
             if name == head:
-                cpu = c
+                cpu = {"value": round(rate, 4), "unit": case.unit, "cores": 1, "kind": "port",
+                       "sample": sample + f", 1 of {len(os.sched_getaffinity(0))} cores"}
         per[name] = entry
         if name == head:
-            main_res = r
-        del r
-        torch.cuda.empty_cache()
+            line_main = {"case": case, "ms_step": ms_step, "k_ms": k_ms, "achieved": achieved}
+        else:
+            del case
+            torch.cuda.empty_cache()
 
-    cfg = CONFIGS[head]
+    case = line_main["case"]
     line = {
         "metric": METRIC,
-        "value": round(main_res["gbps"], 2),
-        "unit": "GB/s",
+        "value": round(case.rate(line_main["ms_step"] * 1e-3), 2),
+        "unit": case.unit,
         "n_gpus": 1,
         "steps": args.steps,
         "warmup": args.warmup,
-        "ms_per_step": round(main_res["ms_per_step"], 5),
+        "ms_per_step": round(line_main["ms_step"], 5),
         "higher_is_better": True,
         "scaling": "weak",
         "vs_baseline": None,
-        "dtype": "f32",
-        "data": "synthetic (torch.randn on device, seeded)",
-        "config": {"workload": f"{head}: rmsnorm_tile Tile[16,128,F32] over X{list(cfg['shape'])}, "
-                               "P(batch=16) x P(tiles=8192), round_robin(4), TaskWindow(8192, STALL)",
-                   "baseline_config": cfg["baseline_config"], "bytes_per_step": main_res["bytes"],
-                   "target": "hip_gfx950"},
-        "roofline": {"bound": "hbm", "achieved": round(main_res["achieved_gbps"], 1), "peak": HBM_PEAK_GBS,
-                     "unit": "GB/s", "frac": round(main_res["frac"], 4), "traffic": load_traffic(head)},
+        "dtype": "f32" if case.unit == "GB/s" else "bf16",
+        "data": "synthetic (torch RNG on device, seeded)",
+        "config": {"workload": case.describe(), "baseline_config": case.baseline_config,
+                   "work_per_step": case.work, "target": "hip_gfx950"},
+        "roofline": {"bound": case.bound, "achieved": round(line_main["achieved"], 2), "peak": case.peak(),
+                     "unit": case.unit, "frac": round(line_main["achieved"] / case.peak(), 4),
+                     "traffic": load_traffic(head)},
         "cpu_baseline": cpu,
         "configs": per,
     }

@@ -104,6 +104,53 @@ bool classify_rows(const KernelDef& k, KernelAnalysis& a) {
     return true;
 }
 
+// MFMA GEMM pattern: Matmul(a, b) -> r1; optional Add(c, r1) -> r2; Store(c, r2|r1).
+GemmInfo classify_gemm(const KernelDef& k, const KernelAnalysis& a) {
+    GemmInfo g;
+    std::vector<const OpInfo*> ops;
+    for (const auto& op : k.ops)
+        if (op.kind != OpKind::Constant) ops.push_back(&op);
+    if (ops.size() != 2 && ops.size() != 3) return g;
+    const OpInfo& mm = *ops[0];
+    if (mm.kind != OpKind::Matmul || mm.result <= 0) return g;
+    const int pa = a.param_of[mm.operands[0]], pb = a.param_of[mm.operands[1]];
+    if (pa < 0 || pb < 0) return g;
+    int stored_val = mm.result;
+    int pc = -1;
+    if (ops.size() == 3) {
+        const OpInfo& add = *ops[1];
+        if (add.kind != OpKind::Add || add.operands.size() != 2) return g;
+        const int x = add.operands[0], y = add.operands[1];
+        const int other = x == mm.result ? y : (y == mm.result ? x : -1);
+        if (other < 0 || a.param_of[other] < 0) return g;
+        pc = a.param_of[other];
+        stored_val = add.result;
+        g.accumulate = true;
+    }
+    const OpInfo& st = *ops.back();
+    if (st.kind != OpKind::Store || st.operands[1] != stored_val) return g;
+    if (pc >= 0 && a.param_of[st.operands[0]] != pc) return g;
+    pc = a.param_of[st.operands[0]];
+    if (pc < 0 || pa == pb || pa == pc || pb == pc) return g;
+    const ValueInfo* va = a.by_id[k.params[pa].id];
+    const ValueInfo* vb = a.by_id[k.params[pb].id];
+    const ValueInfo* vc = a.by_id[k.params[pc].id];
+    if (va->dtype != vb->dtype || (va->dtype != DType::BF16 && va->dtype != DType::F16)) return g;
+    if (vc->dtype != DType::F32) return g;
+    const int M = va->rows, K = va->cols, N = vb->cols;
+    if (M % 64 || N % 64 || K % 16 || M > 256 || N > 256) return g;
+    if (2 * (M + N) * (K + 8) * 2 > 160 * 1024) return g;
+    g.ok = true;
+    g.a = a.tensor_ordinal[pa];
+    g.b = a.tensor_ordinal[pb];
+    g.c = a.tensor_ordinal[pc];
+    g.m = M;
+    g.n = N;
+    g.k = K;
+    g.f16 = va->dtype == DType::F16;
+    return g;
+}
+
 }  // namespace
 
 KernelAnalysis analyze_kernel(const KernelDef& k) {
@@ -312,7 +359,12 @@ KernelAnalysis analyze_kernel(const KernelDef& k) {
             refuse(k, std::string("tensor params of dtype ") + dtype_name(v->dtype) + " are not supported");
         if (v->dtype == DType::F64) refuse(k, "f64 tensor params are not supported");
     }
-    a.family = classify_rows(k, a) ? Family::RowProgram : Family::TileProgram;
+    if (classify_rows(k, a)) {
+        a.family = Family::RowProgram;
+    } else {
+        a.gemm = classify_gemm(k, a);
+        a.family = a.gemm.ok ? Family::Gemm : Family::TileProgram;
+    }
     return a;
 }
 

@@ -19,6 +19,16 @@ enum class Family { RowProgram, TileProgram, Gemm };
 // Role of a value inside a row program.
 enum class RowClass { None, Full, RowVec, RowVecT, ColVec, ColVecT, Scalar };
 
+// A kernel of the form  acc = matmul(a, b); [out = add(c, acc);] store(c, out|acc)
+// with bf16/f16 a, b and an fp32 c: runs on MFMA with the accumulator on chip.
+struct GemmInfo {
+    bool ok = false;
+    int a = -1, b = -1, c = -1;  // tensor ordinals
+    int m = 0, n = 0, k = 0;
+    bool f16 = false;
+    bool accumulate = false;     // c + a@b (InOut accumulator) instead of a@b
+};
+
 struct KernelAnalysis {
     const KernelDef* def = nullptr;
     int max_id = 0;
@@ -39,6 +49,7 @@ struct KernelAnalysis {
     int rows = 0, cols = 0;
     std::vector<RowClass> row_class;       // value id -> class
     std::string not_row_reason;
+    GemmInfo gemm;
 };
 
 // Throws CompileError for kernels the reference lowering cannot compute.

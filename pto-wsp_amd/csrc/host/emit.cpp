@@ -87,7 +87,7 @@ std::string offset_expr(int p, int nvars, int first_term, int nterms) {
 
 }  // namespace
 
-RowLayout row_layout(int cols, int vw) {
+RowLayout row_layout(int cols, int vw, int up_cap) {
     RowLayout l;
     l.vw = vw;
     const int n = cols / vw;
@@ -96,7 +96,8 @@ RowLayout row_layout(int cols, int vw) {
     l.g = g;
     l.nv = n / g;
     int up = 32 / (l.nv * vw);
-    l.up = up < 1 ? 1 : (up > 8 ? 8 : up);
+    if (up_cap < 1) up_cap = 1;
+    l.up = up < 1 ? 1 : (up > up_cap ? up_cap : up);
     return l;
 }
 
@@ -108,7 +109,8 @@ namespace {
 EmittedKernel emit_row(const Module& m, const KernelAnalysis& a, const LaunchSpec& L, const EmitSpec& spec) {
     (void)m;
     const KernelDef& k = *a.def;
-    const RowLayout lay = row_layout(a.cols, spec.vec_width);
+    const RowLayout lay = row_layout(a.cols, spec.vec_width, spec.row_up);
+    const char* nt = spec.nontemporal ? ", true" : "";
     const int R = a.rows, C = a.cols, ng = static_cast<int>(L.grid.size());
     const int rpw = 64 / lay.g, ch = rpw * lay.up;
     const bool chunk_in_task = R % ch == 0;
@@ -182,7 +184,7 @@ EmittedKernel emit_row(const Module& m, const KernelAnalysis& a, const LaunchSpe
     for (const auto& [id, p] : loads) {
         switch (cls(id)) {
             case RowClass::Full:
-                o << "    RS ld" << id << "[UP];\n#pragma unroll\n    for (int u = 0; u < UP; ++u) row_load<NV, VW, G>(ld" << id
+                o << "    RS ld" << id << "[UP];\n#pragma unroll\n    for (int u = 0; u < UP; ++u) row_load<NV, VW, G" << nt << ">(ld" << id
                   << "[u], (const float*)tb" << p << "[u] + (i64)rr[u] * A.s3[" << p << "], A.s4[" << p << "], j);\n";
                 break;
             case RowClass::RowVec:
@@ -226,7 +228,7 @@ EmittedKernel emit_row(const Module& m, const KernelAnalysis& a, const LaunchSpe
                     waited = true;
                 }
                 if (cls(s) == RowClass::Full)
-                    o << "      if (ok[u]) row_store<NV, VW, G>((float*)tb" << p << "[u] + (i64)rr[u] * A.s3[" << p << "], "
+                    o << "      if (ok[u]) row_store<NV, VW, G" << nt << ">((float*)tb" << p << "[u] + (i64)rr[u] * A.s3[" << p << "], "
                       << vname(s) << ", A.s4[" << p << "], j);\n";
                 else
                     o << "      if (ok[u] && j == 0) ((float*)tb" << p << "[u])[(i64)rr[u] * A.s3[" << p << "]] = " << vname(s)
@@ -467,9 +469,75 @@ EmittedKernel emit_tile(const Module& m, const KernelAnalysis& a, const LaunchSp
     return ek;
 }
 
+// ---------------------------------------------------------------------------
+// GEMM (MFMA) programs
+// ---------------------------------------------------------------------------
+EmittedKernel emit_gemm(const Module& m, const KernelAnalysis& a, const LaunchSpec& L, const EmitSpec& spec) {
+    (void)m;
+    (void)spec;
+    const KernelDef& k = *a.def;
+    const GemmInfo& g = a.gemm;
+    const int ng = static_cast<int>(L.grid.size()), ni = static_cast<int>(L.inner.size());
+    const int nvars = ng + ni;
+    EmittedKernel ek;
+    ek.threads = 256;
+    ek.row_program = false;
+    std::ostringstream o;
+    o << "#include \"ptowsp_device.h\"\nusing namespace ptowsp;\n";
+    o << "// gemm program: kernel " << k.name << ", " << g.m << "x" << g.n << "x" << g.k << (g.f16 ? " f16" : " bf16")
+      << (g.accumulate ? ", accumulate" : "") << "\n";
+    o << "extern \"C\" __global__ void __launch_bounds__(256) ptowsp_entry(const LaunchArgs A) {\n";
+    o << "  typedef GemmTile<" << g.m << ", " << g.n << ", " << g.k << ", " << (g.f16 ? "true" : "false") << "> GT;\n";
+    o << "  __shared__ __attribute__((aligned(16))) u16 lds[GT::kLdsElems];\n";
+    o << "  i64 vars[" << (nvars > 0 ? nvars : 1) << "];\n  (void)vars;\n";
+    o << "  for (i64 t = blockIdx.x; t < A.ntasks; t += gridDim.x) {\n";
+    emit_decode(o, "    ", ng, "t");
+    o << "    i64 iters = 1;\n";
+    for (int i = 0; i < ni; ++i) o << "    iters *= A.ext[" << ng + i << "];\n";
+    o << "    if (iters <= 0) continue;\n";
+    // The output view does not move with the in-kernel loops (checked on the host).
+    o << "    float* pc = reinterpret_cast<float*>(A.base[" << g.c << "] + (" << offset_expr(g.c, ng, 0, 0) << ") * 4);\n";
+    o << "    GT::Acc cacc;\n";
+    if (g.accumulate) o << "    GT::c_io<false>(cacc, pc, A.s3[" << g.c << "]);\n";
+    else o << "    GT::zero(cacc);\n";
+    // Operand pointers of in-kernel iteration `it` (mixed radix over the inner loops).
+    o << "    auto operands = [&](i64 it, const u16*& pa, const u16*& pb) {\n";
+    for (int i = ni - 1; i >= 0; --i) {
+        const int v = ng + i;
+        o << "      vars[" << v << "] = it % A.ext[" << v << "]; it /= A.ext[" << v << "];\n";
+    }
+    o << "      pa = reinterpret_cast<const u16*>(A.base[" << g.a << "] + (" << offset_expr(g.a, nvars, 0, 0) << ") * 2);\n";
+    o << "      pb = reinterpret_cast<const u16*>(A.base[" << g.b << "] + (" << offset_expr(g.b, nvars, 0, 0) << ") * 2);\n";
+    o << "    };\n";
+    o << "    const u16* pa;\n    const u16* pb;\n";
+    o << "    operands(0, pa, pb);\n";
+    o << "    GT::Regs regs;\n";
+    o << "    GT::gload(regs, pa, A.s3[" << g.a << "], pb, A.s3[" << g.b << "]);\n";
+    o << "    for (i64 it = 0; it < iters; ++it) {\n";
+    o << "      u16* stage = lds + (it & 1) * GT::kStage;\n";
+    o << "      GT::lstore(stage, regs);\n";
+    o << "      __syncthreads();\n";
+    o << "      if (it + 1 < iters) {\n";
+    o << "        operands(it + 1, pa, pb);\n";
+    o << "        GT::gload(regs, pa, A.s3[" << g.a << "], pb, A.s3[" << g.b << "]);\n";
+    o << "      }\n";
+    o << "      GT::Acc acc;\n      GT::zero(acc);\n      GT::mma(acc, stage);\n";
+    if (g.accumulate) o << "      GT::add(cacc, acc);\n";
+    else o << "      cacc = acc;\n";
+    o << "    }\n";
+    o << "    GT::c_io<true>(cacc, pc, A.s3[" << g.c << "]);\n";
+    o << "    __syncthreads();\n";
+    o << "  }\n}\n";
+    ek.source = o.str();
+    ek.entry = "ptowsp_entry";
+    ek.lds_bytes = static_cast<size_t>(2 * (g.m + g.n) * (g.k + 8) * 2);
+    return ek;
+}
+
 }  // namespace
 
 EmittedKernel emit_launch(const Module& m, const KernelAnalysis& a, const LaunchSpec& L, const EmitSpec& spec) {
+    if (spec.gemm && a.family == Family::Gemm && !spec.serial) return emit_gemm(m, a, L, spec);
     bool indirect = false;
     for (int c : spec.indirect_count) indirect = indirect || c > 0;
     if (a.family == Family::RowProgram && L.inner.empty() && !indirect && !spec.serial) return emit_row(m, a, L, spec);

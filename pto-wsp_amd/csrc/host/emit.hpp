@@ -19,6 +19,12 @@ struct EmitSpec {
     // when tasks of the grid write overlapping memory (the result then
     // depends on the reference's sequential order).
     bool serial = false;
+    // Row programs: cap on passes per wave iteration, and non-temporal
+    // (streaming) global accesses for full-row tiles.
+    int row_up = 8;
+    bool nontemporal = false;
+    // GEMM family on MFMA (only when strides and alignment allow it).
+    bool gemm = false;
 };
 
 struct EmittedKernel {
@@ -38,6 +44,6 @@ EmittedKernel emit_launch(const Module& m, const KernelAnalysis& a, const Launch
 struct RowLayout {
     int vw = 1, g = 1, nv = 1, up = 1;
 };
-RowLayout row_layout(int cols, int vw);
+RowLayout row_layout(int cols, int vw, int up_cap = 8);
 
 }  // namespace ptowsp

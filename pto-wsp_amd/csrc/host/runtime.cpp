@@ -4,7 +4,9 @@
 
 #include <algorithm>
 #include <chrono>
+#include <cstdlib>
 #include <cstring>
+#include <functional>
 #include <map>
 #include <memory>
 #include <sstream>
@@ -264,6 +266,25 @@ int pick_vec_width(const KernelAnalysis& a, const LaunchArgs& A, int nvars) {
     return 1;
 }
 
+// Launch-shape defaults of the row-program family, from a sweep on MI355X
+// (2 passes per wave iteration with non-temporal loads/stores was fastest
+// for both the rmsnorm and the softmax configurations);
+// PTOWSP_ROW_UNROLL / PTOWSP_NONTEMPORAL override them.
+struct Tuning {
+    int row_up = 2;
+    bool nontemporal = true;
+};
+
+const Tuning& tuning() {
+    static const Tuning t = [] {
+        Tuning v;
+        if (const char* s = std::getenv("PTOWSP_ROW_UNROLL")) v.row_up = std::max(1, std::atoi(s));
+        if (const char* s = std::getenv("PTOWSP_NONTEMPORAL")) v.nontemporal = std::atoi(s) != 0;
+        return v;
+    }();
+    return t;
+}
+
 // True when two different tasks of the grid may touch the same element of a
 // tensor that the launch writes.  P() promises independent iterations; a
 // workload that breaks the promise (overlapping output views) still gets
@@ -288,26 +309,63 @@ bool grid_write_hazard(const KernelAnalysis& a, const LaunchSpec& L, const Launc
             for (int v = 0; v < nvars; ++v)
                 if (A.coef[q][v] != A.coef[p][v]) return true;
         }
-        // Footprint of one task: its tile swept over the in-kernel loops.
-        int64_t width = (vp->rows - 1) * std::llabs(A.s3[p]) + (vp->cols - 1) * std::llabs(A.s4[p]) + 1;
+        // (stride, extent) of every index that moves the written element:
+        // tile rows/cols, in-kernel loops, grid loops.
+        std::vector<std::pair<int64_t, int64_t>> tile_dims, grid_dims;
+        tile_dims.emplace_back(std::llabs(A.s3[p]), vp->rows);
+        tile_dims.emplace_back(std::llabs(A.s4[p]), vp->cols);
         for (size_t i = 0; i < L.inner.size(); ++i) {
             const int v = ng + static_cast<int>(i);
             if (A.coef[p][v] == 0) continue;
             if (spec.inner_dyn_term[i] >= 0) return true;
-            width += std::llabs(A.coef[p][v]) * std::max<int64_t>(0, A.ext[v] - 1);
+            tile_dims.emplace_back(std::llabs(A.coef[p][v]), A.ext[v]);
         }
-        // Grid dimensions must nest without overlap, like the strides of an array.
-        std::vector<std::pair<int64_t, int64_t>> dims;
-        for (int v = 0; v < ng; ++v)
-            if (A.ext[v] > 1) dims.emplace_back(std::llabs(A.coef[p][v]), A.ext[v]);
-        std::sort(dims.begin(), dims.end());
-        int64_t span = width;
-        for (const auto& [c, e] : dims) {
-            if (c < span) return true;
-            span += c * (e - 1);
-        }
+        for (int v = 0; v < ng; ++v) grid_dims.emplace_back(std::llabs(A.coef[p][v]), A.ext[v]);
+        // Sufficient condition 1: every index nests like the strides of an
+        // array, so the whole map (grid x task) is injective.
+        auto nests = [](std::vector<std::pair<int64_t, int64_t>> dims, int64_t start) {
+            std::sort(dims.begin(), dims.end());
+            int64_t span = start;
+            for (const auto& [c, e] : dims) {
+                if (e <= 1) continue;
+                if (c < span) return false;
+                span += c * (e - 1);
+            }
+            return true;
+        };
+        std::vector<std::pair<int64_t, int64_t>> all = tile_dims;
+        all.insert(all.end(), grid_dims.begin(), grid_dims.end());
+        if (nests(all, 1)) continue;
+        // Sufficient condition 2: one task's footprint fits in an interval and
+        // the grid steps over whole intervals.
+        int64_t width = 1;
+        for (const auto& [c, e] : tile_dims) width += c * std::max<int64_t>(0, e - 1);
+        if (!nests(grid_dims, width)) return true;
     }
     return false;
+}
+
+// The MFMA GEMM template needs unit column strides, 16-byte aligned operand
+// rows at every task and K step, an output tile that stays put across the
+// in-kernel loops, and operands that the launch does not write.
+bool gemm_allowed(const KernelAnalysis& a, const LaunchSpec& L, const LaunchArgs& A, const EmitSpec& spec, int ng,
+                  int nvars) {
+    if (a.family != Family::Gemm || spec.serial) return false;
+    for (int c : spec.indirect_count)
+        if (c) return false;
+    for (int t : spec.inner_dyn_term)
+        if (t >= 0) return false;
+    const GemmInfo& g = a.gemm;
+    if (A.s4[g.a] != 1 || A.s4[g.b] != 1 || A.s4[g.c] != 1) return false;
+    if (reinterpret_cast<uintptr_t>(A.base[g.a]) % 16 || reinterpret_cast<uintptr_t>(A.base[g.b]) % 16) return false;
+    if (A.s3[g.a] % 8 || A.s3[g.b] % 8) return false;
+    for (int v = 0; v < nvars; ++v) {
+        if (A.coef[g.a][v] % 8 || A.coef[g.b][v] % 8) return false;
+        if (v >= ng && A.coef[g.c][v] != 0) return false;
+    }
+    const int tc = L.targs[g.c]->tid;
+    if (L.targs[g.a]->tid == tc || L.targs[g.b]->tid == tc) return false;
+    return true;
 }
 
 BuiltLaunch build_launch(RunEnv& E, const LaunchSpec& L) {
@@ -450,13 +508,17 @@ BuiltLaunch build_launch(RunEnv& E, const LaunchSpec& L) {
     }
     A.err = P->d_err;
     B.spec.serial = grid_write_hazard(a, L, A, B.spec, ng, nvars);
+    B.spec.row_up = tuning().row_up;
+    B.spec.nontemporal = tuning().nontemporal;
+    B.spec.gemm = gemm_allowed(a, L, A, B.spec, ng, nvars);
     B.spec.vec_width = a.family == Family::RowProgram ? pick_vec_width(a, A, nvars) : 1;
     return B;
 }
 
 std::string spec_key(const EmitSpec& s) {
     std::ostringstream o;
-    o << "vw" << s.vec_width << (s.serial ? ";serial" : "") << ";i";
+    o << "vw" << s.vec_width << (s.serial ? ";serial" : "") << ";up" << s.row_up << (s.nontemporal ? ";nt" : "")
+      << (s.gemm ? ";gemm" : "") << ";i";
     for (int c : s.indirect_count) o << c << ",";
     o << ";d";
     for (int c : s.inner_dyn_term) o << c << ",";
@@ -677,6 +739,9 @@ int ptowsp_hip_precompile(ptowsp_program* P, int index, int flags, const char** 
             const KernelAnalysis& a = P->ka[L.kernel];
             EmitSpec spec;
             spec.serial = (flags & 1) != 0;
+            spec.row_up = tuning().row_up;
+            spec.nontemporal = tuning().nontemporal;
+            spec.gemm = a.family == Family::Gemm && !spec.serial;
             spec.indirect_count.assign(L.targs.size(), 0);
             for (size_t p = 0; p < L.targs.size(); ++p)
                 for (const auto& e : L.targs[p]->idx)

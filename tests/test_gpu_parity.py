@@ -216,3 +216,59 @@ def test_ragged_axis_rebinding(gpu):
     prog.execute()
     prog.synchronize()
     np.testing.assert_array_equal(y.reshape(3), [1, 1, 1])
+
+
+def _rel_fro(got, ref):
+    return float(np.linalg.norm((got - ref).ravel()) / np.linalg.norm(ref.ravel()))
+
+
+@pytest.mark.parametrize("tiles", [(128, 128, 64), (64, 64, 16), (128, 64, 32)])
+def test_bgemm_bf16_mfma_accumulate(gpu, tiles):
+    """bf16 x bf16 -> fp32 on MFMA with the InOut accumulator kept on chip (nonzero initial C)."""
+    tm, tn, tk = tiles
+    rng = np.random.default_rng(5)
+    a = W.bf16_round(rng.uniform(-1, 1, (2, 256, 512)).astype(np.float32))
+    b = W.bf16_round(rng.uniform(-1, 1, (2, 512, 256)).astype(np.float32))
+    c0 = rng.standard_normal((2, 256, 256)).astype(np.float32)
+    ga = {"a": a, "b": b, "c": c0.copy()}
+    ca = {"a": a.copy(), "b": b.copy(), "c": c0.copy()}
+    prog = run_hip(W.rr4(W.bgemm(ga, tm, tn, tk, W.BF16)))
+    ref = run_workload(W.rr4(W.bgemm(ca, tm, tn, tk, W.BF16)))
+    assert prog._native.kernel_family("gemm_tile") == "gemm"
+    rel = _rel_fro(ga["c"], ca["c"])
+    assert rel <= 1e-2, rel      # north_star tolerance for bf16 matmul
+    assert rel <= 1e-5, rel      # observed: only fp32 summation order differs
+    exact = c0.astype(np.float64) + W.bf16_to_f32(a).astype(np.float64) @ W.bf16_to_f32(b).astype(np.float64)
+    assert _rel_fro(ga["c"], exact) <= 1e-5
+    assert prog.stats.total_cycles == ref.total_cycles
+
+
+def test_bgemm_plain_store_keeps_last_k_step(gpu):
+    """store(c, matmul(a, b)) inside P.seq(k): each step overwrites C, so C = A[:, k_last] @ B[k_last]."""
+    rng = np.random.default_rng(6)
+    a = W.bf16_round(rng.uniform(-1, 1, (1, 128, 256)).astype(np.float32))
+    b = W.bf16_round(rng.uniform(-1, 1, (1, 256, 128)).astype(np.float32))
+    ga = {"a": a, "b": b, "c": np.zeros((1, 128, 128), np.float32)}
+    ca = {"a": a.copy(), "b": b.copy(), "c": np.zeros((1, 128, 128), np.float32)}
+    run_hip(W.bgemm(ga, 64, 64, 64, W.BF16, plain=True))
+    run_workload(W.bgemm(ca, 64, 64, 64, W.BF16, plain=True))
+    assert _rel_fro(ga["c"], ca["c"]) <= 1e-5
+    last = W.bf16_to_f32(a)[0, :, 192:].astype(np.float64) @ W.bf16_to_f32(b)[0, 192:, :].astype(np.float64)
+    assert _rel_fro(ga["c"][0], last) <= 1e-5
+
+
+def test_bgemm_f16_mfma_device_tensors(gpu):
+    import torch
+
+    rng = np.random.default_rng(7)
+    a = rng.uniform(-1, 1, (3, 128, 192)).astype(np.float16)
+    b = rng.uniform(-1, 1, (3, 192, 128)).astype(np.float16)
+    ad, bd = torch.from_numpy(a).to(gpu), torch.from_numpy(b).to(gpu)
+    cd = torch.zeros((3, 128, 128), device=gpu, dtype=torch.float32)
+    from pto_wsp import DType
+
+    prog = run_hip(W.rr4(W.bgemm({"a": ad, "b": bd, "c": cd}, 64, 64, 64, DType.F16)))
+    ca = {"a": a.copy(), "b": b.copy(), "c": np.zeros((3, 128, 128), np.float32)}
+    ref = run_workload(W.rr4(W.bgemm(ca, 64, 64, 64, DType.F16)))
+    assert _rel_fro(cd.cpu().numpy(), ca["c"]) <= 1e-5
+    assert prog.stats.total_cycles == ref.total_cycles

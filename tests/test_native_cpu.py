@@ -64,6 +64,9 @@ def _cases():
         "softmax": (lambda: W.rr4(W.softmax({"x": xs, "y": np.zeros_like(xs)})), {}),
         "softmax3": (lambda: W.rr4(W.softmax3(W.softmax3_arrays(lg))), {}),
         "bgemm_f16": (lambda: W.rr4(W.bgemm({"a": a16, "b": b16, "c": np.zeros((1, 64, 64), np.float32)})), {}),
+        "bgemm_bf16": (lambda: W.rr4(W.bgemm({"a": W.bf16_round(np.ones((1, 256, 256), np.float32)),
+                                               "b": W.bf16_round(np.ones((1, 256, 256), np.float32)),
+                                               "c": np.zeros((1, 256, 256), np.float32)}, 128, 128, 64, W.BF16)), {}),
         "decode": (lambda: W.rr4(W.decode_attention({"q": q, "k_t": k.T.copy(), "v": v, "o": np.zeros((1, 16), np.float32)}), 1024), {}),
         "attention": (lambda: W.rr4(W.tiled_attention(W.attention_arrays(qa, qa, qa, 8), 8)), {}),
         "copy": (lambda: W.copy_tiles({"a": np.arange(64, dtype=np.float32).reshape(4, 4, 4),
@@ -118,7 +121,12 @@ def test_family_selection():
     assert prog.kernel_cycles("rmsnorm_tile") == 4 * 2048 + 3 * 16
     a = np.zeros((1, 64, 64), np.float16)
     prog = NativeProgram(workload_to_codegen_ir(W.bgemm({"a": a, "b": a, "c": np.zeros((1, 64, 64), np.float32)}), "g").module)
-    assert prog.kernel_family("gemm_tile") in ("gemm", "tile_program")
+    assert prog.kernel_family("gemm_tile") == "tile_program"  # 16x16 tiles: below the MFMA tile minimum
+    a = np.zeros((1, 256, 256), np.uint16)
+    prog = NativeProgram(workload_to_codegen_ir(
+        W.bgemm({"a": a, "b": a, "c": np.zeros((1, 256, 256), np.float32)}, 128, 128, 64, W.BF16), "g").module)
+    assert prog.kernel_family("gemm_tile") == "gemm"
+    assert "gemm program" in prog.precompile(0)
 
 
 def _compile_err(w, match):

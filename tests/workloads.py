@@ -131,20 +131,29 @@ def softmax3_arrays(logits: np.ndarray) -> dict:
 
 
 # ---------------------------------------------------------------- bgemm (examples/bgemm pattern)
-def bgemm(arrs: dict, tm: int = 16, tn: int = 16, tk: int = 16, dtype=F16):
-    """C[b] += A[b] @ B[b] over tiles with a P.seq K loop and an InOut accumulator."""
+def bgemm(arrs: dict, tm: int = 16, tn: int = 16, tk: int = 16, dtype=F16, plain: bool = False):
+    """C[b] += A[b] @ B[b] over tiles with a P.seq K loop and an InOut accumulator.
+    plain=True stores matmul(a, b) alone (the last K step wins, as in the reference)."""
     a, b_, c = arrs["a"], arrs["b"], arrs["c"]
     B, M, K = a.shape
     N = b_.shape[2]
-    at = a.reshape(B, M // tm, tm, K // tk, tk).transpose(0, 1, 3, 2, 4)
-    bt = b_.reshape(B, K // tk, tk, N // tn, tn).transpose(0, 3, 1, 2, 4)
-    ct = c.reshape(B, M // tm, tm, N // tn, tn).transpose(0, 1, 3, 2, 4)
+    def perm(x, axes):  # numpy or torch
+        return x.permute(*axes) if hasattr(x, "permute") else x.transpose(*axes)
+
+    at = perm(a.reshape(B, M // tm, tm, K // tk, tk), (0, 1, 3, 2, 4))
+    bt = perm(b_.reshape(B, K // tk, tk, N // tn, tn), (0, 3, 1, 2, 4))
+    ct = perm(c.reshape(B, M // tm, tm, N // tn, tn), (0, 1, 3, 2, 4))
     A, Bm, C = T(at, dtype), T(bt, dtype), T(ct)
 
-    @kernel
-    def gemm_tile(a_tile: In[Tile[tm, tk, dtype]], b_tile: In[Tile[tk, tn, dtype]], c_tile: InOut[Tile[tm, tn, F32]]):
-        acc = pto.matmul(a_tile, b_tile)
-        pto.store(c_tile, pto.add(c_tile, acc))
+    if plain:
+        @kernel
+        def gemm_tile(a_tile: In[Tile[tm, tk, dtype]], b_tile: In[Tile[tk, tn, dtype]], c_tile: Out[Tile[tm, tn, F32]]):
+            pto.store(c_tile, pto.matmul(a_tile, b_tile))
+    else:
+        @kernel
+        def gemm_tile(a_tile: In[Tile[tm, tk, dtype]], b_tile: In[Tile[tk, tn, dtype]], c_tile: InOut[Tile[tm, tn, F32]]):
+            acc = pto.matmul(a_tile, b_tile)
+            pto.store(c_tile, pto.add(c_tile, acc))
 
     batch, mt, nt, kt = Dense[B](), Dense[M // tm](), Dense[N // tn](), Dense[K // tk]()
 
