@@ -84,7 +84,8 @@ int ptowsp_hip_kernel_family(const ptowsp_program* prog, const char* kernel);
  * touching a GPU (hiprtc only); returns the source of launch `index` through
  * `source`, valid until the next call.  flags bit 0: build the variant that
  * runs all tasks of a launch in program order (used when grid tasks write
- * overlapping memory). */
+ * overlapping memory); bit 1: build GEMM launches with 2x2 neighbouring tasks
+ * of the last two grid loops merged into one workgroup block. */
 int ptowsp_hip_precompile(ptowsp_program* prog, int index, int flags, const char** source);
 
 /* Evaluates only the cpu_sim cycle model (total_cycles, task_count) for the

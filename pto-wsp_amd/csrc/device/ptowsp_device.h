@@ -267,22 +267,34 @@ __device__ inline void tile_store_i(char* p, const i64* src, i64 s3, i64 s4) {
 }
 
 // ---------------------------------------------------------------------------
-// GEMM tiles: C[M,N] (fp32) from A[M,K] x B[K,N] (bf16 or f16) on MFMA
+// GEMM blocks: C[BM,BN] (fp32) (+)= sum over K steps of A[BM,BK] x B[BK,BN]
+// (bf16 or f16) on MFMA v_mfma_f32_32x32x16
 // ---------------------------------------------------------------------------
 //
-// One workgroup (4 waves, 2x2) owns the M x N tile; wave (wm, wn) computes
-// the (M/2) x (N/2) quadrant as 32x32 blocks of v_mfma_f32_32x32x16_*.
-// K steps are staged through LDS, double-buffered: A keeps its [m][k]
-// layout; B is transposed on the way in (register 4x8 transpose) to
-// Bt[n][k], so both MFMA operands are read as 8 consecutive k values.
-// Lane l of a 32x32x16 MFMA holds row/col (l % 32), k = 8*(l/32) .. +7, and
-// accumulator element e sits at row (e/4)*8 + (l/32)*4 + e%4, col l % 32.
+// A workgroup of WM x WN waves owns a BM x BN block of C (one task's tile, or
+// several neighbouring tasks' tiles merged by the host).  Wave (wm, wn) holds
+// its (BM/WM) x (BN/WN) quadrant in registers as 32x32 MFMA blocks for the
+// whole K loop; for an accumulating kernel the block starts from C.
+//
+// K steps go through two LDS stages filled by direct buffer->LDS loads (each
+// wave instruction moves 1 KiB, no VGPR staging):
+//   A stage [BM][BK]: 16-byte chunk c of row m lives at chunk c ^ swa(m), so
+//     the 32 rows of an MFMA operand read hit distinct banks;
+//   B stage [BK][BN] (k-major, as in memory): 32-byte segment g of row k lives
+//     at g ^ (k & 3); the MFMA B operand is read with ds_read_b64_tr_b16,
+//     which transposes 16-bit elements across each group of 16 lanes.
+// MFMA 32x32x16 lane l holds A row / B column (l % 32) with k = 8*(l/32)..+7;
+// accumulator element e sits at row (e/4)*8 + (l/32)*4 + e%4, column l % 32.
+// ds_read_b64_tr_b16: in each 16-lane group, lane l receives element (l % 4)
+// of the 8-byte chunks addressed by lanes 16*(l/16) + (l%16)/4 + 4e, e = 0..3.
 
 typedef unsigned int u32x2 __attribute__((ext_vector_type(2)));
 typedef unsigned int u32x4 __attribute__((ext_vector_type(4)));
+typedef short s16x4 __attribute__((ext_vector_type(4)));
 typedef __bf16 bf16x8 __attribute__((ext_vector_type(8)));
 typedef _Float16 f16x8 __attribute__((ext_vector_type(8)));
 typedef float f32x16 __attribute__((ext_vector_type(16)));
+typedef __amdgpu_buffer_rsrc_t buf_rsrc;
 
 template <bool F16>
 __device__ inline f32x16 mfma_32x32x16(u32x4 a, u32x4 b, f32x16 c) {
@@ -293,141 +305,197 @@ __device__ inline f32x16 mfma_32x32x16(u32x4 a, u32x4 b, f32x16 c) {
                                                        0);
 }
 
-template <int M, int N, int K, bool F16>
-struct GemmTile {
-    static_assert(M % 64 == 0 && N % 64 == 0 && K % 16 == 0, "GEMM tile shape");
-    static constexpr int AP = K + 8;  // LDS row pitch (16-bit elements) of A[m][k]
-    static constexpr int BP = K + 8;  // LDS row pitch of Bt[n][k]
-    static constexpr int ABUF = M * AP;
-    static constexpr int BBUF = N * BP;
-    static constexpr int kStage = ABUF + BBUF;
-    static constexpr int kLdsElems = 2 * kStage;
-    static constexpr int BI = M / 64, BJ = N / 64;
-    static constexpr int ACH = M * K / 8;
-    static constexpr int AQ = (ACH + 255) / 256;
-    static constexpr int BBLK = (K / 4) * (N / 8);
-    static constexpr int BQ = (BBLK + 255) / 256;
+__device__ inline int wave_index() { return __builtin_amdgcn_readfirstlane(static_cast<int>(threadIdx.x >> 6)); }
 
-    struct Regs {
-        u32x4 a[AQ];
-        u32x4 b[BQ][4];
-    };
+// Raw dword buffer descriptor for p (no range check: offsets are bounded on the host).
+__device__ inline u32x4 buffer_words(const void* p) {
+    const u64 a = reinterpret_cast<u64>(p);
+    u32x4 r;
+    r.x = __builtin_amdgcn_readfirstlane(static_cast<u32>(a));
+    r.y = __builtin_amdgcn_readfirstlane(static_cast<u32>(a >> 32) & 0xFFFFu);
+    r.z = 0xFFFFFFFFu;
+    r.w = 0x00020000u;
+    return r;
+}
+
+__device__ inline u32 lds_address(const void* p) {
+    return static_cast<u32>(reinterpret_cast<u64>((const __attribute__((address_space(3))) void*)p));
+}
+
+// 16 bytes per lane from global (descriptor + voff + soff) into LDS at
+// lds_addr + 16*lane.  Written as inline asm so that the compiler's wait-count
+// pass does not serialise later LDS reads behind it; callers wait with
+// wait_vmcnt<0>() and a barrier before the stage is read.  M0 is restored.
+__device__ inline void dma16(u32x4 rsrc, int voff, int soff, u32 lds_addr) {
+    u32 saved;
+    asm volatile(
+        "s_mov_b32 %0, m0\n\t"
+        "s_mov_b32 m0, %4\n\t"
+        "s_nop 0\n\t"
+        "buffer_load_dwordx4 %1, %2, %3 offen lds\n\t"
+        "s_nop 0\n\t"
+        "s_mov_b32 m0, %0"
+        : "=&s"(saved)
+        : "v"(voff), "s"(rsrc), "s"(__builtin_amdgcn_readfirstlane(soff)), "s"(__builtin_amdgcn_readfirstlane(lds_addr))
+        : "memory");
+}
+
+// s_waitcnt on vmcnt only (gfx9 encoding; expcnt and lgkmcnt left at their maxima).
+template <int N>
+__device__ inline void wait_vmcnt() {
+    __builtin_amdgcn_s_waitcnt((N & 15) | ((N >> 4) << 14) | (7 << 4) | (15 << 8));
+}
+
+// Position of workgroup w among n workgroups dispatched round-robin over the
+// 8 XCDs, so that each XCD (own L2) gets a contiguous run of tiles.
+__device__ inline i64 xcd_order(i64 w, i64 n) {
+    const i64 q = n / 8, r = n % 8, x = w % 8, l = w / 8;
+    return x * q + (x < r ? x : r) + l;
+}
+
+template <int BM, int BN, int BK, int WM, int WN, bool F16>
+struct GemmBlock {
+    static constexpr int NW = WM * WN, NT = 64 * NW, KS = BK / 16;
+    static constexpr int TM = BM / WM, TN = BN / WN, FI = TM / 32, FJ = TN / 32;
+    static constexpr int CH = BK / 8;                  // 16-byte chunks per A row
+    static constexpr int RPL = CH >= 8 ? 1 : 8 / CH;   // A rows per 128-byte LDS line
+    static constexpr int SWM = (CH < 8 ? CH : 8) - 1;
+    static constexpr int ARPB = 1024 / (2 * BK);       // A rows per 1 KiB load
+    static constexpr int BCPR = BN / 8;                // 16-byte chunks per B row
+    static constexpr int BRPB = 1024 / (2 * BN);       // B rows per 1 KiB load
+    static constexpr int ABLK = BM * BK * 2 / 1024, BBLK = BK * BN * 2 / 1024;
+    static constexpr int AQ = (ABLK + NW - 1) / NW, BQ = (BBLK + NW - 1) / NW;
+    static constexpr int ASZ = BM * BK, STAGE = ASZ + BK * BN;
+    static constexpr int kLdsElems = 2 * STAGE;
+    static_assert(TM % 32 == 0 && TN % 32 == 0 && BK % 16 == 0 && (BK & (BK - 1)) == 0, "GEMM block shape");
+    static_assert(BN >= 64 && BN <= 512 && (BM * BK * 2) % 1024 == 0 && (BK * BN * 2) % 1024 == 0, "GEMM block shape");
+
     struct Acc {
-        f32x16 v[BI][BJ];
+        f32x16 v[FI][FJ];
+    };
+    struct Offs {
+        int a[AQ];
+        int b[BQ];
     };
 
-    // A element (m,k) at pa[m*s3a + k]; B element (k,n) at pb[k*s3b + n].
-    __device__ static void gload(Regs& r, const u16* pa, i64 s3a, const u16* pb, i64 s3b) {
-        const int tid = threadIdx.x;
+    __device__ static int swa(int m) { return ((m / RPL) ^ (m >> 3)) & SWM; }
+
+    // Per-lane byte offsets, from the block's A / B origin at the first K step,
+    // of the chunks this wave moves (lda / ldb: row pitch in elements).
+    __device__ static void offsets(Offs& o, int lda, int ldb) {
+        const int lane = threadIdx.x & 63, w = wave_index();
 #pragma unroll
         for (int q = 0; q < AQ; ++q) {
-            const int c = tid + q * 256;
-            if (c < ACH) {
-                const int row = c / (K / 8), col = (c % (K / 8)) * 8;
-                r.a[q] = *reinterpret_cast<const u32x4*>(pa + row * s3a + col);
-            }
+            const int m = (w * AQ + q) * ARPB + lane / CH, p = lane % CH;
+            o.a[q] = (m * lda + ((p ^ swa(m)) << 3)) * 2;
         }
 #pragma unroll
         for (int q = 0; q < BQ; ++q) {
-            const int blk = tid + q * 256;
-            if (blk < BBLK) {
-                const int k0 = (blk / (N / 8)) * 4, n0 = (blk % (N / 8)) * 8;
-#pragma unroll
-                for (int i = 0; i < 4; ++i) r.b[q][i] = *reinterpret_cast<const u32x4*>(pb + (k0 + i) * s3b + n0);
-            }
+            const int k = (w * BQ + q) * BRPB + lane / BCPR, p = lane % BCPR;
+            const int c = (((p >> 1) ^ (k & 3)) << 1) | (p & 1);
+            o.b[q] = (k * ldb + c * 8) * 2;
         }
     }
 
-    __device__ static void lstore(u16* stage, const Regs& r) {
-        const int tid = threadIdx.x;
-        u16* as = stage;
-        u16* bs = stage + ABUF;
+    // Issues the direct loads of one K step (soa / sob: its uniform byte offsets).
+    __device__ static void load(u16* stage, const Offs& o, u32x4 ra, int soa, u32x4 rb, int sob) {
+        const int w = wave_index();
+        const u32 base = lds_address(stage);
 #pragma unroll
-        for (int q = 0; q < AQ; ++q) {
-            const int c = tid + q * 256;
-            if (c < ACH) {
-                const int row = c / (K / 8), col = (c % (K / 8)) * 8;
-                *reinterpret_cast<u32x4*>(as + row * AP + col) = r.a[q];
-            }
-        }
+        for (int q = 0; q < AQ; ++q)
+            if (AQ * NW == ABLK || w * AQ + q < ABLK) dma16(ra, o.a[q], soa, base + (w * AQ + q) * 1024);
 #pragma unroll
-        for (int q = 0; q < BQ; ++q) {
-            const int blk = tid + q * 256;
-            if (blk < BBLK) {
-                const int k0 = (blk / (N / 8)) * 4, n0 = (blk % (N / 8)) * 8;
-#pragma unroll
-                for (int w = 0; w < 4; ++w) {
-                    // words w of rows k0..k0+3 hold columns n0+2w (low half) and n0+2w+1 (high half)
-                    const u32 x0 = r.b[q][0][w], x1 = r.b[q][1][w], x2 = r.b[q][2][w], x3 = r.b[q][3][w];
-                    u32x2 lo, hi;
-                    lo.x = (x0 & 0xFFFFu) | (x1 << 16);
-                    lo.y = (x2 & 0xFFFFu) | (x3 << 16);
-                    hi.x = (x0 >> 16) | (x1 & 0xFFFF0000u);
-                    hi.y = (x2 >> 16) | (x3 & 0xFFFF0000u);
-                    *reinterpret_cast<u32x2*>(bs + (n0 + 2 * w) * BP + k0) = lo;
-                    *reinterpret_cast<u32x2*>(bs + (n0 + 2 * w + 1) * BP + k0) = hi;
-                }
-            }
-        }
+        for (int q = 0; q < BQ; ++q)
+            if (BQ * NW == BBLK || w * BQ + q < BBLK) dma16(rb, o.b[q], sob, base + ASZ * 2 + (w * BQ + q) * 1024);
     }
 
-    __device__ static void zero(Acc& a) {
-#pragma unroll
-        for (int i = 0; i < BI; ++i)
-#pragma unroll
-            for (int j = 0; j < BJ; ++j)
-#pragma unroll
-                for (int e = 0; e < 16; ++e) a.v[i][j][e] = 0.0f;
-    }
-
-    // acc = A_stage x B_stage over the K of one stage, into a zeroed accumulator.
     __device__ static void mma(Acc& acc, const u16* stage) {
-        const int lane = threadIdx.x & 63, wave = threadIdx.x >> 6;
-        const int wm = wave >> 1, wn = wave & 1;
-        const u16* as = stage;
-        const u16* bs = stage + ABUF;
-        const int r = lane & 31, kh = (lane >> 5) * 8;
+        const int lane = threadIdx.x & 63, wave = wave_index();
+        const int wm = wave / WN, wn = wave % WN;
+        const int r = lane & 31, kc = lane >> 5;
+        const int g = lane >> 4, a4 = lane & 3, e = (lane >> 2) & 3;
+        const u16* as = stage + (wm * TM + r) * BK;
+        const u16* bs = stage + ASZ;
 #pragma unroll
-        for (int kk = 0; kk < K; kk += 16) {
-            u32x4 af[BI], bf[BJ];
+        for (int kk = 0; kk < BK; kk += 16) {
+            u32x4 af[FI], bf[FJ];
 #pragma unroll
-            for (int i = 0; i < BI; ++i)
-                af[i] = *reinterpret_cast<const u32x4*>(as + (wm * (M / 2) + i * 32 + r) * AP + kk + kh);
+            for (int i = 0; i < FI; ++i)
+                af[i] = *reinterpret_cast<const u32x4*>(as + i * 32 * BK + ((((kk >> 3) + kc) ^ swa(wm * TM + i * 32 + r)) << 3));
 #pragma unroll
-            for (int j = 0; j < BJ; ++j)
-                bf[j] = *reinterpret_cast<const u32x4*>(bs + (wn * (N / 2) + j * 32 + r) * BP + kk + kh);
+            for (int j = 0; j < FJ; ++j) {
+                const int n = wn * TN + j * 32 + 16 * (g & 1) + 4 * a4;
+                const int pn = (((n >> 4) ^ e) << 4) | (n & 15);
+                const int k = kk + 8 * (g >> 1) + e;
+                const s16x4 lo = __builtin_amdgcn_ds_read_tr16_b64_v4i16((__attribute__((address_space(3))) s16x4*)(bs + k * BN + pn));
+                const s16x4 hi =
+                    __builtin_amdgcn_ds_read_tr16_b64_v4i16((__attribute__((address_space(3))) s16x4*)(bs + (k + 4) * BN + pn));
+                const u32x2 l2 = __builtin_bit_cast(u32x2, lo), h2 = __builtin_bit_cast(u32x2, hi);
+                bf[j] = u32x4{l2.x, l2.y, h2.x, h2.y};
+            }
 #pragma unroll
-            for (int i = 0; i < BI; ++i)
+            for (int i = 0; i < FI; ++i)
 #pragma unroll
-                for (int j = 0; j < BJ; ++j) acc.v[i][j] = mfma_32x32x16<F16>(af[i], bf[j], acc.v[i][j]);
+                for (int j = 0; j < FJ; ++j) acc.v[i][j] = mfma_32x32x16<F16>(af[i], bf[j], acc.v[i][j]);
         }
     }
 
-    // c = c + a, elementwise fp32 (the TADD of the accumulate pattern).
-    __device__ static void add(Acc& c, const Acc& a) {
+    // C block I/O in the accumulator layout (ldc: row pitch in elements).
+    template <bool STORE>
+    __device__ static void c_io(Acc& acc, buf_rsrc rc, int ldc) {
+        const int lane = threadIdx.x & 63, wave = wave_index();
+        const int wm = wave / WN, wn = wave % WN;
+        const int vc = ((lane >> 5) * 4 * ldc + (lane & 31)) * 4;
+        const int so = (wm * TM * ldc + wn * TN) * 4;
 #pragma unroll
-        for (int i = 0; i < BI; ++i)
+        for (int i = 0; i < FI; ++i)
 #pragma unroll
-            for (int j = 0; j < BJ; ++j)
+            for (int e = 0; e < 16; ++e) {
+                const int s = so + (i * 32 + (e >> 2) * 8 + (e & 3)) * ldc * 4;
 #pragma unroll
-                for (int e = 0; e < 16; ++e) c.v[i][j][e] = c.v[i][j][e] + a.v[i][j][e];
+                for (int j = 0; j < FJ; ++j) {
+                    if constexpr (STORE)
+                        __builtin_amdgcn_raw_buffer_store_b32(__float_as_uint(acc.v[i][j][e]), rc, vc + j * 128, s, 2);
+                    else
+                        acc.v[i][j][e] = __uint_as_float(__builtin_amdgcn_raw_buffer_load_b32(rc, vc + j * 128, s, 2));
+                }
+            }
     }
 
-    template <bool STORE>
-    __device__ static void c_io(Acc& c, float* pc, i64 s3c) {
-        const int lane = threadIdx.x & 63, wave = threadIdx.x >> 6;
-        const int wm = wave >> 1, wn = wave & 1;
+    // K steps it0 .. iters-1; off(it, soa, sob) gives step it's byte offsets
+    // from the step-0 origins pa / pb.  ACC: the block starts from C.
+    template <bool ACC, class Off>
+    __device__ static void run(u16* lds, const u16* pa, int lda, const u16* pb, int ldb, float* pc, int ldc, i64 it0,
+                               i64 iters, Off off) {
+        const u32x4 ra = buffer_words(pa), rb = buffer_words(pb);
+        const buf_rsrc rc = __builtin_amdgcn_make_buffer_rsrc(pc, 0, -1, 0x00020000);
+        Offs o;
+        offsets(o, lda, ldb);
+        Acc acc;
+        if constexpr (ACC) {
+            c_io<false>(acc, rc, ldc);
+        } else {
 #pragma unroll
-        for (int i = 0; i < BI; ++i)
+            for (int i = 0; i < FI; ++i)
 #pragma unroll
-            for (int j = 0; j < BJ; ++j)
-#pragma unroll
-                for (int e = 0; e < 16; ++e) {
-                    const int row = wm * (M / 2) + i * 32 + (e >> 2) * 8 + (lane >> 5) * 4 + (e & 3);
-                    const int col = wn * (N / 2) + j * 32 + (lane & 31);
-                    if constexpr (STORE) pc[row * s3c + col] = c.v[i][j][e];
-                    else c.v[i][j][e] = pc[row * s3c + col];
-                }
+                for (int j = 0; j < FJ; ++j) acc.v[i][j] = f32x16{};
+        }
+        wait_vmcnt<0>();
+        __syncthreads();  // the previous block's last stage reads are done
+        int soa, sob;
+        off(it0, soa, sob);
+        load(lds, o, ra, soa, rb, sob);
+        for (i64 it = it0; it < iters; ++it) {
+            wait_vmcnt<0>();
+            __syncthreads();
+            const int cur = static_cast<int>((it - it0) & 1);
+            if (it + 1 < iters) {
+                off(it + 1, soa, sob);
+                load(lds + (cur ^ 1) * STAGE, o, ra, soa, rb, sob);
+            }
+            mma(acc, lds + cur * STAGE);
+        }
+        c_io<true>(acc, rc, ldc);
     }
 };
 

@@ -138,8 +138,11 @@ GemmInfo classify_gemm(const KernelDef& k, const KernelAnalysis& a) {
     if (va->dtype != vb->dtype || (va->dtype != DType::BF16 && va->dtype != DType::F16)) return g;
     if (vc->dtype != DType::F32) return g;
     const int M = va->rows, K = va->cols, N = vb->cols;
-    if (M % 64 || N % 64 || K % 16 || M > 256 || N > 256) return g;
-    if (2 * (M + N) * (K + 8) * 2 > 160 * 1024) return g;
+    // MFMA block shapes: 64..256 rows / columns, K step a power of two in 16..128,
+    // two LDS stages of A and B within 160 KiB.
+    if (M % 64 || N % 64 || M > 256 || N > 256) return g;
+    if (K != 16 && K != 32 && K != 64 && K != 128) return g;
+    if (2 * (M + N) * K * 2 > 160 * 1024) return g;
     g.ok = true;
     g.a = a.tensor_ordinal[pa];
     g.b = a.tensor_ordinal[pb];

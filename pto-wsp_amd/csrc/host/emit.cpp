@@ -474,63 +474,66 @@ EmittedKernel emit_tile(const Module& m, const KernelAnalysis& a, const LaunchSp
 // ---------------------------------------------------------------------------
 EmittedKernel emit_gemm(const Module& m, const KernelAnalysis& a, const LaunchSpec& L, const EmitSpec& spec) {
     (void)m;
-    (void)spec;
     const KernelDef& k = *a.def;
     const GemmInfo& g = a.gemm;
     const int ng = static_cast<int>(L.grid.size()), ni = static_cast<int>(L.inner.size());
     const int nvars = ng + ni;
+    const int fm = spec.gemm_vm >= 0 ? 2 : 1, fn = spec.gemm_vn >= 0 ? 2 : 1;
+    const int bm = g.m * fm, bn = g.n * fn;
+    const int wm = gemm_waves_m(), wn = gemm_waves_n(bn);
     EmittedKernel ek;
-    ek.threads = 256;
+    ek.threads = 64 * wm * wn;
     ek.row_program = false;
+    ek.tasks_per_block = fm * fn;
     std::ostringstream o;
     o << "#include \"ptowsp_device.h\"\nusing namespace ptowsp;\n";
-    o << "// gemm program: kernel " << k.name << ", " << g.m << "x" << g.n << "x" << g.k << (g.f16 ? " f16" : " bf16")
-      << (g.accumulate ? ", accumulate" : "") << "\n";
-    o << "extern \"C\" __global__ void __launch_bounds__(256) ptowsp_entry(const LaunchArgs A) {\n";
-    o << "  typedef GemmTile<" << g.m << ", " << g.n << ", " << g.k << ", " << (g.f16 ? "true" : "false") << "> GT;\n";
-    o << "  __shared__ __attribute__((aligned(16))) u16 lds[GT::kLdsElems];\n";
+    o << "// gemm program: kernel " << k.name << ", task tile " << g.m << "x" << g.n << "x" << g.k << (g.f16 ? " f16" : " bf16")
+      << (g.accumulate ? ", accumulate" : "") << "; block " << bm << "x" << bn << " (" << fm * fn << " tasks)\n";
+    o << "extern \"C\" __global__ void __launch_bounds__(" << ek.threads << ") ptowsp_entry(const LaunchArgs A) {\n";
+    o << "  typedef GemmBlock<" << bm << ", " << bn << ", " << g.k << ", " << wm << ", " << wn << ", "
+      << (g.f16 ? "true" : "false") << "> GB;\n";
+    o << "  __shared__ __attribute__((aligned(1024))) u16 lds[GB::kLdsElems];\n";
     o << "  i64 vars[" << (nvars > 0 ? nvars : 1) << "];\n  (void)vars;\n";
-    o << "  for (i64 t = blockIdx.x; t < A.ntasks; t += gridDim.x) {\n";
-    emit_decode(o, "    ", ng, "t");
+    o << "  const i64 nblk = A.ntasks / " << fm * fn << ";\n";
+    o << "  for (i64 w = blockIdx.x; w < nblk; w += gridDim.x) {\n";
+    o << "    i64 q_ = (i64)gridDim.x >= nblk ? xcd_order(w, nblk) : w;\n";
+    // Decode the block index over the grid with the merged extents divided.
+    for (int v = ng - 1; v >= 0; --v) {
+        const int f = v == spec.gemm_vm ? fm : (v == spec.gemm_vn ? fn : 1);
+        const std::string ext = f > 1 ? "(A.ext[" + std::to_string(v) + "] / " + std::to_string(f) + ")" : "A.ext[" + std::to_string(v) + "]";
+        if (v > 0) o << "    vars[" << v << "] = q_ % " << ext << "; q_ /= " << ext << ";\n";
+        else o << "    vars[0] = q_;\n";
+        if (f > 1) o << "    vars[" << v << "] *= " << f << ";\n";
+    }
     o << "    i64 iters = 1;\n";
     for (int i = 0; i < ni; ++i) o << "    iters *= A.ext[" << ng + i << "];\n";
     o << "    if (iters <= 0) continue;\n";
+    for (int i = 0; i < ni; ++i) o << "    vars[" << ng + i << "] = 0;\n";
+    o << "    const u16* pa = reinterpret_cast<const u16*>(A.base[" << g.a << "] + (" << offset_expr(g.a, nvars, 0, 0) << ") * 2);\n";
+    o << "    const u16* pb = reinterpret_cast<const u16*>(A.base[" << g.b << "] + (" << offset_expr(g.b, nvars, 0, 0) << ") * 2);\n";
     // The output view does not move with the in-kernel loops (checked on the host).
-    o << "    float* pc = reinterpret_cast<float*>(A.base[" << g.c << "] + (" << offset_expr(g.c, ng, 0, 0) << ") * 4);\n";
-    o << "    GT::Acc cacc;\n";
-    if (g.accumulate) o << "    GT::c_io<false>(cacc, pc, A.s3[" << g.c << "]);\n";
-    else o << "    GT::zero(cacc);\n";
-    // Operand pointers of in-kernel iteration `it` (mixed radix over the inner loops).
-    o << "    auto operands = [&](i64 it, const u16*& pa, const u16*& pb) {\n";
-    for (int i = ni - 1; i >= 0; --i) {
-        const int v = ng + i;
-        o << "      vars[" << v << "] = it % A.ext[" << v << "]; it /= A.ext[" << v << "];\n";
+    o << "    float* pc = reinterpret_cast<float*>(A.base[" << g.c << "] + (" << offset_expr(g.c, nvars, 0, 0) << ") * 4);\n";
+    // Byte offsets of in-kernel iteration `it` from iteration 0 (mixed radix over the inner loops).
+    o << "    auto off = [&](i64 it, int& soa, int& sob) {\n";
+    o << "      i64 oa = 0, ob = 0;\n";
+    if (ni == 1) {
+        o << "      oa = A.coef[" << g.a << "][" << ng << "] * it; ob = A.coef[" << g.b << "][" << ng << "] * it;\n";
+    } else {
+        for (int i = ni - 1; i >= 0; --i) {
+            const int v = ng + i;
+            o << "      { const i64 x = it % A.ext[" << v << "]; it /= A.ext[" << v << "]; oa += A.coef[" << g.a << "][" << v
+              << "] * x; ob += A.coef[" << g.b << "][" << v << "] * x; }\n";
+        }
     }
-    o << "      pa = reinterpret_cast<const u16*>(A.base[" << g.a << "] + (" << offset_expr(g.a, nvars, 0, 0) << ") * 2);\n";
-    o << "      pb = reinterpret_cast<const u16*>(A.base[" << g.b << "] + (" << offset_expr(g.b, nvars, 0, 0) << ") * 2);\n";
+    o << "      soa = static_cast<int>(oa * 2); sob = static_cast<int>(ob * 2);\n";
     o << "    };\n";
-    o << "    const u16* pa;\n    const u16* pb;\n";
-    o << "    operands(0, pa, pb);\n";
-    o << "    GT::Regs regs;\n";
-    o << "    GT::gload(regs, pa, A.s3[" << g.a << "], pb, A.s3[" << g.b << "]);\n";
-    o << "    for (i64 it = 0; it < iters; ++it) {\n";
-    o << "      u16* stage = lds + (it & 1) * GT::kStage;\n";
-    o << "      GT::lstore(stage, regs);\n";
-    o << "      __syncthreads();\n";
-    o << "      if (it + 1 < iters) {\n";
-    o << "        operands(it + 1, pa, pb);\n";
-    o << "        GT::gload(regs, pa, A.s3[" << g.a << "], pb, A.s3[" << g.b << "]);\n";
-    o << "      }\n";
-    o << "      GT::Acc acc;\n      GT::zero(acc);\n      GT::mma(acc, stage);\n";
-    if (g.accumulate) o << "      GT::add(cacc, acc);\n";
-    else o << "      cacc = acc;\n";
-    o << "    }\n";
-    o << "    GT::c_io<true>(cacc, pc, A.s3[" << g.c << "]);\n";
-    o << "    __syncthreads();\n";
+    o << "    GB::template run<" << (g.accumulate ? "true" : "false") << ">(lds, pa, static_cast<int>(A.s3[" << g.a
+      << "]), pb, static_cast<int>(A.s3[" << g.b << "]), pc, static_cast<int>(A.s3[" << g.c << "]), "
+      << (g.accumulate ? "0" : "iters - 1") << ", iters, off);\n";
     o << "  }\n}\n";
     ek.source = o.str();
     ek.entry = "ptowsp_entry";
-    ek.lds_bytes = static_cast<size_t>(2 * (g.m + g.n) * (g.k + 8) * 2);
+    ek.lds_bytes = static_cast<size_t>(2 * (bm + bn) * g.k * 2);
     return ek;
 }
 

@@ -25,7 +25,14 @@ struct EmitSpec {
     bool nontemporal = false;
     // GEMM family on MFMA (only when strides and alignment allow it).
     bool gemm = false;
+    // GEMM: grid variables whose neighbouring tasks are merged into one
+    // workgroup block (factor 2 along rows / columns of C), or -1.
+    int gemm_vm = -1, gemm_vn = -1;
 };
+
+// Waves of a GEMM block: 2 along M, 4 along N for 256-wide blocks, else 2.
+inline int gemm_waves_n(int bn) { return bn >= 256 ? 4 : 2; }
+inline int gemm_waves_m() { return 2; }
 
 struct EmittedKernel {
     std::string source;
@@ -34,6 +41,7 @@ struct EmittedKernel {
     int rows_per_chunk = 0;     // row programs: rows handled per wave iteration
     int waves_per_block = 4;
     bool row_program = false;
+    int tasks_per_block = 1;    // GEMM: tasks merged into one workgroup
     size_t lds_bytes = 0;
 };
 

@@ -348,8 +348,13 @@ bool grid_write_hazard(const KernelAnalysis& a, const LaunchSpec& L, const Launc
 // The MFMA GEMM template needs unit column strides, 16-byte aligned operand
 // rows at every task and K step, an output tile that stays put across the
 // in-kernel loops, and operands that the launch does not write.
-bool gemm_allowed(const KernelAnalysis& a, const LaunchSpec& L, const LaunchArgs& A, const EmitSpec& spec, int ng,
-                  int nvars) {
+// Chooses the MFMA GEMM path for a launch of a GEMM-family kernel and, where
+// neighbouring tasks' tiles are contiguous in A, B and C, the grid variables
+// whose task pairs are merged into one workgroup block.  Returns false (tile
+// program fallback) when strides, alignment or offset ranges do not allow the
+// direct buffer->LDS loads of the GEMM block.
+bool gemm_allowed(const KernelAnalysis& a, const LaunchSpec& L, const LaunchArgs& A, EmitSpec& spec, int ng, int nvars) {
+    spec.gemm_vm = spec.gemm_vn = -1;
     if (a.family != Family::Gemm || spec.serial) return false;
     for (int c : spec.indirect_count)
         if (c) return false;
@@ -358,13 +363,40 @@ bool gemm_allowed(const KernelAnalysis& a, const LaunchSpec& L, const LaunchArgs
     const GemmInfo& g = a.gemm;
     if (A.s4[g.a] != 1 || A.s4[g.b] != 1 || A.s4[g.c] != 1) return false;
     if (reinterpret_cast<uintptr_t>(A.base[g.a]) % 16 || reinterpret_cast<uintptr_t>(A.base[g.b]) % 16) return false;
+    if (reinterpret_cast<uintptr_t>(A.base[g.c]) % 4) return false;
     if (A.s3[g.a] % 8 || A.s3[g.b] % 8) return false;
     for (int v = 0; v < nvars; ++v) {
         if (A.coef[g.a][v] % 8 || A.coef[g.b][v] % 8) return false;
         if (v >= ng && A.coef[g.c][v] != 0) return false;
+        if (v >= ng && (A.coef[g.a][v] < 0 || A.coef[g.b][v] < 0)) return false;
     }
     const int tc = L.targs[g.c]->tid;
     if (L.targs[g.a]->tid == tc || L.targs[g.b]->tid == tc) return false;
+    // Merge candidates: rows of C move with A's rows, columns with B's.
+    const int64_t M = g.m, N = g.n;
+    for (int v = 0; v < ng; ++v) {
+        if (A.ext[v] <= 0 || A.ext[v] % 2) continue;
+        if (spec.gemm_vm < 0 && A.coef[g.a][v] == M * A.s3[g.a] && A.coef[g.c][v] == M * A.s3[g.c] && A.coef[g.b][v] == 0)
+            spec.gemm_vm = v;
+        else if (spec.gemm_vn < 0 && A.coef[g.b][v] == N && A.coef[g.c][v] == N && A.coef[g.a][v] == 0)
+            spec.gemm_vn = v;
+    }
+    auto lds_fits = [&](int64_t bm, int64_t bn) { return bm <= 256 && bn <= 256 && 2 * (bm + bn) * g.k * 2 <= 160 * 1024; };
+    if (spec.gemm_vm >= 0 && spec.gemm_vn >= 0 && !lds_fits(2 * M, 2 * N)) spec.gemm_vm = -1;
+    if (spec.gemm_vm >= 0 && !lds_fits(2 * M, spec.gemm_vn >= 0 ? 2 * N : N)) spec.gemm_vm = -1;
+    if (spec.gemm_vn >= 0 && !lds_fits(spec.gemm_vm >= 0 ? 2 * M : M, 2 * N)) spec.gemm_vn = -1;
+    const int64_t bm = M * (spec.gemm_vm >= 0 ? 2 : 1), bn = N * (spec.gemm_vn >= 0 ? 2 : 1);
+    // Buffer offsets (32-bit) from a block's step-0 origins.
+    int64_t ka = 0, kb = 0;
+    for (int v = ng; v < nvars; ++v) {
+        ka += A.coef[g.a][v] * std::max<int64_t>(0, A.ext[v] - 1);
+        kb += A.coef[g.b][v] * std::max<int64_t>(0, A.ext[v] - 1);
+    }
+    const int64_t lim = int64_t(1) << 31;
+    if (A.s3[g.a] >= lim || A.s3[g.b] >= lim || A.s3[g.c] >= lim) return false;
+    if (((bm - 1) * A.s3[g.a] + g.k) * 2 + ka * 2 >= lim) return false;
+    if (((g.k - 1) * A.s3[g.b] + bn) * 2 + kb * 2 >= lim) return false;
+    if (((bm - 1) * A.s3[g.c] + bn) * 4 >= lim) return false;
     return true;
 }
 
@@ -511,6 +543,7 @@ BuiltLaunch build_launch(RunEnv& E, const LaunchSpec& L) {
     B.spec.row_up = tuning().row_up;
     B.spec.nontemporal = tuning().nontemporal;
     B.spec.gemm = gemm_allowed(a, L, A, B.spec, ng, nvars);
+    if (!B.spec.gemm) B.spec.gemm_vm = B.spec.gemm_vn = -1;
     B.spec.vec_width = a.family == Family::RowProgram ? pick_vec_width(a, A, nvars) : 1;
     return B;
 }
@@ -518,7 +551,7 @@ BuiltLaunch build_launch(RunEnv& E, const LaunchSpec& L) {
 std::string spec_key(const EmitSpec& s) {
     std::ostringstream o;
     o << "vw" << s.vec_width << (s.serial ? ";serial" : "") << ";up" << s.row_up << (s.nontemporal ? ";nt" : "")
-      << (s.gemm ? ";gemm" : "") << ";i";
+      << (s.gemm ? ";gemm" : "") << ";m" << s.gemm_vm << ";n" << s.gemm_vn << ";i";
     for (int c : s.indirect_count) o << c << ",";
     o << ";d";
     for (int c : s.inner_dyn_term) o << c << ",";
@@ -557,7 +590,7 @@ void enqueue_launch(RunEnv& E, int li, hipStream_t stream, uint64_t& launches) {
         const int64_t chunks = (rows + ek.rows_per_chunk - 1) / ek.rows_per_chunk;
         blocks = (chunks + ek.waves_per_block - 1) / ek.waves_per_block;
     } else {
-        blocks = B.spec.serial ? 1 : B.ntasks;
+        blocks = B.spec.serial ? 1 : B.ntasks / ek.tasks_per_block;
     }
     blocks = std::max<int64_t>(1, std::min<int64_t>(blocks, int64_t(1) << 20));
     void* params[] = {&B.args};
@@ -761,6 +794,12 @@ int ptowsp_hip_precompile(ptowsp_program* P, int index, int flags, const char** 
                         while (vw > 1 && shape.back() % vw) vw /= 2;
                 }
                 spec.vec_width = vw;
+            }
+            const int ng = static_cast<int>(L.grid.size());
+            if ((flags & 2) && spec.gemm && ng >= 2 && a.gemm.m <= 128 && a.gemm.n <= 128 &&
+                2 * (2 * a.gemm.m + 2 * a.gemm.n) * a.gemm.k * 2 <= 160 * 1024) {
+                spec.gemm_vm = ng - 2;
+                spec.gemm_vn = ng - 1;
             }
             const EmittedKernel& ek = emitted_for(P, static_cast<int>(li), spec);
             (void)jit_compile(ek.source);

@@ -243,6 +243,48 @@ def test_bgemm_bf16_mfma_accumulate(gpu, tiles):
     assert prog.stats.total_cycles == ref.total_cycles
 
 
+@pytest.mark.parametrize("shape,tiles", [
+    ((1, 384, 384, 256), (128, 128, 128)),   # odd tile counts: no merge, K step 128
+    ((1, 256, 192, 128), (64, 64, 32)),      # rows merged only (block 128x64)
+    ((3, 512, 512, 128), (128, 128, 64)),    # 12 merged blocks: XCD order with a remainder
+    ((1, 128, 256, 64), (128, 64, 16)),      # columns merged only (block 128x128, K step 16)
+])
+def test_bgemm_bf16_mfma_block_shapes(gpu, shape, tiles):
+    """GEMM blocks with and without task merging against float64 and the oracle."""
+    nb, m, n, k = shape
+    tm, tn, tk = tiles
+    rng = np.random.default_rng(11)
+    a = W.bf16_round(rng.uniform(-1, 1, (nb, m, k)).astype(np.float32))
+    b = W.bf16_round(rng.uniform(-1, 1, (nb, k, n)).astype(np.float32))
+    c0 = rng.standard_normal((nb, m, n)).astype(np.float32)
+    ga = {"a": a, "b": b, "c": c0.copy()}
+    ca = {"a": a.copy(), "b": b.copy(), "c": c0.copy()}
+    prog = run_hip(W.bgemm(ga, tm, tn, tk, W.BF16))
+    ref = run_workload(W.bgemm(ca, tm, tn, tk, W.BF16))
+    assert prog._native.kernel_family("gemm_tile") == "gemm"
+    assert _rel_fro(ga["c"], ca["c"]) <= 1e-5
+    exact = c0.astype(np.float64) + W.bf16_to_f32(a).astype(np.float64) @ W.bf16_to_f32(b).astype(np.float64)
+    assert _rel_fro(ga["c"], exact) <= 1e-5
+    assert prog.stats.total_cycles == ref.total_cycles
+
+
+def test_bgemm_two_inner_loops(gpu):
+    """K split over two P.seq loops: in-kernel iterations decode a mixed radix."""
+    rng = np.random.default_rng(12)
+    a = W.bf16_round(rng.uniform(-1, 1, (2, 128, 512)).astype(np.float32))
+    b = W.bf16_round(rng.uniform(-1, 1, (2, 512, 128)).astype(np.float32))
+    c0 = rng.standard_normal((2, 128, 128)).astype(np.float32)
+    ga = {"a": a, "b": b, "c": c0.copy()}
+    ca = {"a": a.copy(), "b": b.copy(), "c": c0.copy()}
+    prog = run_hip(W.bgemm_split_k(ga, 64, 64, 64, 2))
+    ref = run_workload(W.bgemm_split_k(ca, 64, 64, 64, 2))
+    assert prog._native.kernel_family("gemm_tile") == "gemm"
+    assert _rel_fro(ga["c"], ca["c"]) <= 1e-5
+    exact = c0.astype(np.float64) + W.bf16_to_f32(a).astype(np.float64) @ W.bf16_to_f32(b).astype(np.float64)
+    assert _rel_fro(ga["c"], exact) <= 1e-5
+    assert prog.stats.total_cycles == ref.total_cycles
+
+
 def test_bgemm_plain_store_keeps_last_k_step(gpu):
     """store(c, matmul(a, b)) inside P.seq(k): each step overwrites C, so C = A[:, k_last] @ B[k_last]."""
     rng = np.random.default_rng(6)

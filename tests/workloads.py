@@ -168,6 +168,34 @@ def bgemm(arrs: dict, tm: int = 16, tn: int = 16, tk: int = 16, dtype=F16, plain
     return bgemm_wl()
 
 
+def bgemm_split_k(arrs: dict, tm: int, tn: int, tk: int, k_outer: int, dtype=BF16):
+    """bgemm with the K loop split into two nested P.seq loops (k = ko * (K/tk/k_outer) + ki)."""
+    a, b_, c = arrs["a"], arrs["b"], arrs["c"]
+    B, M, K = a.shape
+    N = b_.shape[2]
+    kin = K // tk // k_outer
+    at = a.reshape(B, M // tm, tm, k_outer, kin, tk).transpose(0, 1, 3, 4, 2, 5)
+    bt = b_.reshape(B, k_outer, kin, tk, N // tn, tn).transpose(0, 4, 1, 2, 3, 5)
+    ct = c.reshape(B, M // tm, tm, N // tn, tn).transpose(0, 1, 3, 2, 4)
+    A, Bm, C = T(at, dtype), T(bt, dtype), T(ct)
+
+    @kernel
+    def gemm_tile(a_tile: In[Tile[tm, tk, dtype]], b_tile: In[Tile[tk, tn, dtype]], c_tile: InOut[Tile[tm, tn, F32]]):
+        pto.store(c_tile, pto.add(c_tile, pto.matmul(a_tile, b_tile)))
+
+    @workload
+    def split_wl():
+        for b in P(Dense[B]()):
+            for m in P(Dense[M // tm]()):
+                for n in P(Dense[N // tn]()):
+                    # named: P.seq defaults every loop variable to "i", so nested loops would shadow
+                    for ko in P.seq(Dense[k_outer](), name="ko"):
+                        for ki in P.seq(Dense[kin](), name="ki"):
+                            gemm_tile[b, m, n, ko, ki](a_tile=A[b][m][ko][ki], b_tile=Bm[b][n][ko][ki], c_tile=C[b][m][n])
+
+    return split_wl()
+
+
 # ---------------------------------------------------------------- decode / attention (f32 examples)
 def decode_attention(arrs: dict):
     """examples/flashinfer_decode: one task, whole KV in one tile."""
