@@ -78,7 +78,8 @@ int ptowsp_hip_num_launches(const ptowsp_program* prog);
 /* cpu_sim cycles of one task of `kernel` (reference
  * include/pto/wsp/codegen/abi/ptoisa_bridge.hpp:54-303), or UINT64_MAX. */
 uint64_t ptowsp_hip_kernel_cycles(const ptowsp_program* prog, const char* kernel);
-/* Family chosen for `kernel`: 0 row program, 1 tile program, 2 gemm; -1 unknown. */
+/* Family chosen for `kernel`: 0 row program, 1 tile program, 2 gemm, 3 decode (online
+ * softmax over pages); -1 unknown. */
 int ptowsp_hip_kernel_family(const ptowsp_program* prog, const char* kernel);
 /* Emits and builds every launch for contiguous row-major tensors without
  * touching a GPU (hiprtc only); returns the source of launch `index` through

@@ -330,7 +330,11 @@ static void parse_axis(Lex* L, Node* n) {
     if (strcmp(k, "dense") == 0) { n->axis_kind = AX_DENSE; n->axis_size = tok_i64(L); }
     else if (strcmp(k, "dyn") == 0) { n->axis_kind = AX_DYN; n->axis_a = tok_str(L); }
     else if (strcmp(k, "ragged") == 0) { n->axis_kind = AX_RAGGED; n->axis_a = tok_str(L); n->axis_b = tok_str(L); }
-    else if (strcmp(k, "dynt") == 0) { n->axis_kind = AX_DYNT; n->axis_expr = parse_iexpr(L); }
+    else if (strcmp(k, "dynt") == 0) {
+        n->axis_kind = AX_DYNT;
+        (void)tok_i64(L); /* max extent: a sizing hint for the HIP backend */
+        n->axis_expr = parse_iexpr(L);
+    }
     else fail("module text: bad axis kind '%s'", k);
 }
 
@@ -870,9 +874,14 @@ static uint64_t run_kernel(Kernel* k, Work* w, View* views, const uint64_t* scal
                 if (!av->tile || !bv->tile) fail("kernel %s: Matmul expects tile operands", kn);
                 int M = av->rows, K = av->cols, N = bv->cols;
                 if (bv->rows != K) fail("kernel %s: Matmul K mismatch", kn);
-                int ok = (av->dtype == DT_F32 && bv->dtype == DT_F32) ||
-                         (av->dtype == DT_F16 && bv->dtype == DT_F16) ||
-                         (av->dtype == DT_BF16 && bv->dtype == DT_BF16);
+                /* f32 x f32 and f16 x f16 as in the reference (:863-873); extensions:
+                 * bf16 x bf16, and a 16-bit float operand with an f32 one (the 16-bit
+                 * operand is upcast exactly; f32 math). */
+                int f32a = av->dtype == DT_F32, f32b = bv->dtype == DT_F32;
+                int h16a = av->dtype == DT_F16 || av->dtype == DT_BF16;
+                int h16b = bv->dtype == DT_F16 || bv->dtype == DT_BF16;
+                int ok = (f32a && f32b) || (av->dtype == DT_F16 && bv->dtype == DT_F16) ||
+                         (av->dtype == DT_BF16 && bv->dtype == DT_BF16) || (f32a && h16b) || (h16a && f32b);
                 if (!ok || res->dtype != DT_F32)
                     fail("kernel %s: Matmul: unsupported dtype combination %s x %s -> %s", kn,
                          k_dtype_names[av->dtype], k_dtype_names[bv->dtype], k_dtype_names[res->dtype]);

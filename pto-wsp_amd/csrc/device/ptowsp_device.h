@@ -499,4 +499,232 @@ struct GemmBlock {
     }
 };
 
+// ---------------------------------------------------------------------------
+// Decode: online softmax over 16-token pages (flashinfer_decode pattern)
+// ---------------------------------------------------------------------------
+//
+// The pages of one unit (sequence b, KV group g) are split into chunks; one
+// wave folds a chunk into a partial (m, l, o) for the unit's G query rows,
+// starting from (-inf, 0, 0), and DecodeCombine folds the partials of a unit
+// in chunk order into the accumulators.  Per page:
+//  * scores on MFMA v_mfma_f32_16x16x32 (one per 32-wide head-dim slice):
+//    A = the K page (lane l: token l%16, head dims 8*(l/16)..+7 of the slice),
+//    B = q^T (lane l: query row l%16, zero for rows >= G); lane l then holds
+//    query row l%16 for tokens 4*(l/16)..+3;
+//  * row max / row sum over the 16 tokens: 4 values in the lane, then lanes
+//    l^16 and l^32;
+//  * p and the rescale factor pass through LDS; p @ v runs in fp32 on the
+//    VALU with lane l owning head-dim columns (D/64)*l ..; the sum over the 16
+//    tokens runs in token order, mul then add (as the oracle's TMATMUL).
+
+typedef float f32x4v_t __attribute__((ext_vector_type(4)));
+
+template <bool F16>
+__device__ inline f32x4v_t mfma_16x16x32(u32x4 a, u32x4 b, f32x4v_t c) {
+    if constexpr (F16)
+        return __builtin_amdgcn_mfma_f32_16x16x32_f16(__builtin_bit_cast(f16x8, a), __builtin_bit_cast(f16x8, b), c, 0, 0, 0);
+    else
+        return __builtin_amdgcn_mfma_f32_16x16x32_bf16(__builtin_bit_cast(bf16x8, a), __builtin_bit_cast(bf16x8, b), c, 0, 0,
+                                                       0);
+}
+
+// 16-bit float (bf16 or f16) in the low / high half of a dword, as f32.
+template <bool F16>
+__device__ inline float h16_lo(u32 w) {
+    if constexpr (F16) return static_cast<float>(__builtin_bit_cast(_Float16, static_cast<u16>(w & 0xFFFFu)));
+    else return __uint_as_float(w << 16);
+}
+template <bool F16>
+__device__ inline float h16_hi(u32 w) {
+    if constexpr (F16) return static_cast<float>(__builtin_bit_cast(_Float16, static_cast<u16>(w >> 16)));
+    else return __uint_as_float(w & 0xFFFF0000u);
+}
+
+// Orders LDS traffic between the lanes of one wave (LDS executes a wave's
+// instructions in order; this keeps the compiler from reordering them).
+__device__ inline void wave_lds_fence() { __builtin_amdgcn_fence(__ATOMIC_SEQ_CST, "wavefront"); }
+
+template <int G, int D, bool F16, bool MASK>
+struct DecodeWave {
+    static_assert(G >= 1 && G <= 16 && (D == 64 || D == 128 || D == 256), "decode shape");
+    static constexpr int NS = D / 32;    // head-dim slices, one MFMA each
+    static constexpr int DPL = D / 64;   // head-dim columns per lane in p @ v
+    static constexpr int kLdsFloats = G * 16 + 16;  // p rows, then the rescale factors
+    // Chunk partial layout: m[G], l[G], o[G][D].
+    static constexpr int kPartFloats = 2 * G + G * D;
+
+    struct Page {
+        u32x4 k[NS];
+        u32 v[16 * (DPL == 4 ? 2 : 1)];  // DPL 1: one 16-bit value per token (low half)
+        f32x4v_t mask;
+    };
+
+    // kp: K page (token t at kp + t*ks, head dims contiguous); vp: V page
+    // (token t at vp + t*vs, head dims contiguous); mp: mask row (contiguous).
+    __device__ static void load_page(Page& pg, const u16* kp, i64 ks, const u16* vp, i64 vs, const float* mp) {
+        const int lane = threadIdx.x & 63, t = lane & 15, quad = lane >> 4;
+#pragma unroll
+        for (int j = 0; j < NS; ++j)
+            pg.k[j] = __builtin_nontemporal_load(reinterpret_cast<const u32x4*>(kp + t * ks + 32 * j + 8 * quad));
+#pragma unroll
+        for (int tt = 0; tt < 16; ++tt) {
+            if constexpr (DPL == 4) {
+                const u32x2 w = __builtin_nontemporal_load(reinterpret_cast<const u32x2*>(vp + tt * vs + 4 * lane));
+                pg.v[2 * tt] = w.x;
+                pg.v[2 * tt + 1] = w.y;
+            } else if constexpr (DPL == 2) {
+                pg.v[tt] = __builtin_nontemporal_load(reinterpret_cast<const u32*>(vp + tt * vs + 2 * lane));
+            } else {
+                pg.v[tt] = vp[tt * vs + lane];
+            }
+        }
+        if constexpr (MASK) pg.mask = *reinterpret_cast<const f32x4v_t*>(mp + 4 * quad);
+    }
+
+    // Folds pages [p0, p1) into part; ptrs(p, kp, vp, mp) gives page p's bases.
+    template <class PagePtrs>
+    __device__ static void run(i64 p0, i64 p1, const u16* q, i64 qs, float scale, PagePtrs ptrs, i64 ks, i64 vs, float* lds,
+                               float* part) {
+        const int lane = threadIdx.x & 63, h = lane & 15, quad = lane >> 4;
+        u32x4 qb[NS];
+#pragma unroll
+        for (int j = 0; j < NS; ++j) {
+            qb[j] = u32x4{0u, 0u, 0u, 0u};
+            if (h < G) qb[j] = *reinterpret_cast<const u32x4*>(q + h * qs + 32 * j + 8 * quad);
+        }
+        float m = -__builtin_inff(), l = 0.0f;
+        float o[G][DPL];
+#pragma unroll
+        for (int g = 0; g < G; ++g)
+#pragma unroll
+            for (int j = 0; j < DPL; ++j) o[g][j] = 0.0f;
+        Page cur, nxt;
+        const u16 *kp, *vp;
+        const float* mp;
+        ptrs(p0, kp, vp, mp);
+        load_page(cur, kp, ks, vp, vs, mp);
+        for (i64 p = p0; p < p1; ++p) {
+            if (p + 1 < p1) {
+                ptrs(p + 1, kp, vp, mp);
+                load_page(nxt, kp, ks, vp, vs, mp);
+            }
+            f32x4v_t acc = {0.0f, 0.0f, 0.0f, 0.0f};
+#pragma unroll
+            for (int j = 0; j < NS; ++j) acc = mfma_16x16x32<F16>(cur.k[j], qb[j], acc);
+            float sc[4];
+#pragma unroll
+            for (int i = 0; i < 4; ++i) {
+                sc[i] = acc[i] * scale;
+                if constexpr (MASK) sc[i] = sc[i] - cur.mask[i];
+            }
+            float pm = fmaxf(fmaxf(sc[0], sc[1]), fmaxf(sc[2], sc[3]));
+            pm = fmaxf(pm, __shfl_xor(pm, 16));
+            pm = fmaxf(pm, __shfl_xor(pm, 32));
+            const float mn = fmaxf(m, pm);
+            const float a = expf(m - mn);
+            float e[4];
+#pragma unroll
+            for (int i = 0; i < 4; ++i) e[i] = expf(sc[i] - mn);
+            float ps = ((e[0] + e[1]) + e[2]) + e[3];
+            ps = ps + __shfl_xor(ps, 16);
+            ps = ps + __shfl_xor(ps, 32);
+            l = l * a + ps;
+            m = mn;
+            if (h < G) {
+                *reinterpret_cast<f32x4v_t*>(lds + h * 16 + 4 * quad) = f32x4v_t{e[0], e[1], e[2], e[3]};
+                if (quad == 0) lds[G * 16 + h] = a;
+            }
+            wave_lds_fence();
+            float pv[G][DPL];
+#pragma unroll
+            for (int g = 0; g < G; ++g)
+#pragma unroll
+                for (int j = 0; j < DPL; ++j) pv[g][j] = 0.0f;
+#pragma unroll
+            for (int t4 = 0; t4 < 4; ++t4) {
+                f32x4v_t pg4[G];
+#pragma unroll
+                for (int g = 0; g < G; ++g) pg4[g] = *reinterpret_cast<const f32x4v_t*>(lds + g * 16 + 4 * t4);
+#pragma unroll
+                for (int i = 0; i < 4; ++i) {
+                    const int tt = 4 * t4 + i;
+                    float vv[DPL];
+                    if constexpr (DPL == 4) {
+                        vv[0] = h16_lo<F16>(cur.v[2 * tt]);
+                        vv[1] = h16_hi<F16>(cur.v[2 * tt]);
+                        vv[2] = h16_lo<F16>(cur.v[2 * tt + 1]);
+                        vv[3] = h16_hi<F16>(cur.v[2 * tt + 1]);
+                    } else if constexpr (DPL == 2) {
+                        vv[0] = h16_lo<F16>(cur.v[tt]);
+                        vv[1] = h16_hi<F16>(cur.v[tt]);
+                    } else {
+                        vv[0] = h16_lo<F16>(cur.v[tt]);
+                    }
+#pragma unroll
+                    for (int g = 0; g < G; ++g)
+#pragma unroll
+                        for (int j = 0; j < DPL; ++j) pv[g][j] = pv[g][j] + pg4[g][i] * vv[j];
+                }
+            }
+#pragma unroll
+            for (int g = 0; g < G; ++g) {
+                const float ag = lds[G * 16 + g];
+#pragma unroll
+                for (int j = 0; j < DPL; ++j) o[g][j] = o[g][j] * ag + pv[g][j];
+            }
+            wave_lds_fence();
+            cur = nxt;
+        }
+        if (quad == 0 && h < G) {
+            part[h] = m;
+            part[G + h] = l;
+        }
+#pragma unroll
+        for (int g = 0; g < G; ++g)
+#pragma unroll
+            for (int j = 0; j < DPL; ++j) part[2 * G + g * D + DPL * lane + j] = o[g][j];
+    }
+};
+
+// Folds the chunk partials of one unit, in chunk order, into its (m, l, o)
+// accumulators: m' = max(m, mc), l' = l*e^(m-m') + lc*e^(mc-m'), o likewise.
+template <int G, int D>
+struct DecodeCombine {
+    static constexpr int DPL = D / 64;
+    __device__ static void run(i64 nch, const float* part, i64 pstride, float* m, i64 ms3, float* l, i64 ls3, float* o,
+                               i64 os3, i64 os4) {
+        const int lane = threadIdx.x & 63;
+        float mm[G], ll[G], oo[G][DPL];
+#pragma unroll
+        for (int g = 0; g < G; ++g) {
+            mm[g] = m[g * ms3];
+            ll[g] = l[g * ls3];
+#pragma unroll
+            for (int j = 0; j < DPL; ++j) oo[g][j] = o[g * os3 + (DPL * lane + j) * os4];
+        }
+        for (i64 c = 0; c < nch; ++c) {
+            const float* pc = part + c * pstride;
+#pragma unroll
+            for (int g = 0; g < G; ++g) {
+                const float mc = pc[g], lc = pc[G + g];
+                const float mn = fmaxf(mm[g], mc);
+                const float a = expf(mm[g] - mn), b = expf(mc - mn);
+                ll[g] = ll[g] * a + lc * b;
+#pragma unroll
+                for (int j = 0; j < DPL; ++j) oo[g][j] = oo[g][j] * a + pc[2 * G + g * D + DPL * lane + j] * b;
+                mm[g] = mn;
+            }
+        }
+#pragma unroll
+        for (int g = 0; g < G; ++g) {
+            if (lane == 0) {
+                m[g * ms3] = mm[g];
+                l[g * ls3] = ll[g];
+            }
+#pragma unroll
+            for (int j = 0; j < DPL; ++j) o[g * os3 + (DPL * lane + j) * os4] = oo[g][j];
+        }
+    }
+};
+
 }  // namespace ptowsp

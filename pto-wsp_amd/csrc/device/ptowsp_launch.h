@@ -42,7 +42,8 @@ struct LaunchArgs {
     i64 ntasks;
     u64 scal[kMaxScalars];
     IndirectTerm ind[kMaxIndirect];
-    int* err;  // 1: indirect index out of range, 2: tile outside its tensor
+    int* err;  // 1: indirect index out of range, 2: tile outside its tensor,
+               // 3: a tensor-bound loop extent above its declared maximum
 };
 
 }  // namespace ptowsp

@@ -8,6 +8,9 @@
 // (src/python/pto_codegen.cpp:2507-2545).
 #include "analysis.hpp"
 
+#include <map>
+#include <set>
+
 #include <algorithm>
 
 namespace ptowsp {
@@ -154,6 +157,163 @@ GemmInfo classify_gemm(const KernelDef& k, const KernelAnalysis& a) {
     return g;
 }
 
+// Recognizes the online-softmax decode step (see DecodeInfo) by its dataflow,
+// starting from the three accumulator stores.  Binary ops may take their
+// operands in either order; every non-constant op must belong to the pattern.
+DecodeInfo classify_decode(const KernelDef& k, const KernelAnalysis& a) {
+    DecodeInfo info;
+    std::map<int, const OpInfo*> def;
+    int n_ops = 0;
+    std::vector<const OpInfo*> stores;
+    for (const auto& op : k.ops) {
+        if (op.result > 0) def[op.result] = &op;
+        if (op.kind == OpKind::Constant) continue;
+        ++n_ops;
+        if (op.kind == OpKind::Store) stores.push_back(&op);
+    }
+    if (stores.size() != 3) return info;
+    auto producer = [&](int id, OpKind kind) -> const OpInfo* {
+        auto it = def.find(id);
+        return it != def.end() && it->second->kind == kind && it->second->operands.size() == 2 ? it->second : nullptr;
+    };
+    auto unary = [&](int id, OpKind kind) -> const OpInfo* {
+        auto it = def.find(id);
+        return it != def.end() && it->second->kind == kind && it->second->operands.size() == 1 ? it->second : nullptr;
+    };
+    auto param = [&](int id) { return id >= 0 && id < static_cast<int>(a.param_of.size()) ? a.param_of[id] : -1; };
+    std::set<const OpInfo*> used;
+    // Each store: target param and the stored value.
+    int pm = -1, pl = -1, po = -1, xm = -1, xl = -1, xo = -1;
+    for (const OpInfo* st : stores) {
+        const int tp = param(st->operands[0]);
+        if (tp < 0) return info;
+        const int x = st->operands[1];
+        if (producer(x, OpKind::Max)) { pm = tp; xm = x; }
+        else if (const OpInfo* add = producer(x, OpKind::Add)) {
+            bool is_o = false;
+            for (int w : add->operands) is_o = is_o || producer(w, OpKind::Matmul) != nullptr;
+            if (is_o) { po = tp; xo = x; } else { pl = tp; xl = x; }
+        } else {
+            return info;
+        }
+        used.insert(st);
+    }
+    if (pm < 0 || pl < 0 || po < 0) return info;
+    const int m_id = k.params[pm].id, l_id = k.params[pl].id, o_id = k.params[po].id;
+    // m' = max(m, rowmax(s))
+    const OpInfo* mx = producer(xm, OpKind::Max);
+    int rm = -1;
+    if (mx->operands[0] == m_id) rm = mx->operands[1];
+    else if (mx->operands[1] == m_id) rm = mx->operands[0];
+    const OpInfo* rowmax = rm > 0 ? unary(rm, OpKind::RowMax) : nullptr;
+    if (!rowmax) return info;
+    used.insert(mx);
+    used.insert(rowmax);
+    const int s_id = rowmax->operands[0];
+    // s = mul(matmul(q, k_t), c) [- mask]
+    int s2 = s_id, mask_p = -1;
+    if (const OpInfo* sub = producer(s_id, OpKind::Sub)) {
+        mask_p = param(sub->operands[1]);
+        if (mask_p < 0) return info;
+        // The mask must apply one value per token: a column broadcast, or the same
+        // [1, PG] shape when there is one query row.  When the score tile is square
+        // the reference's rule makes a [1,R] operand a row broadcast
+        // (src/python/pto_codegen.cpp:1094-1105): not this pattern.
+        const size_t oi = static_cast<size_t>(sub - k.ops.data());
+        if (oi >= a.bin_mode.size()) return info;
+        if (a.bin_mode[oi] != BinMode::ColExpand && a.bin_mode[oi] != BinMode::Same) return info;
+        s2 = sub->operands[0];
+        used.insert(sub);
+    }
+    const OpInfo* mul = producer(s2, OpKind::Mul);
+    if (!mul) return info;
+    int s1 = -1;
+    double scale = 0.0;
+    for (int w = 0; w < 2; ++w) {
+        auto it = def.find(mul->operands[w]);
+        if (it != def.end() && it->second->kind == OpKind::Constant && it->second->has_value) {
+            scale = it->second->value;
+            s1 = mul->operands[1 - w];
+        }
+    }
+    const OpInfo* qk = s1 > 0 ? producer(s1, OpKind::Matmul) : nullptr;
+    if (!qk) return info;
+    used.insert(mul);
+    used.insert(qk);
+    const int pq = param(qk->operands[0]), pkt = param(qk->operands[1]);
+    if (pq < 0 || pkt < 0) return info;
+    // p = exp(s - m'), a = exp(m - m')
+    auto is_exp_sub = [&](int id, int x, int y) -> bool {
+        const OpInfo* e = unary(id, OpKind::Exp);
+        const OpInfo* sb = e ? producer(e->operands[0], OpKind::Sub) : nullptr;
+        if (!sb || sb->operands[0] != x || sb->operands[1] != y) return false;
+        used.insert(e);
+        used.insert(sb);
+        return true;
+    };
+    // l' = l*a + rowsum(p), o' = o*a + p @ v (operands of add / mul in any order)
+    auto split_update = [&](int x, int acc_id, OpKind other_kind, const OpInfo*& other, int& alpha) -> bool {
+        const OpInfo* add = producer(x, OpKind::Add);
+        if (!add) return false;
+        for (int w = 0; w < 2; ++w) {
+            const OpInfo* ml = producer(add->operands[w], OpKind::Mul);
+            const OpInfo* ot = other_kind == OpKind::RowSum ? unary(add->operands[1 - w], other_kind)
+                                                            : producer(add->operands[1 - w], other_kind);
+            if (!ml || !ot) continue;
+            if (ml->operands[0] == acc_id) alpha = ml->operands[1];
+            else if (ml->operands[1] == acc_id) alpha = ml->operands[0];
+            else continue;
+            other = ot;
+            used.insert(add);
+            used.insert(ml);
+            used.insert(ot);
+            return true;
+        }
+        return false;
+    };
+    const OpInfo *rowsum = nullptr, *pv = nullptr;
+    int alpha_l = -1, alpha_o = -1;
+    if (!split_update(xl, l_id, OpKind::RowSum, rowsum, alpha_l)) return info;
+    if (!split_update(xo, o_id, OpKind::Matmul, pv, alpha_o)) return info;
+    const int p_id = rowsum->operands[0];
+    if (pv->operands[0] != p_id) return info;
+    const int pv_p = param(pv->operands[1]);
+    if (pv_p < 0) return info;
+    if (!is_exp_sub(p_id, s_id, xm)) return info;
+    if (!is_exp_sub(alpha_l, m_id, xm)) return info;
+    if (alpha_o != alpha_l && !is_exp_sub(alpha_o, m_id, xm)) return info;
+    if (static_cast<int>(used.size()) != n_ops) return info;
+    // Shapes and dtypes.
+    auto vi = [&](int pidx) { return a.by_id[k.params[pidx].id]; };
+    const ValueInfo *q = vi(pq), *kt = vi(pkt), *v = vi(pv_p), *m = vi(pm), *l = vi(pl), *o = vi(po);
+    const int G = q->rows, D = q->cols, PG = kt->cols;
+    if (q->dtype != kt->dtype || q->dtype != v->dtype || (q->dtype != DType::BF16 && q->dtype != DType::F16)) return info;
+    if (m->dtype != DType::F32 || l->dtype != DType::F32 || o->dtype != DType::F32) return info;
+    if (kt->rows != D || v->rows != PG || v->cols != D || m->rows != G || m->cols != 1 || l->rows != G || l->cols != 1 ||
+        o->rows != G || o->cols != D)
+        return info;
+    if (mask_p >= 0) {
+        const ValueInfo* mk = vi(mask_p);
+        if (mk->dtype != DType::F32 || mk->rows != 1 || mk->cols != PG) return info;
+    }
+    // Device template shapes: 16-token pages, up to 16 query rows, head dim 64 / 128 / 256.
+    if (PG != 16 || G < 1 || G > 16 || (D != 64 && D != 128 && D != 256)) return info;
+    info.ok = true;
+    info.q = a.tensor_ordinal[pq];
+    info.kt = a.tensor_ordinal[pkt];
+    info.v = a.tensor_ordinal[pv_p];
+    info.mask = mask_p >= 0 ? a.tensor_ordinal[mask_p] : -1;
+    info.m = a.tensor_ordinal[pm];
+    info.l = a.tensor_ordinal[pl];
+    info.o = a.tensor_ordinal[po];
+    info.g = G;
+    info.d = D;
+    info.pg = PG;
+    info.f16 = q->dtype == DType::F16;
+    info.scale = static_cast<float>(scale);
+    return info;
+}
+
 }  // namespace
 
 KernelAnalysis analyze_kernel(const KernelDef& k) {
@@ -284,9 +444,13 @@ KernelAnalysis analyze_kernel(const KernelDef& k) {
                 const ValueInfo* bv = val(op.operands[1]);
                 if (!av->tile || !bv->tile) refuse(k, "Matmul expects tile operands");
                 if (av->cols != bv->rows) refuse(k, "Matmul K mismatch");
+                // f32 x f32, f16 x f16 (reference :863-873); bf16 x bf16 and a 16-bit float
+                // operand with an f32 one (exact upcast, f32 math) are extensions.
+                auto h16 = [](DType d) { return d == DType::F16 || d == DType::BF16; };
                 const bool ok = (av->dtype == DType::F32 && bv->dtype == DType::F32) ||
                                 (av->dtype == DType::F16 && bv->dtype == DType::F16) ||
-                                (av->dtype == DType::BF16 && bv->dtype == DType::BF16);
+                                (av->dtype == DType::BF16 && bv->dtype == DType::BF16) ||
+                                (av->dtype == DType::F32 && h16(bv->dtype)) || (h16(av->dtype) && bv->dtype == DType::F32);
                 if (!ok || res->dtype != DType::F32)
                     refuse(k, std::string("Matmul: unsupported dtype combination ") + dtype_name(av->dtype) + " x " +
                                   dtype_name(bv->dtype) + " -> " + dtype_name(res->dtype));
@@ -366,7 +530,8 @@ KernelAnalysis analyze_kernel(const KernelDef& k) {
         a.family = Family::RowProgram;
     } else {
         a.gemm = classify_gemm(k, a);
-        a.family = a.gemm.ok ? Family::Gemm : Family::TileProgram;
+        a.decode = a.gemm.ok ? DecodeInfo{} : classify_decode(k, a);
+        a.family = a.gemm.ok ? Family::Gemm : (a.decode.ok ? Family::Decode : Family::TileProgram);
     }
     return a;
 }

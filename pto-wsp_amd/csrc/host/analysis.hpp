@@ -14,7 +14,7 @@ namespace ptowsp {
 // How a binary op combines its operands (src/python/pto_codegen.cpp:1078-1107).
 enum class BinMode { Same, RowExpand, ColExpand, ScalarRight, ScalarLeft };
 
-enum class Family { RowProgram, TileProgram, Gemm };
+enum class Family { RowProgram, TileProgram, Gemm, Decode };
 
 // Role of a value inside a row program.
 enum class RowClass { None, Full, RowVec, RowVecT, ColVec, ColVecT, Scalar };
@@ -27,6 +27,19 @@ struct GemmInfo {
     int m = 0, n = 0, k = 0;
     bool f16 = false;
     bool accumulate = false;     // c + a@b (InOut accumulator) instead of a@b
+};
+
+// Online-softmax decode step (flashinfer_decode over pages): with s = (q @ k_t)
+// * scale [- mask], m' = max(m, rowmax(s)), p = exp(s - m'), a = exp(m - m'):
+// l <- l*a + rowsum(p), o <- o*a + p @ v, m <- m'.  Folding the pages of a
+// P.seq loop in any grouping gives the same (m, l, o) up to fp32 rounding.
+struct DecodeInfo {
+    bool ok = false;
+    int q = -1, kt = -1, v = -1, mask = -1;  // tensor ordinals (mask -1: none)
+    int m = -1, l = -1, o = -1;              // accumulators (InOut)
+    int g = 0, d = 0, pg = 0;                // query rows, head dim, tokens per page
+    bool f16 = false;                        // q / k / v are f16 (else bf16)
+    float scale = 1.0f;                      // score scale (a Constant)
 };
 
 struct KernelAnalysis {
@@ -50,6 +63,7 @@ struct KernelAnalysis {
     std::vector<RowClass> row_class;       // value id -> class
     std::string not_row_reason;
     GemmInfo gemm;
+    DecodeInfo decode;
 };
 
 // Throws CompileError for kernels the reference lowering cannot compute.

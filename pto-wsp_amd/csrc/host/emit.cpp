@@ -537,10 +537,133 @@ EmittedKernel emit_gemm(const Module& m, const KernelAnalysis& a, const LaunchSp
     return ek;
 }
 
+// ---------------------------------------------------------------------------
+// Decode programs (online softmax over pages, split into chunks)
+// ---------------------------------------------------------------------------
+// Launch arguments beyond the kernel's tensors: base[ntens] is the chunk
+// partial scratch; scal[kMaxScalars-1] is the number of chunks per unit and
+// scal[kMaxScalars-2] the declared maximum page count (larger extents raise
+// error 3 and are cut to the chunk capacity).
+EmittedKernel emit_decode(const Module& m, const KernelAnalysis& a, const LaunchSpec& L, const EmitSpec& spec) {
+    (void)m;
+    const KernelDef& k = *a.def;
+    const DecodeInfo& d = a.decode;
+    const int ng = static_cast<int>(L.grid.size());
+    const int nvars = ng + 1;
+    const int ntens = static_cast<int>(a.tensor_param_index.size());
+    const int C = spec.decode_chunk;
+    std::vector<int> first_term(ntens, 0);
+    for (int p = 1; p < ntens; ++p) first_term[p] = first_term[p - 1] + spec.indirect_count[p - 1];
+    auto nterms = [&](int p) { return spec.indirect_count[p]; };
+    const std::string tmpl = "DecodeWave<" + std::to_string(d.g) + ", " + std::to_string(d.d) + ", " +
+                             (d.f16 ? "true" : "false") + ", " + (d.mask >= 0 ? "true" : "false") + ">";
+    std::ostringstream scale;
+    scale.precision(9);
+    scale << std::scientific << d.scale << "f";
+
+    EmittedKernel ek;
+    ek.threads = 256;
+    ek.row_program = false;
+    ek.combine_entry = "ptowsp_combine";
+    ek.part_floats = 2 * d.g + d.g * d.d;
+    std::ostringstream o;
+    o << "#include \"ptowsp_device.h\"\nusing namespace ptowsp;\n";
+    o << "// decode program: kernel " << k.name << ", " << d.g << " query rows, head dim " << d.d << (d.f16 ? " f16" : " bf16")
+      << (d.mask >= 0 ? ", masked" : "") << ", chunks of " << C << " pages\n";
+    // Unit decode + extent, shared by both kernels.
+    auto unit_prologue = [&](const std::string& unit) {
+        o << "  i64 vars[" << nvars << "];\n";
+        o << "  { i64 q_ = " << unit << ";\n";
+        for (int v = ng - 1; v >= 1; --v) o << "    vars[" << v << "] = q_ % A.ext[" << v << "]; q_ /= A.ext[" << v << "];\n";
+        if (ng > 0) o << "    vars[0] = q_;";
+        o << " }\n";
+        o << "  vars[" << ng << "] = 0;\n";
+        const int term = spec.inner_dyn_term.empty() ? -1 : spec.inner_dyn_term[0];
+        if (term >= 0) o << "  i64 npg = indirect_index(A, " << term << ", vars, " << ng << ");\n";
+        else o << "  i64 npg = A.ext[" << ng << "];\n";
+        o << "  if (npg < 0) npg = 0;\n";
+    };
+    auto ptr = [&](int p, const std::string& type, int esize) {
+        return "reinterpret_cast<" + type + ">(A.base[" + std::to_string(p) + "] + (" +
+               offset_expr(p, nvars, first_term[p], nterms(p)) + ") * " + std::to_string(esize) + ")";
+    };
+    // Chunk kernel.
+    o << "extern \"C\" __global__ void __launch_bounds__(256) ptowsp_entry(const LaunchArgs A) {\n";
+    o << "  typedef " << tmpl << " DW;\n";
+    o << "  __shared__ __attribute__((aligned(16))) float lds_all[4][DW::kLdsFloats];\n";
+    o << "  const int wave = __builtin_amdgcn_readfirstlane(static_cast<int>(threadIdx.x >> 6));\n";
+    o << "  const i64 wid = (i64)blockIdx.x * 4 + wave;\n";
+    o << "  const i64 mc = (i64)A.scal[" << kMaxScalars - 1 << "];\n";
+    o << "  const i64 unit = wid / mc, chunk = wid % mc;\n";
+    o << "  if (unit >= A.ntasks) return;\n";
+    unit_prologue("unit");
+    o << "  if (npg > mc * " << C << ") npg = mc * " << C << ";\n";
+    o << "  const i64 p0 = chunk * " << C << ";\n";
+    o << "  if (p0 >= npg) return;\n";
+    o << "  const i64 p1 = p0 + " << C << " < npg ? p0 + " << C << " : npg;\n";
+    auto unit_check = [&](int p, int rows, int cols) {
+        o << "  { const i64 o_ = " << offset_expr(p, nvars, first_term[p], nterms(p)) << ";\n";
+        o << "    if (o_ < 0 || o_ + (i64)" << rows - 1 << " * A.s3[" << p << "] + (i64)" << cols - 1 << " * A.s4[" << p
+          << "] >= A.span[" << p << "]) { if ((threadIdx.x & 63) == 0) *A.err = 2; return; } }\n";
+    };
+    unit_check(d.q, d.g, d.d);
+    o << "  const u16* qp = " << ptr(d.q, "const u16*", 2) << ";\n";
+    // Page bases with a bounds check; an out-of-range page raises the error flag
+    // and reads the tensor's first page instead.
+    auto checked = [&](int p, int rows, int cols, const std::string& var) {
+        o << "    i64 " << var << " = " << offset_expr(p, nvars, first_term[p], nterms(p)) << ";\n";
+        o << "    if (" << var << " < 0 || " << var << " + (i64)" << rows - 1 << " * A.s3[" << p << "] + (i64)" << cols - 1
+          << " * A.s4[" << p << "] >= A.span[" << p << "]) { *A.err = 2; " << var << " = 0; }\n";
+    };
+    o << "  auto ptrs = [&](i64 pg, const u16*& kp, const u16*& vp, const float*& mp) {\n";
+    o << "    vars[" << ng << "] = pg;\n";
+    checked(d.kt, d.d, d.pg, "ok");
+    checked(d.v, d.pg, d.d, "ov");
+    o << "    kp = reinterpret_cast<const u16*>(A.base[" << d.kt << "] + ok * 2);\n";
+    o << "    vp = reinterpret_cast<const u16*>(A.base[" << d.v << "] + ov * 2);\n";
+    if (d.mask >= 0) {
+        checked(d.mask, 1, d.pg, "om");
+        o << "    mp = reinterpret_cast<const float*>(A.base[" << d.mask << "] + om * 4);\n";
+    } else {
+        o << "    mp = nullptr;\n";
+    }
+    o << "  };\n";
+    o << "  float* part = reinterpret_cast<float*>(A.base[" << ntens << "]) + (unit * mc + chunk) * DW::kPartFloats;\n";
+    o << "  DW::run(p0, p1, qp, A.s3[" << d.q << "], " << scale.str() << ", ptrs, A.s4[" << d.kt << "], A.s3[" << d.v
+      << "], lds_all[wave], part);\n";
+    o << "}\n\n";
+    // Combine kernel: one wave per unit.
+    o << "extern \"C\" __global__ void __launch_bounds__(256) ptowsp_combine(const LaunchArgs A) {\n";
+    o << "  const int wave = __builtin_amdgcn_readfirstlane(static_cast<int>(threadIdx.x >> 6));\n";
+    o << "  const i64 unit = (i64)blockIdx.x * 4 + wave;\n";
+    o << "  if (unit >= A.ntasks) return;\n";
+    o << "  const i64 mc = (i64)A.scal[" << kMaxScalars - 1 << "];\n";
+    unit_prologue("unit");
+    o << "  if (npg > (i64)A.scal[" << kMaxScalars - 2 << "]) { if ((threadIdx.x & 63) == 0) *A.err = 3; }\n";
+    o << "  if (npg > mc * " << C << ") npg = mc * " << C << ";\n";
+    o << "  const i64 nch = (npg + " << C - 1 << ") / " << C << ";\n";
+    unit_check(d.m, d.g, 1);
+    unit_check(d.l, d.g, 1);
+    unit_check(d.o, d.g, d.d);
+    o << "  float* mp = " << ptr(d.m, "float*", 4) << ";\n";
+    o << "  float* lp = " << ptr(d.l, "float*", 4) << ";\n";
+    o << "  float* op = " << ptr(d.o, "float*", 4) << ";\n";
+    o << "  const float* part = reinterpret_cast<const float*>(A.base[" << ntens << "]) + unit * mc * "
+      << ek.part_floats << ";\n";
+    o << "  DecodeCombine<" << d.g << ", " << d.d << ">::run(nch, part, " << ek.part_floats << ", mp, A.s3[" << d.m
+      << "], lp, A.s3[" << d.l << "], op, A.s3[" << d.o << "], A.s4[" << d.o << "]);\n";
+    o << "}\n";
+    ek.source = o.str();
+    ek.entry = "ptowsp_entry";
+    ek.lds_bytes = static_cast<size_t>(4 * (d.g * 16 + 16) * 4);
+    return ek;
+}
+
 }  // namespace
 
 EmittedKernel emit_launch(const Module& m, const KernelAnalysis& a, const LaunchSpec& L, const EmitSpec& spec) {
     if (spec.gemm && a.family == Family::Gemm && !spec.serial) return emit_gemm(m, a, L, spec);
+    if (spec.decode && a.family == Family::Decode && !spec.serial) return emit_decode(m, a, L, spec);
     bool indirect = false;
     for (int c : spec.indirect_count) indirect = indirect || c > 0;
     if (a.family == Family::RowProgram && L.inner.empty() && !indirect && !spec.serial) return emit_row(m, a, L, spec);

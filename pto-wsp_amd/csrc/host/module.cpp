@@ -214,7 +214,11 @@ Axis parse_axis(Lexer& L) {
     if (k == "dense") { a.kind = AxisKind::Dense; a.size = L.i64(); }
     else if (k == "dyn") { a.kind = AxisKind::Dyn; a.a = L.str(); }
     else if (k == "ragged") { a.kind = AxisKind::Ragged; a.a = L.str(); a.b = L.str(); }
-    else if (k == "dynt") { a.kind = AxisKind::DynTensor; a.expr = parse_index(L); }
+    else if (k == "dynt") {
+        a.kind = AxisKind::DynTensor;
+        a.max = L.i64();
+        a.expr = parse_index(L);
+    }
     else throw CompileError("module text: bad axis kind '" + k + "'");
     return a;
 }

@@ -92,7 +92,8 @@ struct Axis {
     AxisKind kind = AxisKind::Dense;
     int64_t size = 0;
     std::string a, b;  // Dyn: runtime key; Ragged: outer / lengths symbol names
-    IndexExpr expr;    // DynTensor
+    IndexExpr expr;    // DynTensor: the i32 element holding the extent
+    int64_t max = 0;   // DynTensor: declared upper bound of the extent
 };
 
 enum class NodeKind { Empty, ParallelFor, ForEach, Combine, Sequential, Task, Select, Cond };

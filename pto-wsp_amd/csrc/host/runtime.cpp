@@ -8,6 +8,7 @@
 #include <cstring>
 #include <functional>
 #include <map>
+#include <set>
 #include <memory>
 #include <sstream>
 #include <string>
@@ -83,8 +84,11 @@ struct ptowsp_program {
     CycleResult cycles;
     bool cycles_valid = false;
     std::string precompiled_source;
+    void* scratch = nullptr;  // decode: chunk partials
+    size_t scratch_bytes = 0;
 
     ~ptowsp_program() {
+        if (scratch) (void)hipFree(scratch);
         for (void* b : stage_buf)
             if (b) (void)hipFree(b);
         if (d_err) (void)hipFree(d_err);
@@ -400,6 +404,53 @@ bool gemm_allowed(const KernelAnalysis& a, const LaunchSpec& L, const LaunchArgs
     return true;
 }
 
+// Chooses the split-chunk decode path for a Decode-family kernel: one in-kernel
+// (page) loop; q and the accumulators fixed along it; strides and alignment
+// that the 128-bit / 32-bit loads of DecodeWave need.  Otherwise the launch
+// stays a tile program.
+bool decode_allowed(const KernelAnalysis& a, const LaunchSpec& L, const LaunchArgs& A, const EmitSpec& spec, int ng) {
+    if (a.family != Family::Decode || spec.serial || L.inner.size() != 1) return false;
+    // The last two scalar slots carry the chunk count and the declared page maximum.
+    if (L.task->scalar_args.size() + 2 > static_cast<size_t>(kMaxScalars)) return false;
+    if (L.inner[0].axis->kind == AxisKind::DynTensor && L.inner[0].axis->max <= 0) return false;
+    const DecodeInfo& d = a.decode;
+    const int nvars = ng + 1;
+    const int ntens = static_cast<int>(a.tensor_param_index.size());
+    if (ntens >= kMaxParams) return false;
+    std::vector<int> first(ntens, 0);
+    for (int p = 1; p < ntens; ++p) first[p] = first[p - 1] + spec.indirect_count[p - 1];
+    auto aligned = [&](int p, int64_t elems, int esize) {
+        if (reinterpret_cast<uintptr_t>(A.base[p]) % (elems * esize)) return false;
+        for (int v = 0; v < nvars; ++v)
+            if (A.coef[p][v] % elems) return false;
+        for (int t = 0; t < spec.indirect_count[p]; ++t)
+            if (A.ind[first[p] + t].stride % elems) return false;
+        return true;
+    };
+    for (int p : {d.q, d.m, d.l, d.o}) {
+        if (spec.indirect_count[p] != 0 || A.coef[p][ng] != 0) return false;
+    }
+    const int dpl = d.d / 64;
+    if (A.s4[d.q] != 1 || A.s3[d.q] % 8 || !aligned(d.q, 8, 2)) return false;
+    if (A.s3[d.kt] != 1 || A.s4[d.kt] % 8 || !aligned(d.kt, 8, 2)) return false;
+    if (A.s4[d.v] != 1 || A.s3[d.v] % dpl || !aligned(d.v, dpl, 2)) return false;
+    if (d.mask >= 0 && (A.s4[d.mask] != 1 || !aligned(d.mask, 4, 4))) return false;
+    std::set<int> tids;
+    for (int p : {d.q, d.kt, d.v, d.m, d.l, d.o}) tids.insert(L.targs[p]->tid);
+    if (d.mask >= 0) tids.insert(L.targs[d.mask]->tid);
+    if (static_cast<int>(tids.size()) != (d.mask >= 0 ? 7 : 6)) return false;
+    return true;
+}
+
+int decode_chunk_pages() {
+    static const int c = [] {
+        const char* e = std::getenv("PTOWSP_DECODE_CHUNK");
+        const int v = e ? std::atoi(e) : 16;
+        return v >= 1 && v <= 1024 ? v : 16;
+    }();
+    return c;
+}
+
 BuiltLaunch build_launch(RunEnv& E, const LaunchSpec& L) {
     ptowsp_program* P = E.P;
     const KernelAnalysis& a = P->ka[L.kernel];
@@ -544,6 +595,8 @@ BuiltLaunch build_launch(RunEnv& E, const LaunchSpec& L) {
     B.spec.nontemporal = tuning().nontemporal;
     B.spec.gemm = gemm_allowed(a, L, A, B.spec, ng, nvars);
     if (!B.spec.gemm) B.spec.gemm_vm = B.spec.gemm_vn = -1;
+    B.spec.decode = decode_allowed(a, L, A, B.spec, ng);
+    B.spec.decode_chunk = B.spec.decode ? decode_chunk_pages() : 16;
     B.spec.vec_width = a.family == Family::RowProgram ? pick_vec_width(a, A, nvars) : 1;
     return B;
 }
@@ -551,7 +604,8 @@ BuiltLaunch build_launch(RunEnv& E, const LaunchSpec& L) {
 std::string spec_key(const EmitSpec& s) {
     std::ostringstream o;
     o << "vw" << s.vec_width << (s.serial ? ";serial" : "") << ";up" << s.row_up << (s.nontemporal ? ";nt" : "")
-      << (s.gemm ? ";gemm" : "") << ";m" << s.gemm_vm << ";n" << s.gemm_vn << ";i";
+      << (s.gemm ? ";gemm" : "") << ";m" << s.gemm_vm << ";n" << s.gemm_vn << (s.decode ? ";dec" : "") << s.decode_chunk
+      << ";i";
     for (int c : s.indirect_count) o << c << ",";
     o << ";d";
     for (int c : s.inner_dyn_term) o << c << ",";
@@ -568,6 +622,46 @@ const EmittedKernel& emitted_for(ptowsp_program* P, int li, const EmitSpec& spec
     return c.emitted.emplace(key, std::move(ek)).first->second;
 }
 
+// Decode launch: the chunk kernel (one wave per unit x chunk of pages) and
+// the combine kernel (one wave per unit) back to back on `stream`.  The chunk
+// partials live in a program-owned scratch buffer (grown on demand).
+void enqueue_decode(ptowsp_program* P, int li, BuiltLaunch& B, const EmittedKernel& ek, const JitKernel& jk,
+                    hipStream_t stream, uint64_t& launches) {
+    const LaunchSpec& L = P->plan.launches[li];
+    const KernelAnalysis& a = P->ka[L.kernel];
+    const int ng = static_cast<int>(L.grid.size());
+    const Axis& ax = *L.inner[0].axis;
+    const int64_t maxp = std::max<int64_t>(0, ax.kind == AxisKind::DynTensor ? ax.max : B.args.ext[ng]);
+    const int64_t C = B.spec.decode_chunk;
+    const int64_t mc = std::max<int64_t>(1, (maxp + C - 1) / C);
+    const int64_t waves = B.ntasks * mc;
+    const int64_t blocks = (waves + 3) / 4, cblocks = (B.ntasks + 3) / 4;
+    if (blocks > 0x7FFFFFFF) throw std::runtime_error("decode launch: too many page chunks for one grid");
+    const size_t need = static_cast<size_t>(waves) * static_cast<size_t>(ek.part_floats) * sizeof(float);
+    if (need > P->scratch_bytes) {
+        if (P->scratch) check(hipFree(P->scratch), "hipFree(scratch)");
+        P->scratch = nullptr;
+        P->scratch_bytes = 0;
+        check(hipMalloc(&P->scratch, need), "hipMalloc(decode scratch)");
+        P->scratch_bytes = need;
+    }
+    const int ntens = static_cast<int>(a.tensor_param_index.size());
+    B.args.base[ntens] = static_cast<char*>(P->scratch);
+    B.args.span[ntens] = static_cast<int64_t>(need / sizeof(float));
+    B.args.scal[kMaxScalars - 1] = static_cast<uint64_t>(mc);
+    B.args.scal[kMaxScalars - 2] = static_cast<uint64_t>(maxp);
+    LaunchCache& c = P->cache[li];
+    const std::string key = spec_key(B.spec) + "#combine";
+    auto it = c.by_spec.find(key);
+    const JitKernel* comb = it != c.by_spec.end() ? it->second : (c.by_spec[key] = &jit_kernel(ek.source, ek.combine_entry));
+    void* params[] = {&B.args};
+    check(hipModuleLaunchKernel(jk.function, static_cast<unsigned>(blocks), 1, 1, 256, 1, 1, 0, stream, params, nullptr),
+          "hipModuleLaunchKernel(decode)");
+    check(hipModuleLaunchKernel(comb->function, static_cast<unsigned>(cblocks), 1, 1, 256, 1, 1, 0, stream, params, nullptr),
+          "hipModuleLaunchKernel(decode combine)");
+    launches += 2;
+}
+
 void enqueue_launch(RunEnv& E, int li, hipStream_t stream, uint64_t& launches) {
     ptowsp_program* P = E.P;
     BuiltLaunch B = build_launch(E, P->plan.launches[li]);
@@ -582,6 +676,10 @@ void enqueue_launch(RunEnv& E, int li, hipStream_t stream, uint64_t& launches) {
         c.by_spec[key] = jk;
     } else {
         jk = it->second;
+    }
+    if (B.spec.decode) {
+        enqueue_decode(P, li, B, ek, *jk, stream, launches);
+        return;
     }
     int64_t blocks;
     if (ek.row_program) {
@@ -775,6 +873,7 @@ int ptowsp_hip_precompile(ptowsp_program* P, int index, int flags, const char** 
             spec.row_up = tuning().row_up;
             spec.nontemporal = tuning().nontemporal;
             spec.gemm = a.family == Family::Gemm && !spec.serial;
+            spec.decode = a.family == Family::Decode && !spec.serial && L.inner.size() == 1;
             spec.indirect_count.assign(L.targs.size(), 0);
             for (size_t p = 0; p < L.targs.size(); ++p)
                 for (const auto& e : L.targs[p]->idx)
@@ -903,8 +1002,9 @@ int ptowsp_hip_synchronize(ptowsp_program* P, ptowsp_timing* timing) {
         if (err) {
             const int zero = 0;
             check(hipMemcpy(P->d_err, &zero, sizeof(int), hipMemcpyHostToDevice), "hipMemcpy(err reset)");
-            throw std::runtime_error(err == 1 ? "an indirect tensor index was out of range (tasks skipped)"
-                                              : "a task's tile fell outside its tensor (tasks skipped)");
+            throw std::runtime_error(err == 1   ? "an indirect tensor index was out of range (tasks skipped)"
+                                     : err == 3 ? "a loop extent read from a tensor exceeded its declared maximum"
+                                                : "a task's tile fell outside its tensor (tasks skipped)");
         }
         if (timing) *timing = ptowsp_timing{static_cast<double>(dev_ms), P->h2d_ms, d2h};
         return 0;

@@ -152,7 +152,7 @@ class _Writer:
     def axis(self, axis: Any, var_name: str) -> str:
         bound = getattr(axis, "extent_view", None)
         if isinstance(bound, Tensor):
-            return "dynt " + self.index_expr(bound)
+            return f"dynt {int(axis.size)} " + self.index_expr(bound)
         if isinstance(axis, DenseDyn):
             return f"dyn {enc(var_name)}"
         if isinstance(axis, Ragged):

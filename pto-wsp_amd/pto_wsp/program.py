@@ -163,7 +163,7 @@ class Program:
             kw = node._kwargs
             if node._kind in ("parallel_for", "for_each"):
                 axis, var = kw.get("axis"), kw.get("var_name")
-                if var and hasattr(axis, "size"):
+                if var and hasattr(axis, "size") and getattr(axis, "extent_view", None) is None:
                     try:
                         out[str(var)] = int(axis.size)
                     except Exception:  # noqa: BLE001

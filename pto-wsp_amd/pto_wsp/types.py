@@ -52,19 +52,35 @@ class Dense(Generic[N]):
 
 
 class DenseDyn:
-    """Axis whose extent is read at run time (``Program.set_axis_sizes``).
+    """Axis whose extent is read at run time.
 
-    ``size`` is the default used until the program is told otherwise.
+    ``DenseDyn(size)`` is the reference's axis (``python/pto_wsp/types.py:36-47``):
+    one extent per loop variable name, rebound with ``Program.set_axis_sizes``;
+    ``size`` is the default until then.
+
+    Extension (per-outer extents, e.g. pages per sequence of a paged KV cache):
+    ``DenseDyn(max_size, extent=N[b])`` takes the extent of each loop instance
+    from one element of an I32 tensor, indexed by enclosing loop variables.
+    ``max_size`` is then only an upper bound used for sizing.
     """
 
-    def __init__(self, size: int) -> None:
+    def __init__(self, size: int, extent=None) -> None:
         self._size = int(size)
+        if extent is not None:
+            from_tensor = getattr(extent, "base", None)
+            if from_tensor is None or getattr(from_tensor, "dtype", None) != DType.I32:
+                raise TypeError("DenseDyn extent must be an element view of an I32 tensor")
+            if tuple(extent.shape) != ():
+                raise TypeError(f"DenseDyn extent must select one element (view shape {tuple(extent.shape)})")
+        self.extent_view = extent
 
     @property
     def size(self) -> int:
         return self._size
 
     def __repr__(self) -> str:
+        if self.extent_view is not None:
+            return f"DenseDyn({self._size}, extent={self.extent_view!r})"
         return f"DenseDyn({self._size})"
 
 

@@ -314,3 +314,75 @@ def test_bgemm_f16_mfma_device_tensors(gpu):
     ref = run_workload(W.rr4(W.bgemm(ca, 64, 64, 64, DType.F16)))
     assert _rel_fro(cd.cpu().numpy(), ca["c"]) <= 1e-5
     assert prog.stats.total_cycles == ref.total_cycles
+
+
+# ---------------------------------------------------------------- paged GQA decode
+def _decode_case(lengths, hkv, group, d, page=16, seed=0, masked=True, f16=False):
+    ga = W.paged_decode_arrays(lengths, hkv, group, d, page=page, seed=seed, f16=f16)
+    ca = {k: v.copy() for k, v in ga.items()}
+    dt = W.F16 if f16 else W.BF16
+    prog = run_hip(W.paged_decode(ga, masked=masked, dtype=dt))
+    ref = run_workload(W.paged_decode(ca, masked=masked, dtype=dt))
+    return prog, ref, ga, ca
+
+
+@pytest.mark.parametrize("lengths,hkv,group,d", [
+    ([37, 16, 200, 1, 256, 513], 2, 4, 128),    # partial, exact, single-token and multi-chunk sequences
+    ([300, 77], 1, 8, 64),                       # head dim 64 (one column per lane), 8 query rows
+    ([129, 40], 2, 1, 256),                      # head dim 256, one query row
+])
+def test_paged_decode_family(gpu, lengths, hkv, group, d):
+    prog, ref, ga, ca = _decode_case(lengths, hkv, group, d, seed=len(lengths))
+    assert prog._native.kernel_family("decode_page") == "decode"
+    # chunked folding reassociates fp32 sums: per element rtol 2e-5 with an atol
+    # of 2e-5 of the tensor's largest magnitude (entries near zero cancel)
+    for k in ("m", "l", "o", "out"):
+        np.testing.assert_allclose(ga[k], ca[k], rtol=2e-5, atol=2e-5 * float(np.abs(ca[k]).max()), err_msg=k)
+    assert _rel_fro(ga["out"], W.paged_decode_ref(ga)) <= 1e-5
+    assert prog.stats.total_cycles == ref.total_cycles and prog.stats.task_count == ref.task_count
+
+
+def test_paged_decode_sixteen_rows(gpu):
+    """16 query rows fill every MFMA column.  Unmasked it is the decode family; with
+    the [1,16] mask on a square [16,16] score tile the reference's broadcast rule
+    subtracts mask[row] (a row broadcast, src/python/pto_codegen.cpp:1094-1105),
+    so the launch stays a tile program and matches the oracle, not a token mask."""
+    prog, ref, ga, ca = _decode_case([96, 512, 16], 1, 16, 128, seed=3, masked=False)
+    assert prog._native.kernel_family("decode_page") == "decode"
+    for k in ("m", "l", "o", "out"):
+        np.testing.assert_allclose(ga[k], ca[k], rtol=2e-5, atol=2e-5 * float(np.abs(ca[k]).max()), err_msg=k)
+    assert _rel_fro(ga["out"], W.paged_decode_ref(ga)) <= 1e-5
+    prog, ref, ga, ca = _decode_case([90, 40], 1, 16, 128, seed=3, masked=True)
+    assert prog._native.kernel_family("decode_page") == "tile_program"
+    for k in ("m", "l", "o", "out"):
+        np.testing.assert_allclose(ga[k], ca[k], rtol=1e-5, atol=1e-5 * float(np.abs(ca[k]).max()), err_msg=k)
+
+
+def test_paged_decode_f16_and_unmasked(gpu):
+    lengths = [64, 160, 32]                      # multiples of the page: no mask needed
+    prog, ref, ga, ca = _decode_case(lengths, 2, 4, 128, seed=5, masked=False, f16=True)
+    assert prog._native.kernel_family("decode_page") == "decode"
+    np.testing.assert_allclose(ga["out"], ca["out"], rtol=2e-5, atol=2e-5 * float(np.abs(ca["out"]).max()))
+    assert _rel_fro(ga["out"], W.paged_decode_ref(ga)) <= 1e-5
+
+
+def test_paged_decode_tile_program_path(gpu):
+    """8-token pages are outside the decode template: the tile program runs the page loop in order."""
+    prog, ref, ga, ca = _decode_case([37, 8, 61], 2, 4, 64, page=8, seed=3)
+    assert prog._native.kernel_family("decode_page") == "tile_program"
+    for k in ("m", "l", "o", "out"):
+        np.testing.assert_allclose(ga[k], ca[k], rtol=1e-5, atol=1e-6, err_msg=k)
+    assert _rel_fro(ga["out"], W.paged_decode_ref(ga)) <= 1e-5
+
+
+def test_paged_decode_extent_above_declared_maximum_raises(gpu):
+    """A page count above DenseDyn's declared maximum is reported by synchronize()
+    (forced from the host; every device access stays bounds-checked)."""
+    from pto_wsp import ExecutionError
+
+    ga = W.paged_decode_arrays([40, 20], 1, 4, 128, seed=2)
+    ga["npages"][1] = ga["page_table"].shape[1] + 1
+    prog = W.paged_decode(ga).compile(target="hip_gfx950")
+    prog.execute()
+    with pytest.raises(ExecutionError, match="declared maximum"):
+        prog.synchronize()

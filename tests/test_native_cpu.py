@@ -73,6 +73,8 @@ def _cases():
                                        "b": np.zeros((4, 4, 4), np.float32)}), {}),
         "dense_dyn": (lambda: W.dense_dyn_mm({"a": np.ones((4, 4, 4), np.float32), "b": np.ones((4, 4, 4), np.float32),
                                               "c": np.zeros((4, 4, 4), np.float32)}), {"b": 3}),
+        "paged_decode": (lambda: W.paged_decode(W.paged_decode_arrays([37, 16, 200], 2, 4, 128, seed=1)), {}),
+        "paged_decode_p8": (lambda: W.paged_decode(W.paged_decode_arrays([37, 9], 1, 4, 64, page=8, seed=1)), {}),
     }
 
 
@@ -127,6 +129,15 @@ def test_family_selection():
         W.bgemm({"a": a, "b": a, "c": np.zeros((1, 256, 256), np.float32)}, 128, 128, 64, W.BF16), "g").module)
     assert prog.kernel_family("gemm_tile") == "gemm"
     assert "gemm program" in prog.precompile(0)
+    prog = NativeProgram(workload_to_codegen_ir(W.paged_decode(W.paged_decode_arrays([20, 5], 2, 4, 128)), "d").module)
+    assert prog.kernel_family("decode_page") == "decode"
+    assert prog.kernel_family("normalize") == "row_program"
+    assert "decode program" in prog.precompile(0)
+    # the same body with one op changed (rowsum -> rowmax) is no longer the decode pattern
+    src = workload_to_codegen_ir(W.paged_decode(W.paged_decode_arrays([20, 5], 2, 4, 128)), "d").module
+    assert "O RowSum" in src
+    prog = NativeProgram(src.replace("O RowSum", "O RowMax"))
+    assert prog.kernel_family("decode_page") == "tile_program"
 
 
 def _compile_err(w, match):

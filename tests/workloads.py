@@ -255,6 +255,117 @@ def attention_arrays(q, k, v, tile_seq):
     return {"q": q.copy(), "k_t": kt, "v": v.copy(), "o": np.zeros_like(q)}
 
 
+# ---------------------------------------------------------------- paged GQA decode (config 5)
+def paged_decode(arrs: dict, scale: float | None = None, masked: bool = True, dtype=BF16):
+    """flashinfer_decode over a paged KV cache: P(batch) x P(kv_head) x P.seq(pages).
+
+    Per (b, g) the kernel folds one 16-token page into running (m, l, o) with
+    online softmax for the G query heads of KV group g; the page comes from the
+    page table (indirect index) and the page count of sequence b from npages[b]
+    (a tensor-bound DenseDyn).  The last page's padding tokens are masked with a
+    [1, page] penalty (0 or 1e30) subtracted from the scores.  A second launch
+    writes out = o / l.
+
+    arrs: q [B, Hkv, G, D] bf16 bits; k_cache, v_cache [P, Hkv, page, D] bf16 bits;
+    page_table [B, max_pages] i32; npages [B] i32; mask [B, max_pages, 1, page] f32;
+    m [B, Hkv, G, 1] f32 (-inf); l [B, Hkv, G, 1] f32 (0); o [B, Hkv, G, D] f32 (0);
+    out [B, Hkv, G, D] f32.
+    """
+    q, kc, vc = arrs["q"], arrs["k_cache"], arrs["v_cache"]
+    B, Hkv, G, D = q.shape
+    page = kc.shape[2]
+    max_pages = arrs["page_table"].shape[1]
+    sc = float(scale if scale is not None else 1.0 / math.sqrt(D))
+
+    def perm(x, axes):  # numpy or torch
+        return x.permute(*axes) if hasattr(x, "permute") else x.transpose(*axes)
+
+    Q, KT, V = T(q, dtype), T(perm(kc, (0, 1, 3, 2)), dtype), T(vc, dtype)
+    PT, NP = T(arrs["page_table"], I32), T(arrs["npages"], I32)
+    MASK, M, L, O, OUT = T(arrs["mask"]), T(arrs["m"]), T(arrs["l"]), T(arrs["o"]), T(arrs["out"])
+
+    @kernel
+    def decode_page(q: In[Tile[G, D, dtype]], k_t: In[Tile[D, page, dtype]], v: In[Tile[page, D, dtype]],
+                    mask: In[Tile[1, page, F32]], m_acc: InOut[Tile[G, 1, F32]], l_acc: InOut[Tile[G, 1, F32]],
+                    o_acc: InOut[Tile[G, D, F32]]):
+        s = pto.mul(pto.matmul(q, k_t), pto.constant(sc, F32))
+        if masked:
+            s = pto.sub(s, mask)
+        m_new = pto.max(m_acc, pto.rowmax(s))
+        p = pto.exp(pto.sub(s, m_new))
+        alpha = pto.exp(pto.sub(m_acc, m_new))
+        pto.store(l_acc, pto.add(pto.mul(l_acc, alpha), pto.rowsum(p)))
+        pto.store(o_acc, pto.add(pto.mul(o_acc, alpha), pto.matmul(p, v)))
+        pto.store(m_acc, m_new)
+
+    @kernel
+    def normalize(o_acc: In[Tile[G, D, F32]], l_acc: In[Tile[G, 1, F32]], out: Out[Tile[G, D, F32]]):
+        pto.store(out, pto.div(o_acc, l_acc))
+
+    @workload
+    def paged_decode_wl():
+        for b in P(Dense[B]()):
+            for g in P(Dense[Hkv]()):
+                for pg in P.seq(DenseDyn(max_pages, extent=NP[b]), name="pg"):
+                    decode_page[b, g, pg](q=Q[b][g], k_t=KT[PT[b][pg]][g], v=V[PT[b][pg]][g], mask=MASK[b][pg],
+                                          m_acc=M[b][g], l_acc=L[b][g], o_acc=O[b][g])
+        for b in P(Dense[B]()):
+            for g in P(Dense[Hkv]()):
+                normalize[b, g](o_acc=O[b][g], l_acc=L[b][g], out=OUT[b][g])
+
+    return paged_decode_wl()
+
+
+def paged_decode_arrays(lengths, hkv: int, group: int, d: int, page: int = 16, seed: int = 0,
+                        spare_pages: int = 3, f16: bool = False) -> dict:
+    """Seeded numpy inputs: bf16 q / K / V ~ N(0,1); page table = a random permutation of the
+    physical pages (plus a few never-referenced spares)."""
+    rng = np.random.default_rng(seed)
+    lengths = np.asarray(lengths, np.int64)
+    B = len(lengths)
+    npages = (lengths + page - 1) // page
+    max_pages = int(npages.max())
+    total = int(npages.sum()) + spare_pages
+    phys = rng.permutation(total).astype(np.int32)
+    pt = np.zeros((B, max_pages), np.int32)
+    mask = np.zeros((B, max_pages, 1, page), np.float32)
+    off = 0
+    for b in range(B):
+        n = int(npages[b])
+        pt[b, :n] = phys[off:off + n]
+        off += n
+        t = np.arange(max_pages * page).reshape(max_pages, page)
+        mask[b, :, 0, :] = np.where(t < lengths[b], 0.0, 1e30)
+    if f16:
+        bf = lambda shape: rng.standard_normal(shape).astype(np.float16)
+    else:
+        bf = lambda shape: bf16_round(rng.standard_normal(shape).astype(np.float32))
+    return {"q": bf((B, hkv, group, d)), "k_cache": bf((total, hkv, page, d)), "v_cache": bf((total, hkv, page, d)),
+            "page_table": pt, "npages": npages.astype(np.int32), "mask": mask,
+            "m": np.full((B, hkv, group, 1), -np.inf, np.float32), "l": np.zeros((B, hkv, group, 1), np.float32),
+            "o": np.zeros((B, hkv, group, d), np.float32), "out": np.zeros((B, hkv, group, d), np.float32),
+            "lengths": lengths}
+
+
+def paged_decode_ref(arrs: dict) -> np.ndarray:
+    """float64 softmax(q k^T / sqrt(d)) v over each sequence's valid tokens."""
+    up = (lambda x: x.astype(np.float64)) if arrs["q"].dtype == np.float16 else (lambda x: bf16_to_f32(x).astype(np.float64))
+    q, kc, vc = up(arrs["q"]), up(arrs["k_cache"]), up(arrs["v_cache"])
+    B, Hkv, G, D = q.shape
+    page = kc.shape[2]
+    out = np.zeros((B, Hkv, G, D))
+    for b in range(B):
+        L = int(arrs["lengths"][b])
+        n = (L + page - 1) // page
+        pages = arrs["page_table"][b, :n]
+        k = kc[pages].transpose(1, 0, 2, 3).reshape(Hkv, n * page, D)[:, :L]
+        v = vc[pages].transpose(1, 0, 2, 3).reshape(Hkv, n * page, D)[:, :L]
+        s = np.einsum("hgd,htd->hgt", q[b], k) / math.sqrt(D)
+        w = np.exp(s - s.max(-1, keepdims=True))
+        out[b] = np.einsum("hgt,htd->hgd", w / w.sum(-1, keepdims=True), v)
+    return out
+
+
 # ---------------------------------------------------------------- small reference tests
 def matmul_tile(arrs: dict, m: int, k: int, n: int, dtype=F32):
     """tests/test_codegen_execute_basic.py / examples/validated_matmul: C[b][0] = A[b][0] @ B[b][0]."""
