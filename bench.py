@@ -121,8 +121,156 @@ def bgemm_workload(A, Bm, C, tm=128, tn=128, tk=64):
     return rr4(bgemm())
 
 
+def decode_workload(t, page=16):
+    """flashinfer_decode over a paged KV cache: for each sequence b and
+    KV head g, P.seq over the sequence's pages folds one 16-token page into running
+    (m, l, o) for the 4 query heads of the group (online softmax); a second launch
+    writes out = o / l.  The page count of sequence b is npages[b] (a tensor-bound
+    DenseDyn, declared maximum 512 pages), the page comes from the page table, and
+    padding tokens of the last page are masked by a 0 / 1e30 penalty row."""
+    import math
+
+    from pto_wsp import DType, Dense, DenseDyn, In, InOut, Out, P, Tensor, Tile, kernel, pto, workload
+
+    bf16, f32, i32 = DType.BF16, DType.F32, DType.I32
+    B, Hkv, G, D = tuple(t["q"].shape)
+    max_pages = t["page_table"].shape[1]
+    sc = 1.0 / math.sqrt(D)
+
+    def T(x, dt):
+        return Tensor(data=x, shape=tuple(x.shape), dtype=dt)
+
+    kt = t["k_cache"].permute(0, 1, 3, 2) if hasattr(t["k_cache"], "permute") else t["k_cache"].transpose(0, 1, 3, 2)
+    Q, KT, V = T(t["q"], bf16), T(kt, bf16), T(t["v_cache"], bf16)
+    PT, NP, MASK = T(t["page_table"], i32), T(t["npages"], i32), T(t["mask"], f32)
+    M, L, O, OUT = T(t["m"], f32), T(t["l"], f32), T(t["o"], f32), T(t["out"], f32)
+
+    @kernel
+    def decode_page(q: In[Tile[G, D, bf16]], k_t: In[Tile[D, page, bf16]], v: In[Tile[page, D, bf16]],
+                    mask: In[Tile[1, page, f32]], m_acc: InOut[Tile[G, 1, f32]], l_acc: InOut[Tile[G, 1, f32]],
+                    o_acc: InOut[Tile[G, D, f32]]):
+        s = pto.sub(pto.mul(pto.matmul(q, k_t), pto.constant(sc, f32)), mask)
+        m_new = pto.max(m_acc, pto.rowmax(s))
+        p = pto.exp(pto.sub(s, m_new))
+        alpha = pto.exp(pto.sub(m_acc, m_new))
+        pto.store(l_acc, pto.add(pto.mul(l_acc, alpha), pto.rowsum(p)))
+        pto.store(o_acc, pto.add(pto.mul(o_acc, alpha), pto.matmul(p, v)))
+        pto.store(m_acc, m_new)
+
+    @kernel
+    def normalize(o_acc: In[Tile[G, D, f32]], l_acc: In[Tile[G, 1, f32]], out: Out[Tile[G, D, f32]]):
+        pto.store(out, pto.div(o_acc, l_acc))
+
+    @workload
+    def paged_decode():
+        for b in P(Dense[B]()):
+            for g in P(Dense[Hkv]()):
+                for pg in P.seq(DenseDyn(max_pages, extent=NP[b]), name="pg"):
+                    decode_page[b, g, pg](q=Q[b][g], k_t=KT[PT[b][pg]][g], v=V[PT[b][pg]][g], mask=MASK[b][pg],
+                                          m_acc=M[b][g], l_acc=L[b][g], o_acc=O[b][g])
+        for b in P(Dense[B]()):
+            for g in P(Dense[Hkv]()):
+                normalize[b, g](o_acc=O[b][g], l_acc=L[b][g], out=OUT[b][g])
+
+    return rr4(paged_decode())
+
+
+class DecodeCase:
+    unit, bound, dtype = "GB/s", "hbm", "bf16"
+
+    def __init__(self, name, batch, hq, hkv, d, lmin, lmax, seed, baseline_config, page=16):
+        self.name, self.batch, self.hq, self.hkv, self.d = name, batch, hq, hkv, d
+        self.lmin, self.lmax, self.seed, self.page = lmin, lmax, seed, page
+        self.baseline_config = baseline_config
+
+    def setup(self, dev):
+        import numpy as np
+        import torch
+
+        rng = np.random.default_rng(self.seed)
+        B, page, G = self.batch, self.page, self.hq // self.hkv
+        self.lengths = rng.integers(self.lmin, self.lmax + 1, size=B)
+        npages = (self.lengths + page - 1) // page
+        max_pages = (self.lmax + page - 1) // page
+        total = int(npages.sum())
+        phys = rng.permutation(total).astype(np.int32)
+        pt = np.zeros((B, max_pages), np.int32)
+        mask = np.zeros((B, max_pages, 1, page), np.float32)
+        tok = np.arange(max_pages * page).reshape(max_pages, page)
+        off = 0
+        for b in range(B):
+            pt[b, :npages[b]] = phys[off:off + npages[b]]
+            off += npages[b]
+            mask[b, :, 0, :] = np.where(tok < self.lengths[b], 0.0, 1e30)
+        g = torch.Generator(device=dev)
+        g.manual_seed(self.seed)
+        shape_kv = (total, self.hkv, page, self.d)
+        t = {"q": torch.randn((B, self.hkv, G, self.d), generator=g, device=dev, dtype=torch.bfloat16),
+             "k_cache": torch.randn(shape_kv, generator=g, device=dev, dtype=torch.bfloat16),
+             "v_cache": torch.randn(shape_kv, generator=g, device=dev, dtype=torch.bfloat16),
+             "page_table": torch.from_numpy(pt).to(dev), "npages": torch.from_numpy(npages.astype(np.int32)).to(dev),
+             "mask": torch.from_numpy(mask).to(dev),
+             "m": torch.full((B, self.hkv, G, 1), float("-inf"), device=dev),
+             "l": torch.zeros((B, self.hkv, G, 1), device=dev), "o": torch.zeros((B, self.hkv, G, self.d), device=dev),
+             "out": torch.zeros((B, self.hkv, G, self.d), device=dev)}
+        self.t = t
+        self.prog = decode_workload(t, page).compile(target="hip_gfx950")
+        ntok = int(self.lengths.sum())
+        # Algorithmic bytes: K and V of the valid tokens, q (bf16), out (f32), the page table entries used.
+        self.work = ntok * self.hkv * self.d * 2 * 2 + B * self.hq * self.d * 2 + B * self.hq * self.d * 4 + 4 * total
+
+    def before_step(self):
+        self.t["m"].fill_(float("-inf"))
+        self.t["l"].zero_()
+        self.t["o"].zero_()
+
+    def peak(self):
+        return HBM_PEAK_GBS
+
+    def rate(self, seconds):
+        return self.work / seconds / 1e9
+
+    def describe(self):
+        return (f"{self.name}: paged GQA decode, batch {self.batch}, {self.hq} query / {self.hkv} KV heads, head dim "
+                f"{self.d}, bf16 Q/K/V N(0,1), lengths U[{self.lmin},{self.lmax}] (sum {int(self.lengths.sum())}), "
+                f"{self.page}-token pages, permuted page table; P(batch) x P(kv_head) x P.seq(DenseDyn(pages)) "
+                "+ normalize")
+
+    def cpu(self, budget_s):
+        """Oracle on a bounded sample: the first 16 sequences (all KV heads), same inputs."""
+        import numpy as np
+        import torch
+
+        from oracle.runner import run_workload
+
+        del budget_s
+        nb = 16
+        self.before_step()
+        self.prog.execute()
+        self.prog.synchronize()
+        u16 = lambda x: x.contiguous().view(torch.int16).cpu().numpy().view(np.uint16)
+        h = {"q": u16(self.t["q"][:nb]), "k_cache": u16(self.t["k_cache"]), "v_cache": u16(self.t["v_cache"]),
+             "page_table": self.t["page_table"][:nb].cpu().numpy(), "npages": self.t["npages"][:nb].cpu().numpy(),
+             "mask": self.t["mask"][:nb].cpu().numpy()}
+        G = self.hq // self.hkv
+        h["m"] = np.full((nb, self.hkv, G, 1), -np.inf, np.float32)
+        h["l"] = np.zeros((nb, self.hkv, G, 1), np.float32)
+        h["o"] = np.zeros((nb, self.hkv, G, self.d), np.float32)
+        h["out"] = np.zeros((nb, self.hkv, G, self.d), np.float32)
+        t0 = time.perf_counter()
+        run_workload(decode_workload(h, self.page))
+        sec = time.perf_counter() - t0
+        ntok = int(self.lengths[:nb].sum())
+        nbytes = ntok * self.hkv * self.d * 4 + nb * self.hq * self.d * 6 + 4 * int(h["npages"].sum())
+        got = self.t["out"][:nb].cpu().numpy()
+        rel = float(np.linalg.norm(got - h["out"]) / np.linalg.norm(h["out"]))
+        self.cpu_rel = rel
+        sample = f"sequences 0-15 of the batch ({ntok} tokens, all {self.hkv} KV heads), one oracle run"
+        return nbytes / sec / 1e9, sample, rel <= 1e-2
+
+
 class RowCase:
-    unit, bound = "GB/s", "hbm"
+    unit, bound, dtype = "GB/s", "hbm", "f32"
 
     def __init__(self, name, kind, shape, sigma, seed, baseline_config):
         self.name, self.kind, self.shape, self.sigma, self.seed = name, kind, shape, sigma, seed
@@ -170,7 +318,7 @@ class RowCase:
 
 
 class GemmCase:
-    unit, bound = "TFLOP/s", "mfma"
+    unit, bound, dtype = "TFLOP/s", "mfma", "bf16"
 
     def __init__(self, name, nb, m, n, k, seed, baseline_config):
         self.name, self.nb, self.m, self.n, self.k, self.seed = name, nb, m, n, k, seed
@@ -229,6 +377,7 @@ CASES = {
     "rmsnorm_bw": lambda: RowCase("rmsnorm_bw", "rmsnorm", (16, 8192, 16, 128), 1.0, 0, 1),
     "softmax": lambda: RowCase("softmax", "softmax", (8, 4096, 32, 512), 3.0, 0, 2),
     "bgemm": lambda: GemmCase("bgemm", 64, 2048, 2048, 2048, 0, 3),
+    "paged_decode": lambda: DecodeCase("paged_decode", 64, 32, 8, 128, 512, 8192, 0, 4),
     # Not a BASELINE config: a plain tile copy of known size (1 GiB in, 1 GiB
     # out) through the same backend, used to calibrate rocprofv3 traffic
     # counters and as the achievable-bandwidth reference.
@@ -252,13 +401,16 @@ def load_traffic(name):
 def time_case(case, steps, warmup):
     import torch
 
+    before = getattr(case, "before_step", lambda: None)
     for _ in range(warmup):
+        before()
         case.prog.execute()
         case.prog.synchronize()
     torch.cuda.synchronize()
     kernel_ms = []
     t0 = time.perf_counter()
     for _ in range(steps):
+        before()
         case.prog.execute()
         case.prog.synchronize()
         kernel_ms.append(case.prog.stats.device_time_ms)
@@ -331,7 +483,7 @@ def main():
         "higher_is_better": True,
         "scaling": "weak",
         "vs_baseline": None,
-        "dtype": "f32" if case.unit == "GB/s" else "bf16",
+        "dtype": case.dtype,
         "data": "synthetic (torch RNG on device, seeded)",
         "config": {"workload": case.describe(), "baseline_config": case.baseline_config,
                    "work_per_step": case.work, "target": "hip_gfx950"},

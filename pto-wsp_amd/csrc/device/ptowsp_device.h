@@ -22,7 +22,7 @@ __device__ inline float bits_f32(u64 b) { return __uint_as_float(static_cast<u32
 
 // Reads one element of an indirect index; out-of-range indices are clamped
 // to 0 after raising the error flag, so the access stays in bounds.
-__device__ inline i64 indirect_index(const LaunchArgs& A, int k, const i64* vars, int nvars) {
+__device__ inline i64 indirect_value(const LaunchArgs& A, int k, const i64* vars, int nvars) {
     const IndirectTerm& t = A.ind[k];
     i64 off = t.c;
     for (int v = 0; v < nvars; ++v) off += t.coef[v] * vars[v];
@@ -32,7 +32,10 @@ __device__ inline i64 indirect_index(const LaunchArgs& A, int k, const i64* vars
         *A.err = 1;
         idx = 0;
     }
-    return idx * t.stride;
+    return idx;
+}
+__device__ inline i64 indirect_index(const LaunchArgs& A, int k, const i64* vars, int nvars) {
+    return indirect_value(A, k, vars, nvars) * A.ind[k].stride;
 }
 
 // ---------------------------------------------------------------------------
@@ -503,19 +506,19 @@ struct GemmBlock {
 // Decode: online softmax over 16-token pages (flashinfer_decode pattern)
 // ---------------------------------------------------------------------------
 //
-// The pages of one unit (sequence b, KV group g) are split into chunks; one
-// wave folds a chunk into a partial (m, l, o) for the unit's G query rows,
-// starting from (-inf, 0, 0), and DecodeCombine folds the partials of a unit
-// in chunk order into the accumulators.  Per page:
+// The pages of one unit (sequence b, KV group g) are folded by one or more
+// waves (DecodeSplit); each wave folds its pages into a partial (m, l, o) for
+// the unit's G query rows, starting from (-inf, 0, 0), and DecodeCombine folds
+// the unit's partials in page order into the accumulators.  Per page:
 //  * scores on MFMA v_mfma_f32_16x16x32 (one per 32-wide head-dim slice):
-//    A = the K page (lane l: token l%16, head dims 8*(l/16)..+7 of the slice),
-//    B = q^T (lane l: query row l%16, zero for rows >= G); lane l then holds
-//    query row l%16 for tokens 4*(l/16)..+3;
-//  * row max / row sum over the 16 tokens: 4 values in the lane, then lanes
-//    l^16 and l^32;
-//  * p and the rescale factor pass through LDS; p @ v runs in fp32 on the
-//    VALU with lane l owning head-dim columns (D/64)*l ..; the sum over the 16
-//    tokens runs in token order, mul then add (as the oracle's TMATMUL).
+//    A = q (lane l: query row l%16, zero for rows >= G, head dims
+//    8*(l/16)..+7 of the slice), B = the K page (lane l: token l%16); lane l
+//    then holds query rows 4*(l/16)..+3 for token l%16;
+//  * the scores pass through LDS so that each pass holds one (query row,
+//    token) per lane; row max and row sum over a 16-lane DPP row;
+//  * p and the rescale factor pass through LDS; p @ v runs in fp32 FMAs on
+//    the VALU, lane l owning tokens 4*(l/16)..+3 of every page and head dims
+//    (D/16)*(l%16)..; the four token groups are summed once per partial.
 
 typedef float f32x4v_t __attribute__((ext_vector_type(4)));
 
@@ -544,153 +547,287 @@ __device__ inline float h16_hi(u32 w) {
 // instructions in order; this keeps the compiler from reordering them).
 __device__ inline void wave_lds_fence() { __builtin_amdgcn_fence(__ATOMIC_SEQ_CST, "wavefront"); }
 
+// Reduction over the 16 lanes of a DPP row (xor 1, xor 2, then the half-row
+// and row mirrors); every lane of the row ends with the row's result.
+template <class Op>
+__device__ inline float row16_reduce(float x, Op op) {
+    auto dpp = [](float v, int ctrl) {
+        switch (ctrl) {
+            case 0: return __int_as_float(__builtin_amdgcn_update_dpp(0, __float_as_int(v), 0xB1, 0xF, 0xF, false));
+            case 1: return __int_as_float(__builtin_amdgcn_update_dpp(0, __float_as_int(v), 0x4E, 0xF, 0xF, false));
+            case 2: return __int_as_float(__builtin_amdgcn_update_dpp(0, __float_as_int(v), 0x141, 0xF, 0xF, false));
+            default: return __int_as_float(__builtin_amdgcn_update_dpp(0, __float_as_int(v), 0x140, 0xF, 0xF, false));
+        }
+    };
+    x = op(x, dpp(x, 0));
+    x = op(x, dpp(x, 1));
+    x = op(x, dpp(x, 2));
+    x = op(x, dpp(x, 3));
+    return x;
+}
+
+// Partials pass between waves of different XCDs (each XCD has its own L2).
+// They are written and read as relaxed agent-scope atomics, which the
+// compiler issues with the sc1 policy (coherent across the XCDs' L2s), so no
+// L2 write-back or invalidate is needed for them; publish() orders a wave's
+// partial stores before its completion count: it waits until the stores are
+// done (vmcnt 0), with compiler barriers on both sides.
+__device__ inline void coherent_store(float* p, float v) { __hip_atomic_store(p, v, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT); }
+__device__ inline float coherent_load(const float* p) {
+    return __hip_atomic_load(const_cast<float*>(p), __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+}
+__device__ inline void publish() {
+    __atomic_signal_fence(__ATOMIC_SEQ_CST);
+    wait_vmcnt<0>();
+    __atomic_signal_fence(__ATOMIC_SEQ_CST);
+}
+// Unit completion count: the wave that brings it to `parts` (returned true)
+// folds the unit and sets the count back to zero for the next launch.
+__device__ inline bool arrive(int* cnt, int parts) {
+    int old = 0;
+    if ((threadIdx.x & 63) == 0) old = __hip_atomic_fetch_add(cnt, 1, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+    old = __builtin_amdgcn_readfirstlane(old);
+    __atomic_signal_fence(__ATOMIC_SEQ_CST);
+    return old == parts - 1;
+}
+__device__ inline void reset_count(int* cnt) {
+    if ((threadIdx.x & 63) == 0) __hip_atomic_store(cnt, 0, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+}
+
 template <int G, int D, bool F16, bool MASK>
 struct DecodeWave {
-    static_assert(G >= 1 && G <= 16 && (D == 64 || D == 128 || D == 256), "decode shape");
-    static constexpr int NS = D / 32;    // head-dim slices, one MFMA each
-    static constexpr int DPL = D / 64;   // head-dim columns per lane in p @ v
-    static constexpr int kLdsFloats = G * 16 + 16;  // p rows, then the rescale factors
+    static_assert(G >= 1 && G <= 16 && (D == 64 || D == 128 || D == 256) && G * D <= 1024, "decode shape");
+    static constexpr int NS = D / 32;          // head-dim slices of the score MFMA
+    static constexpr int DV = D / 16;          // head-dim columns per lane in p @ v
+    static constexpr int NP = (G + 3) / 4;     // softmax passes of 4 query rows x 16 tokens
+    static constexpr int kLdsFloats = G * 16 + 16;  // scores / p rows, then the rescale factors
     // Chunk partial layout: m[G], l[G], o[G][D].
     static constexpr int kPartFloats = 2 * G + G * D;
 
     struct Page {
-        u32x4 k[NS];
-        u32 v[16 * (DPL == 4 ? 2 : 1)];  // DPL 1: one 16-bit value per token (low half)
-        f32x4v_t mask;
+        u32x4 k[NS];           // lane l: token l%16, head dims 32*j + 8*(l/16) .. +7
+        u32 v[4][DV / 2];      // lane l: tokens 4*(l/16) + i, head dims DV*(l%16) .. +DV-1
+        float mask;            // token l%16
     };
 
-    // kp: K page (token t at kp + t*ks, head dims contiguous); vp: V page
-    // (token t at vp + t*vs, head dims contiguous); mp: mask row (contiguous).
-    __device__ static void load_page(Page& pg, const u16* kp, i64 ks, const u16* vp, i64 vs, const float* mp) {
-        const int lane = threadIdx.x & 63, t = lane & 15, quad = lane >> 4;
-#pragma unroll
-        for (int j = 0; j < NS; ++j)
-            pg.k[j] = __builtin_nontemporal_load(reinterpret_cast<const u32x4*>(kp + t * ks + 32 * j + 8 * quad));
-#pragma unroll
-        for (int tt = 0; tt < 16; ++tt) {
-            if constexpr (DPL == 4) {
-                const u32x2 w = __builtin_nontemporal_load(reinterpret_cast<const u32x2*>(vp + tt * vs + 4 * lane));
-                pg.v[2 * tt] = w.x;
-                pg.v[2 * tt + 1] = w.y;
-            } else if constexpr (DPL == 2) {
-                pg.v[tt] = __builtin_nontemporal_load(reinterpret_cast<const u32*>(vp + tt * vs + 2 * lane));
-            } else {
-                pg.v[tt] = vp[tt * vs + lane];
-            }
-        }
-        if constexpr (MASK) pg.mask = *reinterpret_cast<const f32x4v_t*>(mp + 4 * quad);
+    // Per-lane byte offsets within a page, fixed for a launch: K (token t at
+    // t*ks elements, head dims contiguous), V (token t at t*vs), mask (token t).
+    struct Lanes {
+        u32 k, v, m;
+        u32 vrow;  // bytes between consecutive V tokens
+    };
+    __device__ static Lanes lanes(i64 ks, i64 vs) {
+        const int lane = threadIdx.x & 63, t = lane & 15, grp = lane >> 4;
+        Lanes r;
+        r.k = static_cast<u32>((t * ks + 8 * grp) * 2);
+        r.v = static_cast<u32>((4 * grp * vs + DV * t) * 2);
+        r.m = static_cast<u32>(t * 4);
+        r.vrow = static_cast<u32>(vs * 2);
+        return r;
     }
 
-    // Folds pages [p0, p1) into part; ptrs(p, kp, vp, mp) gives page p's bases.
-    template <class PagePtrs>
-    __device__ static void run(i64 p0, i64 p1, const u16* q, i64 qs, float scale, PagePtrs ptrs, i64 ks, i64 vs, float* lds,
-                               float* part) {
-        const int lane = threadIdx.x & 63, h = lane & 15, quad = lane >> 4;
-        u32x4 qb[NS];
+    // kp, vp, mp: wave-uniform page bases (buffer loads, streaming).
+    __device__ static void load_page(Page& pg, const u16* kp, const u16* vp, const float* mp, const Lanes& ln) {
+        const buf_rsrc rk = __builtin_amdgcn_make_buffer_rsrc(const_cast<u16*>(kp), 0, -1, 0x00020000);
+        const buf_rsrc rv = __builtin_amdgcn_make_buffer_rsrc(const_cast<u16*>(vp), 0, -1, 0x00020000);
+#pragma unroll
+        for (int j = 0; j < NS; ++j)
+            pg.k[j] = __builtin_bit_cast(u32x4, __builtin_amdgcn_raw_buffer_load_b128(rk, ln.k + 64 * j, 0, 2));
+#pragma unroll
+        for (int i = 0; i < 4; ++i) {
+            const u32 so = i * ln.vrow;
+            if constexpr (DV == 16) {
+                const u32x4 a = __builtin_bit_cast(u32x4, __builtin_amdgcn_raw_buffer_load_b128(rv, ln.v, so, 2));
+                const u32x4 b = __builtin_bit_cast(u32x4, __builtin_amdgcn_raw_buffer_load_b128(rv, ln.v + 16, so, 2));
+                pg.v[i][0] = a.x; pg.v[i][1] = a.y; pg.v[i][2] = a.z; pg.v[i][3] = a.w;
+                pg.v[i][4] = b.x; pg.v[i][5] = b.y; pg.v[i][6] = b.z; pg.v[i][7] = b.w;
+            } else if constexpr (DV == 8) {
+                const u32x4 a = __builtin_bit_cast(u32x4, __builtin_amdgcn_raw_buffer_load_b128(rv, ln.v, so, 2));
+                pg.v[i][0] = a.x; pg.v[i][1] = a.y; pg.v[i][2] = a.z; pg.v[i][3] = a.w;
+            } else {
+                const u32x2 a = __builtin_bit_cast(u32x2, __builtin_amdgcn_raw_buffer_load_b64(rv, ln.v, so, 2));
+                pg.v[i][0] = a.x; pg.v[i][1] = a.y;
+            }
+        }
+        if constexpr (MASK) {
+            const buf_rsrc rm = __builtin_amdgcn_make_buffer_rsrc(const_cast<float*>(mp), 0, -1, 0x00020000);
+            pg.mask = __uint_as_float(__builtin_amdgcn_raw_buffer_load_b32(rm, ln.m, 0, 2));
+        }
+    }
+
+    struct State {
+        float m[NP], l[NP];    // query row 4*pass + l/16, replicated over its 16 lanes
+        float o[G][DV];        // partial over this lane's 4 tokens of every page
+    };
+
+    __device__ static void step(State& st, const Page& pg, const u32x4* qa, float scale, float* lds) {
+        const int lane = threadIdx.x & 63, t = lane & 15, grp = lane >> 4;
+        // Scores: A = q (query rows), B = K^T; lane l holds rows 4*(l/16) + j, token l%16.
+        f32x4v_t acc = {0.0f, 0.0f, 0.0f, 0.0f};
+#pragma unroll
+        for (int j = 0; j < NS; ++j) acc = mfma_16x16x32<F16>(qa[j], pg.k[j], acc);
+#pragma unroll
+        for (int j = 0; j < 4; ++j) {
+            const int h = 4 * grp + j;
+            float sc = acc[j] * scale;
+            if constexpr (MASK) sc = sc - pg.mask;
+            if (h < G) lds[h * 16 + t] = sc;
+        }
+        wave_lds_fence();
+        // Online softmax, one (query row, token) per lane and pass.
+        auto fmax_ = [](float a, float b) { return fmaxf(a, b); };
+        auto fadd_ = [](float a, float b) { return a + b; };
+#pragma unroll
+        for (int r = 0; r < NP; ++r) {
+            const int h = 4 * r + grp;
+            const float sc = h < G ? lds[h * 16 + t] : 0.0f;
+            const float mn = fmaxf(st.m[r], row16_reduce(sc, fmax_));
+            const float a = expf(st.m[r] - mn);
+            const float e = expf(sc - mn);
+            st.l[r] = st.l[r] * a + row16_reduce(e, fadd_);
+            st.m[r] = mn;
+            if (h < G) {
+                lds[h * 16 + t] = e;
+                if (t == 0) lds[G * 16 + h] = a;
+            }
+        }
+        wave_lds_fence();
+        // o <- o * a + p @ v over this lane's 4 tokens (token by token, each
+        // unpacked v value used by every query row at once).
+        f32x4v_t p4[G];
+#pragma unroll
+        for (int g = 0; g < G; ++g) {
+            const float ag = lds[G * 16 + g];
+            p4[g] = *reinterpret_cast<const f32x4v_t*>(lds + g * 16 + 4 * grp);
+#pragma unroll
+            for (int e = 0; e < DV; ++e) st.o[g][e] = st.o[g][e] * ag;
+        }
+        wave_lds_fence();
+#pragma unroll
+        for (int i = 0; i < 4; ++i)
+#pragma unroll
+            for (int w = 0; w < DV / 2; ++w) {
+                const float lo = h16_lo<F16>(pg.v[i][w]), hi = h16_hi<F16>(pg.v[i][w]);
+#pragma unroll
+                for (int g = 0; g < G; ++g) {
+                    st.o[g][2 * w] = __builtin_fmaf(p4[g][i], lo, st.o[g][2 * w]);
+                    st.o[g][2 * w + 1] = __builtin_fmaf(p4[g][i], hi, st.o[g][2 * w + 1]);
+                }
+            }
+    }
+
+    // q rows as the MFMA's A operand (rows >= G are zero).
+    __device__ static void load_q(u32x4 (&qa)[NS], const u16* q, i64 qs) {
+        const int lane = threadIdx.x & 63, t = lane & 15, grp = lane >> 4;
 #pragma unroll
         for (int j = 0; j < NS; ++j) {
-            qb[j] = u32x4{0u, 0u, 0u, 0u};
-            if (h < G) qb[j] = *reinterpret_cast<const u32x4*>(q + h * qs + 32 * j + 8 * quad);
+            qa[j] = u32x4{0u, 0u, 0u, 0u};
+            if (t < G) qa[j] = *reinterpret_cast<const u32x4*>(q + t * qs + 32 * j + 8 * grp);
         }
-        float m = -__builtin_inff(), l = 0.0f;
-        float o[G][DPL];
+    }
+
+    __device__ static void init(State& st) {
+#pragma unroll
+        for (int r = 0; r < NP; ++r) {
+            st.m[r] = -__builtin_inff();
+            st.l[r] = 0.0f;
+        }
 #pragma unroll
         for (int g = 0; g < G; ++g)
 #pragma unroll
-            for (int j = 0; j < DPL; ++j) o[g][j] = 0.0f;
-        Page cur, nxt;
+            for (int e = 0; e < DV; ++e) st.o[g][e] = 0.0f;
+    }
+
+    // Folds pages [p0, p1) (p0 < p1) into st; ptrs(p, kp, vp, mp) gives page
+    // p's bases.  Two page buffers alternate; each prefetch is unconditional
+    // (the page index is clamped to p1-1) so the wait before each step counts
+    // one page of loads.
+    template <class PagePtrs>
+    __device__ static void fold(State& st, i64 p0, i64 p1, const u32x4 (&qa)[NS], float scale, PagePtrs ptrs, i64 ks,
+                                i64 vs, float* lds) {
+        const Lanes ln = lanes(ks, vs);
+        Page pa, pb;
         const u16 *kp, *vp;
         const float* mp;
         ptrs(p0, kp, vp, mp);
-        load_page(cur, kp, ks, vp, vs, mp);
-        for (i64 p = p0; p < p1; ++p) {
-            if (p + 1 < p1) {
-                ptrs(p + 1, kp, vp, mp);
-                load_page(nxt, kp, ks, vp, vs, mp);
-            }
-            f32x4v_t acc = {0.0f, 0.0f, 0.0f, 0.0f};
+        load_page(pa, kp, vp, mp, ln);
+        for (i64 p = p0; p < p1; p += 2) {
+            ptrs(p + 1 < p1 ? p + 1 : p1 - 1, kp, vp, mp);
+            load_page(pb, kp, vp, mp, ln);
+            step(st, pa, qa, scale, lds);
+            if (p + 1 >= p1) break;
+            ptrs(p + 2 < p1 ? p + 2 : p1 - 1, kp, vp, mp);
+            load_page(pa, kp, vp, mp, ln);
+            step(st, pb, qa, scale, lds);
+        }
+    }
+
+    // Writes st as a partial (m[G], l[G], o[G][D]) after summing the four
+    // token groups (lanes l, l^16, l^32, l^48).
+    __device__ static void store(const State& st, float* part) {
+        const int lane = threadIdx.x & 63, t = lane & 15, grp = lane >> 4;
+        if (t == 0) {
 #pragma unroll
-            for (int j = 0; j < NS; ++j) acc = mfma_16x16x32<F16>(cur.k[j], qb[j], acc);
-            float sc[4];
-#pragma unroll
-            for (int i = 0; i < 4; ++i) {
-                sc[i] = acc[i] * scale;
-                if constexpr (MASK) sc[i] = sc[i] - cur.mask[i];
-            }
-            float pm = fmaxf(fmaxf(sc[0], sc[1]), fmaxf(sc[2], sc[3]));
-            pm = fmaxf(pm, __shfl_xor(pm, 16));
-            pm = fmaxf(pm, __shfl_xor(pm, 32));
-            const float mn = fmaxf(m, pm);
-            const float a = expf(m - mn);
-            float e[4];
-#pragma unroll
-            for (int i = 0; i < 4; ++i) e[i] = expf(sc[i] - mn);
-            float ps = ((e[0] + e[1]) + e[2]) + e[3];
-            ps = ps + __shfl_xor(ps, 16);
-            ps = ps + __shfl_xor(ps, 32);
-            l = l * a + ps;
-            m = mn;
-            if (h < G) {
-                *reinterpret_cast<f32x4v_t*>(lds + h * 16 + 4 * quad) = f32x4v_t{e[0], e[1], e[2], e[3]};
-                if (quad == 0) lds[G * 16 + h] = a;
-            }
-            wave_lds_fence();
-            float pv[G][DPL];
-#pragma unroll
-            for (int g = 0; g < G; ++g)
-#pragma unroll
-                for (int j = 0; j < DPL; ++j) pv[g][j] = 0.0f;
-#pragma unroll
-            for (int t4 = 0; t4 < 4; ++t4) {
-                f32x4v_t pg4[G];
-#pragma unroll
-                for (int g = 0; g < G; ++g) pg4[g] = *reinterpret_cast<const f32x4v_t*>(lds + g * 16 + 4 * t4);
-#pragma unroll
-                for (int i = 0; i < 4; ++i) {
-                    const int tt = 4 * t4 + i;
-                    float vv[DPL];
-                    if constexpr (DPL == 4) {
-                        vv[0] = h16_lo<F16>(cur.v[2 * tt]);
-                        vv[1] = h16_hi<F16>(cur.v[2 * tt]);
-                        vv[2] = h16_lo<F16>(cur.v[2 * tt + 1]);
-                        vv[3] = h16_hi<F16>(cur.v[2 * tt + 1]);
-                    } else if constexpr (DPL == 2) {
-                        vv[0] = h16_lo<F16>(cur.v[tt]);
-                        vv[1] = h16_hi<F16>(cur.v[tt]);
-                    } else {
-                        vv[0] = h16_lo<F16>(cur.v[tt]);
-                    }
-#pragma unroll
-                    for (int g = 0; g < G; ++g)
-#pragma unroll
-                        for (int j = 0; j < DPL; ++j) pv[g][j] = pv[g][j] + pg4[g][i] * vv[j];
+            for (int r = 0; r < NP; ++r) {
+                const int h = 4 * r + grp;
+                if (h < G) {
+                    coherent_store(part + h, st.m[r]);
+                    coherent_store(part + G + h, st.l[r]);
                 }
             }
-#pragma unroll
-            for (int g = 0; g < G; ++g) {
-                const float ag = lds[G * 16 + g];
-#pragma unroll
-                for (int j = 0; j < DPL; ++j) o[g][j] = o[g][j] * ag + pv[g][j];
-            }
-            wave_lds_fence();
-            cur = nxt;
-        }
-        if (quad == 0 && h < G) {
-            part[h] = m;
-            part[G + h] = l;
         }
 #pragma unroll
         for (int g = 0; g < G; ++g)
 #pragma unroll
-            for (int j = 0; j < DPL; ++j) part[2 * G + g * D + DPL * lane + j] = o[g][j];
+            for (int e = 0; e < DV; ++e) {
+                float x = st.o[g][e];
+                x = x + __shfl_xor(x, 16);
+                x = x + __shfl_xor(x, 32);
+                if (grp == 0) coherent_store(part + 2 * G + g * D + DV * t + e, x);
+            }
     }
 };
 
-// Folds the chunk partials of one unit, in chunk order, into its (m, l, o)
-// accumulators: m' = max(m, mc), l' = l*e^(m-m') + lc*e^(mc-m'), o likewise.
+// Balanced split of a decode launch over the resident waves: the units' page
+// counts are concatenated in unit order (prefix pre[0..U], pre[U] = T pages in
+// all) and wave w of W folds global pages [w*T/W, (w+1)*T/W), with W at
+// most T so that every wave holds at least one page.  A wave writes
+// one partial per unit it touches, into slot unit + w (slots are distinct
+// because the first wave of unit u+1 is at least the last wave of unit u);
+// unit u's partials are the consecutive slots u + wave_of(pre[u]) ..
+// u + wave_of(pre[u+1]-1).
+struct DecodeSplit {
+    static constexpr int kMaxUnits = 4096;  // prefix held in LDS by every block
+    // Wave holding global page p: the largest w with w*T/W <= p.
+    __device__ static i64 wave_of(i64 p, i64 T, i64 W) { return ((p + 1) * W - 1) / T; }
+    // Largest u in [0, U) with pre[u] <= s, for 0 <= s < pre[U] (a non-empty unit).
+    __device__ static int unit_of(const int* pre, int U, i64 s) {
+        int lo = 0, hi = U;
+        while (hi - lo > 1) {
+            const int mid = (lo + hi) >> 1;
+            if (pre[mid] <= s) lo = mid;
+            else hi = mid;
+        }
+        return lo;
+    }
+};
+
 template <int G, int D>
 struct DecodeCombine {
     static constexpr int DPL = D / 64;
+    static constexpr int CB = 2;  // partials loaded together
+    __device__ static void fold(float (&mm)[G], float (&ll)[G], float (&oo)[G][DPL], const float* mc, const float* lc,
+                                const float (*oc)[DPL]) {
+#pragma unroll
+        for (int g = 0; g < G; ++g) {
+            const float mn = fmaxf(mm[g], mc[g]);
+            const float a = expf(mm[g] - mn), b = expf(mc[g] - mn);
+            ll[g] = ll[g] * a + lc[g] * b;
+#pragma unroll
+            for (int j = 0; j < DPL; ++j) oo[g][j] = oo[g][j] * a + oc[g][j] * b;
+            mm[g] = mn;
+        }
+    }
     __device__ static void run(i64 nch, const float* part, i64 pstride, float* m, i64 ms3, float* l, i64 ls3, float* o,
                                i64 os3, i64 os4) {
         const int lane = threadIdx.x & 63;
@@ -702,18 +839,34 @@ struct DecodeCombine {
 #pragma unroll
             for (int j = 0; j < DPL; ++j) oo[g][j] = o[g * os3 + (DPL * lane + j) * os4];
         }
-        for (i64 c = 0; c < nch; ++c) {
+        i64 c = 0;
+        for (; c + CB <= nch; c += CB) {
+            float mc[CB][G], lc[CB][G], oc[CB][G][DPL];
+#pragma unroll
+            for (int b = 0; b < CB; ++b) {
+                const float* pc = part + (c + b) * pstride;
+#pragma unroll
+                for (int g = 0; g < G; ++g) {
+                    mc[b][g] = coherent_load(pc + g);
+                    lc[b][g] = coherent_load(pc + G + g);
+#pragma unroll
+                    for (int j = 0; j < DPL; ++j) oc[b][g][j] = coherent_load(pc + 2 * G + g * D + DPL * lane + j);
+                }
+            }
+#pragma unroll
+            for (int b = 0; b < CB; ++b) fold(mm, ll, oo, mc[b], lc[b], oc[b]);
+        }
+        for (; c < nch; ++c) {
             const float* pc = part + c * pstride;
+            float mc[G], lc[G], oc[G][DPL];
 #pragma unroll
             for (int g = 0; g < G; ++g) {
-                const float mc = pc[g], lc = pc[G + g];
-                const float mn = fmaxf(mm[g], mc);
-                const float a = expf(mm[g] - mn), b = expf(mc - mn);
-                ll[g] = ll[g] * a + lc * b;
+                mc[g] = coherent_load(pc + g);
+                lc[g] = coherent_load(pc + G + g);
 #pragma unroll
-                for (int j = 0; j < DPL; ++j) oo[g][j] = oo[g][j] * a + pc[2 * G + g * D + DPL * lane + j] * b;
-                mm[g] = mn;
+                for (int j = 0; j < DPL; ++j) oc[g][j] = coherent_load(pc + 2 * G + g * D + DPL * lane + j);
             }
+            fold(mm, ll, oo, mc, lc, oc);
         }
 #pragma unroll
         for (int g = 0; g < G; ++g) {

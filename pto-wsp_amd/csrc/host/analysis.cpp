@@ -296,8 +296,9 @@ DecodeInfo classify_decode(const KernelDef& k, const KernelAnalysis& a) {
         const ValueInfo* mk = vi(mask_p);
         if (mk->dtype != DType::F32 || mk->rows != 1 || mk->cols != PG) return info;
     }
-    // Device template shapes: 16-token pages, up to 16 query rows, head dim 64 / 128 / 256.
-    if (PG != 16 || G < 1 || G > 16 || (D != 64 && D != 128 && D != 256)) return info;
+    // Device template shapes: 16-token pages, up to 16 query rows, head dim 64 / 128 / 256,
+    // at most 64 partial outputs per lane (G * D / 16).
+    if (PG != 16 || G < 1 || G > 16 || (D != 64 && D != 128 && D != 256) || G * D > 1024) return info;
     info.ok = true;
     info.q = a.tensor_ordinal[pq];
     info.kt = a.tensor_ordinal[pkt];

@@ -538,12 +538,18 @@ EmittedKernel emit_gemm(const Module& m, const KernelAnalysis& a, const LaunchSp
 }
 
 // ---------------------------------------------------------------------------
-// Decode programs (online softmax over pages, split into chunks)
+// Decode programs (online softmax over pages, balanced over resident waves)
 // ---------------------------------------------------------------------------
-// Launch arguments beyond the kernel's tensors: base[ntens] is the chunk
-// partial scratch; scal[kMaxScalars-1] is the number of chunks per unit and
-// scal[kMaxScalars-2] the declared maximum page count (larger extents raise
-// error 3 and are cut to the chunk capacity).
+// One kernel, launched with one block per resident slot.  Every block first
+// scans the units' page counts into LDS; then wave w of W = min(resident
+// waves, T) folds global pages [w*T/W, (w+1)*T/W) (DecodeSplit) and writes
+// one partial per unit it touches.  The wave that completes a unit (the only one, or the last to
+// arrive on the unit's counter) folds the unit's partials in page order into
+// the accumulators and resets the counter.  Launch arguments beyond the
+// kernel's tensors: base[ntens] is the scratch (int32 counters, one per unit,
+// zero between launches, then the partials);
+// scal[kMaxScalars-1] is the declared maximum page count (larger extents
+// raise error 3 and are cut to it).
 EmittedKernel emit_decode(const Module& m, const KernelAnalysis& a, const LaunchSpec& L, const EmitSpec& spec) {
     (void)m;
     const KernelDef& k = *a.def;
@@ -551,7 +557,6 @@ EmittedKernel emit_decode(const Module& m, const KernelAnalysis& a, const Launch
     const int ng = static_cast<int>(L.grid.size());
     const int nvars = ng + 1;
     const int ntens = static_cast<int>(a.tensor_param_index.size());
-    const int C = spec.decode_chunk;
     std::vector<int> first_term(ntens, 0);
     for (int p = 1; p < ntens; ++p) first_term[p] = first_term[p - 1] + spec.indirect_count[p - 1];
     auto nterms = [&](int p) { return spec.indirect_count[p]; };
@@ -564,98 +569,182 @@ EmittedKernel emit_decode(const Module& m, const KernelAnalysis& a, const Launch
     EmittedKernel ek;
     ek.threads = 256;
     ek.row_program = false;
-    ek.combine_entry = "ptowsp_combine";
     ek.part_floats = 2 * d.g + d.g * d.d;
     std::ostringstream o;
     o << "#include \"ptowsp_device.h\"\nusing namespace ptowsp;\n";
     o << "// decode program: kernel " << k.name << ", " << d.g << " query rows, head dim " << d.d << (d.f16 ? " f16" : " bf16")
-      << (d.mask >= 0 ? ", masked" : "") << ", chunks of " << C << " pages\n";
-    // Unit decode + extent, shared by both kernels.
-    auto unit_prologue = [&](const std::string& unit) {
-        o << "  i64 vars[" << nvars << "];\n";
-        o << "  { i64 q_ = " << unit << ";\n";
-        for (int v = ng - 1; v >= 1; --v) o << "    vars[" << v << "] = q_ % A.ext[" << v << "]; q_ /= A.ext[" << v << "];\n";
-        if (ng > 0) o << "    vars[0] = q_;";
-        o << " }\n";
-        o << "  vars[" << ng << "] = 0;\n";
-        const int term = spec.inner_dyn_term.empty() ? -1 : spec.inner_dyn_term[0];
-        if (term >= 0) o << "  i64 npg = indirect_index(A, " << term << ", vars, " << ng << ");\n";
-        else o << "  i64 npg = A.ext[" << ng << "];\n";
-        o << "  if (npg < 0) npg = 0;\n";
+      << (d.mask >= 0 ? ", masked" : "") << ", pages balanced over the resident waves\n";
+    auto decode_vars = [&](const std::string& unit, const std::string& ind) {
+        if (ng == 0) return;
+        o << ind << "{ i64 q_ = " << unit << ";\n";
+        for (int v = ng - 1; v >= 1; --v)
+            o << ind << "  vars[" << v << "] = q_ % A.ext[" << v << "]; q_ /= A.ext[" << v << "];\n";
+        o << ind << "  vars[0] = q_; }\n";
     };
     auto ptr = [&](int p, const std::string& type, int esize) {
         return "reinterpret_cast<" + type + ">(A.base[" + std::to_string(p) + "] + (" +
                offset_expr(p, nvars, first_term[p], nterms(p)) + ") * " + std::to_string(esize) + ")";
     };
-    // Chunk kernel.
-    o << "extern \"C\" __global__ void __launch_bounds__(256) ptowsp_entry(const LaunchArgs A) {\n";
-    o << "  typedef " << tmpl << " DW;\n";
-    o << "  __shared__ __attribute__((aligned(16))) float lds_all[4][DW::kLdsFloats];\n";
-    o << "  const int wave = __builtin_amdgcn_readfirstlane(static_cast<int>(threadIdx.x >> 6));\n";
-    o << "  const i64 wid = (i64)blockIdx.x * 4 + wave;\n";
-    o << "  const i64 mc = (i64)A.scal[" << kMaxScalars - 1 << "];\n";
-    o << "  const i64 unit = wid / mc, chunk = wid % mc;\n";
-    o << "  if (unit >= A.ntasks) return;\n";
-    unit_prologue("unit");
-    o << "  if (npg > mc * " << C << ") npg = mc * " << C << ";\n";
-    o << "  const i64 p0 = chunk * " << C << ";\n";
-    o << "  if (p0 >= npg) return;\n";
-    o << "  const i64 p1 = p0 + " << C << " < npg ? p0 + " << C << " : npg;\n";
-    auto unit_check = [&](int p, int rows, int cols) {
-        o << "  { const i64 o_ = " << offset_expr(p, nvars, first_term[p], nterms(p)) << ";\n";
-        o << "    if (o_ < 0 || o_ + (i64)" << rows - 1 << " * A.s3[" << p << "] + (i64)" << cols - 1 << " * A.s4[" << p
-          << "] >= A.span[" << p << "]) { if ((threadIdx.x & 63) == 0) *A.err = 2; return; } }\n";
+    // Bounds check of a unit's fixed tile (q, m, l, o): sets `flag` and the
+    // error code 2 when it falls outside its tensor.
+    auto unit_check = [&](int p, int rows, int cols, const std::string& flag) {
+        o << "      { const i64 o_ = " << offset_expr(p, nvars, first_term[p], nterms(p)) << ";\n";
+        o << "        if (o_ < 0 || o_ + (i64)" << rows - 1 << " * A.s3[" << p << "] + (i64)" << cols - 1 << " * A.s4[" << p
+          << "] >= A.span[" << p << "]) { " << flag << " = true; if (lane == 0) *A.err = 2; } }\n";
     };
-    unit_check(d.q, d.g, d.d);
-    o << "  const u16* qp = " << ptr(d.q, "const u16*", 2) << ";\n";
-    // Page bases with a bounds check; an out-of-range page raises the error flag
-    // and reads the tensor's first page instead.
+    // Three waves per SIMD fit the two page buffers without spills for
+    // head dims up to 128 and G*D up to 512; larger shapes keep the
+    // compiler's choice.
+    const bool occ3 = d.d <= 128 && d.g * d.d <= 512;
+    o << "extern \"C\" __global__ void __launch_bounds__(256) "
+      << (occ3 ? "__attribute__((amdgpu_waves_per_eu(3))) " : "") << "ptowsp_entry(const LaunchArgs A) {\n";
+    o << "  typedef " << tmpl << " DW;\n";
+    o << "  static_assert(DecodeSplit::kMaxUnits == " << kDecodeMaxUnits << ", \"unit limit\");\n";
+    o << "  __shared__ __attribute__((aligned(16))) float lds_all[4][DW::kLdsFloats];\n";
+    o << "  __shared__ int pre[DecodeSplit::kMaxUnits + 1];\n";
+    o << "  __shared__ int wsum[4];\n";
+    o << "  const int tid = threadIdx.x, lane = tid & 63;\n";
+    o << "  const int wave = __builtin_amdgcn_readfirstlane(tid >> 6);\n";
+    o << "  const int U = static_cast<int>(A.ntasks);\n";
+    o << "  const i64 maxp = (i64)A.scal[" << kMaxScalars - 1 << "];\n";
+    o << "  i64 vars[" << nvars << "];\n";
+    // Prefix of the page counts: thread t owns units t*per .. t*per+per-1.
+    o << "  {\n";
+    o << "    const int per = (U + 255) >> 8, u0 = tid * per;\n";
+    o << "    int n_[DecodeSplit::kMaxUnits / 256];\n";
+    o << "    int run = 0;\n";
+    o << "#pragma unroll\n";
+    o << "    for (int i = 0; i < DecodeSplit::kMaxUnits / 256; ++i) {\n";
+    o << "      n_[i] = 0;\n";
+    o << "      if (i < per && u0 + i < U) {\n";
+    decode_vars("u0 + i", "        ");
+    o << "        vars[" << ng << "] = 0;\n";
+    {
+        const int term = spec.inner_dyn_term.empty() ? -1 : spec.inner_dyn_term[0];
+        if (term >= 0) o << "        i64 npg = indirect_index(A, " << term << ", vars, " << ng << ");\n";
+        else o << "        i64 npg = A.ext[" << ng << "];\n";
+    }
+    o << "        if (npg < 0) npg = 0;\n";
+    o << "        if (npg > maxp) { npg = maxp; if (blockIdx.x == 0) *A.err = 3; }\n";
+    o << "        n_[i] = static_cast<int>(npg);\n";
+    o << "        run += n_[i];\n";
+    o << "      }\n";
+    o << "    }\n";
+    o << "    int x = run;\n";
+    o << "#pragma unroll\n";
+    o << "    for (int d_ = 1; d_ < 64; d_ <<= 1) { const int y = __shfl_up(x, d_); if (lane >= d_) x += y; }\n";
+    o << "    if (lane == 63) wsum[wave] = x;\n";
+    o << "    __syncthreads();\n";
+    o << "    int base = x - run;\n";
+    o << "    for (int j = 0; j < wave; ++j) base += wsum[j];\n";
+    o << "#pragma unroll\n";
+    o << "    for (int i = 0; i < DecodeSplit::kMaxUnits / 256; ++i)\n";
+    o << "      if (i < per && u0 + i < U) { pre[u0 + i] = base; base += n_[i]; }\n";
+    o << "    if (tid == 0) pre[U] = wsum[0] + wsum[1] + wsum[2] + wsum[3];\n";
+    o << "    __syncthreads();\n";
+    o << "  }\n";
+    // Values read from LDS are wave-uniform: readfirstlane keeps the page
+    // loop's control and addresses in scalar registers.
+    o << "  const i64 T = __builtin_amdgcn_readfirstlane(pre[U]);\n";
+    // Active waves: at most one per page, so that every active wave holds at
+    // least one page and a unit's partials fill consecutive slots.
+    o << "  const i64 W = (i64)gridDim.x * 4 < T ? (i64)gridDim.x * 4 : T, w = (i64)blockIdx.x * 4 + wave;\n";
+    o << "  if (w >= W) return;\n";
+    o << "  i64 s = w * T / W;\n";
+    o << "  const i64 b = (w + 1) * T / W;\n";
+    o << "  if (s >= b) return;\n";
+    o << "  int* cnt = reinterpret_cast<int*>(A.base[" << ntens << "]);\n";
+    o << "  float* partials = reinterpret_cast<float*>(A.base[" << ntens << "] + DecodeSplit::kMaxUnits * 4);\n";
+    o << "  float* lds = lds_all[wave];\n";
+    o << "  int u = __builtin_amdgcn_readfirstlane(DecodeSplit::unit_of(pre, U, s));\n";
+    o << "  for (;;) {\n";
+    o << "    const i64 su = __builtin_amdgcn_readfirstlane(pre[u]), eu = __builtin_amdgcn_readfirstlane(pre[u + 1]);\n";
+    o << "    const i64 e = eu < b ? eu : b;\n";
+    decode_vars("u", "    ");
+    o << "    vars[" << ng << "] = 0;\n";
+    o << "    {\n";
+    o << "      bool bad = false;\n";
+    unit_check(d.q, d.g, d.d, "bad");
+    o << "      DW::State st;\n";
+    o << "      DW::init(st);\n";
+    o << "      if (!bad) {\n";
+    o << "        u32x4 qa[DW::NS];\n";
+    o << "        DW::load_q(qa, " << ptr(d.q, "const u16*", 2) << ", A.s3[" << d.q << "]);\n";
+    // Sub-runs of at most 64 pages: lane i holds page c0+i's indirect indices.
+    std::vector<int> page_terms;
+    for (int p : {d.kt, d.v, d.mask})
+        if (p >= 0)
+            for (int t = 0; t < nterms(p); ++t) page_terms.push_back(first_term[p] + t);
+    o << "        for (i64 c0 = s - su; c0 < e - su; c0 += 64) {\n";
+    o << "          const i64 c1 = c0 + 64 < e - su ? c0 + 64 : e - su;\n";
+    if (!page_terms.empty()) {
+        o << "          i64 vl[" << nvars << "];\n";
+        o << "          for (int i = 0; i < " << nvars << "; ++i) vl[i] = vars[i];\n";
+        o << "          { const i64 pl = c0 + lane; vl[" << ng << "] = pl < c1 ? pl : c1 - 1; }\n";
+        for (int kk : page_terms)
+            o << "          const int iv" << kk << " = static_cast<int>(indirect_value(A, " << kk << ", vl, " << nvars << "));\n";
+    }
+    // Page bases with a bounds check; an out-of-range page raises the error
+    // flag and reads the tensor's first page instead.
+    auto page_off = [&](int p) {
+        std::ostringstream e;
+        e << "(i64)0";
+        for (int v = 0; v < nvars; ++v) e << " + A.coef[" << p << "][" << v << "] * vars[" << v << "]";
+        for (int t = 0; t < nterms(p); ++t) {
+            const int kk = first_term[p] + t;
+            e << " + A.ind[" << kk << "].stride * (i64)__builtin_amdgcn_readlane(iv" << kk << ", static_cast<int>(pg - c0))";
+        }
+        return e.str();
+    };
     auto checked = [&](int p, int rows, int cols, const std::string& var) {
-        o << "    i64 " << var << " = " << offset_expr(p, nvars, first_term[p], nterms(p)) << ";\n";
-        o << "    if (" << var << " < 0 || " << var << " + (i64)" << rows - 1 << " * A.s3[" << p << "] + (i64)" << cols - 1
+        o << "            i64 " << var << " = " << page_off(p) << ";\n";
+        o << "            if (" << var << " < 0 || " << var << " + (i64)" << rows - 1 << " * A.s3[" << p << "] + (i64)" << cols - 1
           << " * A.s4[" << p << "] >= A.span[" << p << "]) { *A.err = 2; " << var << " = 0; }\n";
     };
-    o << "  auto ptrs = [&](i64 pg, const u16*& kp, const u16*& vp, const float*& mp) {\n";
-    o << "    vars[" << ng << "] = pg;\n";
+    o << "          auto ptrs = [&](i64 pg, const u16*& kp, const u16*& vp, const float*& mp) {\n";
+    o << "            vars[" << ng << "] = pg;\n";
     checked(d.kt, d.d, d.pg, "ok");
     checked(d.v, d.pg, d.d, "ov");
-    o << "    kp = reinterpret_cast<const u16*>(A.base[" << d.kt << "] + ok * 2);\n";
-    o << "    vp = reinterpret_cast<const u16*>(A.base[" << d.v << "] + ov * 2);\n";
+    o << "            kp = reinterpret_cast<const u16*>(A.base[" << d.kt << "] + ok * 2);\n";
+    o << "            vp = reinterpret_cast<const u16*>(A.base[" << d.v << "] + ov * 2);\n";
     if (d.mask >= 0) {
         checked(d.mask, 1, d.pg, "om");
-        o << "    mp = reinterpret_cast<const float*>(A.base[" << d.mask << "] + om * 4);\n";
+        o << "            mp = reinterpret_cast<const float*>(A.base[" << d.mask << "] + om * 4);\n";
     } else {
-        o << "    mp = nullptr;\n";
+        o << "            mp = nullptr;\n";
     }
-    o << "  };\n";
-    o << "  float* part = reinterpret_cast<float*>(A.base[" << ntens << "]) + (unit * mc + chunk) * DW::kPartFloats;\n";
-    o << "  DW::run(p0, p1, qp, A.s3[" << d.q << "], " << scale.str() << ", ptrs, A.s4[" << d.kt << "], A.s3[" << d.v
-      << "], lds_all[wave], part);\n";
-    o << "}\n\n";
-    // Combine kernel: one wave per unit.
-    o << "extern \"C\" __global__ void __launch_bounds__(256) ptowsp_combine(const LaunchArgs A) {\n";
-    o << "  const int wave = __builtin_amdgcn_readfirstlane(static_cast<int>(threadIdx.x >> 6));\n";
-    o << "  const i64 unit = (i64)blockIdx.x * 4 + wave;\n";
-    o << "  if (unit >= A.ntasks) return;\n";
-    o << "  const i64 mc = (i64)A.scal[" << kMaxScalars - 1 << "];\n";
-    unit_prologue("unit");
-    o << "  if (npg > (i64)A.scal[" << kMaxScalars - 2 << "]) { if ((threadIdx.x & 63) == 0) *A.err = 3; }\n";
-    o << "  if (npg > mc * " << C << ") npg = mc * " << C << ";\n";
-    o << "  const i64 nch = (npg + " << C - 1 << ") / " << C << ";\n";
-    unit_check(d.m, d.g, 1);
-    unit_check(d.l, d.g, 1);
-    unit_check(d.o, d.g, d.d);
-    o << "  float* mp = " << ptr(d.m, "float*", 4) << ";\n";
-    o << "  float* lp = " << ptr(d.l, "float*", 4) << ";\n";
-    o << "  float* op = " << ptr(d.o, "float*", 4) << ";\n";
-    o << "  const float* part = reinterpret_cast<const float*>(A.base[" << ntens << "]) + unit * mc * "
-      << ek.part_floats << ";\n";
-    o << "  DecodeCombine<" << d.g << ", " << d.d << ">::run(nch, part, " << ek.part_floats << ", mp, A.s3[" << d.m
-      << "], lp, A.s3[" << d.l << "], op, A.s3[" << d.o << "], A.s4[" << d.o << "]);\n";
+    o << "          };\n";
+    o << "          DW::fold(st, c0, c1, qa, " << scale.str() << ", ptrs, A.s4[" << d.kt << "], A.s3[" << d.v << "], lds);\n";
+    o << "        }\n";
+    o << "        vars[" << ng << "] = 0;\n";
+    o << "      }\n";
+    // Partial, then the unit's completion.
+    o << "      const i64 wf = DecodeSplit::wave_of(su, T, W), wl = DecodeSplit::wave_of(eu - 1, T, W);\n";
+    o << "      const int parts = static_cast<int>(wl - wf + 1);\n";
+    o << "      DW::store(st, partials + (u + w) * DW::kPartFloats);\n";
+    o << "      publish();\n";
+    o << "      const bool last = parts == 1 || arrive(cnt + u, parts);\n";
+    o << "      if (last) {\n";
+    o << "        bool bad_acc = false;\n";
+    unit_check(d.m, d.g, 1, "bad_acc");
+    unit_check(d.l, d.g, 1, "bad_acc");
+    unit_check(d.o, d.g, d.d, "bad_acc");
+    o << "        if (!bad_acc)\n";
+    o << "          DecodeCombine<" << d.g << ", " << d.d << ">::run(parts, partials + (u + wf) * DW::kPartFloats, DW::kPartFloats, "
+      << ptr(d.m, "float*", 4) << ", A.s3[" << d.m << "], " << ptr(d.l, "float*", 4) << ", A.s3[" << d.l << "], "
+      << ptr(d.o, "float*", 4) << ", A.s3[" << d.o << "], A.s4[" << d.o << "]);\n";
+    o << "        if (parts > 1) reset_count(cnt + u);\n";
+    o << "      }\n";
+    o << "    }\n";
+    o << "    s = e;\n";
+    o << "    if (s >= b) break;\n";
+    o << "    ++u;\n";
+    o << "    while (__builtin_amdgcn_readfirstlane(pre[u + 1]) <= s) ++u;\n";
+    o << "  }\n";
     o << "}\n";
     ek.source = o.str();
     ek.entry = "ptowsp_entry";
-    ek.lds_bytes = static_cast<size_t>(4 * (d.g * 16 + 16) * 4);
+    ek.lds_bytes = static_cast<size_t>(4 * (d.g * 16 + 16) * 4 + (kDecodeMaxUnits + 1 + 4) * 4);
     return ek;
 }
 

@@ -28,11 +28,14 @@ struct EmitSpec {
     // GEMM: grid variables whose neighbouring tasks are merged into one
     // workgroup block (factor 2 along rows / columns of C), or -1.
     int gemm_vm = -1, gemm_vn = -1;
-    // Decode family (online softmax over pages): split the in-kernel page
-    // loop into chunks of `decode_chunk` pages folded by separate waves.
+    // Decode family (online softmax over pages): the in-kernel page loop of
+    // every unit is split over the resident waves.
     bool decode = false;
-    int decode_chunk = 16;
 };
+
+// Units (grid tasks) of one decode launch at most: every block holds their
+// page-count prefix in LDS (DecodeSplit::kMaxUnits on the device).
+constexpr int kDecodeMaxUnits = 4096;
 
 // Waves of a GEMM block: 2 along M, 4 along N for 256-wide blocks, else 2.
 inline int gemm_waves_n(int bn) { return bn >= 256 ? 4 : 2; }
@@ -46,8 +49,7 @@ struct EmittedKernel {
     int waves_per_block = 4;
     bool row_program = false;
     int tasks_per_block = 1;    // GEMM: tasks merged into one workgroup
-    std::string combine_entry;  // decode: second kernel folding the chunk partials
-    int part_floats = 0;        // decode: floats per chunk partial
+    int part_floats = 0;        // decode: floats per partial (m, l, o of one unit)
     size_t lds_bytes = 0;
 };
 

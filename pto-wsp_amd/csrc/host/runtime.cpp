@@ -10,6 +10,7 @@
 #include <map>
 #include <set>
 #include <memory>
+#include <mutex>
 #include <sstream>
 #include <string>
 #include <vector>
@@ -84,7 +85,7 @@ struct ptowsp_program {
     CycleResult cycles;
     bool cycles_valid = false;
     std::string precompiled_source;
-    void* scratch = nullptr;  // decode: chunk partials
+    void* scratch = nullptr;  // decode: unit counters and partials
     size_t scratch_bytes = 0;
 
     ~ptowsp_program() {
@@ -157,6 +158,7 @@ struct RunEnv {
     RuntimeContext* ctx;
     std::vector<TensorState> ts;
     std::vector<std::pair<std::string, int64_t>> host_vars;
+    std::map<int, std::vector<int32_t>> idx_host;  // device index tensors read on the host, copied once per run
 };
 
 int64_t axis_extent(RunEnv& E, const Axis& a) {
@@ -177,12 +179,22 @@ int64_t axis_extent(RunEnv& E, const Axis& a) {
 }
 
 // Reads one int32 element of an index tensor (host or device resident).
+// Host view of a device-resident i32 index tensor, copied on first use in a run.
+const std::vector<int32_t>& index_host_copy(RunEnv& E, int tid) {
+    auto it = E.idx_host.find(tid);
+    if (it != E.idx_host.end()) return it->second;
+    const TensorState& t = E.ts[tid];
+    std::vector<int32_t> v(static_cast<size_t>(std::max<int64_t>(t.span, 0)));
+    if (!v.empty()) check(hipMemcpy(v.data(), t.dev, v.size() * 4, hipMemcpyDeviceToHost), "hipMemcpy(index tensor)");
+    return E.idx_host.emplace(tid, std::move(v)).first->second;
+}
+
 int64_t read_index_elem(RunEnv& E, int tid, int64_t off) {
     const TensorState& t = E.ts[tid];
     if (off < 0 || off >= t.span) throw std::runtime_error("index tensor element out of range");
     int32_t v = 0;
     if (t.host) std::memcpy(&v, t.host + off * 4, 4);
-    else check(hipMemcpy(&v, t.dev + off * 4, 4, hipMemcpyDeviceToHost), "hipMemcpy(index)");
+    else v = index_host_copy(E, tid)[static_cast<size_t>(off)];
     return v;
 }
 
@@ -404,19 +416,25 @@ bool gemm_allowed(const KernelAnalysis& a, const LaunchSpec& L, const LaunchArgs
     return true;
 }
 
-// Chooses the split-chunk decode path for a Decode-family kernel: one in-kernel
-// (page) loop; q and the accumulators fixed along it; strides and alignment
-// that the 128-bit / 32-bit loads of DecodeWave need.  Otherwise the launch
-// stays a tile program.
+// Chooses the balanced decode path for a Decode-family kernel: one in-kernel
+// (page) loop; q and the accumulators fixed along it; at most
+// kDecodeMaxUnits units and fewer than 2^31 pages in all; strides and
+// alignment that the 128-bit / 32-bit loads of DecodeWave need.  Otherwise
+// the launch stays a tile program.
 bool decode_allowed(const KernelAnalysis& a, const LaunchSpec& L, const LaunchArgs& A, const EmitSpec& spec, int ng) {
     if (a.family != Family::Decode || spec.serial || L.inner.size() != 1) return false;
-    // The last two scalar slots carry the chunk count and the declared page maximum.
-    if (L.task->scalar_args.size() + 2 > static_cast<size_t>(kMaxScalars)) return false;
-    if (L.inner[0].axis->kind == AxisKind::DynTensor && L.inner[0].axis->max <= 0) return false;
+    // The last scalar slot carries the declared page maximum.
+    if (L.task->scalar_args.size() + 1 > static_cast<size_t>(kMaxScalars)) return false;
+    const Axis& ax = *L.inner[0].axis;
+    if (ax.kind == AxisKind::DynTensor && ax.max <= 0) return false;
+    const int64_t maxp = ax.kind == AxisKind::DynTensor ? ax.max : A.ext[ng];
+    int64_t units = 1;
+    for (int v = 0; v < ng; ++v) units *= A.ext[v];
+    if (units < 1 || units > kDecodeMaxUnits || maxp < 0 || maxp >= (int64_t(1) << 31) / units) return false;
     const DecodeInfo& d = a.decode;
     const int nvars = ng + 1;
     const int ntens = static_cast<int>(a.tensor_param_index.size());
-    if (ntens >= kMaxParams) return false;
+    if (ntens + 1 > kMaxParams) return false;  // one extra slot: counters and partials
     std::vector<int> first(ntens, 0);
     for (int p = 1; p < ntens; ++p) first[p] = first[p - 1] + spec.indirect_count[p - 1];
     auto aligned = [&](int p, int64_t elems, int esize) {
@@ -430,25 +448,19 @@ bool decode_allowed(const KernelAnalysis& a, const LaunchSpec& L, const LaunchAr
     for (int p : {d.q, d.m, d.l, d.o}) {
         if (spec.indirect_count[p] != 0 || A.coef[p][ng] != 0) return false;
     }
-    const int dpl = d.d / 64;
+    const int dv = std::min(d.d / 16, 8);  // V loads: 8 (d 64) or 16 bytes per lane and token
     if (A.s4[d.q] != 1 || A.s3[d.q] % 8 || !aligned(d.q, 8, 2)) return false;
     if (A.s3[d.kt] != 1 || A.s4[d.kt] % 8 || !aligned(d.kt, 8, 2)) return false;
-    if (A.s4[d.v] != 1 || A.s3[d.v] % dpl || !aligned(d.v, dpl, 2)) return false;
-    if (d.mask >= 0 && (A.s4[d.mask] != 1 || !aligned(d.mask, 4, 4))) return false;
+    if (A.s4[d.v] != 1 || A.s3[d.v] % dv || !aligned(d.v, dv, 2)) return false;
+    if (d.mask >= 0 && (A.s4[d.mask] != 1 || !aligned(d.mask, 1, 4))) return false;
+    // Page loads use 32-bit byte offsets from the page base.
+    const int64_t lim = int64_t(1) << 30;
+    if (A.s4[d.kt] >= lim / 16 || A.s3[d.v] >= lim / 16) return false;
     std::set<int> tids;
     for (int p : {d.q, d.kt, d.v, d.m, d.l, d.o}) tids.insert(L.targs[p]->tid);
     if (d.mask >= 0) tids.insert(L.targs[d.mask]->tid);
     if (static_cast<int>(tids.size()) != (d.mask >= 0 ? 7 : 6)) return false;
     return true;
-}
-
-int decode_chunk_pages() {
-    static const int c = [] {
-        const char* e = std::getenv("PTOWSP_DECODE_CHUNK");
-        const int v = e ? std::atoi(e) : 16;
-        return v >= 1 && v <= 1024 ? v : 16;
-    }();
-    return c;
 }
 
 BuiltLaunch build_launch(RunEnv& E, const LaunchSpec& L) {
@@ -596,7 +608,6 @@ BuiltLaunch build_launch(RunEnv& E, const LaunchSpec& L) {
     B.spec.gemm = gemm_allowed(a, L, A, B.spec, ng, nvars);
     if (!B.spec.gemm) B.spec.gemm_vm = B.spec.gemm_vn = -1;
     B.spec.decode = decode_allowed(a, L, A, B.spec, ng);
-    B.spec.decode_chunk = B.spec.decode ? decode_chunk_pages() : 16;
     B.spec.vec_width = a.family == Family::RowProgram ? pick_vec_width(a, A, nvars) : 1;
     return B;
 }
@@ -604,7 +615,7 @@ BuiltLaunch build_launch(RunEnv& E, const LaunchSpec& L) {
 std::string spec_key(const EmitSpec& s) {
     std::ostringstream o;
     o << "vw" << s.vec_width << (s.serial ? ";serial" : "") << ";up" << s.row_up << (s.nontemporal ? ";nt" : "")
-      << (s.gemm ? ";gemm" : "") << ";m" << s.gemm_vm << ";n" << s.gemm_vn << (s.decode ? ";dec" : "") << s.decode_chunk
+      << (s.gemm ? ";gemm" : "") << ";m" << s.gemm_vm << ";n" << s.gemm_vn << (s.decode ? ";dec" : "")
       << ";i";
     for (int c : s.indirect_count) o << c << ",";
     o << ";d";
@@ -622,9 +633,28 @@ const EmittedKernel& emitted_for(ptowsp_program* P, int li, const EmitSpec& spec
     return c.emitted.emplace(key, std::move(ek)).first->second;
 }
 
-// Decode launch: the chunk kernel (one wave per unit x chunk of pages) and
-// the combine kernel (one wave per unit) back to back on `stream`.  The chunk
-// partials live in a program-owned scratch buffer (grown on demand).
+// Blocks of `f` (256 threads) resident on the whole GPU at once.
+int64_t resident_blocks(hipFunction_t f) {
+    static std::mutex mu;
+    static std::map<std::pair<int, hipFunction_t>, int64_t> memo;
+    int dev = 0;
+    check(hipGetDevice(&dev), "hipGetDevice");
+    std::lock_guard<std::mutex> lock(mu);
+    auto it = memo.find({dev, f});
+    if (it != memo.end()) return it->second;
+    int per_cu = 0, cus = 0;
+    check(hipDeviceGetAttribute(&cus, hipDeviceAttributeMultiprocessorCount, dev), "hipDeviceGetAttribute");
+    check(hipModuleOccupancyMaxActiveBlocksPerMultiprocessor(&per_cu, f, 256, 0), "hipModuleOccupancyMaxActiveBlocksPerMultiprocessor");
+    const int64_t r = std::max<int64_t>(1, static_cast<int64_t>(per_cu) * cus);
+    memo[{dev, f}] = r;
+    return r;
+}
+
+// One launch of the balanced decode kernel (emit_decode): one block per
+// resident slot.  The program's scratch starts with kDecodeMaxUnits int32
+// counters, zeroed when the scratch is allocated and left at zero by every
+// launch; the partials follow, one slot per (unit, wave) pair: units + waves
+// slots.
 void enqueue_decode(ptowsp_program* P, int li, BuiltLaunch& B, const EmittedKernel& ek, const JitKernel& jk,
                     hipStream_t stream, uint64_t& launches) {
     const LaunchSpec& L = P->plan.launches[li];
@@ -632,34 +662,29 @@ void enqueue_decode(ptowsp_program* P, int li, BuiltLaunch& B, const EmittedKern
     const int ng = static_cast<int>(L.grid.size());
     const Axis& ax = *L.inner[0].axis;
     const int64_t maxp = std::max<int64_t>(0, ax.kind == AxisKind::DynTensor ? ax.max : B.args.ext[ng]);
-    const int64_t C = B.spec.decode_chunk;
-    const int64_t mc = std::max<int64_t>(1, (maxp + C - 1) / C);
-    const int64_t waves = B.ntasks * mc;
-    const int64_t blocks = (waves + 3) / 4, cblocks = (B.ntasks + 3) / 4;
-    if (blocks > 0x7FFFFFFF) throw std::runtime_error("decode launch: too many page chunks for one grid");
-    const size_t need = static_cast<size_t>(waves) * static_cast<size_t>(ek.part_floats) * sizeof(float);
+    const int64_t grid = resident_blocks(jk.function);
+    const int64_t waves = 4 * grid;
+    const size_t count_bytes = static_cast<size_t>(kDecodeMaxUnits) * sizeof(int32_t);
+    const size_t part_bytes = static_cast<size_t>(B.ntasks + waves) * static_cast<size_t>(ek.part_floats) * sizeof(float);
+    const size_t need = count_bytes + part_bytes;
     if (need > P->scratch_bytes) {
         if (P->scratch) check(hipFree(P->scratch), "hipFree(scratch)");
         P->scratch = nullptr;
         P->scratch_bytes = 0;
         check(hipMalloc(&P->scratch, need), "hipMalloc(decode scratch)");
+        check(hipMemset(P->scratch, 0, count_bytes), "hipMemset(decode counters)");
+        check(hipDeviceSynchronize(), "hipDeviceSynchronize");
         P->scratch_bytes = need;
     }
     const int ntens = static_cast<int>(a.tensor_param_index.size());
+    if (ntens >= kMaxParams) throw std::runtime_error("decode launch: no argument slot for its scratch");
     B.args.base[ntens] = static_cast<char*>(P->scratch);
     B.args.span[ntens] = static_cast<int64_t>(need / sizeof(float));
-    B.args.scal[kMaxScalars - 1] = static_cast<uint64_t>(mc);
-    B.args.scal[kMaxScalars - 2] = static_cast<uint64_t>(maxp);
-    LaunchCache& c = P->cache[li];
-    const std::string key = spec_key(B.spec) + "#combine";
-    auto it = c.by_spec.find(key);
-    const JitKernel* comb = it != c.by_spec.end() ? it->second : (c.by_spec[key] = &jit_kernel(ek.source, ek.combine_entry));
+    B.args.scal[kMaxScalars - 1] = static_cast<uint64_t>(maxp);
     void* params[] = {&B.args};
-    check(hipModuleLaunchKernel(jk.function, static_cast<unsigned>(blocks), 1, 1, 256, 1, 1, 0, stream, params, nullptr),
+    check(hipModuleLaunchKernel(jk.function, static_cast<unsigned>(grid), 1, 1, 256, 1, 1, 0, stream, params, nullptr),
           "hipModuleLaunchKernel(decode)");
-    check(hipModuleLaunchKernel(comb->function, static_cast<unsigned>(cblocks), 1, 1, 256, 1, 1, 0, stream, params, nullptr),
-          "hipModuleLaunchKernel(decode combine)");
-    launches += 2;
+    launches += 1;
 }
 
 void enqueue_launch(RunEnv& E, int li, hipStream_t stream, uint64_t& launches) {
@@ -779,7 +804,6 @@ CycleResult cycles_for(RunEnv& E) {
     env.axis_size = [&](const std::string& n) { return E.ctx->get_axis_size(E.ctx->ctx, n.c_str()); };
     env.symbol_u64 = [&](uint64_t id) { return E.ctx->get_symbol_u64(E.ctx->ctx, id); };
     env.symbol_ptr = [&](uint64_t id) { return static_cast<const int32_t*>(E.ctx->get_symbol_ptr(E.ctx->ctx, id)); };
-    bool uses_tensor_extents = false;
     std::ostringstream key;
     std::function<void(const Node*)> walk = [&](const Node* n) {
         if (!n) return;
@@ -793,22 +817,33 @@ CycleResult cycles_for(RunEnv& E) {
                     for (int64_t i = 0; i < outer; ++i) key << len[i] << ",";
                 key << ";";
             }
-            if (a.kind == AxisKind::DynTensor) uses_tensor_extents = true;
+            if (a.kind == AxisKind::DynTensor) {
+                // Key on the whole extent tensor's contents (small: one count per outer index).
+                const int tid = a.expr.tid;
+                const TensorState& t = E.ts[tid];
+                uint64_t h = 0xcbf29ce484222325ull;
+                auto mix = [&](int32_t x) {
+                    for (int b = 0; b < 4; ++b) h = (h ^ ((static_cast<uint32_t>(x) >> (8 * b)) & 0xFF)) * 0x100000001b3ull;
+                };
+                if (t.host)
+                    for (int64_t i = 0; i < t.span; ++i) mix(reinterpret_cast<const int32_t*>(t.host)[i]);
+                else
+                    for (int32_t x : index_host_copy(E, tid)) mix(x);
+                key << "t" << tid << ":" << t.span << ":" << h << ";";
+            }
         }
         walk(n->body.get());
         for (const auto& c : n->kids) walk(c.get());
     };
     walk(P->m.root.get());
-    if (!uses_tensor_extents && P->cycles_valid && P->cycle_key == key.str()) return P->cycles;
+    if (P->cycles_valid && P->cycle_key == key.str()) return P->cycles;
     env.index_value = [&](const IndexExpr& e, const std::vector<std::pair<std::string, int64_t>>& vars) {
         return eval_index_host(E, e, vars);
     };
     CycleResult r = run_cycle_model(P->m, P->ka, env);
-    if (!uses_tensor_extents) {
-        P->cycle_key = key.str();
-        P->cycles = r;
-        P->cycles_valid = true;
-    }
+    P->cycle_key = key.str();
+    P->cycles = r;
+    P->cycles_valid = true;
     return r;
 }
 
@@ -914,7 +949,7 @@ int ptowsp_hip_precompile(ptowsp_program* P, int index, int flags, const char** 
 int ptowsp_hip_cycle_model(ptowsp_program* P, RuntimeContext* ctx, ptowsp_run_info* info) {
     try {
         if (!P || !ctx) throw std::runtime_error("null argument");
-        RunEnv E{P, ctx, {}, {}};
+        RunEnv E{P, ctx, {}, {}, {}};
         const size_t nt = P->m.tensors.size();
         E.ts.assign(nt, TensorState{});
         for (size_t t = 0; t < nt; ++t) {
@@ -960,7 +995,7 @@ int ptowsp_hip_launch(ptowsp_program* P, RuntimeContext* ctx, void* hip_stream, 
             check(hipEventCreate(&P->ev1), "hipEventCreate");
             P->have_events = true;
         }
-        RunEnv E{P, ctx, {}, {}};
+        RunEnv E{P, ctx, {}, {}, {}};
         resolve_tensors(E, stream);
         const CycleResult cyc = cycles_for(E);
         uint64_t launches = 0;

@@ -3,6 +3,12 @@ oracle over every element, plus size-independent invariants of the math.
 
 rmsnorm_tile over X[16,8192,16,128] f32 ~ N(0,1)  (1 GiB in)
 row softmax over X[8,4096,32,512] f32 ~ N(0,3)    (2 GiB in)
+bgemm, A,B[64,2048,2048] bf16 U(-1,1), C fp32, 128x128 tiles, K step 64
+paged GQA decode, 64 sequences of 512..8192 tokens, 32/8 heads, d 128
+
+For configs 3 and 4 the oracle runs on a slice (it is single-threaded); the
+whole output is checked against float64 references computed on the GPU for
+a spread of batches, and through invariants of the math.
 """
 
 import numpy as np
@@ -69,4 +75,79 @@ def test_config2_softmax_full(gpu):
     assert float((s - 1.0).abs().max()) < 1e-5
     assert float(y.min()) >= 0.0
     del x, y, yref
+    torch.cuda.empty_cache()
+
+
+def test_config3_bgemm_full(gpu):
+    import torch
+
+    from test_gpu_parity import _rel_fro  # noqa: F401  (same metric)
+
+    dev = torch.device("cuda:0")
+    g = torch.Generator(device=dev)
+    g.manual_seed(0)
+    a = (torch.rand((64, 2048, 2048), generator=g, device=dev) * 2 - 1).to(torch.bfloat16)
+    b = (torch.rand((64, 2048, 2048), generator=g, device=dev) * 2 - 1).to(torch.bfloat16)
+    c = torch.zeros((64, 2048, 2048), device=dev, dtype=torch.float32)
+    prog = W.rr4(W.bgemm({"a": a, "b": b, "c": c}, 128, 128, 64, W.BF16)).compile(target="hip_gfx950")
+    assert prog._native.kernel_family("gemm_tile") == "gemm"
+    prog.execute()
+    prog.synchronize()
+    assert prog.stats.task_count == 64 * 16 * 16 * 32
+    for bi in (0, 21, 63):
+        ref = a[bi].double() @ b[bi].double()
+        rel = float((c[bi].double() - ref).norm() / ref.norm())
+        assert rel <= 1e-5, (bi, rel)
+    # Oracle on a slice: batch 0, m-tiles 0-1, all n, all k.
+    a0 = a[:1, :256].contiguous().view(torch.int16).cpu().numpy().view(np.uint16)
+    b0 = b[:1].contiguous().view(torch.int16).cpu().numpy().view(np.uint16)
+    c0 = np.zeros((1, 256, 2048), np.float32)
+    run_workload(W.bgemm({"a": a0, "b": b0, "c": c0}, 128, 128, 64, W.BF16))
+    got = c[0, :256].cpu().numpy()
+    assert float(np.linalg.norm(got - c0[0]) / np.linalg.norm(c0[0])) <= 1e-5
+    del a, b, c
+    torch.cuda.empty_cache()
+
+
+def test_config4_paged_decode_full(gpu):
+    import torch
+
+    dev = torch.device("cuda:0")
+    t = W.paged_decode_torch(dev, 64, 32, 8, 128, 512, 8192, seed=0)
+    prog = W.rr4(W.paged_decode(t)).compile(target="hip_gfx950")
+    assert prog._native.kernel_family("decode_page") == "decode"
+    prog.execute()
+    prog.synchronize()
+    lengths = t["lengths"]
+    npg = (lengths + 15) // 16
+    assert prog.stats.task_count == 8 * int(npg.sum()) + 64 * 8
+    out = t["out"]
+    # float64 reference on the GPU for a spread of sequences
+    for b in (0, 1, 31, 62, 63):
+        L, n = int(lengths[b]), int(npg[b])
+        pages = t["page_table"][b, :n].long()
+        k = t["k_cache"][pages].double().permute(1, 0, 2, 3).reshape(8, n * 16, 128)[:, :L]
+        v = t["v_cache"][pages].double().permute(1, 0, 2, 3).reshape(8, n * 16, 128)[:, :L]
+        q = t["q"][b].double()                                        # [8, 4, 128]
+        s = torch.matmul(q, k.transpose(1, 2).contiguous()) / (128 ** 0.5)
+        ref = torch.matmul(torch.softmax(s, dim=-1), v)
+        rel = float((out[b].double() - ref).norm() / ref.norm())
+        assert rel <= 1e-5, (b, rel)
+    # Invariants for every sequence: l >= 1 (the max term contributes exp(0)),
+    # and each output is a convex combination of that sequence's V rows.
+    assert float(t["l"].min()) >= 1.0 - 1e-6
+    assert bool(torch.isfinite(out).all())
+    assert float(out.abs().max()) <= float(t["v_cache"].float().abs().max()) + 1e-4
+    # Oracle on a slice: the first 4 sequences, all KV heads.
+    u16 = lambda x: x.contiguous().view(torch.int16).cpu().numpy().view(np.uint16)
+    nb = 4
+    h = {"q": u16(t["q"][:nb]), "k_cache": u16(t["k_cache"]), "v_cache": u16(t["v_cache"]),
+         "page_table": t["page_table"][:nb].cpu().numpy(), "npages": t["npages"][:nb].cpu().numpy(),
+         "mask": t["mask"][:nb].cpu().numpy(), "m": np.full((nb, 8, 4, 1), -np.inf, np.float32),
+         "l": np.zeros((nb, 8, 4, 1), np.float32), "o": np.zeros((nb, 8, 4, 128), np.float32),
+         "out": np.zeros((nb, 8, 4, 128), np.float32)}
+    run_workload(W.paged_decode(h))
+    got = out[:nb].cpu().numpy()
+    np.testing.assert_allclose(got, h["out"], rtol=2e-5, atol=2e-5 * float(np.abs(h["out"]).max()))
+    del t
     torch.cuda.empty_cache()

@@ -347,12 +347,12 @@ def test_paged_decode_sixteen_rows(gpu):
     the [1,16] mask on a square [16,16] score tile the reference's broadcast rule
     subtracts mask[row] (a row broadcast, src/python/pto_codegen.cpp:1094-1105),
     so the launch stays a tile program and matches the oracle, not a token mask."""
-    prog, ref, ga, ca = _decode_case([96, 512, 16], 1, 16, 128, seed=3, masked=False)
+    prog, ref, ga, ca = _decode_case([96, 512, 16], 1, 16, 64, seed=3, masked=False)
     assert prog._native.kernel_family("decode_page") == "decode"
     for k in ("m", "l", "o", "out"):
         np.testing.assert_allclose(ga[k], ca[k], rtol=2e-5, atol=2e-5 * float(np.abs(ca[k]).max()), err_msg=k)
     assert _rel_fro(ga["out"], W.paged_decode_ref(ga)) <= 1e-5
-    prog, ref, ga, ca = _decode_case([90, 40], 1, 16, 128, seed=3, masked=True)
+    prog, ref, ga, ca = _decode_case([90, 40], 1, 16, 64, seed=3, masked=True)
     assert prog._native.kernel_family("decode_page") == "tile_program"
     for k in ("m", "l", "o", "out"):
         np.testing.assert_allclose(ga[k], ca[k], rtol=1e-5, atol=1e-5 * float(np.abs(ca[k]).max()), err_msg=k)

@@ -347,6 +347,40 @@ def paged_decode_arrays(lengths, hkv: int, group: int, d: int, page: int = 16, s
             "lengths": lengths}
 
 
+def paged_decode_torch(dev, batch: int, hq: int, hkv: int, d: int, lmin: int, lmax: int, seed: int = 0,
+                       page: int = 16) -> dict:
+    """Config-5 sized inputs on the device: lengths ~ U[lmin, lmax] and a permuted page
+    table from numpy (seeded), bf16 q / K / V ~ N(0,1) from torch's device RNG."""
+    import torch
+
+    rng = np.random.default_rng(seed)
+    G = hq // hkv
+    lengths = rng.integers(lmin, lmax + 1, size=batch)
+    npages = (lengths + page - 1) // page
+    max_pages = (lmax + page - 1) // page
+    total = int(npages.sum())
+    phys = rng.permutation(total).astype(np.int32)
+    pt = np.zeros((batch, max_pages), np.int32)
+    mask = np.zeros((batch, max_pages, 1, page), np.float32)
+    tok = np.arange(max_pages * page).reshape(max_pages, page)
+    off = 0
+    for b in range(batch):
+        pt[b, :npages[b]] = phys[off:off + npages[b]]
+        off += npages[b]
+        mask[b, :, 0, :] = np.where(tok < lengths[b], 0.0, 1e30)
+    g = torch.Generator(device=dev)
+    g.manual_seed(seed)
+    kv = (total, hkv, page, d)
+    return {"q": torch.randn((batch, hkv, G, d), generator=g, device=dev, dtype=torch.bfloat16),
+            "k_cache": torch.randn(kv, generator=g, device=dev, dtype=torch.bfloat16),
+            "v_cache": torch.randn(kv, generator=g, device=dev, dtype=torch.bfloat16),
+            "page_table": torch.from_numpy(pt).to(dev), "npages": torch.from_numpy(npages.astype(np.int32)).to(dev),
+            "mask": torch.from_numpy(mask).to(dev),
+            "m": torch.full((batch, hkv, G, 1), float("-inf"), device=dev),
+            "l": torch.zeros((batch, hkv, G, 1), device=dev), "o": torch.zeros((batch, hkv, G, d), device=dev),
+            "out": torch.zeros((batch, hkv, G, d), device=dev), "lengths": lengths}
+
+
 def paged_decode_ref(arrs: dict) -> np.ndarray:
     """float64 softmax(q k^T / sqrt(d)) v over each sequence's valid tokens."""
     up = (lambda x: x.astype(np.float64)) if arrs["q"].dtype == np.float16 else (lambda x: bf16_to_f32(x).astype(np.float64))
