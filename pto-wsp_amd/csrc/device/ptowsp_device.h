@@ -738,33 +738,13 @@ struct DecodeWave {
             for (int e = 0; e < DV; ++e) st.o[g][e] = 0.0f;
     }
 
-    // Folds pages [p0, p1) (p0 < p1) into st; ptrs(p, kp, vp, mp) gives page
-    // p's bases.  Two page buffers alternate; each prefetch is unconditional
-    // (the page index is clamped to p1-1) so the wait before each step counts
-    // one page of loads.
-    template <class PagePtrs>
-    __device__ static void fold(State& st, i64 p0, i64 p1, const u32x4 (&qa)[NS], float scale, PagePtrs ptrs, i64 ks,
-                                i64 vs, float* lds) {
-        const Lanes ln = lanes(ks, vs);
-        Page pa, pb;
-        const u16 *kp, *vp;
-        const float* mp;
-        ptrs(p0, kp, vp, mp);
-        load_page(pa, kp, vp, mp, ln);
-        for (i64 p = p0; p < p1; p += 2) {
-            ptrs(p + 1 < p1 ? p + 1 : p1 - 1, kp, vp, mp);
-            load_page(pb, kp, vp, mp, ln);
-            step(st, pa, qa, scale, lds);
-            if (p + 1 >= p1) break;
-            ptrs(p + 2 < p1 ? p + 2 : p1 - 1, kp, vp, mp);
-            load_page(pa, kp, vp, mp, ln);
-            step(st, pb, qa, scale, lds);
-        }
-    }
-
     // Writes st as a partial (m[G], l[G], o[G][D]) after summing the four
-    // token groups (lanes l, l^16, l^32, l^48).
+    // token groups (lanes l, l^16, l^32, l^48).  o is kept in lane order:
+    // head dim DV*t + e sits at position 16*e + t (part_dim maps back), so
+    // store i of every lane l writes position 64*i + l (e = 4*i + l/16) and
+    // each store instruction covers 256 contiguous bytes.
     __device__ static void store(const State& st, float* part) {
+        static_assert(DV % 4 == 0, "lane-order partial");
         const int lane = threadIdx.x & 63, t = lane & 15, grp = lane >> 4;
         if (t == 0) {
 #pragma unroll
@@ -777,29 +757,49 @@ struct DecodeWave {
             }
         }
 #pragma unroll
-        for (int g = 0; g < G; ++g)
+        for (int g = 0; g < G; ++g) {
+            float x[DV];
 #pragma unroll
             for (int e = 0; e < DV; ++e) {
-                float x = st.o[g][e];
-                x = x + __shfl_xor(x, 16);
-                x = x + __shfl_xor(x, 32);
-                if (grp == 0) coherent_store(part + 2 * G + g * D + DV * t + e, x);
+                x[e] = st.o[g][e];
+                x[e] = x[e] + __shfl_xor(x[e], 16);
+                x[e] = x[e] + __shfl_xor(x[e], 32);
             }
+#pragma unroll
+            for (int i = 0; i < DV / 4; ++i) {
+                const float y = grp == 0 ? x[4 * i] : grp == 1 ? x[4 * i + 1] : grp == 2 ? x[4 * i + 2] : x[4 * i + 3];
+                coherent_store(part + 2 * G + g * D + 64 * i + lane, y);
+            }
+        }
     }
 };
 
-// Balanced split of a decode launch over the resident waves: the units' page
-// counts are concatenated in unit order (prefix pre[0..U], pre[U] = T pages in
-// all) and wave w of W folds global pages [w*T/W, (w+1)*T/W), with W at
-// most T so that every wave holds at least one page.  A wave writes
-// one partial per unit it touches, into slot unit + w (slots are distinct
-// because the first wave of unit u+1 is at least the last wave of unit u);
-// unit u's partials are the consecutive slots u + wave_of(pre[u]) ..
-// u + wave_of(pre[u+1]-1).
+// Head dim held at position p of a partial's o row (see DecodeWave::store).
+template <int D>
+__device__ inline int part_dim(int p) {
+    return (D / 16) * (p & 15) + (p >> 4);
+}
+
+// Balanced split of a decode launch over the resident waves.  The units'
+// pages are concatenated in unit order (page prefix pre[0..U], pre[U] = T)
+// and so are their scheduling costs: a non-empty unit costs its pages plus
+// kUnitCost leading positions that hold no page, for the work a wave does
+// at every unit it starts (partial store, q switch, stalled ring), so that
+// ranges with many short units get fewer pages (cost prefix cpre[0..U],
+// cpre[U] = TC).  Wave w of W <= TC owns cost positions [w*TC/W,
+// (w+1)*TC/W), i.e. the pages [page_at(w*TC/W), page_at((w+1)*TC/W)).  A
+// wave writes one partial per unit it touches, into slot unit + w (slots are
+// distinct because the first wave of unit u+1 is at least the last wave of
+// unit u); unit u's partials are the consecutive slots u + wf .. u + wl, wf
+// and wl the waves of its first page (cost position cpre[u] + kUnitCost)
+// and last page (cpre[u+1] - 1).  A wave whose cost range holds no page
+// lies before the first page of a unit, never between two waves of one.
 struct DecodeSplit {
-    static constexpr int kMaxUnits = 4096;  // prefix held in LDS by every block
-    // Wave holding global page p: the largest w with w*T/W <= p.
-    __device__ static i64 wave_of(i64 p, i64 T, i64 W) { return ((p + 1) * W - 1) / T; }
+    static constexpr int kMaxUnits = 4096;  // prefixes held in LDS by every block
+    static constexpr int kUnitCost = 3;
+    __device__ static int cost(int pages) { return pages > 0 ? pages + kUnitCost : 0; }
+    // Wave holding cost position p: the largest w with w*TC/W <= p.
+    __device__ static i64 wave_of(i64 p, i64 TC, i64 W) { return ((p + 1) * W - 1) / TC; }
     // Largest u in [0, U) with pre[u] <= s, for 0 <= s < pre[U] (a non-empty unit).
     __device__ static int unit_of(const int* pre, int U, i64 s) {
         int lo = 0, hi = U;
@@ -809,6 +809,217 @@ struct DecodeSplit {
             else hi = mid;
         }
         return lo;
+    }
+    // First page at or after cost position v (T for v >= TC).
+    __device__ static i64 page_at(const int* pre, const int* cpre, int U, i64 v) {
+        if (v >= cpre[U]) return pre[U];
+        const int u = unit_of(cpre, U, v);
+        const i64 off = v - cpre[u] - kUnitCost;
+        return pre[u] + (off > 0 ? off : 0);
+    }
+};
+
+// i64 held by lane i (i wave-uniform), as a wave-uniform value.
+__device__ inline i64 readlane64(i64 x, int i) {
+    const u64 b = static_cast<u64>(x);
+    const u32 lo = static_cast<u32>(__builtin_amdgcn_readlane(static_cast<int>(static_cast<u32>(b)), i));
+    const u32 hi = static_cast<u32>(__builtin_amdgcn_readlane(static_cast<int>(static_cast<u32>(b >> 32)), i));
+    return static_cast<i64>((static_cast<u64>(hi) << 32) | lo);
+}
+
+// Element offsets of one page: K^T tile, V tile, mask row.
+struct PageOffs {
+    i64 k, v, m;
+};
+
+// The addressing hooks of a decode launch (see DecodeStream), from lambdas.
+template <class P, class B, class Q, class S, class C>
+struct DecodeFns {
+    P page;
+    B bases;
+    Q q;
+    S slot;
+    C combine;
+};
+template <class P, class B, class Q, class S, class C>
+__device__ inline DecodeFns<P, B, Q, S, C> decode_fns(P p, B b, Q q, S s, C c) {
+    return DecodeFns<P, B, Q, S, C>{p, b, q, s, c};
+}
+
+// One decode wave's pages [s, b) of the launch (units laid end to end, see
+// DecodeSplit) folded as a single stream: the NB-page register ring keeps
+// loading across unit boundaries and across the 64-page runs of page-table
+// offsets (lane i of a run holds page r0+i's offsets; the next run is read
+// 64 pages ahead), so the wave never waits for a page table or q read.
+//
+// At the end of a unit's pages in this wave the partial is stored and its
+// completion deferred: vector memory operations of a wave complete in issue
+// order, so NB folded pages later (page loads issued after the stores have
+// returned) the stores are complete and the arrival is counted; NB pages
+// after that the count's old value has returned, and the last arriver folds
+// the unit's partials.  A second unit end while one is pending, and the end
+// of the stream, complete it at once (waiting for the stores).
+//
+// F provides: page(g, PageOffs&) per lane; bases(PageOffs, kp, vp, mp);
+// q(u) (q tile of unit u, or null when out of range); slot(u) (this wave's
+// partial of unit u); combine(u, parts, first_slot).
+template <class DW, int NB>
+struct DecodeStream {
+    struct Pending {
+        int unit, parts, phase, wait;  // phase 0: none, 1: stores issued, 2: arrival issued
+        i64 first;                     // first partial slot of the unit
+        int old_v;                     // arrival count before this wave's (lane 0)
+    };
+
+    __device__ static void arrive_issue(Pending& pd, int* cnt) {
+        int r = 0;
+        if ((threadIdx.x & 63) == 0) r = __hip_atomic_fetch_add(cnt + pd.unit, 1, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+        pd.old_v = r;
+    }
+    template <class F>
+    __device__ static void finish(Pending& pd, int* cnt, F& f) {
+        bool last = true;
+        if (pd.parts > 1) {
+            last = __builtin_amdgcn_readfirstlane(pd.old_v) == pd.parts - 1;
+            __atomic_signal_fence(__ATOMIC_SEQ_CST);
+        }
+        if (last) {
+            f.combine(pd.unit, pd.parts, pd.first);
+            if (pd.parts > 1) reset_count(cnt + pd.unit);
+        }
+        pd.phase = 0;
+    }
+    // Completes a pending unit now.
+    template <class F>
+    __device__ static void flush(Pending& pd, int* cnt, F& f) {
+        if (pd.phase == 0) return;
+        if (pd.phase == 1) {
+            publish();
+            if (pd.parts > 1) arrive_issue(pd, cnt);
+        }
+        finish(pd, cnt, f);
+    }
+    // One folded page of progress on a pending unit.
+    template <class F>
+    __device__ static void tick(Pending& pd, int* cnt, F& f) {
+        if (pd.phase == 0 || --pd.wait > 0) return;
+        if (pd.phase == 1 && pd.parts > 1) {
+            __atomic_signal_fence(__ATOMIC_SEQ_CST);
+            arrive_issue(pd, cnt);
+            pd.phase = 2;
+            pd.wait = NB;
+            return;
+        }
+        finish(pd, cnt, f);
+    }
+
+    // Next unit after u with at least one page.
+    __device__ static int next_unit(const int* pre, int u) {
+        int n = u + 1;
+        while (__builtin_amdgcn_readfirstlane(pre[n + 1]) == __builtin_amdgcn_readfirstlane(pre[n])) ++n;
+        return n;
+    }
+
+    template <class F>
+    __device__ static void run(F& f, const int* pre, const int* cpre, int U, i64 TC, i64 W, i64 w, i64 s, i64 b, int* cnt,
+                               float scale, i64 ks, i64 vs, i64 qs, float* lds) {
+        const int lane = threadIdx.x & 63;
+        const typename DW::Lanes ln = DW::lanes(ks, vs);
+        const typename DW::Lanes dummy = {0u, 0u, 0u, ln.vrow};
+        // Page-table runs.
+        i64 r0 = s;
+        PageOffs rc, rn;
+        f.page(s + lane < b ? s + lane : b - 1, rc);
+        rn = rc;
+        if (s + 64 < b) f.page(s + 64 + lane < b ? s + 64 + lane : b - 1, rn);
+        auto load = [&](typename DW::Page& pg, i64 g) {
+            const bool real = g < b;
+            const int i = static_cast<int>((real ? g : b - 1) - r0);
+            const PageOffs& src = i < 64 ? rc : rn;
+            const int li = i & 63;
+            PageOffs po;
+            po.k = readlane64(src.k, li);
+            po.v = readlane64(src.v, li);
+            po.m = readlane64(src.m, li);
+            const u16 *kp, *vp;
+            const float* mp;
+            f.bases(po, kp, vp, mp);
+            // Past the stream's end the ring is still filled (so that every
+            // step waits for the same number of loads), from one 16-byte line.
+            DW::load_page(pg, kp, vp, mp, real ? ln : dummy);
+        };
+        // Unit state.
+        int u = DecodeSplit::unit_of(pre, U, s);
+        u = __builtin_amdgcn_readfirstlane(u);
+        i64 eu = __builtin_amdgcn_readfirstlane(pre[u + 1]);
+        if (eu > b) eu = b;
+        typename DW::State st;
+        DW::init(st);
+        u32x4 qa[DW::NS], qn[DW::NS];
+        // A q tile out of range (error already flagged) folds with q = 0;
+        // every step runs, so that its page waits order the partial stores.
+        auto get_q = [&](u32x4 (&dst)[DW::NS], int unit) {
+            const u16* qp = f.q(unit);
+            if (qp) {
+                DW::load_q(dst, qp, qs);
+            } else {
+#pragma unroll
+                for (int j = 0; j < DW::NS; ++j) dst[j] = u32x4{0u, 0u, 0u, 0u};
+            }
+        };
+        get_q(qa, u);
+        int un = u;
+        if (eu < b) {
+            un = next_unit(pre, u);
+            get_q(qn, un);
+        }
+        Pending pd;
+        pd.phase = 0;
+        typename DW::Page pg[NB];
+#pragma unroll
+        for (int i = 0; i < NB - 1; ++i) load(pg[i], s + i);
+        for (i64 g = s;; g += NB) {
+#pragma unroll
+            for (int i = 0; i < NB; ++i) {
+                const i64 gi = g + i;
+                load(pg[(i + NB - 1) % NB], gi + NB - 1);
+                DW::step(st, pg[i], qa, scale, lds);
+                tick(pd, cnt, f);
+                if (gi + 1 == eu) {
+                    // Unit u's pages in this wave are folded.
+                    flush(pd, cnt, f);
+                    const i64 cs = __builtin_amdgcn_readfirstlane(cpre[u]);
+                    const i64 ce = __builtin_amdgcn_readfirstlane(cpre[u + 1]);
+                    const i64 wf = DecodeSplit::wave_of(cs + DecodeSplit::kUnitCost, TC, W);
+                    const i64 wl = DecodeSplit::wave_of(ce - 1, TC, W);
+                    pd.unit = u;
+                    pd.parts = static_cast<int>(wl - wf + 1);
+                    pd.first = u + wf;
+                    DW::store(st, f.slot(u));
+                    pd.phase = 1;
+                    pd.wait = NB;
+                    if (eu >= b) {
+                        flush(pd, cnt, f);
+                        return;
+                    }
+                    u = un;
+                    eu = __builtin_amdgcn_readfirstlane(pre[u + 1]);
+                    if (eu > b) eu = b;
+                    DW::init(st);
+#pragma unroll
+                    for (int j = 0; j < DW::NS; ++j) qa[j] = qn[j];
+                    if (eu < b) {
+                        un = next_unit(pre, u);
+                        get_q(qn, un);
+                    }
+                }
+                if (gi + 1 - r0 == 64) {
+                    r0 += 64;
+                    rc = rn;
+                    if (r0 + 64 < b) f.page(r0 + 64 + lane < b ? r0 + 64 + lane : b - 1, rn);
+                }
+            }
+        }
     }
 };
 
@@ -837,7 +1048,7 @@ struct DecodeCombine {
             mm[g] = m[g * ms3];
             ll[g] = l[g * ls3];
 #pragma unroll
-            for (int j = 0; j < DPL; ++j) oo[g][j] = o[g * os3 + (DPL * lane + j) * os4];
+            for (int j = 0; j < DPL; ++j) oo[g][j] = o[g * os3 + part_dim<D>(DPL * lane + j) * os4];
         }
         i64 c = 0;
         for (; c + CB <= nch; c += CB) {
@@ -875,7 +1086,7 @@ struct DecodeCombine {
                 l[g * ls3] = ll[g];
             }
 #pragma unroll
-            for (int j = 0; j < DPL; ++j) o[g * os3 + (DPL * lane + j) * os4] = oo[g][j];
+            for (int j = 0; j < DPL; ++j) o[g * os3 + part_dim<D>(DPL * lane + j) * os4] = oo[g][j];
         }
     }
 };

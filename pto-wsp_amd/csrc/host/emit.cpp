@@ -35,6 +35,10 @@ const char* op_functor(OpKind k) {
 
 int dt_code(DType d) { return static_cast<int>(d); }
 
+// Kernel symbol of a launch: family and traced kernel name, so that profiler
+// traces tell launches apart (kernel names are Python identifiers).
+std::string entry_name(const char* family, const KernelDef& k) { return std::string("ptowsp_") + family + "_" + k.name; }
+
 // Declarations of scalar params and Constant() values (:607-655).
 void emit_scalars(std::ostringstream& o, const KernelAnalysis& a, bool int_ok) {
     const KernelDef& k = *a.def;
@@ -145,7 +149,8 @@ EmittedKernel emit_row(const Module& m, const KernelAnalysis& a, const LaunchSpe
     std::ostringstream o;
     o << "#include \"ptowsp_device.h\"\nusing namespace ptowsp;\n";
     o << "// row program: kernel " << k.name << ", rows " << R << " x cols " << C << ", vw " << lay.vw << "\n";
-    o << "extern \"C\" __global__ void __launch_bounds__(256) ptowsp_entry(const LaunchArgs A) {\n";
+    ek.entry = entry_name("row", k);
+    o << "extern \"C\" __global__ void __launch_bounds__(256) " << ek.entry << "(const LaunchArgs A) {\n";
     o << "  constexpr int R = " << R << ", NV = " << lay.nv << ", VW = " << lay.vw << ", G = " << lay.g
       << ", UP = " << lay.up << ";\n";
     o << "  constexpr int RPW = 64 / G, CH = RPW * UP, WPB = 4;\n";
@@ -294,7 +299,6 @@ EmittedKernel emit_row(const Module& m, const KernelAnalysis& a, const LaunchSpe
     }
     o << "    }\n  }\n}\n";
     ek.source = o.str();
-    ek.entry = "ptowsp_entry";
     return ek;
 }
 
@@ -329,7 +333,8 @@ EmittedKernel emit_tile(const Module& m, const KernelAnalysis& a, const LaunchSp
     std::ostringstream o;
     o << "#include \"ptowsp_device.h\"\nusing namespace ptowsp;\n";
     o << "// tile program: kernel " << k.name << "\n";
-    o << "extern \"C\" __global__ void __launch_bounds__(" << spec.threads << ") ptowsp_entry(const LaunchArgs A) {\n";
+    ek.entry = entry_name("tile", k);
+    o << "extern \"C\" __global__ void __launch_bounds__(" << spec.threads << ") " << ek.entry << "(const LaunchArgs A) {\n";
     o << "  constexpr int NT = " << spec.threads << ";\n";
     for (int id : lds_vals) {
         const ValueInfo* v = a.by_id[id];
@@ -465,7 +470,6 @@ EmittedKernel emit_tile(const Module& m, const KernelAnalysis& a, const LaunchSp
     }
     o << "  }\n}\n";
     ek.source = o.str();
-    ek.entry = "ptowsp_entry";
     return ek;
 }
 
@@ -489,7 +493,8 @@ EmittedKernel emit_gemm(const Module& m, const KernelAnalysis& a, const LaunchSp
     o << "#include \"ptowsp_device.h\"\nusing namespace ptowsp;\n";
     o << "// gemm program: kernel " << k.name << ", task tile " << g.m << "x" << g.n << "x" << g.k << (g.f16 ? " f16" : " bf16")
       << (g.accumulate ? ", accumulate" : "") << "; block " << bm << "x" << bn << " (" << fm * fn << " tasks)\n";
-    o << "extern \"C\" __global__ void __launch_bounds__(" << ek.threads << ") ptowsp_entry(const LaunchArgs A) {\n";
+    ek.entry = entry_name("gemm", k);
+    o << "extern \"C\" __global__ void __launch_bounds__(" << ek.threads << ") " << ek.entry << "(const LaunchArgs A) {\n";
     o << "  typedef GemmBlock<" << bm << ", " << bn << ", " << g.k << ", " << wm << ", " << wn << ", "
       << (g.f16 ? "true" : "false") << "> GB;\n";
     o << "  __shared__ __attribute__((aligned(1024))) u16 lds[GB::kLdsElems];\n";
@@ -532,7 +537,6 @@ EmittedKernel emit_gemm(const Module& m, const KernelAnalysis& a, const LaunchSp
       << (g.accumulate ? "0" : "iters - 1") << ", iters, off);\n";
     o << "  }\n}\n";
     ek.source = o.str();
-    ek.entry = "ptowsp_entry";
     ek.lds_bytes = static_cast<size_t>(2 * (bm + bn) * g.k * 2);
     return ek;
 }
@@ -550,6 +554,9 @@ EmittedKernel emit_gemm(const Module& m, const KernelAnalysis& a, const LaunchSp
 // zero between launches, then the partials);
 // scal[kMaxScalars-1] is the declared maximum page count (larger extents
 // raise error 3 and are cut to it).
+// Pages in the register ring of a decode wave (DecodeWave::fold).
+constexpr int kDecodePageRing = 4;
+
 EmittedKernel emit_decode(const Module& m, const KernelAnalysis& a, const LaunchSpec& L, const EmitSpec& spec) {
     (void)m;
     const KernelDef& k = *a.def;
@@ -592,27 +599,30 @@ EmittedKernel emit_decode(const Module& m, const KernelAnalysis& a, const Launch
         o << "        if (o_ < 0 || o_ + (i64)" << rows - 1 << " * A.s3[" << p << "] + (i64)" << cols - 1 << " * A.s4[" << p
           << "] >= A.span[" << p << "]) { " << flag << " = true; if (lane == 0) *A.err = 2; } }\n";
     };
-    // Three waves per SIMD fit the two page buffers without spills for
-    // head dims up to 128 and G*D up to 512; larger shapes keep the
-    // compiler's choice.
-    const bool occ3 = d.d <= 128 && d.g * d.d <= 512;
-    o << "extern \"C\" __global__ void __launch_bounds__(256) "
-      << (occ3 ? "__attribute__((amdgpu_waves_per_eu(3))) " : "") << "ptowsp_entry(const LaunchArgs A) {\n";
+    // One wave per SIMD (the host reserves LDS so that one block runs per
+    // CU): waves sharing a SIMD are served oldest first under memory
+    // back-pressure, which would leave equal page shares finishing far
+    // apart; alone on its SIMD a wave has the register file for its ring.
+    ek.entry = entry_name("decode", k);
+    o << "extern \"C\" __global__ void __launch_bounds__(256) __attribute__((amdgpu_waves_per_eu(1, 1))) " << ek.entry
+      << "(const LaunchArgs A) {\n";
     o << "  typedef " << tmpl << " DW;\n";
     o << "  static_assert(DecodeSplit::kMaxUnits == " << kDecodeMaxUnits << ", \"unit limit\");\n";
+    o << "  static_assert(DecodeSplit::kUnitCost == " << kDecodeUnitCost << ", \"unit cost\");\n";
     o << "  __shared__ __attribute__((aligned(16))) float lds_all[4][DW::kLdsFloats];\n";
-    o << "  __shared__ int pre[DecodeSplit::kMaxUnits + 1];\n";
-    o << "  __shared__ int wsum[4];\n";
+    o << "  __shared__ int pre[DecodeSplit::kMaxUnits + 1], cpre[DecodeSplit::kMaxUnits + 1];\n";
+    o << "  __shared__ int wsum[4], cwsum[4];\n";
     o << "  const int tid = threadIdx.x, lane = tid & 63;\n";
     o << "  const int wave = __builtin_amdgcn_readfirstlane(tid >> 6);\n";
     o << "  const int U = static_cast<int>(A.ntasks);\n";
     o << "  const i64 maxp = (i64)A.scal[" << kMaxScalars - 1 << "];\n";
     o << "  i64 vars[" << nvars << "];\n";
-    // Prefix of the page counts: thread t owns units t*per .. t*per+per-1.
+    // Prefixes of the page counts (pre) and of the units' scheduling costs
+    // (cpre, DecodeSplit::cost): thread t owns units t*per .. t*per+per-1.
     o << "  {\n";
     o << "    const int per = (U + 255) >> 8, u0 = tid * per;\n";
     o << "    int n_[DecodeSplit::kMaxUnits / 256];\n";
-    o << "    int run = 0;\n";
+    o << "    int run = 0, crun = 0;\n";
     o << "#pragma unroll\n";
     o << "    for (int i = 0; i < DecodeSplit::kMaxUnits / 256; ++i) {\n";
     o << "      n_[i] = 0;\n";
@@ -628,122 +638,100 @@ EmittedKernel emit_decode(const Module& m, const KernelAnalysis& a, const Launch
     o << "        if (npg > maxp) { npg = maxp; if (blockIdx.x == 0) *A.err = 3; }\n";
     o << "        n_[i] = static_cast<int>(npg);\n";
     o << "        run += n_[i];\n";
+    o << "        crun += DecodeSplit::cost(n_[i]);\n";
     o << "      }\n";
     o << "    }\n";
-    o << "    int x = run;\n";
+    o << "    int x = run, cx = crun;\n";
     o << "#pragma unroll\n";
-    o << "    for (int d_ = 1; d_ < 64; d_ <<= 1) { const int y = __shfl_up(x, d_); if (lane >= d_) x += y; }\n";
-    o << "    if (lane == 63) wsum[wave] = x;\n";
+    o << "    for (int d_ = 1; d_ < 64; d_ <<= 1) {\n";
+    o << "      const int y = __shfl_up(x, d_), cy = __shfl_up(cx, d_);\n";
+    o << "      if (lane >= d_) { x += y; cx += cy; }\n";
+    o << "    }\n";
+    o << "    if (lane == 63) { wsum[wave] = x; cwsum[wave] = cx; }\n";
     o << "    __syncthreads();\n";
-    o << "    int base = x - run;\n";
-    o << "    for (int j = 0; j < wave; ++j) base += wsum[j];\n";
+    o << "    int base = x - run, cbase = cx - crun;\n";
+    o << "    for (int j = 0; j < wave; ++j) { base += wsum[j]; cbase += cwsum[j]; }\n";
     o << "#pragma unroll\n";
     o << "    for (int i = 0; i < DecodeSplit::kMaxUnits / 256; ++i)\n";
-    o << "      if (i < per && u0 + i < U) { pre[u0 + i] = base; base += n_[i]; }\n";
-    o << "    if (tid == 0) pre[U] = wsum[0] + wsum[1] + wsum[2] + wsum[3];\n";
+    o << "      if (i < per && u0 + i < U) {\n";
+    o << "        pre[u0 + i] = base; base += n_[i];\n";
+    o << "        cpre[u0 + i] = cbase; cbase += DecodeSplit::cost(n_[i]);\n";
+    o << "      }\n";
+    o << "    if (tid == 0) {\n";
+    o << "      pre[U] = wsum[0] + wsum[1] + wsum[2] + wsum[3];\n";
+    o << "      cpre[U] = cwsum[0] + cwsum[1] + cwsum[2] + cwsum[3];\n";
+    o << "    }\n";
     o << "    __syncthreads();\n";
     o << "  }\n";
     // Values read from LDS are wave-uniform: readfirstlane keeps the page
     // loop's control and addresses in scalar registers.
-    o << "  const i64 T = __builtin_amdgcn_readfirstlane(pre[U]);\n";
-    // Active waves: at most one per page, so that every active wave holds at
-    // least one page and a unit's partials fill consecutive slots.
-    o << "  const i64 W = (i64)gridDim.x * 4 < T ? (i64)gridDim.x * 4 : T, w = (i64)blockIdx.x * 4 + wave;\n";
+    o << "  const i64 TC = __builtin_amdgcn_readfirstlane(cpre[U]);\n";
+    // Active waves: at most one per cost position, so that no wave's cost
+    // range is empty and a unit's partials fill consecutive slots (a wave
+    // whose range holds only cost positions, and no page, returns here).
+    o << "  const i64 W = (i64)gridDim.x * 4 < TC ? (i64)gridDim.x * 4 : TC, w = (i64)blockIdx.x * 4 + wave;\n";
     o << "  if (w >= W) return;\n";
-    o << "  i64 s = w * T / W;\n";
-    o << "  const i64 b = (w + 1) * T / W;\n";
+    o << "  const i64 s = DecodeSplit::page_at(pre, cpre, U, w * TC / W);\n";
+    o << "  const i64 b = DecodeSplit::page_at(pre, cpre, U, (w + 1) * TC / W);\n";
     o << "  if (s >= b) return;\n";
     o << "  int* cnt = reinterpret_cast<int*>(A.base[" << ntens << "]);\n";
     o << "  float* partials = reinterpret_cast<float*>(A.base[" << ntens << "] + DecodeSplit::kMaxUnits * 4);\n";
     o << "  float* lds = lds_all[wave];\n";
-    o << "  int u = __builtin_amdgcn_readfirstlane(DecodeSplit::unit_of(pre, U, s));\n";
-    o << "  for (;;) {\n";
-    o << "    const i64 su = __builtin_amdgcn_readfirstlane(pre[u]), eu = __builtin_amdgcn_readfirstlane(pre[u + 1]);\n";
-    o << "    const i64 e = eu < b ? eu : b;\n";
+    // Offsets of global page g (per lane): its unit, the page index within
+    // the unit, the affine and page-table terms; an out-of-range page raises
+    // the error flag and reads the tensor's first page instead.
+    o << "  auto f_page = [&](i64 g, PageOffs& po) {\n";
+    o << "    const int uu = DecodeSplit::unit_of(pre, U, g);\n";
+    o << "    i64 vars[" << nvars << "];\n";
+    decode_vars("uu", "    ");
+    o << "    vars[" << ng << "] = g - pre[uu];\n";
+    auto checked = [&](int p, int rows, int cols, const std::string& field) {
+        o << "    { i64 o_ = " << offset_expr(p, nvars, first_term[p], nterms(p)) << ";\n";
+        o << "      if (o_ < 0 || o_ + (i64)" << rows - 1 << " * A.s3[" << p << "] + (i64)" << cols - 1 << " * A.s4[" << p
+          << "] >= A.span[" << p << "]) { *A.err = 2; o_ = 0; }\n";
+        o << "      po." << field << " = o_; }\n";
+    };
+    checked(d.kt, d.d, d.pg, "k");
+    checked(d.v, d.pg, d.d, "v");
+    if (d.mask >= 0) checked(d.mask, 1, d.pg, "m");
+    else o << "    po.m = 0;\n";
+    o << "  };\n";
+    o << "  auto f_bases = [&](const PageOffs& po, const u16*& kp, const u16*& vp, const float*& mp) {\n";
+    o << "    kp = reinterpret_cast<const u16*>(A.base[" << d.kt << "] + po.k * 2);\n";
+    o << "    vp = reinterpret_cast<const u16*>(A.base[" << d.v << "] + po.v * 2);\n";
+    if (d.mask >= 0) o << "    mp = reinterpret_cast<const float*>(A.base[" << d.mask << "] + po.m * 4);\n";
+    else o << "    mp = nullptr;\n";
+    o << "  };\n";
+    // q tile of unit u (null, with error 2, when it falls outside q).
+    o << "  auto f_q = [&](int u) -> const u16* {\n";
+    o << "    i64 vars[" << nvars << "];\n";
     decode_vars("u", "    ");
     o << "    vars[" << ng << "] = 0;\n";
-    o << "    {\n";
-    o << "      bool bad = false;\n";
+    o << "    bool bad = false;\n";
     unit_check(d.q, d.g, d.d, "bad");
-    o << "      DW::State st;\n";
-    o << "      DW::init(st);\n";
-    o << "      if (!bad) {\n";
-    o << "        u32x4 qa[DW::NS];\n";
-    o << "        DW::load_q(qa, " << ptr(d.q, "const u16*", 2) << ", A.s3[" << d.q << "]);\n";
-    // Sub-runs of at most 64 pages: lane i holds page c0+i's indirect indices.
-    std::vector<int> page_terms;
-    for (int p : {d.kt, d.v, d.mask})
-        if (p >= 0)
-            for (int t = 0; t < nterms(p); ++t) page_terms.push_back(first_term[p] + t);
-    o << "        for (i64 c0 = s - su; c0 < e - su; c0 += 64) {\n";
-    o << "          const i64 c1 = c0 + 64 < e - su ? c0 + 64 : e - su;\n";
-    if (!page_terms.empty()) {
-        o << "          i64 vl[" << nvars << "];\n";
-        o << "          for (int i = 0; i < " << nvars << "; ++i) vl[i] = vars[i];\n";
-        o << "          { const i64 pl = c0 + lane; vl[" << ng << "] = pl < c1 ? pl : c1 - 1; }\n";
-        for (int kk : page_terms)
-            o << "          const int iv" << kk << " = static_cast<int>(indirect_value(A, " << kk << ", vl, " << nvars << "));\n";
-    }
-    // Page bases with a bounds check; an out-of-range page raises the error
-    // flag and reads the tensor's first page instead.
-    auto page_off = [&](int p) {
-        std::ostringstream e;
-        e << "(i64)0";
-        for (int v = 0; v < nvars; ++v) e << " + A.coef[" << p << "][" << v << "] * vars[" << v << "]";
-        for (int t = 0; t < nterms(p); ++t) {
-            const int kk = first_term[p] + t;
-            e << " + A.ind[" << kk << "].stride * (i64)__builtin_amdgcn_readlane(iv" << kk << ", static_cast<int>(pg - c0))";
-        }
-        return e.str();
-    };
-    auto checked = [&](int p, int rows, int cols, const std::string& var) {
-        o << "            i64 " << var << " = " << page_off(p) << ";\n";
-        o << "            if (" << var << " < 0 || " << var << " + (i64)" << rows - 1 << " * A.s3[" << p << "] + (i64)" << cols - 1
-          << " * A.s4[" << p << "] >= A.span[" << p << "]) { *A.err = 2; " << var << " = 0; }\n";
-    };
-    o << "          auto ptrs = [&](i64 pg, const u16*& kp, const u16*& vp, const float*& mp) {\n";
-    o << "            vars[" << ng << "] = pg;\n";
-    checked(d.kt, d.d, d.pg, "ok");
-    checked(d.v, d.pg, d.d, "ov");
-    o << "            kp = reinterpret_cast<const u16*>(A.base[" << d.kt << "] + ok * 2);\n";
-    o << "            vp = reinterpret_cast<const u16*>(A.base[" << d.v << "] + ov * 2);\n";
-    if (d.mask >= 0) {
-        checked(d.mask, 1, d.pg, "om");
-        o << "            mp = reinterpret_cast<const float*>(A.base[" << d.mask << "] + om * 4);\n";
-    } else {
-        o << "            mp = nullptr;\n";
-    }
-    o << "          };\n";
-    o << "          DW::fold(st, c0, c1, qa, " << scale.str() << ", ptrs, A.s4[" << d.kt << "], A.s3[" << d.v << "], lds);\n";
-    o << "        }\n";
-    o << "        vars[" << ng << "] = 0;\n";
-    o << "      }\n";
-    // Partial, then the unit's completion.
-    o << "      const i64 wf = DecodeSplit::wave_of(su, T, W), wl = DecodeSplit::wave_of(eu - 1, T, W);\n";
-    o << "      const int parts = static_cast<int>(wl - wf + 1);\n";
-    o << "      DW::store(st, partials + (u + w) * DW::kPartFloats);\n";
-    o << "      publish();\n";
-    o << "      const bool last = parts == 1 || arrive(cnt + u, parts);\n";
-    o << "      if (last) {\n";
-    o << "        bool bad_acc = false;\n";
+    o << "    return bad ? nullptr : " << ptr(d.q, "const u16*", 2) << ";\n";
+    o << "  };\n";
+    o << "  auto f_slot = [&](int u) { return partials + ((i64)u + w) * DW::kPartFloats; };\n";
+    // Folds unit u's partials (slots first .. first+parts-1, in page order)
+    // into its accumulators.
+    o << "  auto f_combine = [&](int u, int parts, i64 first) {\n";
+    o << "    i64 vars[" << nvars << "];\n";
+    decode_vars("u", "    ");
+    o << "    vars[" << ng << "] = 0;\n";
+    o << "    bool bad_acc = false;\n";
     unit_check(d.m, d.g, 1, "bad_acc");
     unit_check(d.l, d.g, 1, "bad_acc");
     unit_check(d.o, d.g, d.d, "bad_acc");
-    o << "        if (!bad_acc)\n";
-    o << "          DecodeCombine<" << d.g << ", " << d.d << ">::run(parts, partials + (u + wf) * DW::kPartFloats, DW::kPartFloats, "
+    o << "    if (!bad_acc)\n";
+    o << "      DecodeCombine<" << d.g << ", " << d.d << ">::run(parts, partials + first * DW::kPartFloats, DW::kPartFloats, "
       << ptr(d.m, "float*", 4) << ", A.s3[" << d.m << "], " << ptr(d.l, "float*", 4) << ", A.s3[" << d.l << "], "
       << ptr(d.o, "float*", 4) << ", A.s3[" << d.o << "], A.s4[" << d.o << "]);\n";
-    o << "        if (parts > 1) reset_count(cnt + u);\n";
-    o << "      }\n";
-    o << "    }\n";
-    o << "    s = e;\n";
-    o << "    if (s >= b) break;\n";
-    o << "    ++u;\n";
-    o << "    while (__builtin_amdgcn_readfirstlane(pre[u + 1]) <= s) ++u;\n";
-    o << "  }\n";
+    o << "  };\n";
+    o << "  auto fns = decode_fns(f_page, f_bases, f_q, f_slot, f_combine);\n";
+    o << "  DecodeStream<DW, " << kDecodePageRing << ">::run(fns, pre, cpre, U, TC, W, w, s, b, cnt, " << scale.str() << ", A.s4[" << d.kt
+      << "], A.s3[" << d.v << "], A.s3[" << d.q << "], lds);\n";
     o << "}\n";
     ek.source = o.str();
-    ek.entry = "ptowsp_entry";
     ek.lds_bytes = static_cast<size_t>(4 * (d.g * 16 + 16) * 4 + (kDecodeMaxUnits + 1 + 4) * 4);
     return ek;
 }

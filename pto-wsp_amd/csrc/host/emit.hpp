@@ -36,6 +36,8 @@ struct EmitSpec {
 // Units (grid tasks) of one decode launch at most: every block holds their
 // page-count prefix in LDS (DecodeSplit::kMaxUnits on the device).
 constexpr int kDecodeMaxUnits = 4096;
+// Scheduling cost of starting a unit, in pages (DecodeSplit::kUnitCost).
+constexpr int kDecodeUnitCost = 3;
 
 // Waves of a GEMM block: 2 along M, 4 along N for 256-wide blocks, else 2.
 inline int gemm_waves_n(int bn) { return bn >= 256 ? 4 : 2; }

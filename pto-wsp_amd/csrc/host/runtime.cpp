@@ -430,7 +430,8 @@ bool decode_allowed(const KernelAnalysis& a, const LaunchSpec& L, const LaunchAr
     const int64_t maxp = ax.kind == AxisKind::DynTensor ? ax.max : A.ext[ng];
     int64_t units = 1;
     for (int v = 0; v < ng; ++v) units *= A.ext[v];
-    if (units < 1 || units > kDecodeMaxUnits || maxp < 0 || maxp >= (int64_t(1) << 31) / units) return false;
+    // Page and cost prefixes (pages + kDecodeUnitCost per unit) stay below 2^31.
+    if (units < 1 || units > kDecodeMaxUnits || maxp < 0 || maxp + kDecodeUnitCost >= (int64_t(1) << 31) / units) return false;
     const DecodeInfo& d = a.decode;
     const int nvars = ng + 1;
     const int ntens = static_cast<int>(a.tensor_param_index.size());
@@ -633,25 +634,40 @@ const EmittedKernel& emitted_for(ptowsp_program* P, int li, const EmitSpec& spec
     return c.emitted.emplace(key, std::move(ek)).first->second;
 }
 
-// Blocks of `f` (256 threads) resident on the whole GPU at once.
-int64_t resident_blocks(hipFunction_t f) {
+// Launch shape of a decode kernel: one 256-thread block per CU.  The
+// dynamic LDS reserved per block is just over half a CU's LDS beyond the
+// kernel's own, so that no second block fits on a CU.
+struct DecodeShape {
+    int64_t blocks = 1;
+    unsigned dyn_lds = 0;
+};
+DecodeShape decode_shape(hipFunction_t f) {
     static std::mutex mu;
-    static std::map<std::pair<int, hipFunction_t>, int64_t> memo;
+    static std::map<std::pair<int, hipFunction_t>, DecodeShape> memo;
     int dev = 0;
     check(hipGetDevice(&dev), "hipGetDevice");
     std::lock_guard<std::mutex> lock(mu);
     auto it = memo.find({dev, f});
     if (it != memo.end()) return it->second;
-    int per_cu = 0, cus = 0;
+    int cus = 0, lds_cu = 0, lds_static = 0;
     check(hipDeviceGetAttribute(&cus, hipDeviceAttributeMultiprocessorCount, dev), "hipDeviceGetAttribute");
-    check(hipModuleOccupancyMaxActiveBlocksPerMultiprocessor(&per_cu, f, 256, 0), "hipModuleOccupancyMaxActiveBlocksPerMultiprocessor");
-    const int64_t r = std::max<int64_t>(1, static_cast<int64_t>(per_cu) * cus);
+    check(hipDeviceGetAttribute(&lds_cu, hipDeviceAttributeMaxSharedMemoryPerMultiprocessor, dev), "hipDeviceGetAttribute");
+    check(hipFuncGetAttribute(&lds_static, HIP_FUNC_ATTRIBUTE_SHARED_SIZE_BYTES, f), "hipFuncGetAttribute");
+    DecodeShape r;
+    const int half = lds_cu / 2 + 1024;
+    r.dyn_lds = static_cast<unsigned>(std::max(0, half - lds_static));
+    int per_cu = 0;
+    check(hipModuleOccupancyMaxActiveBlocksPerMultiprocessor(&per_cu, f, 256, r.dyn_lds),
+          "hipModuleOccupancyMaxActiveBlocksPerMultiprocessor");
+    if (per_cu != 1)
+        throw std::runtime_error("decode launch: expected one resident block per CU, occupancy reports " + std::to_string(per_cu));
+    r.blocks = std::max<int64_t>(1, cus);
     memo[{dev, f}] = r;
     return r;
 }
 
 // One launch of the balanced decode kernel (emit_decode): one block per
-// resident slot.  The program's scratch starts with kDecodeMaxUnits int32
+// CU.  The program's scratch starts with kDecodeMaxUnits int32
 // counters, zeroed when the scratch is allocated and left at zero by every
 // launch; the partials follow, one slot per (unit, wave) pair: units + waves
 // slots.
@@ -662,7 +678,8 @@ void enqueue_decode(ptowsp_program* P, int li, BuiltLaunch& B, const EmittedKern
     const int ng = static_cast<int>(L.grid.size());
     const Axis& ax = *L.inner[0].axis;
     const int64_t maxp = std::max<int64_t>(0, ax.kind == AxisKind::DynTensor ? ax.max : B.args.ext[ng]);
-    const int64_t grid = resident_blocks(jk.function);
+    const DecodeShape shape = decode_shape(jk.function);
+    const int64_t grid = shape.blocks;
     const int64_t waves = 4 * grid;
     const size_t count_bytes = static_cast<size_t>(kDecodeMaxUnits) * sizeof(int32_t);
     const size_t part_bytes = static_cast<size_t>(B.ntasks + waves) * static_cast<size_t>(ek.part_floats) * sizeof(float);
@@ -682,7 +699,8 @@ void enqueue_decode(ptowsp_program* P, int li, BuiltLaunch& B, const EmittedKern
     B.args.span[ntens] = static_cast<int64_t>(need / sizeof(float));
     B.args.scal[kMaxScalars - 1] = static_cast<uint64_t>(maxp);
     void* params[] = {&B.args};
-    check(hipModuleLaunchKernel(jk.function, static_cast<unsigned>(grid), 1, 1, 256, 1, 1, 0, stream, params, nullptr),
+    check(hipModuleLaunchKernel(jk.function, static_cast<unsigned>(grid), 1, 1, 256, 1, 1, shape.dyn_lds, stream, params,
+                                nullptr),
           "hipModuleLaunchKernel(decode)");
     launches += 1;
 }

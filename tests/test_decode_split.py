@@ -1,16 +1,22 @@
 """Index math of the balanced decode split (DecodeSplit in
-pto-wsp_amd/csrc/device/ptowsp_device.h and the wave loop emitted by
+pto-wsp_amd/csrc/device/ptowsp_device.h and the wave ranges emitted by
 emit_decode in pto-wsp_amd/csrc/host/emit.cpp), checked by brute force.
 
-Wave w of W = min(resident waves, T) folds global pages [w*T/W, (w+1)*T/W)
-of the T pages of all units laid end to end (so each active wave holds at
-least one page); a wave writes the partial of unit u into slot u + w, and unit u's
-partials are the slots u + wave_of(pre[u]) .. u + wave_of(pre[u+1]-1).  The
-checks: every page is folded exactly once, slots are distinct and below
-U + W, each unit's slots are consecutive and as many as the waves that touch
-it (the count its completion counter waits for)."""
+Units' pages are laid end to end (page prefix pre) and so are their
+scheduling costs (cost prefix cpre: a non-empty unit costs its pages plus
+UNIT_COST leading positions that hold no page).  Wave w of W = min(resident
+waves, TC) owns cost positions [w*TC/W, (w+1)*TC/W), i.e. the pages
+[page_at(w*TC/W), page_at((w+1)*TC/W)); a wave writes the partial of unit u
+into slot u + w, and unit u's partials are the slots u + wf .. u + wl, wf and
+wl the waves of the cost positions of its first and last page.  The checks:
+every page is folded exactly once, slots are distinct and below U + W, each
+unit's slots are consecutive and as many as the waves that touch it (the
+count its completion counter waits for), and the cost split bounds every
+wave's pages plus unit starts."""
 import numpy as np
 import pytest
+
+UNIT_COST = 3
 
 
 def wave_of(p, T, W):
@@ -28,16 +34,33 @@ def unit_of(pre, U, s):
     return lo
 
 
-def walk(counts, W):
-    """The emitted wave loop: yields (wave, unit, first page, end page)."""
-    U = len(counts)
-    pre = [0]
+def cost(n):
+    return n + UNIT_COST if n > 0 else 0
+
+
+def prefixes(counts):
+    pre, cpre = [0], [0]
     for n in counts:
         pre.append(pre[-1] + n)
-    T = pre[U]
-    W = min(W, T)  # active waves: each holds at least one page
+        cpre.append(cpre[-1] + cost(n))
+    return pre, cpre
+
+
+def page_at(pre, cpre, U, v):
+    if v >= cpre[U]:
+        return pre[U]
+    u = unit_of(cpre, U, v)
+    return pre[u] + max(0, v - cpre[u] - UNIT_COST)
+
+
+def walk(counts, W):
+    """The emitted wave ranges and DecodeStream's unit walk: yields (wave, unit, first page, end page)."""
+    U = len(counts)
+    pre, cpre = prefixes(counts)
+    TC = cpre[U]
+    W = min(W, TC)  # active waves: no empty cost range
     for w in range(W):
-        s, b = w * T // W, (w + 1) * T // W
+        s, b = page_at(pre, cpre, U, w * TC // W), page_at(pre, cpre, U, (w + 1) * TC // W)
         if s >= b:
             continue
         u = unit_of(pre, U, s)
@@ -56,12 +79,13 @@ def walk(counts, W):
 
 def check(counts, W):
     U = len(counts)
-    pre = np.concatenate([[0], np.cumsum(counts)]).tolist()
-    T = pre[-1]
-    W = min(W, T)
+    pre, cpre = prefixes(counts)
+    TC = cpre[U]
+    W = min(W, TC)
     seen = [np.zeros(n, dtype=np.int64) for n in counts]
     slots = {}
     per_unit = {}
+    load = {}
     for w, u, p0, p1 in walk(counts, W):
         assert 0 <= p0 < p1 <= counts[u]
         seen[u][p0:p1] += 1
@@ -69,13 +93,17 @@ def check(counts, W):
         assert 0 <= slot < U + W and slot not in slots
         slots[slot] = (w, u)
         per_unit.setdefault(u, []).append(slot)
+        load[w] = load.get(w, 0) + (p1 - p0) + (UNIT_COST if p0 == 0 else 0)
     for u in range(U):
         assert (seen[u] == 1).all(), u
         if counts[u] == 0:
             assert u not in per_unit
             continue
-        wf, wl = wave_of(pre[u], T, W), wave_of(pre[u + 1] - 1, T, W)
+        wf, wl = wave_of(cpre[u] + UNIT_COST, TC, W), wave_of(cpre[u + 1] - 1, TC, W)
         assert per_unit[u] == list(range(u + wf, u + wl + 1)), (u, per_unit[u], wf, wl)
+    # a wave's pages plus the units it starts never exceed its cost range
+    for w, c in load.items():
+        assert c <= (w + 1) * TC // W - w * TC // W + UNIT_COST, (w, c)
     return len(slots)
 
 

@@ -342,6 +342,24 @@ def test_paged_decode_family(gpu, lengths, hkv, group, d):
     assert prog.stats.total_cycles == ref.total_cycles and prog.stats.task_count == ref.task_count
 
 
+def test_paged_decode_long_streams(gpu):
+    """Thousands of pages: every wave folds a long stream of pages that crosses
+    unit and page-table-run boundaries, mixing long units (split over several
+    waves, completed by the last arriver), units shorter than the page ring,
+    and an empty sequence (its accumulators stay untouched)."""
+    lengths = [8192, 1, 0, 17, 5000, 40, 16, 3000, 7777, 2, 600, 4096, 33, 2500]
+    prog, ref, ga, ca = _decode_case(lengths, 8, 4, 128, seed=11)
+    assert prog._native.kernel_family("decode_page") == "decode"
+    assert ref.task_count > 8 * 1024
+    for k in ("m", "l", "o", "out"):
+        np.testing.assert_allclose(ga[k], ca[k], rtol=2e-5, atol=2e-5 * float(np.abs(ca[k][np.isfinite(ca[k])]).max()),
+                                   err_msg=k)
+    assert np.all(ga["m"][2] == -np.inf) and np.all(ga["l"][2] == 0) and np.all(ga["o"][2] == 0)
+    live = np.asarray(lengths) > 0
+    assert _rel_fro(ga["out"][live], W.paged_decode_ref(ga)[live]) <= 1e-5
+    assert prog.stats.total_cycles == ref.total_cycles and prog.stats.task_count == ref.task_count
+
+
 def test_paged_decode_sixteen_rows(gpu):
     """16 query rows fill every MFMA column.  Unmasked it is the decode family; with
     the [1,16] mask on a square [16,16] score tile the reference's broadcast rule

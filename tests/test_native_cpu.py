@@ -86,7 +86,8 @@ def test_emitted_kernels_build_for_gfx950(name):
     prog = NativeProgram(workload_to_codegen_ir(make(), name).module)
     assert prog.num_launches() >= 1
     src = prog.precompile(0)
-    assert "ptowsp_entry" in src
+    assert re.search(r"__global__ void __launch_bounds__\(\d+\) (__attribute__\(\(\w+\(\d+(, \d+)?\)\)\) )?"
+                     r"ptowsp_(row|tile|gemm|decode)_\w+\(", src)
 
 
 @pytest.mark.parametrize("name", ["rmsnorm", "softmax3", "bgemm_f16"])

@@ -390,6 +390,8 @@ def paged_decode_ref(arrs: dict) -> np.ndarray:
     out = np.zeros((B, Hkv, G, D))
     for b in range(B):
         L = int(arrs["lengths"][b])
+        if L == 0:
+            continue  # no tokens: no softmax (left at zero)
         n = (L + page - 1) // page
         pages = arrs["page_table"][b, :n]
         k = kc[pages].transpose(1, 0, 2, 3).reshape(Hkv, n * page, D)[:, :L]
