@@ -931,7 +931,6 @@ struct DecodeStream {
         PageOffs rc, rn;
         f.page(s + lane < b ? s + lane : b - 1, rc);
         rn = rc;
-        if (s + 64 < b) f.page(s + 64 + lane < b ? s + 64 + lane : b - 1, rn);
         auto load = [&](typename DW::Page& pg, i64 g) {
             const bool real = g < b;
             const int i = static_cast<int>((real ? g : b - 1) - r0);
@@ -948,6 +947,11 @@ struct DecodeStream {
             // step waits for the same number of loads), from one 16-byte line.
             DW::load_page(pg, kp, vp, mp, real ? ln : dummy);
         };
+        // The first pages go out before anything else is read.
+        typename DW::Page pg[NB];
+#pragma unroll
+        for (int i = 0; i < NB - 1; ++i) load(pg[i], s + i);
+        if (s + 64 < b) f.page(s + 64 + lane < b ? s + 64 + lane : b - 1, rn);
         // Unit state.
         int u = DecodeSplit::unit_of(pre, U, s);
         u = __builtin_amdgcn_readfirstlane(u);
@@ -975,9 +979,6 @@ struct DecodeStream {
         }
         Pending pd;
         pd.phase = 0;
-        typename DW::Page pg[NB];
-#pragma unroll
-        for (int i = 0; i < NB - 1; ++i) load(pg[i], s + i);
         for (i64 g = s;; g += NB) {
 #pragma unroll
             for (int i = 0; i < NB; ++i) {

@@ -581,12 +581,14 @@ EmittedKernel emit_decode(const Module& m, const KernelAnalysis& a, const Launch
     o << "#include \"ptowsp_device.h\"\nusing namespace ptowsp;\n";
     o << "// decode program: kernel " << k.name << ", " << d.g << " query rows, head dim " << d.d << (d.f16 ? " f16" : " bf16")
       << (d.mask >= 0 ? ", masked" : "") << ", pages balanced over the resident waves\n";
+    // Grid variables of a unit.  Units number at most kDecodeMaxUnits, so
+    // every grid extent and unit index fits 32-bit unsigned arithmetic.
     auto decode_vars = [&](const std::string& unit, const std::string& ind) {
         if (ng == 0) return;
-        o << ind << "{ i64 q_ = " << unit << ";\n";
+        o << ind << "{ u32 q_ = static_cast<u32>(" << unit << ");\n";
         for (int v = ng - 1; v >= 1; --v)
-            o << ind << "  vars[" << v << "] = q_ % A.ext[" << v << "]; q_ /= A.ext[" << v << "];\n";
-        o << ind << "  vars[0] = q_; }\n";
+            o << ind << "  { const u32 e_ = static_cast<u32>(A.ext[" << v << "]); vars[" << v << "] = (i64)(q_ % e_); q_ /= e_; }\n";
+        o << ind << "  vars[0] = (i64)q_; }\n";
     };
     auto ptr = [&](int p, const std::string& type, int esize) {
         return "reinterpret_cast<" + type + ">(A.base[" + std::to_string(p) + "] + (" +
