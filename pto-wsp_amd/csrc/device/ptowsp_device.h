@@ -1040,8 +1040,10 @@ struct DecodeCombine {
             mm[g] = mn;
         }
     }
+    // Folds nch partials (page order) into the unit's accumulators; with out
+    // non-null also writes out = o / l (the normalisation launch folded in).
     __device__ static void run(i64 nch, const float* part, i64 pstride, float* m, i64 ms3, float* l, i64 ls3, float* o,
-                               i64 os3, i64 os4) {
+                               i64 os3, i64 os4, float* out, i64 us3, i64 us4) {
         const int lane = threadIdx.x & 63;
         float mm[G], ll[G], oo[G][DPL];
 #pragma unroll
@@ -1088,6 +1090,23 @@ struct DecodeCombine {
             }
 #pragma unroll
             for (int j = 0; j < DPL; ++j) o[g * os3 + part_dim<D>(DPL * lane + j) * os4] = oo[g][j];
+            if (out) {
+#pragma unroll
+                for (int j = 0; j < DPL; ++j) out[g * us3 + part_dim<D>(DPL * lane + j) * us4] = oo[g][j] / ll[g];
+            }
+        }
+    }
+    // out = o / l of a unit no page folds into (its accumulators as they are).
+    __device__ static void normalize(const float* o, i64 os3, i64 os4, const float* l, i64 ls3, float* out, i64 us3, i64 us4) {
+        const int lane = threadIdx.x & 63;
+#pragma unroll
+        for (int g = 0; g < G; ++g) {
+            const float lg = l[g * ls3];
+#pragma unroll
+            for (int j = 0; j < DPL; ++j) {
+                const int d = DPL * lane + j;
+                out[g * us3 + d * us4] = o[g * os3 + d * os4] / lg;
+            }
         }
     }
 };

@@ -157,6 +157,40 @@ GemmInfo classify_gemm(const KernelDef& k, const KernelAnalysis& a) {
     return g;
 }
 
+// Recognizes store(out, div(o, l)) over params (see NormInfo).
+NormInfo classify_norm(const KernelDef& k, const KernelAnalysis& a) {
+    NormInfo info;
+    const OpInfo *div = nullptr, *store = nullptr;
+    size_t div_index = 0;
+    for (size_t i = 0; i < k.ops.size(); ++i) {
+        const OpInfo& op = k.ops[i];
+        if (op.kind == OpKind::Div && !div) {
+            div = &op;
+            div_index = i;
+        } else if (op.kind == OpKind::Store && !store) {
+            store = &op;
+        } else {
+            return info;
+        }
+    }
+    if (!div || !store || div->operands.size() != 2 || store->operands.size() != 2) return info;
+    if (store->operands[1] != div->result || div_index >= a.bin_mode.size() || a.bin_mode[div_index] != BinMode::RowExpand)
+        return info;
+    auto param = [&](int id) { return id >= 0 && id < static_cast<int>(a.param_of.size()) ? a.param_of[id] : -1; };
+    const int po = param(div->operands[0]), pl = param(div->operands[1]), pout = param(store->operands[0]);
+    if (po < 0 || pl < 0 || pout < 0 || po == pout || pl == pout) return info;
+    const ValueInfo *o = a.by_id[k.params[po].id], *l = a.by_id[k.params[pl].id], *out = a.by_id[k.params[pout].id];
+    if (o->dtype != DType::F32 || l->dtype != DType::F32 || out->dtype != DType::F32) return info;
+    if (l->rows != o->rows || l->cols != 1 || out->rows != o->rows || out->cols != o->cols) return info;
+    info.ok = true;
+    info.o = a.tensor_ordinal[po];
+    info.l = a.tensor_ordinal[pl];
+    info.out = a.tensor_ordinal[pout];
+    info.g = o->rows;
+    info.d = o->cols;
+    return info;
+}
+
 // Recognizes the online-softmax decode step (see DecodeInfo) by its dataflow,
 // starting from the three accumulator stores.  Binary ops may take their
 // operands in either order; every non-constant op must belong to the pattern.
@@ -529,6 +563,7 @@ KernelAnalysis analyze_kernel(const KernelDef& k) {
     }
     if (classify_rows(k, a)) {
         a.family = Family::RowProgram;
+        a.norm = classify_norm(k, a);
     } else {
         a.gemm = classify_gemm(k, a);
         a.decode = a.gemm.ok ? DecodeInfo{} : classify_decode(k, a);

@@ -42,6 +42,17 @@ struct DecodeInfo {
     float scale = 1.0f;                      // score scale (a Constant)
 };
 
+// out = o / l with o a [G,D] and l a [G,1] fp32 param (a row-broadcast
+// divide) stored to a [G,D] fp32 param: the normalisation that follows the
+// page loop of a decode workload.  Launched right after a decode launch
+// over the same grid and the same o / l views, it is applied by the decode
+// kernel to each unit it completes (bit for bit the same division).
+struct NormInfo {
+    bool ok = false;
+    int o = -1, l = -1, out = -1;  // tensor ordinals
+    int g = 0, d = 0;
+};
+
 struct KernelAnalysis {
     const KernelDef* def = nullptr;
     int max_id = 0;
@@ -64,6 +75,7 @@ struct KernelAnalysis {
     std::string not_row_reason;
     GemmInfo gemm;
     DecodeInfo decode;
+    NormInfo norm;
 };
 
 // Throws CompileError for kernels the reference lowering cannot compute.

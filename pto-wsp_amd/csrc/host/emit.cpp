@@ -665,6 +665,22 @@ EmittedKernel emit_decode(const Module& m, const KernelAnalysis& a, const Launch
     o << "    }\n";
     o << "    __syncthreads();\n";
     o << "  }\n";
+    if (spec.decode_norm) {
+        // The folded normalisation's output tile of a unit (slot ntens + 1,
+        // affine over the grid variables), with its bounds check.
+        const int q = ntens + 1;
+        std::ostringstream e;
+        e << "(i64)0";
+        for (int v = 0; v < ng; ++v) e << " + A.coef[" << q << "][" << v << "] * vars[" << v << "]";
+        o << "  auto norm_check = [&](const i64* vars) {\n";
+        o << "    const i64 o_ = " << e.str() << ";\n";
+        o << "    if (o_ < 0 || o_ + (i64)" << d.g - 1 << " * A.s3[" << q << "] + (i64)" << d.d - 1 << " * A.s4[" << q
+          << "] >= A.span[" << q << "]) { if (lane == 0) *A.err = 2; return false; }\n";
+        o << "    return true;\n";
+        o << "  };\n";
+        o << "  auto norm_ptr = [&](const i64* vars) { return reinterpret_cast<float*>(A.base[" << q << "] + (" << e.str()
+          << ") * 4); };\n";
+    }
     // Values read from LDS are wave-uniform: readfirstlane keeps the page
     // loop's control and addresses in scalar registers.
     o << "  const i64 TC = __builtin_amdgcn_readfirstlane(cpre[U]);\n";
@@ -672,10 +688,10 @@ EmittedKernel emit_decode(const Module& m, const KernelAnalysis& a, const Launch
     // range is empty and a unit's partials fill consecutive slots (a wave
     // whose range holds only cost positions, and no page, returns here).
     o << "  const i64 W = (i64)gridDim.x * 4 < TC ? (i64)gridDim.x * 4 : TC, w = (i64)blockIdx.x * 4 + wave;\n";
-    o << "  if (w >= W) return;\n";
+    o << "  if (w < W) {\n";
     o << "  const i64 s = DecodeSplit::page_at(pre, cpre, U, w * TC / W);\n";
     o << "  const i64 b = DecodeSplit::page_at(pre, cpre, U, (w + 1) * TC / W);\n";
-    o << "  if (s >= b) return;\n";
+    o << "  if (s < b) {\n";
     o << "  int* cnt = reinterpret_cast<int*>(A.base[" << ntens << "]);\n";
     o << "  float* partials = reinterpret_cast<float*>(A.base[" << ntens << "] + DecodeSplit::kMaxUnits * 4);\n";
     o << "  float* lds = lds_all[wave];\n";
@@ -724,14 +740,41 @@ EmittedKernel emit_decode(const Module& m, const KernelAnalysis& a, const Launch
     unit_check(d.m, d.g, 1, "bad_acc");
     unit_check(d.l, d.g, 1, "bad_acc");
     unit_check(d.o, d.g, d.d, "bad_acc");
+    if (spec.decode_norm) {
+        o << "    float* out_ = nullptr;\n";
+        o << "    if (!bad_acc) { if (!norm_check(vars)) bad_acc = true; else out_ = norm_ptr(vars); }\n";
+    }
     o << "    if (!bad_acc)\n";
     o << "      DecodeCombine<" << d.g << ", " << d.d << ">::run(parts, partials + first * DW::kPartFloats, DW::kPartFloats, "
       << ptr(d.m, "float*", 4) << ", A.s3[" << d.m << "], " << ptr(d.l, "float*", 4) << ", A.s3[" << d.l << "], "
-      << ptr(d.o, "float*", 4) << ", A.s3[" << d.o << "], A.s4[" << d.o << "]);\n";
+      << ptr(d.o, "float*", 4) << ", A.s3[" << d.o << "], A.s4[" << d.o << "], "
+      << (spec.decode_norm ? "out_, A.s3[" + std::to_string(ntens + 1) + "], A.s4[" + std::to_string(ntens + 1) + "]"
+                           : std::string("nullptr, 0, 0"))
+      << ");\n";
     o << "  };\n";
     o << "  auto fns = decode_fns(f_page, f_bases, f_q, f_slot, f_combine);\n";
     o << "  DecodeStream<DW, " << kDecodePageRing << ">::run(fns, pre, cpre, U, TC, W, w, s, b, cnt, " << scale.str() << ", A.s4[" << d.kt
       << "], A.s3[" << d.v << "], A.s3[" << d.q << "], lds);\n";
+    o << "  }\n";
+    o << "  }\n";
+    if (spec.decode_norm) {
+        const int q = ntens + 1;
+        // Units without pages are never completed by a wave: their output is
+        // the normalisation of the accumulators as they are.
+        o << "  for (int u = blockIdx.x * 4 + wave; u < U; u += gridDim.x * 4) {\n";
+        o << "    if (__builtin_amdgcn_readfirstlane(pre[u + 1]) != __builtin_amdgcn_readfirstlane(pre[u])) continue;\n";
+        o << "    i64 vars[" << nvars << "];\n";
+        decode_vars("u", "    ");
+        o << "    vars[" << ng << "] = 0;\n";
+        o << "    bool bad_acc = false;\n";
+        unit_check(d.l, d.g, 1, "bad_acc");
+        unit_check(d.o, d.g, d.d, "bad_acc");
+        o << "    if (bad_acc || !norm_check(vars)) continue;\n";
+        o << "    DecodeCombine<" << d.g << ", " << d.d << ">::normalize(" << ptr(d.o, "const float*", 4) << ", A.s3[" << d.o
+          << "], A.s4[" << d.o << "], " << ptr(d.l, "const float*", 4) << ", A.s3[" << d.l << "], norm_ptr(vars), A.s3["
+          << q << "], A.s4[" << q << "]);\n";
+        o << "  }\n";
+    }
     o << "}\n";
     ek.source = o.str();
     ek.lds_bytes = static_cast<size_t>(4 * (d.g * 16 + 16) * 4 + (kDecodeMaxUnits + 1 + 4) * 4);

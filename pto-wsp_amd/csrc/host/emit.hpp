@@ -31,6 +31,9 @@ struct EmitSpec {
     // Decode family (online softmax over pages): the in-kernel page loop of
     // every unit is split over the resident waves.
     bool decode = false;
+    // Decode: the next launch (a NormInfo kernel over the same grid and o / l
+    // views) is folded in; its output tensor is argument slot ntens + 1.
+    bool decode_norm = false;
 };
 
 // Units (grid tasks) of one decode launch at most: every block holds their

@@ -159,7 +159,16 @@ struct RunEnv {
     std::vector<TensorState> ts;
     std::vector<std::pair<std::string, int64_t>> host_vars;
     std::map<int, std::vector<int32_t>> idx_host;  // device index tensors read on the host, copied once per run
+    bool timing_started = false;                   // ev0 recorded (just before the first kernel)
 };
+
+// Device time starts at the program's first kernel: host work that precedes
+// it (building launch arguments, compiling) is not counted.
+void start_timing(RunEnv& E, hipStream_t stream) {
+    if (E.timing_started) return;
+    check(hipEventRecord(E.P->ev0, stream), "hipEventRecord");
+    E.timing_started = true;
+}
 
 int64_t axis_extent(RunEnv& E, const Axis& a) {
     switch (a.kind) {
@@ -617,6 +626,7 @@ std::string spec_key(const EmitSpec& s) {
     std::ostringstream o;
     o << "vw" << s.vec_width << (s.serial ? ";serial" : "") << ";up" << s.row_up << (s.nontemporal ? ";nt" : "")
       << (s.gemm ? ";gemm" : "") << ";m" << s.gemm_vm << ";n" << s.gemm_vn << (s.decode ? ";dec" : "")
+      << (s.decode_norm ? ";norm" : "")
       << ";i";
     for (int c : s.indirect_count) o << c << ",";
     o << ";d";
@@ -671,8 +681,9 @@ DecodeShape decode_shape(hipFunction_t f) {
 // counters, zeroed when the scratch is allocated and left at zero by every
 // launch; the partials follow, one slot per (unit, wave) pair: units + waves
 // slots.
-void enqueue_decode(ptowsp_program* P, int li, BuiltLaunch& B, const EmittedKernel& ek, const JitKernel& jk,
-                    hipStream_t stream, uint64_t& launches) {
+void enqueue_decode(RunEnv& E, int li, BuiltLaunch& B, const EmittedKernel& ek, const JitKernel& jk, hipStream_t stream,
+                    uint64_t& launches) {
+    ptowsp_program* P = E.P;
     const LaunchSpec& L = P->plan.launches[li];
     const KernelAnalysis& a = P->ka[L.kernel];
     const int ng = static_cast<int>(L.grid.size());
@@ -699,16 +710,15 @@ void enqueue_decode(ptowsp_program* P, int li, BuiltLaunch& B, const EmittedKern
     B.args.span[ntens] = static_cast<int64_t>(need / sizeof(float));
     B.args.scal[kMaxScalars - 1] = static_cast<uint64_t>(maxp);
     void* params[] = {&B.args};
+    start_timing(E, stream);
     check(hipModuleLaunchKernel(jk.function, static_cast<unsigned>(grid), 1, 1, 256, 1, 1, shape.dyn_lds, stream, params,
                                 nullptr),
           "hipModuleLaunchKernel(decode)");
     launches += 1;
 }
 
-void enqueue_launch(RunEnv& E, int li, hipStream_t stream, uint64_t& launches) {
+void enqueue_built(RunEnv& E, int li, BuiltLaunch& B, hipStream_t stream, uint64_t& launches) {
     ptowsp_program* P = E.P;
-    BuiltLaunch B = build_launch(E, P->plan.launches[li]);
-    if (B.ntasks <= 0) return;
     const EmittedKernel& ek = emitted_for(P, li, B.spec);
     LaunchCache& c = P->cache[li];
     const std::string key = spec_key(B.spec);
@@ -721,7 +731,7 @@ void enqueue_launch(RunEnv& E, int li, hipStream_t stream, uint64_t& launches) {
         jk = it->second;
     }
     if (B.spec.decode) {
-        enqueue_decode(P, li, B, ek, *jk, stream, launches);
+        enqueue_decode(E, li, B, ek, *jk, stream, launches);
         return;
     }
     int64_t blocks;
@@ -735,15 +745,78 @@ void enqueue_launch(RunEnv& E, int li, hipStream_t stream, uint64_t& launches) {
     }
     blocks = std::max<int64_t>(1, std::min<int64_t>(blocks, int64_t(1) << 20));
     void* params[] = {&B.args};
+    start_timing(E, stream);
     check(hipModuleLaunchKernel(jk->function, static_cast<unsigned>(blocks), 1, 1, static_cast<unsigned>(ek.threads), 1, 1,
                                 0, stream, params, nullptr),
           "hipModuleLaunchKernel");
     ++launches;
 }
 
+void enqueue_launch(RunEnv& E, int li, hipStream_t stream, uint64_t& launches) {
+    BuiltLaunch B = build_launch(E, E.P->plan.launches[li]);
+    if (B.ntasks <= 0) return;
+    enqueue_built(E, li, B, stream, launches);
+}
+
+// Launch li on the decode path with launch lj, the next one in program
+// order, folded in when lj is a NormInfo kernel over the same grid, whose
+// o / l tiles are the decode accumulators' and whose output overlaps no
+// tensor of li.  Returns false (nothing launched) otherwise.
+bool enqueue_decode_folded(RunEnv& E, int li, int lj, hipStream_t stream, uint64_t& launches) {
+    ptowsp_program* P = E.P;
+    const LaunchSpec &Li = P->plan.launches[li], &Lj = P->plan.launches[lj];
+    const KernelAnalysis &ai = P->ka[Li.kernel], &aj = P->ka[Lj.kernel];
+    if (ai.family != Family::Decode || !aj.norm.ok || !Lj.inner.empty() || Lj.grid.size() != Li.grid.size()) return false;
+    if (aj.norm.g != ai.decode.g || aj.norm.d != ai.decode.d) return false;
+    const int ntens = static_cast<int>(ai.tensor_param_index.size());
+    if (ntens + 2 > kMaxParams) return false;
+    BuiltLaunch Bi = build_launch(E, Li);
+    if (!Bi.spec.decode || Bi.ntasks <= 0) return false;
+    BuiltLaunch Bj = build_launch(E, Lj);
+    if (Bj.ntasks != Bi.ntasks || Bj.spec.serial) return false;
+    for (int c : Bj.spec.indirect_count)
+        if (c != 0) return false;
+    const int ng = static_cast<int>(Li.grid.size());
+    for (int v = 0; v < ng; ++v)
+        if (Bi.args.ext[v] != Bj.args.ext[v]) return false;
+    auto same_view = [&](int pi, int pj) {
+        if (Bi.args.base[pi] != Bj.args.base[pj] || Bi.args.s3[pi] != Bj.args.s3[pj] || Bi.args.s4[pi] != Bj.args.s4[pj])
+            return false;
+        for (int v = 0; v < ng; ++v)
+            if (Bi.args.coef[pi][v] != Bj.args.coef[pj][v]) return false;
+        return true;
+    };
+    if (!same_view(ai.decode.o, aj.norm.o) || !same_view(ai.decode.l, aj.norm.l)) return false;
+    const int tout = Lj.targs[aj.norm.out]->tid;
+    const TensorState& To = E.ts[tout];
+    const char* out_lo = To.dev;
+    const char* out_hi = To.dev + To.span * 4;
+    for (int p = 0; p < ntens; ++p) {
+        const int t = Li.targs[p]->tid;
+        const TensorState& T = E.ts[t];
+        const size_t es = dtype_size(P->m.tensors[t].dtype);
+        if (t == tout || (T.dev < out_hi && out_lo < T.dev + T.span * static_cast<int64_t>(es))) return false;
+    }
+    const int q = ntens + 1, pj = aj.norm.out;
+    Bi.args.base[q] = Bj.args.base[pj];
+    Bi.args.span[q] = Bj.args.span[pj];
+    Bi.args.s3[q] = Bj.args.s3[pj];
+    Bi.args.s4[q] = Bj.args.s4[pj];
+    for (int v = 0; v < kMaxVars; ++v) Bi.args.coef[q][v] = v < ng ? Bj.args.coef[pj][v] : 0;
+    Bi.spec.decode_norm = true;
+    enqueue_built(E, li, Bi, stream, launches);
+    return true;
+}
+
 void run_items(RunEnv& E, const std::vector<PlanItem>& items, hipStream_t stream, uint64_t& launches) {
-    for (const auto& it : items) {
+    for (size_t i = 0; i < items.size(); ++i) {
+        const PlanItem& it = items[i];
         if (!it.is_loop) {
+            if (i + 1 < items.size() && !items[i + 1].is_loop &&
+                enqueue_decode_folded(E, it.launch, items[i + 1].launch, stream, launches)) {
+                ++i;
+                continue;
+            }
             enqueue_launch(E, it.launch, stream, launches);
             continue;
         }
@@ -1017,8 +1090,8 @@ int ptowsp_hip_launch(ptowsp_program* P, RuntimeContext* ctx, void* hip_stream, 
         resolve_tensors(E, stream);
         const CycleResult cyc = cycles_for(E);
         uint64_t launches = 0;
-        check(hipEventRecord(P->ev0, stream), "hipEventRecord");
         run_items(E, P->plan.items, stream, launches);
+        start_timing(E, stream);
         check(hipEventRecord(P->ev1, stream), "hipEventRecord");
         check(hipGetLastError(), "kernel launch");
         P->stream = stream;

@@ -360,6 +360,28 @@ def test_paged_decode_long_streams(gpu):
     assert prog.stats.total_cycles == ref.total_cycles and prog.stats.task_count == ref.task_count
 
 
+def test_paged_decode_folds_the_normalisation(gpu):
+    """The out = o / l launch that follows the page loop runs inside the decode
+    kernel (one launch) with the same bits as the separate launch; written in
+    place (out is o) it overlaps the decode's own tensors and stays a launch."""
+    lengths = [300, 0, 77, 1]
+    prog, ref, ga, ca = _decode_case(lengths, 2, 4, 128, seed=4)
+    assert prog.stats.launches == 1
+    live = np.asarray(lengths) > 0
+    np.testing.assert_array_equal(ga["out"][live], ga["o"][live] / ga["l"][live])
+    for k in ("m", "l", "o", "out"):
+        np.testing.assert_allclose(ga[k], ca[k], rtol=2e-5, atol=2e-5 * float(np.abs(ca[k][np.isfinite(ca[k])]).max()),
+                                   err_msg=k)
+    assert np.isnan(ga["out"][1]).all() and np.isnan(ca["out"][1]).all()  # 0 / 0 for the empty sequence
+
+    ga = W.paged_decode_arrays(lengths, 2, 4, 128, seed=4)
+    ca = {k: v.copy() for k, v in ga.items()}
+    prog = run_hip(W.paged_decode(ga, out_key="o"))
+    run_workload(W.paged_decode(ca, out_key="o"))
+    assert prog.stats.launches == 2
+    np.testing.assert_allclose(ga["o"], ca["o"], rtol=2e-5, atol=2e-5 * float(np.abs(ca["o"][np.isfinite(ca["o"])]).max()))
+
+
 def test_paged_decode_sixteen_rows(gpu):
     """16 query rows fill every MFMA column.  Unmasked it is the decode family; with
     the [1,16] mask on a square [16,16] score tile the reference's broadcast rule

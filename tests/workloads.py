@@ -256,7 +256,7 @@ def attention_arrays(q, k, v, tile_seq):
 
 
 # ---------------------------------------------------------------- paged GQA decode (config 5)
-def paged_decode(arrs: dict, scale: float | None = None, masked: bool = True, dtype=BF16):
+def paged_decode(arrs: dict, scale: float | None = None, masked: bool = True, dtype=BF16, out_key: str = "out"):
     """flashinfer_decode over a paged KV cache: P(batch) x P(kv_head) x P.seq(pages).
 
     Per (b, g) the kernel folds one 16-token page into running (m, l, o) with
@@ -269,7 +269,8 @@ def paged_decode(arrs: dict, scale: float | None = None, masked: bool = True, dt
     arrs: q [B, Hkv, G, D] bf16 bits; k_cache, v_cache [P, Hkv, page, D] bf16 bits;
     page_table [B, max_pages] i32; npages [B] i32; mask [B, max_pages, 1, page] f32;
     m [B, Hkv, G, 1] f32 (-inf); l [B, Hkv, G, 1] f32 (0); o [B, Hkv, G, D] f32 (0);
-    out [B, Hkv, G, D] f32.
+    out [B, Hkv, G, D] f32.  out_key names the array the second launch writes
+    (out_key="o" normalises in place).
     """
     q, kc, vc = arrs["q"], arrs["k_cache"], arrs["v_cache"]
     B, Hkv, G, D = q.shape
@@ -282,7 +283,8 @@ def paged_decode(arrs: dict, scale: float | None = None, masked: bool = True, dt
 
     Q, KT, V = T(q, dtype), T(perm(kc, (0, 1, 3, 2)), dtype), T(vc, dtype)
     PT, NP = T(arrs["page_table"], I32), T(arrs["npages"], I32)
-    MASK, M, L, O, OUT = T(arrs["mask"]), T(arrs["m"]), T(arrs["l"]), T(arrs["o"]), T(arrs["out"])
+    MASK, M, L, O = T(arrs["mask"]), T(arrs["m"]), T(arrs["l"]), T(arrs["o"])
+    OUT = O if out_key == "o" else T(arrs[out_key])
 
     @kernel
     def decode_page(q: In[Tile[G, D, dtype]], k_t: In[Tile[D, page, dtype]], v: In[Tile[page, D, dtype]],
