@@ -356,7 +356,9 @@ __device__ inline i64 xcd_order(i64 w, i64 n) {
     return x * q + (x < r ? x : r) + l;
 }
 
-template <int BM, int BN, int BK, int WM, int WN, bool F16>
+// NS: LDS stages in the ring (DMA issued NS-1 stages ahead); KSPLIT: LDS
+// stages per task K step (a stage holds BK of the task's BK*KSPLIT columns).
+template <int BM, int BN, int BK, int WM, int WN, bool F16, int NS = 2, int KSPLIT = 1>
 struct GemmBlock {
     static constexpr int NW = WM * WN, NT = 64 * NW, KS = BK / 16;
     static constexpr int TM = BM / WM, TN = BN / WN, FI = TM / 32, FJ = TN / 32;
@@ -369,7 +371,9 @@ struct GemmBlock {
     static constexpr int ABLK = BM * BK * 2 / 1024, BBLK = BK * BN * 2 / 1024;
     static constexpr int AQ = (ABLK + NW - 1) / NW, BQ = (BBLK + NW - 1) / NW;
     static constexpr int ASZ = BM * BK, STAGE = ASZ + BK * BN;
-    static constexpr int kLdsElems = 2 * STAGE;
+    static constexpr int kLdsElems = NS * STAGE;
+    static constexpr int kStageOps = AQ + BQ;  // DMA instructions of one wave per stage
+    static_assert(NS == 2 || (NS == 4 && AQ * NW == ABLK && BQ * NW == BBLK), "stage ring: every wave moves the same share");
     static_assert(TM % 32 == 0 && TN % 32 == 0 && BK % 16 == 0 && (BK & (BK - 1)) == 0, "GEMM block shape");
     static_assert(BN >= 64 && BN <= 512 && (BM * BK * 2) % 1024 == 0 && (BK * BN * 2) % 1024 == 0, "GEMM block shape");
 
@@ -465,8 +469,53 @@ struct GemmBlock {
             }
     }
 
-    // K steps it0 .. iters-1; off(it, soa, sob) gives step it's byte offsets
-    // from the step-0 origins pa / pb.  ACC: the block starts from C.
+    // Writes the block (plus C when ADD_C) in the accumulator layout, one
+    // 32x32 accumulator at a time: the next accumulator's C is read while
+    // this one is added and stored, and scheduling barriers keep the
+    // accumulators apart so that few values sit in VGPRs at once.
+    template <bool ADD_C>
+    __device__ static void c_out(Acc& acc, buf_rsrc rc, int ldc) {
+        const int lane = threadIdx.x & 63, wave = wave_index();
+        const int wm = wave / WN, wn = wave % WN;
+        const int vc = ((lane >> 5) * 4 * ldc + (lane & 31)) * 4;
+        const int so = (wm * TM * ldc + wn * TN) * 4;
+        auto row = [&](int i, int e) { return so + (i * 32 + (e >> 2) * 8 + (e & 3)) * ldc * 4; };
+        float t[2][16];
+        auto fetch = [&](int n, float (&d)[16]) {
+            const int i = n / FJ, j = n % FJ;
+#pragma unroll
+            for (int e = 0; e < 16; ++e) d[e] = __uint_as_float(__builtin_amdgcn_raw_buffer_load_b32(rc, vc + j * 128, row(i, e), 2));
+        };
+        if constexpr (ADD_C) fetch(0, t[0]);
+#pragma unroll
+        for (int n = 0; n < FI * FJ; ++n) {
+            const int i = n / FJ, j = n % FJ;
+            if constexpr (ADD_C) {
+                if (n + 1 < FI * FJ) fetch(n + 1, t[(n + 1) & 1]);
+            }
+#pragma unroll
+            for (int e = 0; e < 16; ++e) {
+                const float x = ADD_C ? t[n & 1][e] + acc.v[i][j][e] : acc.v[i][j][e];
+                __builtin_amdgcn_raw_buffer_store_b32(__float_as_uint(x), rc, vc + j * 128, row(i, e), 2);
+            }
+            __builtin_amdgcn_sched_barrier(0);
+        }
+    }
+
+    // Waits until at most `ahead` stages of this wave's DMA are in flight.
+    __device__ static void wait_stages(i64 ahead) {
+        if constexpr (NS == 2) {
+            wait_vmcnt<0>();
+        } else {
+            if (ahead >= 2) wait_vmcnt<2 * kStageOps>();
+            else if (ahead == 1) wait_vmcnt<kStageOps>();
+            else wait_vmcnt<0>();
+        }
+    }
+
+    // Task K steps it0 .. iters-1, as (iters-it0)*KSPLIT LDS stages; off(it,
+    // soa, sob) gives task step it's byte offsets from the step-0 origins pa /
+    // pb.  The block sums A x B from zero; ACC: then adds C, as c + sum.
     template <bool ACC, class Off>
     __device__ static void run(u16* lds, const u16* pa, int lda, const u16* pb, int ldb, float* pc, int ldc, i64 it0,
                                i64 iters, Off off) {
@@ -475,30 +524,30 @@ struct GemmBlock {
         Offs o;
         offsets(o, lda, ldb);
         Acc acc;
-        if constexpr (ACC) {
-            c_io<false>(acc, rc, ldc);
-        } else {
 #pragma unroll
-            for (int i = 0; i < FI; ++i)
+        for (int i = 0; i < FI; ++i)
 #pragma unroll
-                for (int j = 0; j < FJ; ++j) acc.v[i][j] = f32x16{};
-        }
+            for (int j = 0; j < FJ; ++j) acc.v[i][j] = f32x16{};
+        const i64 nst = (iters - it0) * KSPLIT;
+        auto issue = [&](i64 st) {
+            int soa, sob;
+            off(it0 + st / KSPLIT, soa, sob);
+            const int h = static_cast<int>(st % KSPLIT);
+            load(lds + static_cast<int>(st & (NS - 1)) * STAGE, o, ra, soa + h * BK * 2, rb, sob + h * BK * ldb * 2);
+        };
         wait_vmcnt<0>();
         __syncthreads();  // the previous block's last stage reads are done
-        int soa, sob;
-        off(it0, soa, sob);
-        load(lds, o, ra, soa, rb, sob);
-        for (i64 it = it0; it < iters; ++it) {
-            wait_vmcnt<0>();
+#pragma unroll
+        for (int p = 0; p < NS - 1; ++p)
+            if (p < nst) issue(p);
+        for (i64 st = 0; st < nst; ++st) {
+            const i64 ahead = nst - 1 - st < NS - 2 ? nst - 1 - st : NS - 2;
+            wait_stages(ahead);
             __syncthreads();
-            const int cur = static_cast<int>((it - it0) & 1);
-            if (it + 1 < iters) {
-                off(it + 1, soa, sob);
-                load(lds + (cur ^ 1) * STAGE, o, ra, soa, rb, sob);
-            }
-            mma(acc, lds + cur * STAGE);
+            if (st + NS - 1 < nst) issue(st + NS - 1);
+            mma(acc, lds + static_cast<int>(st & (NS - 1)) * STAGE);
         }
-        c_io<true>(acc, rc, ldc);
+        c_out<ACC>(acc, rc, ldc);
     }
 };
 

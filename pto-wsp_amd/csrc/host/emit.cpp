@@ -484,7 +484,10 @@ EmittedKernel emit_gemm(const Module& m, const KernelAnalysis& a, const LaunchSp
     const int nvars = ng + ni;
     const int fm = spec.gemm_vm >= 0 ? 2 : 1, fn = spec.gemm_vn >= 0 ? 2 : 1;
     const int bm = g.m * fm, bn = g.n * fn;
+    // One LDS stage per task K step, two stages (a 4-stage ring of 32-wide
+    // stages measured slower on 256x256 blocks: twice the barriers).
     const int wm = gemm_waves_m(), wn = gemm_waves_n(bn);
+    const int bk = g.k, ns = 2, ksplit = 1;
     EmittedKernel ek;
     ek.threads = 64 * wm * wn;
     ek.row_program = false;
@@ -494,9 +497,10 @@ EmittedKernel emit_gemm(const Module& m, const KernelAnalysis& a, const LaunchSp
     o << "// gemm program: kernel " << k.name << ", task tile " << g.m << "x" << g.n << "x" << g.k << (g.f16 ? " f16" : " bf16")
       << (g.accumulate ? ", accumulate" : "") << "; block " << bm << "x" << bn << " (" << fm * fn << " tasks)\n";
     ek.entry = entry_name("gemm", k);
-    o << "extern \"C\" __global__ void __launch_bounds__(" << ek.threads << ") " << ek.entry << "(const LaunchArgs A) {\n";
-    o << "  typedef GemmBlock<" << bm << ", " << bn << ", " << g.k << ", " << wm << ", " << wn << ", "
-      << (g.f16 ? "true" : "false") << "> GB;\n";
+    o << "extern \"C\" __global__ void __launch_bounds__(" << ek.threads << ") "
+      << ek.entry << "(const LaunchArgs A) {\n";
+    o << "  typedef GemmBlock<" << bm << ", " << bn << ", " << bk << ", " << wm << ", " << wn << ", "
+      << (g.f16 ? "true" : "false") << ", " << ns << ", " << ksplit << "> GB;\n";
     o << "  __shared__ __attribute__((aligned(1024))) u16 lds[GB::kLdsElems];\n";
     o << "  i64 vars[" << (nvars > 0 ? nvars : 1) << "];\n  (void)vars;\n";
     o << "  const i64 nblk = A.ntasks / " << fm * fn << ";\n";
@@ -537,7 +541,7 @@ EmittedKernel emit_gemm(const Module& m, const KernelAnalysis& a, const LaunchSp
       << (g.accumulate ? "0" : "iters - 1") << ", iters, off);\n";
     o << "  }\n}\n";
     ek.source = o.str();
-    ek.lds_bytes = static_cast<size_t>(2 * (bm + bn) * g.k * 2);
+    ek.lds_bytes = static_cast<size_t>(ns * (bm + bn) * bk * 2);
     return ek;
 }
 
