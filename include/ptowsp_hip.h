@@ -86,7 +86,9 @@ int ptowsp_hip_kernel_family(const ptowsp_program* prog, const char* kernel);
  * `source`, valid until the next call.  flags bit 0: build the variant that
  * runs all tasks of a launch in program order (used when grid tasks write
  * overlapping memory); bit 1: build GEMM launches with 2x2 neighbouring tasks
- * of the last two grid loops merged into one workgroup block. */
+ * of the last two grid loops merged into one workgroup block; bit 2 (with bit
+ * 1): build merged 128x128 tasks with K step 32 or 64 as the two-group
+ * ping-pong GEMM block. */
 int ptowsp_hip_precompile(ptowsp_program* prog, int index, int flags, const char** source);
 
 /* Evaluates only the cpu_sim cycle model (total_cycles, task_count) for the

@@ -552,6 +552,244 @@ struct GemmBlock {
 };
 
 // ---------------------------------------------------------------------------
+// Ping-pong GEMM block: 256x256 C block, 8 waves in two groups of four
+// ---------------------------------------------------------------------------
+//
+// Same LDS layout, operand reads and accumulator layout as
+// GemmBlock<256, 256, BK, 2, 4>: wave w owns rows (w/4)*128..+127 and
+// columns (w%4)*64..+63; group 0 (waves 0-3) and group 1 (waves 4-7) put one
+// wave on each SIMD.  The groups take turns between slots separated by
+// workgroup barriers: while one group runs the 32 (BK = 64) MFMAs of a stage
+// from registers, the other reads the next stage's fragments from LDS, so
+// each SIMD's matrix pipe is fed by one wave while its other wave does the
+// memory work.  Group 1 runs one slot behind group 0:
+//   slot 2j:   group 0 reads stage j (and issues the DMA of stage j+NS-1),
+//              group 1 computes stage j-1;
+//   slot 2j+1: group 0 computes stage j, group 1 reads stage j.
+// Stage j's buffer is last read in slot 2j+1, so its reuse for stage j+NS is
+// issued in slot 2j+2 and has 2*NS-2 slots to land.  Group 0 issues all
+// DMA; wave 0 also touches the A / B lines of stage j+PF (its share of the
+// lines that the blocks sharing those panels will load) so that they are in
+// L2 when their DMA is issued.  Every wave executes the same barriers.
+
+// Workgroup barrier that the compiler schedules nothing across.
+__device__ inline void block_barrier() {
+    __builtin_amdgcn_sched_barrier(0);
+    asm volatile("s_barrier" ::: "memory");
+    __builtin_amdgcn_sched_barrier(0);
+}
+
+__device__ inline void wait_lgkm0() {
+    __builtin_amdgcn_sched_barrier(0);
+    asm volatile("s_waitcnt lgkmcnt(0)" ::: "memory");
+    __builtin_amdgcn_sched_barrier(0);
+}
+
+// 4 bytes per lane from global into LDS at lds_addr + 4*lane; used to pull
+// lines into L2 ahead of their DMA (the LDS bytes are scratch).
+__device__ inline void dma4(u32x4 rsrc, int voff, int soff, u32 lds_addr) {
+    u32 saved;
+    asm volatile(
+        "s_mov_b32 %0, m0\n\t"
+        "s_mov_b32 m0, %4\n\t"
+        "s_nop 0\n\t"
+        "buffer_load_dword %1, %2, %3 offen lds\n\t"
+        "s_nop 0\n\t"
+        "s_mov_b32 m0, %0"
+        : "=&s"(saved)
+        : "v"(voff), "s"(rsrc), "s"(__builtin_amdgcn_readfirstlane(soff)), "s"(__builtin_amdgcn_readfirstlane(lds_addr))
+        : "memory");
+}
+
+template <int BK, bool F16>
+struct GemmPingPong {
+    typedef GemmBlock<256, 256, BK, 2, 4, F16, 2, 1> GB;
+    static constexpr int NS = BK == 64 ? 2 : 4;        // LDS stages (128 KiB)
+    static constexpr int PF = 3;                       // L2 touch distance in stages
+    static constexpr int WN = 4, TM = 128, TN = 64, FI = 4, FJ = 2, KS = BK / 16;
+    static constexpr int CH = BK / 8, ARPB = 1024 / (2 * BK), BCPR = 32, BRPB = 2;
+    static constexpr int ABLK = 256 * BK * 2 / 1024, BBLK = BK * 256 * 2 / 1024;
+    static constexpr int NL = 4, AQ = ABLK / NL, BQ = BBLK / NL;  // group 0 loads
+    static constexpr int ASZ = 256 * BK, STAGE = ASZ + BK * 256;
+    static constexpr int kScratch = 128;               // u16 elements after the stages
+    static constexpr int kLdsElems = NS * STAGE + kScratch;
+    static constexpr int kStageOps = AQ + BQ;
+    static_assert(BK == 64 || BK == 32, "ping-pong K step");
+    static_assert(AQ * NL == ABLK && BQ * NL == BBLK && (NS - 2) * kStageOps <= 63, "ping-pong loads");
+
+    struct Frag {
+        u32x4 a[KS][FI];
+        u32x4 b[KS][FJ];
+    };
+    typedef typename GB::Acc Acc;
+
+    // DMA lane offsets of loader wave w (0..3) for its first A / B chunk.
+    // With row pitches that are multiples of 64 elements (checked on the
+    // host), chunk q of A sits at va with its 16-byte column bits flipped by
+    // q (BK = 64) or by bit 1 of q (BK = 32), and chunk q of B at vb with bit
+    // 6 flipped by q & 1; the row steps q*ARPB / q*BRPB go into the uniform
+    // offset.
+    __device__ static void offsets(int& va, int& vb, int w, int lda, int ldb) {
+        const int lane = threadIdx.x & 63;
+        const int m = w * AQ * ARPB + lane / CH, p = lane % CH;
+        va = (m * lda + ((p ^ GB::swa(m)) << 3)) * 2;
+        const int k = w * BQ * BRPB + lane / BCPR, pb = lane % BCPR;
+        vb = (k * ldb + (((((pb >> 1) ^ (k & 3)) << 1) | (pb & 1)) * 8)) * 2;
+    }
+    __device__ static int a_voff(int va, int q) { return BK == 64 ? va ^ (q << 4) : va ^ ((q & 1) << 5); }
+
+    __device__ static void load(u16* stage, int w, int va, int vb, u32x4 ra, int soa, u32x4 rb, int sob, int lda, int ldb) {
+        const u32 base = lds_address(stage);
+#pragma unroll
+        for (int q = 0; q < AQ; ++q) dma16(ra, a_voff(va, q), soa + q * ARPB * lda * 2, base + (w * AQ + q) * 1024);
+#pragma unroll
+        for (int q = 0; q < BQ; ++q) dma16(rb, vb ^ ((q & 1) << 6), sob + q * BRPB * ldb * 2, base + ASZ * 2 + (w * BQ + q) * 1024);
+    }
+
+    // All fragments of one stage (the address math of GemmBlock::mma).
+    __device__ static void read(Frag& f, const u16* stage, int wm, int wn) {
+        const int lane = threadIdx.x & 63;
+        const int r = lane & 31, kc = lane >> 5;
+        const int g = lane >> 4, a4 = lane & 3, e = (lane >> 2) & 3;
+        const u16* as = stage + (wm * TM + r) * BK;
+        const u16* bs = stage + ASZ;
+#pragma unroll
+        for (int s = 0; s < KS; ++s) {
+            const int kk = s * 16;
+#pragma unroll
+            for (int i = 0; i < FI; ++i)
+                f.a[s][i] = *reinterpret_cast<const u32x4*>(as + i * 32 * BK + ((((kk >> 3) + kc) ^ GB::swa(wm * TM + i * 32 + r)) << 3));
+#pragma unroll
+            for (int j = 0; j < FJ; ++j) {
+                const int n = wn * TN + j * 32 + 16 * (g & 1) + 4 * a4;
+                const int pn = (((n >> 4) ^ e) << 4) | (n & 15);
+                const int k = kk + 8 * (g >> 1) + e;
+                const s16x4 lo = __builtin_amdgcn_ds_read_tr16_b64_v4i16((__attribute__((address_space(3))) s16x4*)(bs + k * 256 + pn));
+                const s16x4 hi =
+                    __builtin_amdgcn_ds_read_tr16_b64_v4i16((__attribute__((address_space(3))) s16x4*)(bs + (k + 4) * 256 + pn));
+                const u32x2 l2 = __builtin_bit_cast(u32x2, lo), h2 = __builtin_bit_cast(u32x2, hi);
+                f.b[s][j] = u32x4{l2.x, l2.y, h2.x, h2.y};
+            }
+        }
+    }
+
+    __device__ static void mma(Acc& acc, const Frag& f) {
+#pragma unroll
+        for (int s = 0; s < KS; ++s)
+#pragma unroll
+            for (int i = 0; i < FI; ++i)
+#pragma unroll
+                for (int j = 0; j < FJ; ++j) acc.v[i][j] = mfma_32x32x16<F16>(f.a[s][i], f.b[s][j], acc.v[i][j]);
+    }
+
+    // Waits until at most `pending` later stages of this wave's DMA are in flight.
+    __device__ static void wait_pending(int pending) {
+        if constexpr (NS == 2) {
+            wait_vmcnt<0>();
+        } else {
+            if (pending >= 2) wait_vmcnt<2 * kStageOps>();
+            else if (pending == 1) wait_vmcnt<kStageOps>();
+            else wait_vmcnt<0>();
+        }
+    }
+
+    // C block (plus C when ACC) written in the accumulator layout; for ACC the
+    // C reads run NB accumulators ahead of the adds.
+    template <bool ACC>
+    __device__ static void c_out(Acc& acc, buf_rsrc rc, int ldc) {
+        if constexpr (!ACC) {
+            GB::template c_out<false>(acc, rc, ldc);
+        } else {
+            constexpr int NF = FI * FJ, NB = 6;
+            const int lane = threadIdx.x & 63, wave = wave_index();
+            const int wm = wave / WN, wn = wave % WN;
+            const int vc = ((lane >> 5) * 4 * ldc + (lane & 31)) * 4;
+            const int so = (wm * TM * ldc + wn * TN) * 4;
+            auto row = [&](int i, int e) { return so + (i * 32 + (e >> 2) * 8 + (e & 3)) * ldc * 4; };
+            float t[NF][16];
+            auto fetch = [&](int n) {
+                const int i = n / FJ, j = n % FJ;
+#pragma unroll
+                for (int e = 0; e < 16; ++e) t[n][e] = __uint_as_float(__builtin_amdgcn_raw_buffer_load_b32(rc, vc + j * 128, row(i, e), 2));
+            };
+#pragma unroll
+            for (int n = 0; n < NB; ++n) fetch(n);
+#pragma unroll
+            for (int n = 0; n < NF; ++n) {
+                const int i = n / FJ, j = n % FJ;
+                if (n + NB < NF) fetch(n + NB);
+#pragma unroll
+                for (int e = 0; e < 16; ++e)
+                    __builtin_amdgcn_raw_buffer_store_b32(__float_as_uint(t[n][e] + acc.v[i][j][e]), rc, vc + j * 128, row(i, e), 2);
+                __builtin_amdgcn_sched_barrier(0);
+            }
+        }
+    }
+
+    // Task K steps it0 .. iters-1 (off(it, soa, sob): step it's byte offsets
+    // from the step-0 origins pa / pb).  The block sums A x B from zero; ACC:
+    // then adds C, as c + sum.  pfa_row / pfb_row (< 0: no L2 touches): the
+    // A rows pfa_row..+31 and B rows pfb_row..+15 of each stage that wave 0
+    // pulls into L2 PF stages ahead.
+    template <bool ACC, class Off>
+    __device__ static void run(u16* lds, const u16* pa, int lda, const u16* pb, int ldb, float* pc, int ldc, i64 it0, i64 iters,
+                               Off off, int pfa_row, int pfb_row) {
+        const int w = wave_index(), grp = w >> 2, wm = w / WN, wn = w % WN;
+        const int lane = threadIdx.x & 63;
+        const u32x4 ra = buffer_words(pa), rb = buffer_words(pb);
+        const buf_rsrc rc = __builtin_amdgcn_make_buffer_rsrc(pc, 0, -1, 0x00020000);
+        const int nst = static_cast<int>(iters - it0);
+        const u32 scratch = lds_address(lds + NS * STAGE);
+        int va, vb;
+        offsets(va, vb, w & 3, lda, ldb);
+        const int pfa_v = (pfa_row + (lane & 31)) * lda * 2, pfb_v = ((pfb_row + (lane >> 2)) * ldb + (lane & 3) * 64) * 2;
+        const bool touch = w == 0 && pfa_row >= 0 && pfb_row >= 0;
+        Acc acc;
+#pragma unroll
+        for (int i = 0; i < FI; ++i)
+#pragma unroll
+            for (int j = 0; j < FJ; ++j) acc.v[i][j] = f32x16{};
+        Frag f;
+        auto issue = [&](int st) {
+            int soa, sob;
+            off(it0 + st, soa, sob);
+            load(lds + (st % NS) * STAGE, w & 3, va, vb, ra, soa, rb, sob, lda, ldb);
+        };
+        wait_vmcnt<0>();
+        block_barrier();  // the previous block's last stage reads are done
+        if (grp == 0) {
+            for (int p = 0; p < NS - 1; ++p)
+                if (p < nst) issue(p);
+            wait_pending(nst - 1 < NS - 2 ? nst - 1 : NS - 2);
+        }
+        block_barrier();
+        if (grp == 1) block_barrier();  // group 1 runs one slot behind
+        for (int j = 0; j < nst; ++j) {
+            if (grp == 0 && j + NS - 1 < nst) issue(j + NS - 1);
+            const bool t = touch && j + PF < nst;
+            if (t) {
+                int soa, sob;
+                off(it0 + j + PF, soa, sob);
+                dma4(ra, pfa_v, soa, scratch);
+                dma4(rb, pfb_v, sob, scratch);
+            }
+            read(f, lds + (j % NS) * STAGE, wm, wn);
+            wait_lgkm0();
+            block_barrier();
+            mma(acc, f);
+            if (grp == 0 && j + 1 < nst) {
+                // wave 0's two touches of this iteration may stay in flight
+                if (NS == 2 && t) wait_vmcnt<2>();
+                else wait_pending((j + NS - 1 < nst ? j + NS - 1 : nst - 1) - (j + 1));
+            }
+            block_barrier();
+        }
+        c_out<ACC>(acc, rc, ldc);
+        if (grp == 0) block_barrier();
+    }
+};
+
+// ---------------------------------------------------------------------------
 // Decode: online softmax over 16-token pages (flashinfer_decode pattern)
 // ---------------------------------------------------------------------------
 //

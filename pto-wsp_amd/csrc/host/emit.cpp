@@ -488,6 +488,8 @@ EmittedKernel emit_gemm(const Module& m, const KernelAnalysis& a, const LaunchSp
     // stages measured slower on 256x256 blocks: twice the barriers).
     const int wm = gemm_waves_m(), wn = gemm_waves_n(bn);
     const int bk = g.k, ns = 2, ksplit = 1;
+    // Ping-pong block: 256x256, K step 32 / 64, row pitches checked on the host.
+    const bool pp = spec.gemm_pingpong && bm == 256 && bn == 256 && (bk == 64 || bk == 32);
     EmittedKernel ek;
     ek.threads = 64 * wm * wn;
     ek.row_program = false;
@@ -495,12 +497,16 @@ EmittedKernel emit_gemm(const Module& m, const KernelAnalysis& a, const LaunchSp
     std::ostringstream o;
     o << "#include \"ptowsp_device.h\"\nusing namespace ptowsp;\n";
     o << "// gemm program: kernel " << k.name << ", task tile " << g.m << "x" << g.n << "x" << g.k << (g.f16 ? " f16" : " bf16")
-      << (g.accumulate ? ", accumulate" : "") << "; block " << bm << "x" << bn << " (" << fm * fn << " tasks)\n";
+      << (g.accumulate ? ", accumulate" : "") << "; block " << bm << "x" << bn << " (" << fm * fn << " tasks)"
+      << (pp ? ", ping-pong" : "") << "\n";
     ek.entry = entry_name("gemm", k);
     o << "extern \"C\" __global__ void __launch_bounds__(" << ek.threads << ") "
       << ek.entry << "(const LaunchArgs A) {\n";
-    o << "  typedef GemmBlock<" << bm << ", " << bn << ", " << bk << ", " << wm << ", " << wn << ", "
-      << (g.f16 ? "true" : "false") << ", " << ns << ", " << ksplit << "> GB;\n";
+    if (pp)
+        o << "  typedef GemmPingPong<" << bk << ", " << (g.f16 ? "true" : "false") << "> GB;\n";
+    else
+        o << "  typedef GemmBlock<" << bm << ", " << bn << ", " << bk << ", " << wm << ", " << wn << ", "
+          << (g.f16 ? "true" : "false") << ", " << ns << ", " << ksplit << "> GB;\n";
     o << "  __shared__ __attribute__((aligned(1024))) u16 lds[GB::kLdsElems];\n";
     o << "  i64 vars[" << (nvars > 0 ? nvars : 1) << "];\n  (void)vars;\n";
     o << "  const i64 nblk = A.ntasks / " << fm * fn << ";\n";
@@ -536,12 +542,23 @@ EmittedKernel emit_gemm(const Module& m, const KernelAnalysis& a, const LaunchSp
     }
     o << "      soa = static_cast<int>(oa * 2); sob = static_cast<int>(ob * 2);\n";
     o << "    };\n";
+    if (pp) {
+        // L2 touches: the blocks that share an A panel (same m block) split its
+        // rows by their n block (8 x 32 rows); those that share a B panel
+        // split the stage's K rows by their m block (BK/16 x 16 rows).
+        if (spec.gemm_vm >= 0 && spec.gemm_vn >= 0)
+            o << "    const int pfa_row = static_cast<int>((vars[" << spec.gemm_vn << "] / " << fn << ") % 8) * 32;\n"
+              << "    const int pfb_row = static_cast<int>((vars[" << spec.gemm_vm << "] / " << fm << ") % " << bk / 16
+              << ") * 16;\n";
+        else
+            o << "    const int pfa_row = -1, pfb_row = -1;\n";
+    }
     o << "    GB::template run<" << (g.accumulate ? "true" : "false") << ">(lds, pa, static_cast<int>(A.s3[" << g.a
       << "]), pb, static_cast<int>(A.s3[" << g.b << "]), pc, static_cast<int>(A.s3[" << g.c << "]), "
-      << (g.accumulate ? "0" : "iters - 1") << ", iters, off);\n";
+      << (g.accumulate ? "0" : "iters - 1") << ", iters, off" << (pp ? ", pfa_row, pfb_row" : "") << ");\n";
     o << "  }\n}\n";
     ek.source = o.str();
-    ek.lds_bytes = static_cast<size_t>(ns * (bm + bn) * bk * 2);
+    ek.lds_bytes = pp ? static_cast<size_t>((bk == 64 ? 2 : 4) * 512 * bk * 2 + 256) : static_cast<size_t>(ns * (bm + bn) * bk * 2);
     return ek;
 }
 

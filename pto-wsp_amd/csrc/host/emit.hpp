@@ -28,6 +28,9 @@ struct EmitSpec {
     // GEMM: grid variables whose neighbouring tasks are merged into one
     // workgroup block (factor 2 along rows / columns of C), or -1.
     int gemm_vm = -1, gemm_vn = -1;
+    // GEMM: 256x256 blocks with K step 32 or 64 and A / B row pitches that
+    // are multiples of 64 elements run as a two-group ping-pong block.
+    bool gemm_pingpong = false;
     // Decode family (online softmax over pages): the in-kernel page loop of
     // every unit is split over the resident waves.
     bool decode = false;

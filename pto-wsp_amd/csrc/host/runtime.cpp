@@ -298,6 +298,7 @@ int pick_vec_width(const KernelAnalysis& a, const LaunchArgs& A, int nvars) {
 struct Tuning {
     int row_up = 2;
     bool nontemporal = true;
+    bool gemm_pingpong = true;
 };
 
 const Tuning& tuning() {
@@ -305,6 +306,7 @@ const Tuning& tuning() {
         Tuning v;
         if (const char* s = std::getenv("PTOWSP_ROW_UNROLL")) v.row_up = std::max(1, std::atoi(s));
         if (const char* s = std::getenv("PTOWSP_NONTEMPORAL")) v.nontemporal = std::atoi(s) != 0;
+        if (const char* s = std::getenv("PTOWSP_GEMM_PINGPONG")) v.gemm_pingpong = std::atoi(s) != 0;
         return v;
     }();
     return t;
@@ -380,6 +382,7 @@ bool grid_write_hazard(const KernelAnalysis& a, const LaunchSpec& L, const Launc
 // direct buffer->LDS loads of the GEMM block.
 bool gemm_allowed(const KernelAnalysis& a, const LaunchSpec& L, const LaunchArgs& A, EmitSpec& spec, int ng, int nvars) {
     spec.gemm_vm = spec.gemm_vn = -1;
+    spec.gemm_pingpong = false;
     if (a.family != Family::Gemm || spec.serial) return false;
     for (int c : spec.indirect_count)
         if (c) return false;
@@ -422,6 +425,8 @@ bool gemm_allowed(const KernelAnalysis& a, const LaunchSpec& L, const LaunchArgs
     if (((bm - 1) * A.s3[g.a] + g.k) * 2 + ka * 2 >= lim) return false;
     if (((g.k - 1) * A.s3[g.b] + bn) * 2 + kb * 2 >= lim) return false;
     if (((bm - 1) * A.s3[g.c] + bn) * 4 >= lim) return false;
+    spec.gemm_pingpong = tuning().gemm_pingpong && bm == 256 && bn == 256 && (g.k == 64 || g.k == 32) &&
+                         A.s3[g.a] % 64 == 0 && A.s3[g.b] % 64 == 0;
     return true;
 }
 
@@ -616,7 +621,10 @@ BuiltLaunch build_launch(RunEnv& E, const LaunchSpec& L) {
     B.spec.row_up = tuning().row_up;
     B.spec.nontemporal = tuning().nontemporal;
     B.spec.gemm = gemm_allowed(a, L, A, B.spec, ng, nvars);
-    if (!B.spec.gemm) B.spec.gemm_vm = B.spec.gemm_vn = -1;
+    if (!B.spec.gemm) {
+        B.spec.gemm_vm = B.spec.gemm_vn = -1;
+        B.spec.gemm_pingpong = false;
+    }
     B.spec.decode = decode_allowed(a, L, A, B.spec, ng);
     B.spec.vec_width = a.family == Family::RowProgram ? pick_vec_width(a, A, nvars) : 1;
     return B;
@@ -625,7 +633,8 @@ BuiltLaunch build_launch(RunEnv& E, const LaunchSpec& L) {
 std::string spec_key(const EmitSpec& s) {
     std::ostringstream o;
     o << "vw" << s.vec_width << (s.serial ? ";serial" : "") << ";up" << s.row_up << (s.nontemporal ? ";nt" : "")
-      << (s.gemm ? ";gemm" : "") << ";m" << s.gemm_vm << ";n" << s.gemm_vn << (s.decode ? ";dec" : "")
+      << (s.gemm ? ";gemm" : "") << ";m" << s.gemm_vm << ";n" << s.gemm_vn << (s.gemm_pingpong ? ";pp" : "")
+      << (s.decode ? ";dec" : "")
       << (s.decode_norm ? ";norm" : "")
       << ";i";
     for (int c : s.indirect_count) o << c << ",";
@@ -1025,6 +1034,7 @@ int ptowsp_hip_precompile(ptowsp_program* P, int index, int flags, const char** 
                 2 * (2 * a.gemm.m + 2 * a.gemm.n) * a.gemm.k * 2 <= 160 * 1024) {
                 spec.gemm_vm = ng - 2;
                 spec.gemm_vn = ng - 1;
+                spec.gemm_pingpong = (flags & 4) && a.gemm.m == 128 && a.gemm.n == 128 && (a.gemm.k == 64 || a.gemm.k == 32);
             }
             const EmittedKernel& ek = emitted_for(P, static_cast<int>(li), spec);
             (void)jit_compile(ek.source);

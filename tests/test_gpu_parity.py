@@ -268,6 +268,49 @@ def test_bgemm_bf16_mfma_block_shapes(gpu, shape, tiles):
     assert prog.stats.total_cycles == ref.total_cycles
 
 
+@pytest.mark.parametrize("shape,tiles,f16,plain,split", [
+    ((2, 256, 256, 64), (128, 128, 64), False, False, 1),     # one K step
+    ((1, 512, 256, 128), (128, 128, 64), False, False, 1),    # two K steps, two blocks
+    ((1, 256, 512, 192), (128, 128, 64), True, False, 1),     # three K steps, f16
+    ((2, 256, 256, 320), (128, 128, 64), False, False, 1),    # five K steps: touches run ahead
+    ((2, 256, 256, 256), (128, 128, 32), False, False, 1),    # K step 32: four-stage ring
+    ((1, 256, 256, 256), (128, 128, 64), False, True, 1),     # plain store: last K step only
+    ((1, 256, 256, 512), (128, 128, 64), False, False, 2),    # K over two P.seq loops
+    ((1, 256, 256, 96), (128, 128, 32), False, False, 1),     # A pitch 96: GemmBlock path
+])
+def test_bgemm_pingpong_block(gpu, shape, tiles, f16, plain, split):
+    """256x256 blocks (2x2 merged 128x128 tasks) on the two-group ping-pong template."""
+    nb, m, n, k = shape
+    tm, tn, tk = tiles
+    rng = np.random.default_rng(13)
+    a = rng.uniform(-1, 1, (nb, m, k)).astype(np.float32)
+    b = rng.uniform(-1, 1, (nb, k, n)).astype(np.float32)
+    if f16:
+        a, b = a.astype(np.float16), b.astype(np.float16)
+        af, bf = a.astype(np.float64), b.astype(np.float64)
+    else:
+        a, b = W.bf16_round(a), W.bf16_round(b)
+        af, bf = W.bf16_to_f32(a).astype(np.float64), W.bf16_to_f32(b).astype(np.float64)
+    c0 = rng.standard_normal((nb, m, n)).astype(np.float32)
+    ga = {"a": a, "b": b, "c": c0.copy()}
+    ca = {"a": a.copy(), "b": b.copy(), "c": c0.copy()}
+    dt = W.F16 if f16 else W.BF16
+    if split > 1:
+        prog = run_hip(W.bgemm_split_k(ga, tm, tn, tk, split, dt))
+        ref = run_workload(W.bgemm_split_k(ca, tm, tn, tk, split, dt))
+    else:
+        prog = run_hip(W.bgemm(ga, tm, tn, tk, dt, plain=plain))
+        ref = run_workload(W.bgemm(ca, tm, tn, tk, dt, plain=plain))
+    assert prog._native.kernel_family("gemm_tile") == "gemm"
+    assert _rel_fro(ga["c"], ca["c"]) <= 1e-5
+    if plain:
+        exact = af[:, :, k - tk:] @ bf[:, k - tk:, :]
+    else:
+        exact = c0.astype(np.float64) + af @ bf
+    assert _rel_fro(ga["c"], exact) <= 1e-5
+    assert prog.stats.total_cycles == ref.total_cycles
+
+
 def test_bgemm_two_inner_loops(gpu):
     """K split over two P.seq loops: in-kernel iterations decode a mixed radix."""
     rng = np.random.default_rng(12)
