@@ -398,14 +398,21 @@ def load_traffic(name):
     return None
 
 
-def time_case(case, steps, warmup):
+def time_case(case, steps, warmup, warm_s=0.0):
+    """W untimed warmup steps (continued until warm_s seconds have passed:
+    the GPU raises its clocks over the first tens of milliseconds of sustained
+    MFMA work), then exactly `steps` timed steps."""
     import torch
 
     before = getattr(case, "before_step", lambda: None)
-    for _ in range(warmup):
+    t_warm = time.perf_counter()
+    done = 0
+    while done < warmup or time.perf_counter() - t_warm < warm_s:
         before()
         case.prog.execute()
         case.prog.synchronize()
+        done += 1
+    case.warmup_done = done
     torch.cuda.synchronize()
     kernel_ms = []
     t0 = time.perf_counter()
@@ -450,12 +457,14 @@ def main():
     for name in names:
         case = CASES[name]()
         case.setup(dev)
-        steps = args.steps if name == head else max(3, args.steps // 4)
-        ms_step, k_ms = time_case(case, steps, args.warmup)
+        # The headline config keeps exactly W warmup steps; every other config
+        # line is measured at steady clocks (at least 0.25 s of warmup).
+        ms_step, k_ms = time_case(case, args.steps, args.warmup, 0.0 if name == head else 0.25)
         achieved = case.rate(k_ms * 1e-3)
         entry = {"baseline_config": case.baseline_config, "kernel_ms": round(k_ms, 5), "ms_per_step": round(ms_step, 5),
                  "achieved": round(achieved, 2), "unit": case.unit, "peak": case.peak(),
-                 "frac": round(achieved / case.peak(), 4), "tasks": case.prog.stats.task_count,
+                 "frac": round(achieved / case.peak(), 4), "warmup": case.warmup_done, "steps": args.steps,
+                 "tasks": case.prog.stats.task_count,
                  "total_cycles": case.prog.stats.total_cycles}
         if not args.no_cpu and name != "rmsnorm_quickstart":
             rate, sample, same = case.cpu(12.0 if name == head else 6.0)

@@ -58,8 +58,18 @@ uint64_t ptowsp_hip_workload_main(ptowsp_program* prog, RuntimeContext* ctx, CSP
 
 /* Non-blocking run behind Program.execute() (reference python/pto_wsp/program.py:670-733):
  * stages host-resident tensors, enqueues every launch on `hip_stream`
- * (a hipStream_t, may be NULL) and returns. */
+ * (a hipStream_t, may be NULL) and returns.  When a loop extent is read from
+ * a device-resident tensor, that tensor is copied asynchronously and the
+ * cycle model runs in ptowsp_hip_synchronize: info->total_cycles is then
+ * UINT64_MAX and ptowsp_hip_run_result gives it after the synchronize (the
+ * reference also fills ProgramStats.total_cycles only when the run thread
+ * ends, python/pto_wsp/program.py:721-733).  `ctx` must stay valid until
+ * the synchronize. */
 int ptowsp_hip_launch(ptowsp_program* prog, RuntimeContext* ctx, void* hip_stream, ptowsp_run_info* info);
+
+/* Cycle model result of the last synchronized run (new: pairs with the
+ * deferred total_cycles of ptowsp_hip_launch).  -1 while a run is pending. */
+int ptowsp_hip_run_result(const ptowsp_program* prog, ptowsp_run_info* info);
 
 /* Program.synchronize() (reference python/pto_wsp/program.py:735-743): waits
  * for the last launch, copies written host-resident tensors back, and

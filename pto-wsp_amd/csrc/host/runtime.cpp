@@ -79,11 +79,24 @@ struct ptowsp_program {
     hipEvent_t ev0 = nullptr, ev1 = nullptr;
     bool have_events = false;
     bool pending = false;
+    // Error flag written by the kernels: pinned host memory mapped into the
+    // device address space, so synchronize() reads it without a copy.
+    int* h_err = nullptr;
     int* d_err = nullptr;
     double h2d_ms = 0.0;
     std::string cycle_key;
     CycleResult cycles;
     bool cycles_valid = false;
+    // A run whose cycle model reads device-resident extent tensors: they are
+    // copied into pinned memory ahead of the kernels and the model runs at
+    // synchronize() from these tensor states and that copy.
+    bool cycles_deferred = false;
+    RuntimeContext* deferred_ctx = nullptr;
+    std::vector<TensorState> deferred_ts;
+    std::vector<std::pair<int, size_t>> deferred_tids;  // tensor id, int32 offset in key_stage
+    int32_t* key_stage = nullptr;
+    size_t key_stage_elems = 0;
+    ptowsp_run_info last_run{};  // cycle model result of the last synchronized run
     std::string precompiled_source;
     void* scratch = nullptr;  // decode: unit counters and partials
     size_t scratch_bytes = 0;
@@ -92,7 +105,8 @@ struct ptowsp_program {
         if (scratch) (void)hipFree(scratch);
         for (void* b : stage_buf)
             if (b) (void)hipFree(b);
-        if (d_err) (void)hipFree(d_err);
+        if (h_err) (void)hipHostFree(h_err);
+        if (key_stage) (void)hipHostFree(key_stage);
         if (ev0) (void)hipEventDestroy(ev0);
         if (ev1) (void)hipEventDestroy(ev1);
     }
@@ -947,6 +961,54 @@ CycleResult cycles_for(RunEnv& E) {
     return r;
 }
 
+// Tensors holding loop extents (DenseDyn bound to a tensor) that live on the
+// device: the cycle-model key reads their contents.
+std::vector<int> device_extent_tensors(RunEnv& E) {
+    std::vector<int> out;
+    std::function<void(const Node*)> walk = [&](const Node* n) {
+        if (!n) return;
+        if ((n->kind == NodeKind::ParallelFor || n->kind == NodeKind::ForEach) && n->axis.kind == AxisKind::DynTensor) {
+            const int tid = n->axis.expr.tid;
+            if (!E.ts[tid].host && std::find(out.begin(), out.end(), tid) == out.end()) out.push_back(tid);
+        }
+        walk(n->body.get());
+        for (const auto& c : n->kids) walk(c.get());
+    };
+    walk(E.P->m.root.get());
+    return out;
+}
+
+// Copies the device extent tensors into pinned memory on `stream` and keeps
+// what the cycle model needs at synchronize().  The copy must see the values
+// the launches start from: it is enqueued ahead of the kernels when a launch
+// writes one of the tensors (`before`), and after them otherwise, so that it
+// does not delay the first kernel.
+void defer_cycles(RunEnv& E, const std::vector<int>& tids, hipStream_t stream) {
+    ptowsp_program* P = E.P;
+    size_t total = 0;
+    P->deferred_tids.clear();
+    for (int tid : tids) {
+        P->deferred_tids.push_back({tid, total});
+        total += static_cast<size_t>(std::max<int64_t>(E.ts[tid].span, 0));
+    }
+    if (total > P->key_stage_elems) {
+        if (P->key_stage) check(hipHostFree(P->key_stage), "hipHostFree(key stage)");
+        P->key_stage = nullptr;
+        P->key_stage_elems = 0;
+        check(hipHostMalloc(reinterpret_cast<void**>(&P->key_stage), total * 4, hipHostMallocDefault), "hipHostMalloc(key stage)");
+        P->key_stage_elems = total;
+    }
+    for (const auto& [tid, off] : P->deferred_tids) {
+        const size_t n = static_cast<size_t>(std::max<int64_t>(E.ts[tid].span, 0));
+        if (n)
+            check(hipMemcpyAsync(P->key_stage + off, E.ts[tid].dev, n * 4, hipMemcpyDeviceToHost, stream),
+                  "hipMemcpyAsync(extent tensor)");
+    }
+    P->deferred_ts = E.ts;
+    P->deferred_ctx = E.ctx;
+    P->cycles_deferred = true;
+}
+
 int fail(const std::exception& e) {
     g_last_error = e.what();
     return -1;
@@ -1087,9 +1149,11 @@ int ptowsp_hip_launch(ptowsp_program* P, RuntimeContext* ctx, void* hip_stream, 
         if (!P || !ctx) throw std::runtime_error("null argument");
         if (P->pending) throw std::runtime_error("Program already started");
         hipStream_t stream = static_cast<hipStream_t>(hip_stream);
-        if (!P->d_err) {
-            check(hipMalloc(reinterpret_cast<void**>(&P->d_err), sizeof(int)), "hipMalloc(err)");
-            check(hipMemset(P->d_err, 0, sizeof(int)), "hipMemset(err)");
+        if (!P->h_err) {
+            check(hipHostMalloc(reinterpret_cast<void**>(&P->h_err), sizeof(int), hipHostMallocMapped | hipHostMallocCoherent),
+                  "hipHostMalloc(err)");
+            __atomic_store_n(P->h_err, 0, __ATOMIC_RELAXED);
+            check(hipHostGetDevicePointer(reinterpret_cast<void**>(&P->d_err), P->h_err, 0), "hipHostGetDevicePointer(err)");
         }
         if (!P->have_events) {
             check(hipEventCreate(&P->ev0), "hipEventCreate");
@@ -1098,20 +1162,24 @@ int ptowsp_hip_launch(ptowsp_program* P, RuntimeContext* ctx, void* hip_stream, 
         }
         RunEnv E{P, ctx, {}, {}, {}};
         resolve_tensors(E, stream);
-        const CycleResult cyc = cycles_for(E);
+        P->cycles_deferred = false;
+        const std::vector<int> dev_ext = device_extent_tensors(E);
+        CycleResult cyc{};
+        bool ext_written = false;
+        for (int tid : dev_ext) ext_written |= E.ts[tid].written;
+        if (dev_ext.empty()) cyc = cycles_for(E);
+        else if (ext_written) defer_cycles(E, dev_ext, stream);
         uint64_t launches = 0;
         run_items(E, P->plan.items, stream, launches);
+        if (!dev_ext.empty() && !ext_written) defer_cycles(E, dev_ext, stream);
         start_timing(E, stream);
         check(hipEventRecord(P->ev1, stream), "hipEventRecord");
         check(hipGetLastError(), "kernel launch");
         P->stream = stream;
         P->pending = true;
-        if (info) {
-            info->total_cycles = cyc.total_cycles;
-            info->task_count = cyc.tasks;
-            info->launches = static_cast<uint32_t>(launches);
-            info->reserved = 0;
-        }
+        P->last_run = ptowsp_run_info{cyc.total_cycles, cyc.tasks, static_cast<uint32_t>(launches), 0};
+        if (P->cycles_deferred) P->last_run.total_cycles = P->last_run.task_count = UINT64_MAX;
+        if (info) *info = P->last_run;
         return 0;
     } catch (const std::exception& e) {
         return fail(e);
@@ -1127,17 +1195,26 @@ int ptowsp_hip_synchronize(ptowsp_program* P, ptowsp_timing* timing) {
         }
         P->pending = false;
         check(hipStreamSynchronize(P->stream), "hipStreamSynchronize");
+        if (P->cycles_deferred) {
+            P->cycles_deferred = false;
+            RunEnv E{P, P->deferred_ctx, P->deferred_ts, {}, {}};
+            for (const auto& [tid, off] : P->deferred_tids) {
+                const size_t n = static_cast<size_t>(std::max<int64_t>(E.ts[tid].span, 0));
+                E.idx_host[tid] = std::vector<int32_t>(P->key_stage + off, P->key_stage + off + n);
+            }
+            const CycleResult cyc = cycles_for(E);
+            P->last_run.total_cycles = cyc.total_cycles;
+            P->last_run.task_count = cyc.tasks;
+        }
         float dev_ms = 0.0f;
         check(hipEventElapsedTime(&dev_ms, P->ev0, P->ev1), "hipEventElapsedTime");
         const auto t0 = std::chrono::steady_clock::now();
         for (const auto& cb : P->copy_back) check(hipMemcpy(cb.host, cb.dev, cb.bytes, hipMemcpyDeviceToHost), "hipMemcpy(D2H)");
         const double d2h = ms_since(t0);
         P->copy_back.clear();
-        int err = 0;
-        check(hipMemcpy(&err, P->d_err, sizeof(int), hipMemcpyDeviceToHost), "hipMemcpy(err)");
+        const int err = __atomic_load_n(P->h_err, __ATOMIC_ACQUIRE);
         if (err) {
-            const int zero = 0;
-            check(hipMemcpy(P->d_err, &zero, sizeof(int), hipMemcpyHostToDevice), "hipMemcpy(err reset)");
+            __atomic_store_n(P->h_err, 0, __ATOMIC_RELAXED);
             throw std::runtime_error(err == 1   ? "an indirect tensor index was out of range (tasks skipped)"
                                      : err == 3 ? "a loop extent read from a tensor exceeded its declared maximum"
                                                 : "a task's tile fell outside its tensor (tasks skipped)");
@@ -1149,12 +1226,24 @@ int ptowsp_hip_synchronize(ptowsp_program* P, ptowsp_timing* timing) {
     }
 }
 
+int ptowsp_hip_run_result(const ptowsp_program* P, ptowsp_run_info* info) {
+    if (!P || !info) {
+        g_last_error = "null argument";
+        return -1;
+    }
+    if (P->pending) {
+        g_last_error = "the run has not been synchronized";
+        return -1;
+    }
+    *info = P->last_run;
+    return 0;
+}
+
 uint64_t ptowsp_hip_workload_main(ptowsp_program* prog, RuntimeContext* ctx, CSPTContext* cspt) {
     (void)cspt;
-    ptowsp_run_info info{};
-    if (ptowsp_hip_launch(prog, ctx, nullptr, &info) != 0) return 0;
+    if (ptowsp_hip_launch(prog, ctx, nullptr, nullptr) != 0) return 0;
     if (ptowsp_hip_synchronize(prog, nullptr) != 0) return 0;
-    return info.total_cycles;
+    return prog->last_run.total_cycles;
 }
 
 ptowsp_runtime* ptowsp_rt_create(void) {

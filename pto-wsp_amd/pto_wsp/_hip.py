@@ -56,6 +56,8 @@ _lib.ptowsp_hip_num_launches.argtypes = [_vp]
 _lib.ptowsp_hip_kernel_cycles.argtypes = [_vp, ctypes.c_char_p]
 _lib.ptowsp_hip_kernel_cycles.restype = ctypes.c_uint64
 _lib.ptowsp_hip_kernel_family.argtypes = [_vp, ctypes.c_char_p]
+_lib.ptowsp_hip_run_result.argtypes = [_vp, ctypes.POINTER(RunInfo)]
+_lib.ptowsp_hip_run_result.restype = ctypes.c_int
 _lib.ptowsp_hip_precompile.argtypes = [_vp, ctypes.c_int, ctypes.c_int, ctypes.POINTER(ctypes.c_char_p)]
 _lib.ptowsp_hip_precompile.restype = ctypes.c_int
 _lib.ptowsp_hip_cycle_model.argtypes = [_vp, _vp, ctypes.POINTER(RunInfo)]
@@ -178,7 +180,28 @@ class NativeProgram:
             raise RuntimeError(_error())
         return src.value.decode() if src.value else ""
 
+    def _bind_key(self, tensors, axis_sizes, symbols_u64, symbols_ptr):
+        """Identity of a binding made only of device-resident torch tensors (storage pointer and
+        strides per tensor, plus the axis sizes and symbols), or None when any tensor is host
+        memory (those are staged through HBM on every launch)."""
+        if torch is None:
+            return None
+        key = []
+        for t in tensors:
+            d = t.data
+            if not isinstance(d, torch.Tensor) or not d.is_cuda:
+                return None
+            key.append((id(d), d.data_ptr(), d.stride()))
+        key.append(tuple(axis_sizes.items()))
+        key.append(tuple(symbols_u64.items()))
+        key.append(tuple((k, id(v)) for k, v in symbols_ptr.items()))
+        return tuple(key)
+
     def _bind(self, tensors, axis_sizes, symbols_u64, symbols_ptr):
+        key = self._bind_key(tensors, axis_sizes, symbols_u64, symbols_ptr)
+        if key is not None and key == getattr(self, "_last_bind", None):
+            return self._last_live, True
+        self._last_bind = None
         _lib.ptowsp_rt_clear(self._rt)
         live = []
         any_cuda = False
@@ -196,12 +219,14 @@ class NativeProgram:
             arr = np.ascontiguousarray(a, dtype=np.int32) if not isinstance(a, np.ndarray) or a.dtype != np.int32 else a
             live.append(arr)
             _lib.ptowsp_rt_set_symbol_ptr(self._rt, int(sid), arr.ctypes.data)
+        if key is not None:
+            self._last_bind, self._last_live = key, live
         return live, any_cuda
 
     def launch(self, tensors, axis_sizes: dict, symbols_u64: dict, symbols_ptr: dict, stream=None) -> LaunchResult:
         live, any_cuda = self._bind(tensors, axis_sizes, symbols_u64, symbols_ptr)
         if stream is None and any_cuda and torch is not None:
-            stream = torch.cuda.current_stream().cuda_stream
+            stream = torch._C._cuda_getCurrentRawStream(torch._C._cuda_getDevice())
         info = RunInfo()
         ctx = _lib.ptowsp_rt_context(self._rt)
         if _lib.ptowsp_hip_launch(self._h, ctx, _vp(stream) if stream else None, ctypes.byref(info)) != 0:
@@ -218,6 +243,13 @@ class NativeProgram:
         if rc != 0:
             raise RuntimeError(_error())
         return LaunchResult(int(info.total_cycles), int(info.task_count), 0)
+
+    def run_result(self) -> LaunchResult:
+        """Cycle model result of the last synchronized run."""
+        info = RunInfo()
+        if _lib.ptowsp_hip_run_result(self._h, ctypes.byref(info)) != 0:
+            raise RuntimeError(_error())
+        return LaunchResult(int(info.total_cycles), int(info.task_count), int(info.launches))
 
     def synchronize(self) -> SyncTiming:
         tm = Timing()

@@ -32,6 +32,7 @@ from typing import Any, Callable
 from pto_wsp.errors import CompileError, ExecutionError
 
 HIP_TARGETS = ("hip_gfx950", "hip", "gfx950", "mi355x")
+_U64_MAX = (1 << 64) - 1
 
 
 class TraceLevel(Enum):
@@ -210,8 +211,13 @@ class Program:
             with self._lock:
                 self._pending = False
             raise
-        self.stats.total_cycles = int(res.total_cycles)
-        self.stats.task_count = int(res.task_count)
+        # UINT64_MAX: the cycle model needs extent tensors that live on the
+        # device; it runs at synchronize() (the reference also sets
+        # total_cycles only when the run completes).
+        self._cycles_pending = res.total_cycles == _U64_MAX
+        if not self._cycles_pending:
+            self.stats.total_cycles = int(res.total_cycles)
+            self.stats.task_count = int(res.task_count)
         self.stats.launches = int(res.launches)
         self.stats.execute_time_ms = (time.perf_counter() - start) * 1000.0
 
@@ -228,6 +234,11 @@ class Program:
         finally:
             with self._lock:
                 self._pending = False
+        if getattr(self, "_cycles_pending", False):
+            res = self._native.run_result()
+            self.stats.total_cycles = int(res.total_cycles)
+            self.stats.task_count = int(res.task_count)
+            self._cycles_pending = False
         self.stats.device_time_ms = timing.device_ms
         self.stats.h2d_ms = timing.h2d_ms
         self.stats.d2h_ms = timing.d2h_ms
