@@ -13,7 +13,7 @@ and the fraction of the MI355X peak, from HIP-event kernel time), and
 ``cpu_baseline`` times this repository's C restatement of the reference
 cpu_sim artifact (oracle/, 1 thread) on the same inputs.
 
-    python bench.py [--gpus 1] [--steps K] [--warmup W] [--config NAME|all] [--no-cpu]
+    python bench.py [--gpus 1] [--steps K] [--warmup W] [--config NAME|all] [--no-cpu] [--warm-s S]
 """
 
 import argparse
@@ -434,6 +434,8 @@ def main():
     ap.add_argument("--warmup", type=int, default=3)
     ap.add_argument("--config", default="all", help=f"one of {list(CASES)} or 'all'")
     ap.add_argument("--no-cpu", action="store_true")
+    ap.add_argument("--warm-s", type=float, default=0.25,
+                    help="minimum warmup time (s) of every config line but the headline")
     args = ap.parse_args()
     if args.gpus != 1:
         print("bench.py: this build runs on one GPU only; --gpus must be 1", file=sys.stderr)
@@ -457,9 +459,9 @@ def main():
     for name in names:
         case = CASES[name]()
         case.setup(dev)
-        # The headline config keeps exactly W warmup steps; every other config
+        # The headline config (rmsnorm_bw) keeps exactly W warmup steps; every other config
         # line is measured at steady clocks (at least 0.25 s of warmup).
-        ms_step, k_ms = time_case(case, args.steps, args.warmup, 0.0 if name == head else 0.25)
+        ms_step, k_ms = time_case(case, args.steps, args.warmup, 0.0 if name == HEADLINE else args.warm_s)
         achieved = case.rate(k_ms * 1e-3)
         entry = {"baseline_config": case.baseline_config, "kernel_ms": round(k_ms, 5), "ms_per_step": round(ms_step, 5),
                  "achieved": round(achieved, 2), "unit": case.unit, "peak": case.peak(),

@@ -509,9 +509,11 @@ EmittedKernel emit_gemm(const Module& m, const KernelAnalysis& a, const LaunchSp
           << (g.f16 ? "true" : "false") << ", " << ns << ", " << ksplit << "> GB;\n";
     o << "  __shared__ __attribute__((aligned(1024))) u16 lds[GB::kLdsElems];\n";
     o << "  i64 vars[" << (nvars > 0 ? nvars : 1) << "];\n  (void)vars;\n";
+    // One workgroup per block (the host launches every block): nothing of
+    // the launch arguments stays live through the K loop.
     o << "  const i64 nblk = A.ntasks / " << fm * fn << ";\n";
-    o << "  for (i64 w = blockIdx.x; w < nblk; w += gridDim.x) {\n";
-    o << "    i64 q_ = (i64)gridDim.x >= nblk ? xcd_order(w, nblk) : w;\n";
+    o << "  {\n    const i64 w = blockIdx.x;\n    if (w >= nblk) return;\n";
+    o << "    i64 q_ = xcd_order(w, nblk);\n";
     // Decode the block index over the grid with the merged extents divided.
     for (int v = ng - 1; v >= 0; --v) {
         const int f = v == spec.gemm_vm ? fm : (v == spec.gemm_vn ? fn : 1);
@@ -522,26 +524,30 @@ EmittedKernel emit_gemm(const Module& m, const KernelAnalysis& a, const LaunchSp
     }
     o << "    i64 iters = 1;\n";
     for (int i = 0; i < ni; ++i) o << "    iters *= A.ext[" << ng + i << "];\n";
-    o << "    if (iters <= 0) continue;\n";
+    o << "    if (iters <= 0) return;\n";
     for (int i = 0; i < ni; ++i) o << "    vars[" << ng + i << "] = 0;\n";
     o << "    const u16* pa = reinterpret_cast<const u16*>(A.base[" << g.a << "] + (" << offset_expr(g.a, nvars, 0, 0) << ") * 2);\n";
     o << "    const u16* pb = reinterpret_cast<const u16*>(A.base[" << g.b << "] + (" << offset_expr(g.b, nvars, 0, 0) << ") * 2);\n";
     // The output view does not move with the in-kernel loops (checked on the host).
     o << "    float* pc = reinterpret_cast<float*>(A.base[" << g.c << "] + (" << offset_expr(g.c, nvars, 0, 0) << ") * 4);\n";
     // Byte offsets of in-kernel iteration `it` from iteration 0 (mixed radix over the inner loops).
-    o << "    auto off = [&](i64 it, int& soa, int& sob) {\n";
-    o << "      i64 oa = 0, ob = 0;\n";
     if (ni == 1) {
-        o << "      oa = A.coef[" << g.a << "][" << ng << "] * it; ob = A.coef[" << g.b << "][" << ng << "] * it;\n";
+        // One in-kernel loop: 32-bit byte steps (the host bounds every
+        // offset below 2^31).
+        o << "    const int da_ = static_cast<int>(A.coef[" << g.a << "][" << ng << "] * 2), db_ = static_cast<int>(A.coef[" << g.b
+          << "][" << ng << "] * 2);\n";
+        o << "    auto off = [=](i64 it, int& soa, int& sob) { soa = static_cast<int>(it) * da_; sob = static_cast<int>(it) * db_; };\n";
     } else {
+        o << "    auto off = [&](i64 it, int& soa, int& sob) {\n";
+        o << "      i64 oa = 0, ob = 0;\n";
         for (int i = ni - 1; i >= 0; --i) {
             const int v = ng + i;
             o << "      { const i64 x = it % A.ext[" << v << "]; it /= A.ext[" << v << "]; oa += A.coef[" << g.a << "][" << v
               << "] * x; ob += A.coef[" << g.b << "][" << v << "] * x; }\n";
         }
+        o << "      soa = static_cast<int>(oa * 2); sob = static_cast<int>(ob * 2);\n";
+        o << "    };\n";
     }
-    o << "      soa = static_cast<int>(oa * 2); sob = static_cast<int>(ob * 2);\n";
-    o << "    };\n";
     if (pp) {
         // L2 touches: the blocks that share an A panel (same m block) split its
         // rows by their n block (8 x 32 rows); those that share a B panel

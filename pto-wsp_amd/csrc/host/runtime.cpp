@@ -766,7 +766,13 @@ void enqueue_built(RunEnv& E, int li, BuiltLaunch& B, hipStream_t stream, uint64
     } else {
         blocks = B.spec.serial ? 1 : B.ntasks / ek.tasks_per_block;
     }
-    blocks = std::max<int64_t>(1, std::min<int64_t>(blocks, int64_t(1) << 20));
+    if (B.spec.gemm && !B.spec.serial) {
+        // GEMM kernels run exactly one block per workgroup.
+        if (blocks > 0x7FFFFFFF) throw std::runtime_error("GEMM launch: more than 2^31-1 blocks");
+    } else {
+        blocks = std::min<int64_t>(blocks, int64_t(1) << 20);
+    }
+    blocks = std::max<int64_t>(1, blocks);
     void* params[] = {&B.args};
     start_timing(E, stream);
     check(hipModuleLaunchKernel(jk->function, static_cast<unsigned>(blocks), 1, 1, static_cast<unsigned>(ek.threads), 1, 1,
