@@ -581,8 +581,6 @@ EmittedKernel emit_gemm(const Module& m, const KernelAnalysis& a, const LaunchSp
 // zero between launches, then the partials);
 // scal[kMaxScalars-1] is the declared maximum page count (larger extents
 // raise error 3 and are cut to it).
-// Pages in the register ring of a decode wave (DecodeWave::fold).
-constexpr int kDecodePageRing = 4;
 
 EmittedKernel emit_decode(const Module& m, const KernelAnalysis& a, const LaunchSpec& L, const EmitSpec& spec) {
     (void)m;
@@ -600,8 +598,9 @@ EmittedKernel emit_decode(const Module& m, const KernelAnalysis& a, const Launch
     scale.precision(9);
     scale << std::scientific << d.scale << "f";
 
+    const int nw = spec.decode_waves, nt = 64 * nw;
     EmittedKernel ek;
-    ek.threads = 256;
+    ek.threads = nt;
     ek.row_program = false;
     ek.part_floats = 2 * d.g + d.g * d.d;
     std::ostringstream o;
@@ -633,14 +632,14 @@ EmittedKernel emit_decode(const Module& m, const KernelAnalysis& a, const Launch
     // back-pressure, which would leave equal page shares finishing far
     // apart; alone on its SIMD a wave has the register file for its ring.
     ek.entry = entry_name("decode", k);
-    o << "extern \"C\" __global__ void __launch_bounds__(256) __attribute__((amdgpu_waves_per_eu(1, 1))) " << ek.entry
-      << "(const LaunchArgs A) {\n";
+    o << "extern \"C\" __global__ void __launch_bounds__(" << nt << ") __attribute__((amdgpu_waves_per_eu(" << nw / 4 << ", "
+      << nw / 4 << "))) " << ek.entry << "(const LaunchArgs A) {\n";
     o << "  typedef " << tmpl << " DW;\n";
     o << "  static_assert(DecodeSplit::kMaxUnits == " << kDecodeMaxUnits << ", \"unit limit\");\n";
     o << "  static_assert(DecodeSplit::kUnitCost == " << kDecodeUnitCost << ", \"unit cost\");\n";
-    o << "  __shared__ __attribute__((aligned(16))) float lds_all[4][DW::kLdsFloats];\n";
+    o << "  __shared__ __attribute__((aligned(16))) float lds_all[" << nw << "][DW::kLdsFloats];\n";
     o << "  __shared__ int pre[DecodeSplit::kMaxUnits + 1], cpre[DecodeSplit::kMaxUnits + 1];\n";
-    o << "  __shared__ int wsum[4], cwsum[4];\n";
+    o << "  __shared__ int wsum[" << nw << "], cwsum[" << nw << "];\n";
     o << "  const int tid = threadIdx.x, lane = tid & 63;\n";
     o << "  const int wave = __builtin_amdgcn_readfirstlane(tid >> 6);\n";
     o << "  const int U = static_cast<int>(A.ntasks);\n";
@@ -649,11 +648,11 @@ EmittedKernel emit_decode(const Module& m, const KernelAnalysis& a, const Launch
     // Prefixes of the page counts (pre) and of the units' scheduling costs
     // (cpre, DecodeSplit::cost): thread t owns units t*per .. t*per+per-1.
     o << "  {\n";
-    o << "    const int per = (U + 255) >> 8, u0 = tid * per;\n";
-    o << "    int n_[DecodeSplit::kMaxUnits / 256];\n";
+    o << "    const int per = (U + " << nt - 1 << ") / " << nt << ", u0 = tid * per;\n";
+    o << "    int n_[DecodeSplit::kMaxUnits / " << nt << "];\n";
     o << "    int run = 0, crun = 0;\n";
     o << "#pragma unroll\n";
-    o << "    for (int i = 0; i < DecodeSplit::kMaxUnits / 256; ++i) {\n";
+    o << "    for (int i = 0; i < DecodeSplit::kMaxUnits / " << nt << "; ++i) {\n";
     o << "      n_[i] = 0;\n";
     o << "      if (i < per && u0 + i < U) {\n";
     decode_vars("u0 + i", "        ");
@@ -681,14 +680,16 @@ EmittedKernel emit_decode(const Module& m, const KernelAnalysis& a, const Launch
     o << "    int base = x - run, cbase = cx - crun;\n";
     o << "    for (int j = 0; j < wave; ++j) { base += wsum[j]; cbase += cwsum[j]; }\n";
     o << "#pragma unroll\n";
-    o << "    for (int i = 0; i < DecodeSplit::kMaxUnits / 256; ++i)\n";
+    o << "    for (int i = 0; i < DecodeSplit::kMaxUnits / " << nt << "; ++i)\n";
     o << "      if (i < per && u0 + i < U) {\n";
     o << "        pre[u0 + i] = base; base += n_[i];\n";
     o << "        cpre[u0 + i] = cbase; cbase += DecodeSplit::cost(n_[i]);\n";
     o << "      }\n";
     o << "    if (tid == 0) {\n";
-    o << "      pre[U] = wsum[0] + wsum[1] + wsum[2] + wsum[3];\n";
-    o << "      cpre[U] = cwsum[0] + cwsum[1] + cwsum[2] + cwsum[3];\n";
+    o << "      int t_ = 0, c_ = 0;\n";
+    o << "      for (int j = 0; j < " << nw << "; ++j) { t_ += wsum[j]; c_ += cwsum[j]; }\n";
+    o << "      pre[U] = t_;\n";
+    o << "      cpre[U] = c_;\n";
     o << "    }\n";
     o << "    __syncthreads();\n";
     o << "  }\n";
@@ -714,7 +715,8 @@ EmittedKernel emit_decode(const Module& m, const KernelAnalysis& a, const Launch
     // Active waves: at most one per cost position, so that no wave's cost
     // range is empty and a unit's partials fill consecutive slots (a wave
     // whose range holds only cost positions, and no page, returns here).
-    o << "  const i64 W = (i64)gridDim.x * 4 < TC ? (i64)gridDim.x * 4 : TC, w = (i64)blockIdx.x * 4 + wave;\n";
+    o << "  const i64 W = (i64)gridDim.x * " << nw << " < TC ? (i64)gridDim.x * " << nw << " : TC, w = (i64)blockIdx.x * " << nw
+      << " + wave;\n";
     o << "  if (w < W) {\n";
     o << "  const i64 s = DecodeSplit::page_at(pre, cpre, U, w * TC / W);\n";
     o << "  const i64 b = DecodeSplit::page_at(pre, cpre, U, (w + 1) * TC / W);\n";
@@ -780,7 +782,7 @@ EmittedKernel emit_decode(const Module& m, const KernelAnalysis& a, const Launch
       << ");\n";
     o << "  };\n";
     o << "  auto fns = decode_fns(f_page, f_bases, f_q, f_slot, f_combine);\n";
-    o << "  DecodeStream<DW, " << kDecodePageRing << ">::run(fns, pre, cpre, U, TC, W, w, s, b, cnt, " << scale.str() << ", A.s4[" << d.kt
+    o << "  DecodeStream<DW, " << spec.decode_ring << ">::run(fns, pre, cpre, U, TC, W, w, s, b, cnt, " << scale.str() << ", A.s4[" << d.kt
       << "], A.s3[" << d.v << "], A.s3[" << d.q << "], lds);\n";
     o << "  }\n";
     o << "  }\n";
@@ -788,7 +790,7 @@ EmittedKernel emit_decode(const Module& m, const KernelAnalysis& a, const Launch
         const int q = ntens + 1;
         // Units without pages are never completed by a wave: their output is
         // the normalisation of the accumulators as they are.
-        o << "  for (int u = blockIdx.x * 4 + wave; u < U; u += gridDim.x * 4) {\n";
+        o << "  for (int u = blockIdx.x * " << nw << " + wave; u < U; u += gridDim.x * " << nw << ") {\n";
         o << "    if (__builtin_amdgcn_readfirstlane(pre[u + 1]) != __builtin_amdgcn_readfirstlane(pre[u])) continue;\n";
         o << "    i64 vars[" << nvars << "];\n";
         decode_vars("u", "    ");

@@ -37,6 +37,10 @@ struct EmitSpec {
     // Decode: the next launch (a NormInfo kernel over the same grid and o / l
     // views) is folded in; its output tensor is argument slot ntens + 1.
     bool decode_norm = false;
+    // Decode: pages in each wave's register ring, and waves per block (4:
+    // one per SIMD; 8: two per SIMD, 256 VGPRs each).
+    int decode_ring = 4;
+    int decode_waves = 4;
 };
 
 // Units (grid tasks) of one decode launch at most: every block holds their

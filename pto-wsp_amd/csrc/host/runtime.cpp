@@ -313,6 +313,8 @@ struct Tuning {
     int row_up = 2;
     bool nontemporal = true;
     bool gemm_pingpong = true;
+    int decode_ring = 4;
+    int decode_waves = 4;
 };
 
 const Tuning& tuning() {
@@ -321,6 +323,8 @@ const Tuning& tuning() {
         if (const char* s = std::getenv("PTOWSP_ROW_UNROLL")) v.row_up = std::max(1, std::atoi(s));
         if (const char* s = std::getenv("PTOWSP_NONTEMPORAL")) v.nontemporal = std::atoi(s) != 0;
         if (const char* s = std::getenv("PTOWSP_GEMM_PINGPONG")) v.gemm_pingpong = std::atoi(s) != 0;
+        if (const char* s = std::getenv("PTOWSP_DECODE_RING")) v.decode_ring = std::min(8, std::max(2, std::atoi(s)));
+        if (const char* s = std::getenv("PTOWSP_DECODE_WAVES")) v.decode_waves = std::atoi(s) == 8 ? 8 : 4;
         return v;
     }();
     return t;
@@ -640,6 +644,8 @@ BuiltLaunch build_launch(RunEnv& E, const LaunchSpec& L) {
         B.spec.gemm_pingpong = false;
     }
     B.spec.decode = decode_allowed(a, L, A, B.spec, ng);
+    B.spec.decode_ring = tuning().decode_ring;
+    B.spec.decode_waves = tuning().decode_waves;
     B.spec.vec_width = a.family == Family::RowProgram ? pick_vec_width(a, A, nvars) : 1;
     return B;
 }
@@ -649,7 +655,7 @@ std::string spec_key(const EmitSpec& s) {
     o << "vw" << s.vec_width << (s.serial ? ";serial" : "") << ";up" << s.row_up << (s.nontemporal ? ";nt" : "")
       << (s.gemm ? ";gemm" : "") << ";m" << s.gemm_vm << ";n" << s.gemm_vn << (s.gemm_pingpong ? ";pp" : "")
       << (s.decode ? ";dec" : "")
-      << (s.decode_norm ? ";norm" : "")
+      << (s.decode_norm ? ";norm" : "") << ";r" << s.decode_ring << ";w" << s.decode_waves
       << ";i";
     for (int c : s.indirect_count) o << c << ",";
     o << ";d";
@@ -674,7 +680,7 @@ struct DecodeShape {
     int64_t blocks = 1;
     unsigned dyn_lds = 0;
 };
-DecodeShape decode_shape(hipFunction_t f) {
+DecodeShape decode_shape(hipFunction_t f, int threads) {
     static std::mutex mu;
     static std::map<std::pair<int, hipFunction_t>, DecodeShape> memo;
     int dev = 0;
@@ -690,7 +696,7 @@ DecodeShape decode_shape(hipFunction_t f) {
     const int half = lds_cu / 2 + 1024;
     r.dyn_lds = static_cast<unsigned>(std::max(0, half - lds_static));
     int per_cu = 0;
-    check(hipModuleOccupancyMaxActiveBlocksPerMultiprocessor(&per_cu, f, 256, r.dyn_lds),
+    check(hipModuleOccupancyMaxActiveBlocksPerMultiprocessor(&per_cu, f, threads, r.dyn_lds),
           "hipModuleOccupancyMaxActiveBlocksPerMultiprocessor");
     if (per_cu != 1)
         throw std::runtime_error("decode launch: expected one resident block per CU, occupancy reports " + std::to_string(per_cu));
@@ -712,9 +718,9 @@ void enqueue_decode(RunEnv& E, int li, BuiltLaunch& B, const EmittedKernel& ek, 
     const int ng = static_cast<int>(L.grid.size());
     const Axis& ax = *L.inner[0].axis;
     const int64_t maxp = std::max<int64_t>(0, ax.kind == AxisKind::DynTensor ? ax.max : B.args.ext[ng]);
-    const DecodeShape shape = decode_shape(jk.function);
+    const DecodeShape shape = decode_shape(jk.function, ek.threads);
     const int64_t grid = shape.blocks;
-    const int64_t waves = 4 * grid;
+    const int64_t waves = static_cast<int64_t>(ek.threads / 64) * grid;
     const size_t count_bytes = static_cast<size_t>(kDecodeMaxUnits) * sizeof(int32_t);
     const size_t part_bytes = static_cast<size_t>(B.ntasks + waves) * static_cast<size_t>(ek.part_floats) * sizeof(float);
     const size_t need = count_bytes + part_bytes;
@@ -734,7 +740,8 @@ void enqueue_decode(RunEnv& E, int li, BuiltLaunch& B, const EmittedKernel& ek, 
     B.args.scal[kMaxScalars - 1] = static_cast<uint64_t>(maxp);
     void* params[] = {&B.args};
     start_timing(E, stream);
-    check(hipModuleLaunchKernel(jk.function, static_cast<unsigned>(grid), 1, 1, 256, 1, 1, shape.dyn_lds, stream, params,
+    check(hipModuleLaunchKernel(jk.function, static_cast<unsigned>(grid), 1, 1, static_cast<unsigned>(ek.threads), 1, 1,
+                                shape.dyn_lds, stream, params,
                                 nullptr),
           "hipModuleLaunchKernel(decode)");
     launches += 1;
@@ -1077,6 +1084,8 @@ int ptowsp_hip_precompile(ptowsp_program* P, int index, int flags, const char** 
             spec.nontemporal = tuning().nontemporal;
             spec.gemm = a.family == Family::Gemm && !spec.serial;
             spec.decode = a.family == Family::Decode && !spec.serial && L.inner.size() == 1;
+            spec.decode_ring = tuning().decode_ring;
+            spec.decode_waves = tuning().decode_waves;
             spec.indirect_count.assign(L.targs.size(), 0);
             for (size_t p = 0; p < L.targs.size(); ++p)
                 for (const auto& e : L.targs[p]->idx)
