@@ -1171,8 +1171,10 @@ int ptowsp_hip_launch(ptowsp_program* P, RuntimeContext* ctx, void* hip_stream, 
             check(hipHostGetDevicePointer(reinterpret_cast<void**>(&P->d_err), P->h_err, 0), "hipHostGetDevicePointer(err)");
         }
         if (!P->have_events) {
-            check(hipEventCreate(&P->ev0), "hipEventCreate");
-            check(hipEventCreate(&P->ev1), "hipEventCreate");
+            // Timing-only events: no system-scope fence (cache writeback) of
+            // their own, which would otherwise be counted as device time.
+            check(hipEventCreateWithFlags(&P->ev0, hipEventDisableSystemFence), "hipEventCreate");
+            check(hipEventCreateWithFlags(&P->ev1, hipEventDisableSystemFence), "hipEventCreate");
             P->have_events = true;
         }
         RunEnv E{P, ctx, {}, {}, {}};
@@ -1186,9 +1188,10 @@ int ptowsp_hip_launch(ptowsp_program* P, RuntimeContext* ctx, void* hip_stream, 
         else if (ext_written) defer_cycles(E, dev_ext, stream);
         uint64_t launches = 0;
         run_items(E, P->plan.items, stream, launches);
-        if (!dev_ext.empty() && !ext_written) defer_cycles(E, dev_ext, stream);
         start_timing(E, stream);
         check(hipEventRecord(P->ev1, stream), "hipEventRecord");
+        // After the end event: the copy is not device time of the program.
+        if (!dev_ext.empty() && !ext_written) defer_cycles(E, dev_ext, stream);
         check(hipGetLastError(), "kernel launch");
         P->stream = stream;
         P->pending = true;
