@@ -469,3 +469,61 @@ def test_paged_decode_extent_above_declared_maximum_raises(gpu):
     prog.execute()
     with pytest.raises(ExecutionError, match="declared maximum"):
         prog.synchronize()
+
+
+# ---------------------------------------------------------------- host path
+def test_device_extent_cycles_follow_the_page_counts(gpu):
+    """Page counts in a device tensor: total_cycles comes from the cycle model at
+    synchronize() and follows the tensor's contents from run to run (the oracle on
+    host copies gives the expected values)."""
+    import torch
+
+    ga = W.paged_decode_arrays([37, 200, 16, 90], 2, 4, 128, seed=21)
+    dev = {k: torch.from_numpy(np.ascontiguousarray(v)).to(gpu) for k, v in ga.items() if k != "lengths"}
+    for k in ("q", "k_cache", "v_cache"):  # bf16 bits held as uint16
+        dev[k] = torch.from_numpy(ga[k].view(np.int16)).to(gpu).view(torch.bfloat16)
+    prog = W.paged_decode(dev).compile(target="hip_gfx950")
+    for npg in ([3, 13, 1, 6], [1, 2, 1, 1], [3, 13, 1, 6]):
+        dev["npages"].copy_(torch.tensor(npg, dtype=torch.int32))
+        for k, v in (("m", -np.inf), ("l", 0.0), ("o", 0.0)):
+            dev[k].fill_(v)
+        prog.execute()
+        prog.synchronize()
+        ca = {k: (v.copy() if isinstance(v, np.ndarray) else v) for k, v in ga.items()}
+        ca["npages"] = np.asarray(npg, np.int32)
+        ref = run_workload(W.paged_decode(ca))
+        assert prog.stats.total_cycles == ref.total_cycles, npg
+        assert prog.stats.task_count == ref.task_count, npg
+        np.testing.assert_allclose(dev["out"].cpu().numpy(), ca["out"], rtol=2e-5,
+                                   atol=2e-5 * float(np.abs(ca["out"]).max()))
+
+
+def test_rebinding_follows_a_swapped_tensor(gpu):
+    """Device tensors are rebound only when their storage changes: swapping the
+    data of the input Tensor between runs is seen by the next run."""
+    import torch
+
+    from pto_wsp import Dense, In, Out, P, Tensor, Tile, kernel, pto, workload
+
+    x1 = torch.randn((2, 4, 16, 128), device=gpu)
+    x2 = torch.randn((2, 4, 16, 128), device=gpu)
+    y = torch.zeros_like(x1)
+    X = Tensor(data=x1, shape=tuple(x1.shape), dtype=W.F32)
+    Y = Tensor(data=y, shape=tuple(y.shape), dtype=W.F32)
+
+    @kernel
+    def scale_tile(x: In[Tile[16, 128, W.F32]], out: Out[Tile[16, 128, W.F32]]):
+        pto.store(out, pto.mul(x, x))
+
+    @workload
+    def wl():
+        for b in P(Dense[2]()):
+            for t in P(Dense[4]()):
+                scale_tile[b, t](x=X[b][t], out=Y[b][t])
+
+    prog = wl().compile(target="hip_gfx950")
+    for x in (x1, x1, x2, x1):
+        X.data = x
+        prog.execute()
+        prog.synchronize()
+        torch.testing.assert_close(y, x * x, rtol=0, atol=0)
