@@ -263,9 +263,10 @@ std::unique_ptr<Node> parse_node(Lexer& L, const Module& m) {
     } else if (k == "sel") {
         n->kind = NodeKind::Select;
         n->var = L.str();
-        (void)L.str();
-        (void)L.str();
-        (void)L.str();
+        n->axis.kind = AxisKind::Select;
+        n->axis.a = L.str();
+        n->axis.b = L.str();
+        n->axis.c = L.str();
         n->body = parse_node(L, m);
     } else if (k == "cond") {
         n->kind = NodeKind::Cond;

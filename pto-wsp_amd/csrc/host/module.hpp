@@ -86,12 +86,14 @@ struct TensorArg {
     std::vector<IndexExpr> idx;
 };
 
-enum class AxisKind { Dense, Dyn, Ragged, DynTensor };
+enum class AxisKind { Dense, Dyn, Ragged, DynTensor, Select };
 
 struct Axis {
     AxisKind kind = AxisKind::Dense;
     int64_t size = 0;
-    std::string a, b;  // Dyn: runtime key; Ragged: outer / lengths symbol names
+    // Dyn: runtime key (a); Ragged: outer / lengths symbol names (a, b);
+    // Select: CSR outer-size / indptr / indices symbol names (a, b, c).
+    std::string a, b, c;
     IndexExpr expr;    // DynTensor: the i32 element holding the extent
     int64_t max = 0;   // DynTensor: declared upper bound of the extent
 };

@@ -3,6 +3,7 @@
 #include <algorithm>
 #include <functional>
 #include <queue>
+#include <stdexcept>
 
 namespace ptowsp {
 
@@ -82,8 +83,19 @@ void lower(const Module& m, const std::vector<KernelAnalysis>& ka, const Node* n
         case NodeKind::Sequential:
             for (const auto& c : n->kids) lower(m, ka, c.get(), ctx, plan, out);
             return;
-        case NodeKind::Select:
-            throw CompileError("P.sel (sparse select) is not supported by the HIP target");
+        case NodeKind::Select: {
+            // The selected indices are host symbols that may change between
+            // runs: a host loop over them, each iteration launching its body
+            // (iterations run in order, as in the reference's artifact loop,
+            // src/python/pto_codegen.cpp:2417-2452, so repeated indices stay
+            // exact).
+            PlanItem loop;
+            loop.is_loop = true;
+            loop.loop = LoopSpec{n->var, &n->axis};
+            lower(m, ka, n->body.get(), ctx, plan, loop.body);
+            out.push_back(std::move(loop));
+            return;
+        }
         case NodeKind::Cond:
             throw CompileError("P.when / cond is not supported by the HIP target");
     }
@@ -145,6 +157,7 @@ struct Walker {
                 return ub;
             }
             case AxisKind::DynTensor: return env.index_value(a.expr, vars);
+            case AxisKind::Select: break;
         }
         return 0;
     }
@@ -183,6 +196,23 @@ struct Walker {
                 uint64_t cur = ready;
                 for (const auto& c : n->kids) cur = eval(c.get(), cur);
                 return cur;
+            }
+            case NodeKind::Select: {
+                // CSR select (src/python/pto_codegen.cpp:2417-2452): every
+                // selected index starts at `ready`.
+                const int64_t outer = static_cast<int64_t>(env.symbol_u64(fnv1a_64(n->axis.a)));
+                const int32_t* indptr = env.symbol_ptr(fnv1a_64(n->axis.b));
+                const int32_t* indices = env.symbol_ptr(fnv1a_64(n->axis.c));
+                if (outer < 0) throw std::runtime_error("P.sel: negative outer size");
+                const int64_t nnz = indptr ? indptr[outer] : 0;
+                uint64_t done = ready;
+                vars.emplace_back(n->var, 0);
+                for (int64_t p = 0; p < nnz; ++p) {
+                    vars.back().second = indices ? indices[p] : 0;
+                    done = std::max(done, eval(n->body.get(), ready));
+                }
+                vars.pop_back();
+                return done;
             }
             case NodeKind::Task: {
                 ++tasks;

@@ -197,6 +197,7 @@ int64_t axis_extent(RunEnv& E, const Axis& a) {
             return ub;
         }
         case AxisKind::DynTensor: throw CompileError("internal: tensor-bound extent evaluated on the host");
+        case AxisKind::Select: throw CompileError("internal: a select axis used as a loop extent");
     }
     return 0;
 }
@@ -856,7 +857,23 @@ void run_items(RunEnv& E, const std::vector<PlanItem>& items, hipStream_t stream
             enqueue_launch(E, it.launch, stream, launches);
             continue;
         }
-        const int64_t ub = axis_extent(E, *it.loop.axis);
+        const Axis& ax = *it.loop.axis;
+        if (ax.kind == AxisKind::Select) {
+            // CSR select: indices[0 .. indptr[outer]) from host symbols, in order.
+            const int64_t outer = static_cast<int64_t>(E.ctx->get_symbol_u64(E.ctx->ctx, fnv1a_64(ax.a)));
+            const int32_t* indptr = static_cast<const int32_t*>(E.ctx->get_symbol_ptr(E.ctx->ctx, fnv1a_64(ax.b)));
+            const int32_t* indices = static_cast<const int32_t*>(E.ctx->get_symbol_ptr(E.ctx->ctx, fnv1a_64(ax.c)));
+            if (outer < 0) throw std::runtime_error("P.sel: negative outer size");
+            const int64_t nnz = indptr ? indptr[outer] : 0;
+            E.host_vars.emplace_back(it.loop.var, 0);
+            for (int64_t p = 0; p < nnz; ++p) {
+                E.host_vars.back().second = indices ? indices[p] : 0;
+                run_items(E, it.body, stream, launches);
+            }
+            E.host_vars.pop_back();
+            continue;
+        }
+        const int64_t ub = axis_extent(E, ax);
         E.host_vars.emplace_back(it.loop.var, 0);
         for (int64_t i = 0; i < ub; ++i) {
             E.host_vars.back().second = i;
@@ -934,6 +951,21 @@ CycleResult cycles_for(RunEnv& E) {
     std::ostringstream key;
     std::function<void(const Node*)> walk = [&](const Node* n) {
         if (!n) return;
+        if (n->kind == NodeKind::Select) {
+            // The selected index list (its contents decide the tasks).
+            const Axis& a = n->axis;
+            const int64_t outer = static_cast<int64_t>(env.symbol_u64(fnv1a_64(a.a)));
+            const int32_t* indptr = env.symbol_ptr(fnv1a_64(a.b));
+            const int32_t* indices = env.symbol_ptr(fnv1a_64(a.c));
+            key << "s" << outer << ":";
+            if (indptr && outer >= 0) {
+                for (int64_t i = 0; i <= outer; ++i) key << indptr[i] << ",";
+                key << "|";
+                if (indices)
+                    for (int64_t i = 0; i < indptr[outer]; ++i) key << indices[i] << ",";
+            }
+            key << ";";
+        }
         if (n->kind == NodeKind::ParallelFor || n->kind == NodeKind::ForEach) {
             const Axis& a = n->axis;
             if (a.kind == AxisKind::Dyn) key << "d" << a.a << "=" << env.axis_size(a.a) << ";";

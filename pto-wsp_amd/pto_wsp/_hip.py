@@ -194,7 +194,12 @@ class NativeProgram:
             key.append((id(d), d.data_ptr(), d.stride()))
         key.append(tuple(axis_sizes.items()))
         key.append(tuple(symbols_u64.items()))
-        key.append(tuple((k, id(v)) for k, v in symbols_ptr.items()))
+        for k, v in symbols_ptr.items():
+            # Only arrays bound as they are (read in place at every launch) can be cached; any
+            # other value is copied to an int32 array at binding time.
+            if not isinstance(v, np.ndarray) or v.dtype != np.int32 or not v.flags.c_contiguous:
+                return None
+            key.append((k, id(v), v.ctypes.data))
         return tuple(key)
 
     def _bind(self, tensors, axis_sizes, symbols_u64, symbols_ptr):
@@ -216,7 +221,7 @@ class NativeProgram:
         for sid, v in symbols_u64.items():
             _lib.ptowsp_rt_set_symbol_u64(self._rt, int(sid), int(v) & 0xFFFFFFFFFFFFFFFF)
         for sid, a in symbols_ptr.items():
-            arr = np.ascontiguousarray(a, dtype=np.int32) if not isinstance(a, np.ndarray) or a.dtype != np.int32 else a
+            arr = np.ascontiguousarray(a, dtype=np.int32)
             live.append(arr)
             _lib.ptowsp_rt_set_symbol_ptr(self._rt, int(sid), arr.ctypes.data)
         if key is not None:

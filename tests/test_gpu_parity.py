@@ -218,6 +218,71 @@ def test_ragged_axis_rebinding(gpu):
     np.testing.assert_array_equal(y.reshape(3), [1, 1, 1])
 
 
+def test_sparse_select_indices_can_change_without_recompile(gpu):
+    """tests/test_codegen_select_sparse.py on the HIP target, plus repeated indices (every
+    occurrence applies, in order) and an empty selection; cycles and tasks as the oracle's."""
+    from pto_wsp import Sparse
+
+    y = np.zeros((4, 1, 1), np.int32)
+    sp = Sparse(outer_size=2, indptr=[0, 2, 3], indices=[0, 2, 1])
+    prog = W.sparse_mark({"y": y}, sp).named("dyn_sparse_select").compile(target="hip_gfx950")
+    sid = id(sp)
+    for outer, indptr, indices, want in [(2, [0, 2, 3], [0, 2, 1], [1, 1, 1, 0]),
+                                         (1, [0, 1], [3], [0, 0, 0, 1]),
+                                         (3, [0, 3, 3, 6], [1, 1, 0, 3, 1, 2], [1, 3, 1, 1]),
+                                         (2, [0, 0, 0], [], [0, 0, 0, 0])]:
+        y[:] = 0
+        prog.set_symbol_u64(f"outer_{sid}", outer)
+        prog.set_symbol_ptr(f"indptr_{sid}", np.asarray(indptr, dtype=np.int32))
+        prog.set_symbol_ptr(f"indices_{sid}", np.asarray(indices, dtype=np.int32))
+        prog.execute()
+        prog.synchronize()
+        np.testing.assert_array_equal(y.reshape(4), np.asarray(want, np.int32))
+        su, sptr = W.sparse_symbols(sp, outer, indptr, indices)
+        ref = run_workload(W.sparse_mark({"y": np.zeros((4, 1, 1), np.int32)}, sp), symbols_u64=su,
+                           symbols_ptr=sptr, module_name="dyn_sparse_select")
+        assert (int(prog.stats.total_cycles), int(prog.stats.task_count)) == (ref.total_cycles, ref.task_count)
+        assert int(prog.stats.task_count) == len(indices)
+    # A selected index past the tensor is refused on the host, before any launch; the program
+    # stays usable.
+    prog.set_symbol_u64(f"outer_{sid}", 1)
+    prog.set_symbol_ptr(f"indptr_{sid}", np.asarray([0, 1], np.int32))
+    prog.set_symbol_ptr(f"indices_{sid}", np.asarray([4], np.int32))
+    with pytest.raises(RuntimeError, match="addressable elements"):
+        prog.execute()
+    y[:] = 0
+    prog.set_symbol_ptr(f"indices_{sid}", np.asarray([2], np.int32))
+    prog.execute()
+    prog.synchronize()
+    np.testing.assert_array_equal(y.reshape(4), [0, 0, 1, 0])
+
+
+def test_sparse_select_on_device_rows(gpu):
+    """Selected tiles of device-resident tensors: each selected tile of y is the rmsnorm of x's,
+    the others keep their contents; fp32 rtol 1e-5 against the oracle on the same symbols."""
+    import torch
+    from pto_wsp import Sparse
+
+    x = np.random.default_rng(7).standard_normal((64, 16, 512), dtype=np.float32)
+    y0 = np.full_like(x, -3.0)
+    sp = Sparse(outer_size=1, indptr=[0, 3], indices=[5, 40, 63])
+    xd, yd = torch.from_numpy(x).to(gpu), torch.from_numpy(y0).to(gpu)
+    prog = W.rmsnorm_select({"x": xd, "y": yd}, sp).compile(target="hip_gfx950")
+    outer, indptr, sel = 2, [0, 3, 5], [5, 40, 63, 0, 17]
+    prog.set_symbol_u64(f"outer_{id(sp)}", outer)
+    prog.set_symbol_ptr(f"indptr_{id(sp)}", np.asarray(indptr, np.int32))
+    prog.set_symbol_ptr(f"indices_{id(sp)}", np.asarray(sel, np.int32))
+    prog.execute()
+    prog.synchronize()
+    ca = {"x": x.copy(), "y": y0.copy()}
+    su, sptr = W.sparse_symbols(sp, outer, indptr, sel)
+    ref = run_workload(W.rmsnorm_select(ca, sp), symbols_u64=su, symbols_ptr=sptr)
+    got = yd.cpu().numpy()
+    np.testing.assert_allclose(got, ca["y"], rtol=1e-5, atol=1e-6)
+    np.testing.assert_array_equal(np.delete(got, sel, axis=0), np.delete(y0, sel, axis=0))
+    assert (int(prog.stats.total_cycles), int(prog.stats.task_count)) == (ref.total_cycles, ref.task_count)
+
+
 def _rel_fro(got, ref):
     return float(np.linalg.norm((got - ref).ravel()) / np.linalg.norm(ref.ravel()))
 

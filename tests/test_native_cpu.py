@@ -5,7 +5,9 @@
   built for gfx950 by hiprtc;
 * the product's cycle model (C++) gives the same total_cycles and task
   count as the oracle (C) on every workload;
-* constructs the HIP target does not lower raise CompileError.
+* constructs the HIP target does not lower (P.when / cond) raise CompileError;
+* a CSR select (P.sel) follows its runtime symbols in the cycle model exactly
+  as the oracle does.
 """
 
 import ctypes
@@ -17,7 +19,7 @@ import pytest
 
 import workloads as W
 from oracle.runner import run_workload
-from pto_wsp import CompileError, DType, Dense, In, Out, P, Ragged, Tensor, Tile, kernel, pto, workload
+from pto_wsp import CompileError, DType, Dense, In, Out, P, Ragged, Sparse, Tensor, Tile, kernel, pto, workload
 from pto_wsp.ir_bridge import workload_to_codegen_ir
 from pto_wsp.program import Program
 
@@ -168,7 +170,7 @@ def test_ops_without_reference_compute_are_refused():
     _compile_err(wl(), "no compute")
 
 
-def test_select_and_cond_are_refused():
+def test_cond_is_refused():
     X = Tensor(data=None, shape=(2, 4, 4), dtype=DType.F32)
 
     @kernel
@@ -187,3 +189,51 @@ def test_ragged_axis_compiles():
     y = np.zeros((3, 1, 1), np.int32)
     r = Ragged(2, [1, 1])
     Program(W.ragged_mark({"y": y}, r), "hip_gfx950", {})
+
+
+# (outer, indptr, indices): the reference test's two bindings, repeated and unordered indices,
+# an empty row, an empty selection.
+_SELECTIONS = [
+    (2, [0, 2, 3], [0, 2, 1]),
+    (1, [0, 1], [3]),
+    (3, [0, 3, 3, 6], [1, 1, 0, 3, 1, 2]),
+    (2, [0, 0, 0], []),
+]
+
+
+def test_select_compiles():
+    y = np.zeros((4, 1, 1), np.int32)
+    sp = Sparse(outer_size=2, indptr=[0, 2, 3], indices=[0, 2, 1])
+    src = workload_to_codegen_ir(W.sparse_mark({"y": y}, sp), "s").module
+    assert f"outer_{id(sp)}" in src and f"indices_{id(sp)}" in src
+    Program(W.sparse_mark({"y": y}, sp), "hip_gfx950", {})
+
+
+@pytest.mark.parametrize("sel", range(len(_SELECTIONS)))
+def test_select_cycle_model_matches_oracle(sel):
+    from pto_wsp._hip import NativeProgram
+
+    outer, indptr, indices = _SELECTIONS[sel]
+    y = np.zeros((4, 1, 1), np.int32)
+    sp = Sparse(outer_size=2, indptr=[0, 2, 3], indices=[0, 2, 1])
+    w = W.sparse_mark({"y": y}, sp)
+    build = workload_to_codegen_ir(w, "s")
+    su, sptr = W.sparse_symbols(sp, outer, indptr, indices)
+    got = NativeProgram(build.module).cycle_model(build.tensors, Program._infer_axis_sizes(w), su, sptr)
+    ref = run_workload(W.sparse_mark({"y": y}, sp), symbols_u64=su, symbols_ptr=sptr, module_name="s")
+    assert (got.total_cycles, got.task_count) == (ref.total_cycles, ref.task_count)
+    assert got.task_count == len(indices)
+    # the oracle applied the selection: one increment per occurrence of each index
+    np.testing.assert_array_equal(y.reshape(4), np.bincount(np.asarray(indices, int), minlength=4))
+
+
+def test_select_without_bound_symbols_runs_nothing():
+    """Unbound symbols read as 0 / null: an empty selection, as in the reference's artifact."""
+    from pto_wsp._hip import NativeProgram
+
+    y = np.zeros((4, 1, 1), np.int32)
+    sp = Sparse(outer_size=2, indptr=[0, 2, 3], indices=[0, 2, 1])
+    w = W.sparse_mark({"y": y}, sp)
+    build = workload_to_codegen_ir(w, "s")
+    got = NativeProgram(build.module).cycle_model(build.tensors, {}, {}, {})
+    assert got.task_count == 0

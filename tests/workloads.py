@@ -491,6 +491,54 @@ def ragged_mark(arrs: dict, ragged: Ragged):
     return wl()
 
 
+def sparse_mark(arrs: dict, sparse):
+    """tests/test_codegen_select_sparse.py: y[e] += 1 for every selected index e of a CSR axis."""
+    Y = T(arrs["y"], I32)
+
+    @kernel
+    def mark(y_tile: InOut[Tile[1, 1, I32]]):
+        v = pto.load(y_tile)
+        one = pto.constant(1.0, I32)
+        pto.store(y_tile, pto.add(v, one))
+
+    @workload
+    def wl():
+        for e in P.sel(sparse, name="e"):
+            mark[e](y_tile=Y[e])
+
+    return wl()
+
+
+def rmsnorm_select(arrs: dict, sparse):
+    """The quickstart rmsnorm tile over the selected rows e of X[rows, R, C] only."""
+    x = arrs["x"]
+    _, R, C = x.shape
+    X, Y = T(arrs["x"]), T(arrs["y"])
+
+    @kernel
+    def rmsnorm_tile(x: In[Tile[R, C, F32]], out: Out[Tile[R, C, F32]]):
+        inv = pto.rsqrt(pto.rowmean(pto.mul(x, x)))
+        pto.store(out, pto.mul(x, inv))
+
+    @workload
+    def wl():
+        for e in P.sel(sparse, name="e"):
+            rmsnorm_tile[e](x=X[e], out=Y[e])
+
+    return wl()
+
+
+def sparse_symbols(sparse, outer: int, indptr, indices):
+    """(symbols_u64, symbols_ptr) binding a CSR selection to ``sparse``'s runtime symbols,
+    keyed by the FNV-1a-64 ids of ``outer_<id>`` / ``indptr_<id>`` / ``indices_<id>``."""
+    from pto_wsp.program import Program
+
+    sid = id(sparse)
+    fnv = Program._fnv1a_64
+    return ({fnv(f"outer_{sid}"): int(outer)},
+            {fnv(f"indptr_{sid}"): np.asarray(indptr, np.int32), fnv(f"indices_{sid}"): np.asarray(indices, np.int32)})
+
+
 # ---------------------------------------------------------------- numpy references (float64)
 def rmsnorm_ref(x):
     x64 = x.astype(np.float64)
