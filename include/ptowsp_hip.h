@@ -116,6 +116,10 @@ int ptowsp_rt_set_axis_size(ptowsp_runtime* rt, const char* name, int64_t size);
 int ptowsp_rt_set_symbol_u64(ptowsp_runtime* rt, uint64_t symbol_id, uint64_t value);
 int ptowsp_rt_set_symbol_ptr(ptowsp_runtime* rt, uint64_t symbol_id, void* ptr);
 void ptowsp_rt_clear(ptowsp_runtime* rt);
+/* Zeroes the 256 slots: the reference's CodegenRuntime starts every run with
+ * fresh zeroed slots (src/python/pto_codegen.cpp:3546-3550); call it before
+ * each ptowsp_hip_launch to get the same. */
+int ptowsp_rt_reset_slots(ptowsp_runtime* rt);
 RuntimeContext* ptowsp_rt_context(ptowsp_runtime* rt);
 
 #ifdef __cplusplus

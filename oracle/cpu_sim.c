@@ -103,9 +103,20 @@ typedef struct IExpr {
 } IExpr;
 
 typedef struct { char kind; char* var; uint64_t u64; } Arg; /* v c s */
+
+/* Scalar expression (the reference's ScalarExpr, include/pto/wsp/ir/ as
+ * emitted by src/python/pto_codegen.cpp:220-300). ty: 'b' bool, 'i' int64_t,
+ * 'u' uint64_t. kind: L literal, P task param, G task tag, A axis var,
+ * Y symbol, S slot, U unary, B binary, T ternary, C cast. */
+typedef struct SX {
+    char kind, ty;
+    uint64_t u;
+    char op[4];
+    struct SX *a, *b, *c;
+} SX;
 typedef struct { char* param; int tid, base_rank, view_rank, nidx; IExpr* idx; } TArg;
 
-enum { N_EMPTY, N_PFOR, N_EACH, N_COMB, N_SEQN, N_TASK, N_SEL, N_COND };
+enum { N_EMPTY, N_PFOR, N_EACH, N_COMB, N_SEQN, N_TASK, N_SEL, N_COND, N_SLOTSET, N_SLOTLD };
 enum { AX_DENSE, AX_DYN, AX_RAGGED, AX_DYNT };
 
 typedef struct Node {
@@ -124,6 +135,11 @@ typedef struct Node {
     Arg *axis, *scal;
     TArg* ten;
     char *sel_outer, *sel_indptr, *sel_indices;
+    SX* pred;                     /* cond */
+    uint32_t slot;                /* slot set / load */
+    uint64_t slot_value;
+    TArg slot_view;
+    int64_t slot_row, slot_col;
 } Node;
 
 typedef struct {
@@ -132,6 +148,7 @@ typedef struct {
     Kernel* kernels;
     Node* root;
     int has_dispatch, dispatch_rr, dispatch_keyed;
+    SX* dispatch_key;
     int64_t num_targets;
     int has_window, window_ok;
     int64_t window_size;
@@ -338,6 +355,43 @@ static void parse_axis(Lex* L, Node* n) {
     else fail("module text: bad axis kind '%s'", k);
 }
 
+static SX* parse_sx(Lex* L) {
+    SX* e = (SX*)alloc(sizeof(SX));
+    char* k = tok(L);
+    if (strcmp(k, "Lb") == 0 || strcmp(k, "Li") == 0 || strcmp(k, "Lu") == 0) {
+        e->kind = 'L';
+        e->ty = k[1] == 'b' ? 'b' : k[1] == 'i' ? 'i' : 'u';
+        e->u = e->ty == 'i' ? (uint64_t)tok_i64(L) : tok_u64(L);
+        if (e->ty == 'b') e->u = e->u != 0;
+    } else if (strcmp(k, "P") == 0 || strcmp(k, "S") == 0 || strcmp(k, "A") == 0 || strcmp(k, "C") == 0) {
+        e->kind = k[0];
+        char* t = tok(L);
+        if (strcmp(t, "b") != 0 && strcmp(t, "i") != 0 && strcmp(t, "u") != 0) fail("scalar expression: bad type '%s'", t);
+        e->ty = t[0];
+        if (k[0] == 'C') e->a = parse_sx(L);
+        else e->u = tok_u64(L);
+    } else if (strcmp(k, "G") == 0 || strcmp(k, "Y") == 0) {
+        e->kind = k[0];
+        e->ty = 'u';
+        e->u = tok_u64(L);
+    } else if (strcmp(k, "U") == 0 || strcmp(k, "B") == 0) {
+        e->kind = k[0];
+        char* op = tok(L);
+        if (strlen(op) > 2) fail("scalar expression: bad operator '%s'", op);
+        strcpy(e->op, op);
+        e->a = parse_sx(L);
+        if (k[0] == 'B') e->b = parse_sx(L);
+    } else if (strcmp(k, "T") == 0) {
+        e->kind = 'T';
+        e->a = parse_sx(L);
+        e->b = parse_sx(L);
+        e->c = parse_sx(L);
+    } else {
+        fail("scalar expression: bad node '%s'", k);
+    }
+    return e;
+}
+
 static Kernel* find_kernel(Module* m, const char* name) {
     for (int i = 0; i < m->nkernels; ++i)
         if (strcmp(m->kernels[i].name, name) == 0) return &m->kernels[i];
@@ -390,9 +444,26 @@ static Node* parse_node(Lex* L, Module* m) {
         n->sel_indptr = tok_str(L);
         n->sel_indices = tok_str(L);
         n->body = parse_node(L, m);
+    } else if (strcmp(k, "slotset") == 0) {
+        n->kind = N_SLOTSET;
+        n->slot = (uint32_t)tok_u64(L);
+        n->slot_value = tok_u64(L);
+    } else if (strcmp(k, "slotld") == 0) {
+        n->kind = N_SLOTLD;
+        n->slot = (uint32_t)tok_u64(L);
+        TArg* t = &n->slot_view;
+        t->tid = (int)tok_i64(L);
+        t->base_rank = (int)tok_i64(L);
+        t->view_rank = (int)tok_i64(L);
+        t->nidx = (int)tok_i64(L);
+        t->idx = (IExpr*)alloc(sizeof(IExpr) * (size_t)(t->nidx + 1));
+        for (int j = 0; j < t->nidx; ++j) t->idx[j] = *parse_iexpr(L);
+        n->slot_row = tok_i64(L);
+        n->slot_col = tok_i64(L);
+        if (t->tid < 0 || t->tid >= m->ntensors) fail("slot_load_u64: bad tensor id %d", t->tid);
     } else if (strcmp(k, "cond") == 0) {
         n->kind = N_COND;
-        (void)tok_str(L);
+        n->pred = parse_sx(L);
         n->nkids = 2;
         n->kids = (Node**)alloc(sizeof(Node*) * 2);
         n->kids[0] = parse_node(L, m);
@@ -485,6 +556,7 @@ static void parse_module(const char* text, Module* m) {
             m->num_targets = tok_i64(&L);
             m->dispatch_rr = strcmp(pol, "round_robin") == 0 || strcmp(pol, "work_steal") == 0;
             m->dispatch_keyed = !m->dispatch_rr;
+            if (tok_i64(&L) != 0) m->dispatch_key = parse_sx(&L);
         } else if (strcmp(d, "W") == 0) {
             m->has_window = 1;
             m->window_size = tok_i64(&L);
@@ -503,8 +575,8 @@ static void parse_module(const char* text, Module* m) {
     }
     expect(&L, "end");
     /* Keyed dispatch needs a ScalarExpr key (src/python/pto_codegen.cpp:1547-1556). */
-    if (m->has_dispatch && m->dispatch_keyed)
-        fail("dispatch policy requires ScalarExpr key (not supported by this module format)");
+    if (m->has_dispatch && m->dispatch_keyed && !m->dispatch_key)
+        fail("dispatch policy requires ScalarExpr key (string-eval is not supported in v9 codegen-first)");
 }
 
 /* ------------------------------------------------------------------ */
@@ -1060,6 +1132,178 @@ static void push_var(Run* R, const char* name, int64_t v) {
     R->nenv++;
 }
 
+/* ---- scalar expressions: the C expression the reference emits for each
+ * node (src/python/pto_codegen.cpp:220-300, slot / param reads :2232-2238,
+ * :2663-2678), evaluated with C's usual arithmetic conversions: _Bool
+ * promotes to int, an unsigned 64-bit operand makes the operation unsigned.
+ * Undefined cases are refused (division by zero, INT64_MIN / -1, shift
+ * counts outside [0, 64)); signed + - * wrap. */
+typedef struct { char t; uint64_t v; } SV;
+
+static char sx_promo(char t) { return t == 'b' ? 'i' : t; }
+static char sx_usual(char a, char b) { return (a == 'u' || b == 'u') ? 'u' : 'i'; }
+static int sx_is_cmp(const char* op) {
+    return !strcmp(op, "<") || !strcmp(op, "<=") || !strcmp(op, ">") || !strcmp(op, ">=") || !strcmp(op, "==") ||
+           !strcmp(op, "!=");
+}
+
+static char sx_type(const SX* e) {
+    switch (e->kind) {
+        case 'L': case 'P': case 'A': case 'S': case 'C': return e->ty;
+        case 'G': case 'Y': return 'u';
+        case 'U': return e->op[0] == '!' ? 'b' : sx_promo(sx_type(e->a));
+        case 'B':
+            if (sx_is_cmp(e->op) || !strcmp(e->op, "&&") || !strcmp(e->op, "||")) return 'b';
+            if (!strcmp(e->op, "<<") || !strcmp(e->op, ">>")) return sx_promo(sx_type(e->a));
+            return sx_usual(sx_promo(sx_type(e->a)), sx_promo(sx_type(e->b)));
+        case 'T': {
+            char t = sx_type(e->b), f = sx_type(e->c);
+            return (t == 'b' && f == 'b') ? 'b' : sx_usual(sx_promo(t), sx_promo(f));
+        }
+    }
+    return 'i';
+}
+
+static SV sx_read(uint64_t raw, char ty) {
+    SV r = {ty, ty == 'b' ? (uint64_t)(raw != 0) : raw};
+    return r;
+}
+
+static SV sx_eval(Run* R, const SX* e, const uint64_t* args, int nargs) {
+    SV r = {'i', 0};
+    switch (e->kind) {
+        case 'L': r.t = e->ty; r.v = e->u; return r;
+        case 'P':
+            if (!args) fail("emit_scalar_expr_cpp: task_param() requires task_param_expr callback");
+            return sx_read(e->u < (uint64_t)nargs ? args[e->u] : 0, e->ty);
+        case 'G':
+        case 'Y': r.t = 'u'; r.v = R->ctx->get_symbol_u64(R->ctx->ctx, e->u); return r;
+        case 'S':
+            return sx_read(R->ctx->get_slot_u64 ? R->ctx->get_slot_u64(R->ctx->ctx, (uint32_t)e->u) : 0, e->ty);
+        case 'A': {
+            for (int i = R->nenv - 1; i >= 0; --i)
+                if (fnv1a_64(R->env[i].name) == e->u) {
+                    if (e->ty == 'b') fail("emit_scalar_expr_cpp: axis_var invalid type");
+                    r.t = e->ty;
+                    r.v = (uint64_t)R->env[i].value;
+                    return r;
+                }
+            fail("emit_scalar_expr_cpp: axis_var not in scope");
+            return r;
+        }
+        case 'U': {
+            SV x = sx_eval(R, e->a, args, nargs);
+            if (e->op[0] == '!') { r.t = 'b'; r.v = x.v == 0; return r; }
+            r.t = sx_promo(x.t);
+            r.v = e->op[0] == '-' ? (uint64_t)0 - x.v : ~x.v;
+            return r;
+        }
+        case 'T': {
+            char t = sx_type(e);
+            SV c = sx_eval(R, e->a, args, nargs);
+            SV x = sx_eval(R, c.v ? e->b : e->c, args, nargs);
+            r.t = t;
+            r.v = t == 'b' ? (x.v != 0) : x.v;
+            return r;
+        }
+        case 'C': {
+            SV x = sx_eval(R, e->a, args, nargs);
+            r.t = e->ty;
+            r.v = e->ty == 'b' ? (uint64_t)(x.v != 0) : x.v;
+            return r;
+        }
+        case 'B': {
+            const char* op = e->op;
+            if (!strcmp(op, "&&") || !strcmp(op, "||")) {
+                SV a = sx_eval(R, e->a, args, nargs);
+                r.t = 'b';
+                if (op[0] == '&' && !a.v) return r;
+                if (op[0] == '|' && a.v) { r.v = 1; return r; }
+                r.v = sx_eval(R, e->b, args, nargs).v != 0;
+                return r;
+            }
+            SV a = sx_eval(R, e->a, args, nargs), b = sx_eval(R, e->b, args, nargs);
+            a.t = sx_promo(a.t);
+            b.t = sx_promo(b.t);
+            if (!strcmp(op, "<<") || !strcmp(op, ">>")) {
+                if ((b.t == 'i' && (int64_t)b.v < 0) || b.v >= 64) fail("scalar expression: shift count out of range");
+                r.t = a.t;
+                if (op[0] == '<') r.v = a.v << b.v;
+                else r.v = a.t == 'i' ? (uint64_t)((int64_t)a.v >> b.v) : a.v >> b.v;
+                return r;
+            }
+            char t = sx_usual(a.t, b.t);
+            if (sx_is_cmp(op)) {
+                int lt, eq;
+                if (t == 'u') { lt = a.v < b.v; eq = a.v == b.v; }
+                else { lt = (int64_t)a.v < (int64_t)b.v; eq = a.v == b.v; }
+                r.t = 'b';
+                if (!strcmp(op, "<")) r.v = lt;
+                else if (!strcmp(op, "<=")) r.v = lt || eq;
+                else if (!strcmp(op, ">")) r.v = !lt && !eq;
+                else if (!strcmp(op, ">=")) r.v = !lt;
+                else if (!strcmp(op, "==")) r.v = eq;
+                else r.v = !eq;
+                return r;
+            }
+            r.t = t;
+            if (!strcmp(op, "+")) r.v = a.v + b.v;
+            else if (!strcmp(op, "-")) r.v = a.v - b.v;
+            else if (!strcmp(op, "*")) r.v = a.v * b.v;
+            else if (!strcmp(op, "&")) r.v = a.v & b.v;
+            else if (!strcmp(op, "|")) r.v = a.v | b.v;
+            else if (!strcmp(op, "^")) r.v = a.v ^ b.v;
+            else if (!strcmp(op, "/") || !strcmp(op, "%")) {
+                if (!b.v) fail("scalar expression: division by zero");
+                if (t == 'u') r.v = op[0] == '/' ? a.v / b.v : a.v % b.v;
+                else {
+                    int64_t x = (int64_t)a.v, y = (int64_t)b.v;
+                    if (x == INT64_MIN && y == -1) fail("scalar expression: signed division overflow");
+                    r.v = (uint64_t)(op[0] == '/' ? x / y : x % y);
+                }
+            } else {
+                fail("scalar expression: bad operator '%s'", op);
+            }
+            return r;
+        }
+    }
+    fail("scalar expression: bad node");
+    return r;
+}
+
+/* `(uint64_t)element` of a slot load (src/python/pto_codegen.cpp:2254-2303). */
+static uint64_t slot_load_value(Run* R, Node* n) {
+    TArg* t = &n->slot_view;
+    int tid = t->tid;
+    int64_t off = 0;
+    for (int d = 0; d < t->nidx; ++d) off += eval_iexpr(R, &t->idx[d]) * R->tstride[tid * 8 + d];
+    int64_t s3 = 0, s4 = 1;
+    if (t->view_rank >= 2) {
+        int d3 = t->base_rank - t->view_rank;
+        s3 = R->tstride[tid * 8 + d3];
+        s4 = R->tstride[tid * 8 + d3 + 1];
+    } else if (t->view_rank == 1) {
+        s4 = R->tstride[tid * 8 + t->base_rank - 1];
+    }
+    off += n->slot_row * s3 + n->slot_col * s4;
+    check_span(R, tid, off, off, "slot_load_u64");
+    int dt = R->m->tensors[tid].dtype;
+    const char* p = R->tbase[tid] + off * k_dtype_size[dt];
+    float f;
+    switch (dt) {
+        case DT_F32: memcpy(&f, p, 4); break;
+        case DT_F16: { uint16_t h; memcpy(&h, p, 2); f = half_to_float(h); break; }
+        case DT_I32: { int32_t x; memcpy(&x, p, 4); return (uint64_t)(int64_t)x; }
+        case DT_U32: { uint32_t x; memcpy(&x, p, 4); return x; }
+        case DT_I64:
+        case DT_U64: { uint64_t x; memcpy(&x, p, 8); return x; }
+        case DT_BOOL: return *(const unsigned char*)p != 0;
+        default: fail("Unsupported dtype for workload codegen: %s", k_dtype_names[dt]); return 0;
+    }
+    if (!(f > -1.0f) || !(f < 18446744073709551616.0f)) fail("slot_load_u64: the element is not representable as u64");
+    return (uint64_t)f;
+}
+
 static uint64_t eval_node(Run* R, Node* n, uint64_t ready);
 
 static uint64_t run_task(Run* R, Node* n, uint64_t ready) {
@@ -1119,7 +1363,28 @@ static uint64_t run_task(Run* R, Node* n, uint64_t ready) {
     uint64_t dur = run_kernel(k, s->w, s->views, s->scal);
     ++g_tasks;
     uint32_t wid = 0;
-    if (R->m->has_dispatch) wid = (uint32_t)(R->rr++ % R->workers);
+    if (R->m->has_dispatch && !R->m->dispatch_key) wid = (uint32_t)(R->rr++ % R->workers);
+    if (R->m->dispatch_key) {
+        /* args = axis args, (rows, cols) per tile param, scalar args
+         * (src/python/pto_codegen.cpp:2503-2545); worker = key % workers
+         * (:2679-2690). */
+        uint64_t args[64];
+        int na = 0;
+        for (int i = 0; i < n->naxis && na < 64; ++i) {
+            Arg* a = &n->axis[i];
+            args[na++] = a->kind == 'v' ? (uint64_t)lookup(R, a->var)
+                       : a->kind == 's' ? R->ctx->get_symbol_u64(R->ctx->ctx, a->u64)
+                                        : a->u64;
+        }
+        for (int i = 0; i < k->nparams && na + 2 <= 64; ++i) {
+            Val* v = k->by_id[k->params[i].id];
+            if (!v->tile) continue;
+            args[na++] = (uint64_t)v->rows;
+            args[na++] = (uint64_t)v->cols;
+        }
+        for (int i = 0; i < n->nscal && na < 64; ++i) args[na++] = s->scal[i];
+        wid = (uint32_t)(sx_eval(R, R->m->dispatch_key, args, na).v % R->workers);
+    }
     return issue(R, dur, wid, ready);
 }
 
@@ -1176,7 +1441,17 @@ static uint64_t eval_node(Run* R, Node* n, uint64_t ready) {
             }
             return done;
         }
-        case N_COND: fail("cond nodes need a ScalarExpr predicate (not supported by this module format)");
+        case N_COND:
+            /* src/python/pto_codegen.cpp:2458-2478. */
+            return eval_node(R, n->kids[sx_eval(R, n->pred, NULL, 0).v ? 0 : 1], ready);
+        case N_SLOTSET:
+            if (R->ctx->set_slot_u64) R->ctx->set_slot_u64(R->ctx->ctx, n->slot, n->slot_value);
+            return ready;
+        case N_SLOTLD: {
+            uint64_t v = slot_load_value(R, n);
+            if (R->ctx->set_slot_u64) R->ctx->set_slot_u64(R->ctx->ctx, n->slot, v);
+            return ready;
+        }
     }
     return ready;
 }
@@ -1238,5 +1513,32 @@ int pto_cpusim_run(const char* module_text, RuntimeContext* ctx, uint64_t* total
 }
 
 uint64_t pto_cpusim_last_task_count(void) { return g_tasks; }
+
+int pto_cpusim_eval_scalar(const char* expr_text, RuntimeContext* ctx, uint64_t* value, char* type) {
+    jmp_buf jb;
+    jmp_buf* prev = g_jmp;
+    g_jmp = &jb;
+    g_err[0] = 0;
+    volatile int rcode = 0;
+    if (setjmp(jb) == 0) {
+        Lex L = {expr_text};
+        SX* e = parse_sx(&L);
+        while (*L.p == ' ' || *L.p == '\n' || *L.p == '\t') ++L.p;
+        if (*L.p) fail("scalar expression: trailing text '%s'", L.p);
+        Module m;
+        memset(&m, 0, sizeof m);
+        Run* R = (Run*)alloc(sizeof(Run));
+        R->m = &m;
+        R->ctx = ctx;
+        SV v = sx_eval(R, e, NULL, 0);
+        *value = v.v;
+        *type = v.t;
+    } else {
+        rcode = -1;
+    }
+    g_jmp = prev;
+    arena_free();
+    return rcode;
+}
 
 const char* pto_cpusim_last_error(void) { return g_err; }

@@ -39,6 +39,12 @@ uint64_t pto_cpusim_last_task_count(void);
 
 const char* pto_cpusim_last_error(void);
 
+/* Evaluates one scalar expression in the module's token form (a cond
+ * predicate or dispatch key) with symbols and slots read through ctx and no
+ * loop variable or task in scope.  Returns 0 and stores the value's bits and
+ * its C type ('b' bool, 'i' int64_t, 'u' uint64_t); -1 on error. */
+int pto_cpusim_eval_scalar(const char* expr_text, RuntimeContext* ctx, uint64_t* value, char* type);
+
 #ifdef __cplusplus
 }
 #endif

@@ -39,6 +39,9 @@ def _load():
         lib.pto_cpusim_run.restype = ctypes.c_int
         lib.pto_cpusim_last_error.restype = ctypes.c_char_p
         lib.pto_cpusim_last_task_count.restype = ctypes.c_uint64
+        lib.pto_cpusim_eval_scalar.argtypes = [ctypes.c_char_p, ctypes.c_void_p, ctypes.POINTER(ctypes.c_uint64),
+                                               ctypes.POINTER(ctypes.c_char)]
+        lib.pto_cpusim_eval_scalar.restype = ctypes.c_int
         _lib = lib
     return _lib
 
@@ -161,6 +164,28 @@ def run_workload(workload, axis_sizes: dict | None = None, symbols_u64: dict | N
     sizes = Program._infer_axis_sizes(workload)
     sizes.update(axis_sizes or {})
     return run_module(build.module, arrays, sizes, symbols_u64, symbols_ptr)
+
+
+def eval_scalar(expr_text: str, symbols_u64: dict | None = None, slots: list | None = None) -> tuple[str, int]:
+    """(C type code, value bits) of one scalar expression in the module's token form."""
+    lib = _load()
+    symbols_u64 = dict(symbols_u64 or {})
+    slots = list(slots or [0] * 256)
+
+    def get_symbol_u64(_ctx, sid):
+        return symbols_u64.get(int(sid), 0) & 0xFFFFFFFFFFFFFFFF
+
+    def get_slot(_ctx, i):
+        return slots[i] if i < len(slots) else 0
+
+    cbs = (_AXIS(lambda _c, _n: 0), _SYMU(get_symbol_u64), _SYMP(lambda _c, _s: None), _SLOTG(get_slot),
+           _SLOTS(lambda _c, _i, _v: None), _TPTR(lambda _c, _t: None), _TSTR(lambda _c, _t, _d: 0),
+           _KERN(lambda _c, _k: None))
+    rc = _RuntimeContext(*cbs, None)
+    value, typ = ctypes.c_uint64(0), ctypes.c_char(b"?")
+    if lib.pto_cpusim_eval_scalar(expr_text.encode(), ctypes.byref(rc), ctypes.byref(value), ctypes.byref(typ)) != 0:
+        raise RuntimeError("cpu_sim oracle: " + lib.pto_cpusim_last_error().decode(errors="replace"))
+    return typ.value.decode(), int(value.value)
 
 
 def f32_symbol(value: float) -> int:

@@ -44,6 +44,7 @@ struct LaunchArgs {
     IndirectTerm ind[kMaxIndirect];
     int* err;  // 1: indirect index out of range, 2: tile outside its tensor,
                // 3: a tensor-bound loop extent above its declared maximum
+    const i64* tlist;  // task-list launches: grid task index of task t (ascending)
 };
 
 }  // namespace ptowsp

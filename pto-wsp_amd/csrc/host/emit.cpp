@@ -166,7 +166,7 @@ EmittedKernel emit_row(const Module& m, const KernelAnalysis& a, const LaunchSpe
     for (int p = 0; p < ntens; ++p) o << "    char* tb" << p << "[UP];\n";
     if (chunk_in_task) {
         o << "    const i64 t = (ch * CH) / R;\n    const int r0 = (int)(ch * CH - t * R);\n";
-        emit_decode(o, "    ", ng, "t");
+        emit_decode(o, "    ", ng, spec.task_list ? "A.tlist[t]" : "t");
         for (int p = 0; p < ntens; ++p) {
             const int es = dtype_size(a.by_id[k.params[a.tensor_param_index[p]].id]->dtype);
             o << "    char* b" << p << " = A.base[" << p << "] + (" << offset_expr(p, ng, 0, 0) << ") * " << es << ";\n";
@@ -178,7 +178,7 @@ EmittedKernel emit_row(const Module& m, const KernelAnalysis& a, const LaunchSpe
         o << "#pragma unroll\n    for (int u = 0; u < UP; ++u) {\n";
         o << "      i64 g = ch * CH + u * RPW + team; ok[u] = g < total; if (!ok[u]) g = 0;\n";
         o << "      const i64 t = g / R; rr[u] = (int)(g - t * R);\n";
-        emit_decode(o, "      ", ng, "t");
+        emit_decode(o, "      ", ng, spec.task_list ? "A.tlist[t]" : "t");
         for (int p = 0; p < ntens; ++p) {
             const int es = dtype_size(a.by_id[k.params[a.tensor_param_index[p]].id]->dtype);
             o << "      tb" << p << "[u] = A.base[" << p << "] + (" << offset_expr(p, ng, 0, 0) << ") * " << es << ";\n";
@@ -344,11 +344,14 @@ EmittedKernel emit_tile(const Module& m, const KernelAnalysis& a, const LaunchSp
     o << "  i64 vars[" << (nvars > 0 ? nvars : 1) << "];\n  (void)vars;\n";
     // Grid loops are decoded from the task index, or, for a serial launch,
     // iterated in program order by a single workgroup.
-    const int decoded = spec.serial ? 0 : ng;
+    // A serial task-list launch decodes each listed task in one workgroup, in
+    // list (program) order.
+    const bool grid_loops = spec.serial && !spec.task_list;
+    const int decoded = grid_loops ? 0 : ng;
     const int looped = nvars - decoded;
-    if (spec.serial) o << "  for (i64 t = blockIdx.x; t < 1; t += gridDim.x) {\n";
+    if (grid_loops) o << "  for (i64 t = blockIdx.x; t < 1; t += gridDim.x) {\n";
     else o << "  for (i64 t = blockIdx.x; t < A.ntasks; t += gridDim.x) {\n";
-    emit_decode(o, "    ", decoded, "t");
+    emit_decode(o, "    ", decoded, spec.task_list ? "A.tlist[t]" : "t");
     std::string ind = "    ";
     for (int i = 0; i < looped; ++i) {
         const int v = decoded + i;

@@ -19,6 +19,9 @@ struct EmitSpec {
     // when tasks of the grid write overlapping memory (the result then
     // depends on the reference's sequential order).
     bool serial = false;
+    // The launch runs the grid tasks listed in A.tlist (ascending), not all
+    // of them: a task mask from a cond on grid variables.
+    bool task_list = false;
     // Row programs: cap on passes per wave iteration, and non-temporal
     // (streaming) global accesses for full-row tiles.
     int row_up = 8;

@@ -223,6 +223,14 @@ Axis parse_axis(Lexer& L) {
     return a;
 }
 
+std::unique_ptr<SExpr> parse_expr(Lexer& L) {
+    try {
+        return parse_scalar([&] { return L.tok(); });
+    } catch (const std::runtime_error& e) {
+        throw CompileError(e.what());
+    }
+}
+
 std::unique_ptr<Node> parse_node(Lexer& L, const Module& m) {
     auto n = std::make_unique<Node>();
     std::string k = L.tok();
@@ -270,9 +278,34 @@ std::unique_ptr<Node> parse_node(Lexer& L, const Module& m) {
         n->body = parse_node(L, m);
     } else if (k == "cond") {
         n->kind = NodeKind::Cond;
-        (void)L.str();
+        n->pred = parse_expr(L);
         n->kids.push_back(parse_node(L, m));
         n->kids.push_back(parse_node(L, m));
+    } else if (k == "slotset") {
+        n->kind = NodeKind::SlotSet;
+        n->slot = static_cast<uint32_t>(L.u64());
+        n->value = L.u64();
+    } else if (k == "slotld") {
+        n->kind = NodeKind::SlotLoad;
+        n->slot = static_cast<uint32_t>(L.u64());
+        TensorArg& t = n->view;
+        t.param = "tensor";
+        t.tid = static_cast<int>(L.i64());
+        t.base_rank = static_cast<int>(L.i64());
+        t.view_rank = static_cast<int>(L.i64());
+        const int64_t ni = L.i64();
+        for (int64_t j = 0; j < ni; ++j) t.idx.push_back(parse_index(L));
+        n->row = L.i64();
+        n->col = L.i64();
+        if (t.tid < 0 || t.tid >= static_cast<int>(m.tensors.size())) throw CompileError("slot_load_u64: bad tensor id");
+        if (t.view_rank < 2) throw CompileError("slot_load_u64 tensor view must be rank>=2");
+        if (static_cast<size_t>(ni) > m.tensors[t.tid].shape.size()) throw CompileError("slot_load_u64: too many indices");
+        switch (m.tensors[t.tid].dtype) {
+            case DType::F32: case DType::F16: case DType::I32: case DType::I64: case DType::U32: case DType::U64:
+            case DType::Bool: break;
+            default:
+                throw CompileError(std::string("Unsupported dtype for workload codegen: ") + dtype_name(m.tensors[t.tid].dtype));
+        }
     } else {
         throw CompileError("module text: bad node kind '" + k + "'");
     }
@@ -326,6 +359,11 @@ Module parse_module(const std::string& text) {
             m.schedule.has_dispatch = true;
             m.schedule.dispatch_policy = L.tok();
             m.schedule.num_targets = L.i64();
+            if (L.i64() != 0) m.schedule.dispatch_key = parse_expr(L);
+            // src/python/pto_codegen.cpp:1547-1556: keyed policies need a ScalarExpr key.
+            const std::string& pol = m.schedule.dispatch_policy;
+            if (pol != "round_robin" && pol != "work_steal" && !m.schedule.dispatch_key)
+                throw CompileError("dispatch policy requires ScalarExpr key (string-eval is not supported in v9 codegen-first)");
         } else if (d == "W") {
             m.schedule.has_window = true;
             m.schedule.window_size = L.i64();

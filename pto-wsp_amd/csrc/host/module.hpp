@@ -16,6 +16,8 @@
 #include <string>
 #include <vector>
 
+#include "scalar.hpp"
+
 namespace ptowsp {
 
 enum class DType : int { F16, BF16, F32, F64, I8, I16, I32, I64, U8, U16, U32, U64, Bool };
@@ -98,7 +100,7 @@ struct Axis {
     int64_t max = 0;   // DynTensor: declared upper bound of the extent
 };
 
-enum class NodeKind { Empty, ParallelFor, ForEach, Combine, Sequential, Task, Select, Cond };
+enum class NodeKind { Empty, ParallelFor, ForEach, Combine, Sequential, Task, Select, Cond, SlotSet, SlotLoad };
 
 struct Node {
     NodeKind kind = NodeKind::Empty;
@@ -111,11 +113,20 @@ struct Node {
     int kernel_index = -1;
     std::vector<ArgRef> axis_args, scalar_args;
     std::vector<TensorArg> tensor_args;
+    // cond: the predicate; kids[0] / kids[1] are the then / else branches
+    std::unique_ptr<SExpr> pred;
+    // slot set / slot load: slot index, value to set, or the tile view and
+    // the (row, col) element of it to load
+    uint32_t slot = 0;
+    uint64_t value = 0;
+    TensorArg view;
+    int64_t row = 0, col = 0;
 };
 
 struct Schedule {
     bool has_dispatch = false;
     std::string dispatch_policy;
+    std::unique_ptr<SExpr> dispatch_key;  // affinity / hash / dispatch_by: worker = key % workers
     int64_t num_targets = 0;
     bool has_window = false;
     int64_t window_size = 0;

@@ -17,7 +17,41 @@ bool is_seq_chain(const Node* n) {
 
 struct Ctx {
     std::vector<LoopSpec> grid, inner;
+    std::vector<std::string> host;  // host-loop variables in scope
+    std::vector<Mask> masks;
 };
+
+bool has_slot_ops(const Node* n) {
+    if (!n) return false;
+    if (n->kind == NodeKind::SlotSet || n->kind == NodeKind::SlotLoad) return true;
+    if (has_slot_ops(n->body.get())) return true;
+    for (const auto& k : n->kids)
+        if (has_slot_ops(k.get())) return true;
+    return false;
+}
+
+// Where a variable an expression reads is bound: 2 grid loop, 1 host or
+// in-kernel loop; the reference's emitter refuses one out of scope
+// (src/python/pto_codegen.cpp:257-263).
+int scope_of(const Ctx& ctx, uint64_t id) {
+    for (auto it = ctx.inner.rbegin(); it != ctx.inner.rend(); ++it)
+        if (fnv1a_64(it->var) == id) return 1;
+    for (auto it = ctx.host.rbegin(); it != ctx.host.rend(); ++it)
+        if (fnv1a_64(*it) == id) return 1;
+    for (auto it = ctx.grid.rbegin(); it != ctx.grid.rend(); ++it)
+        if (fnv1a_64(it->var) == id) return 2;
+    throw CompileError("emit_scalar_expr_cpp: axis_var not in scope");
+}
+
+// True when the expression reads a grid loop variable (checking scope).
+bool reads_grid(const Ctx& ctx, const SExpr& e) {
+    SRefs r;
+    scalar_refs(e, r);
+    bool grid = false;
+    for (uint64_t id : r.axes) grid |= scope_of(ctx, id) == 2;
+    if (r.task_params) throw CompileError("emit_scalar_expr_cpp: task_param() requires task_param_expr callback");
+    return grid;
+}
 
 void lower(const Module& m, const std::vector<KernelAnalysis>& ka, const Node* n, Ctx ctx, Plan& plan,
            std::vector<PlanItem>& out) {
@@ -50,6 +84,12 @@ void lower(const Module& m, const std::vector<KernelAnalysis>& ka, const Node* n
             if (static_cast<int>(n->scalar_args.size()) != nscal)
                 throw CompileError("task " + k.name + ": scalar argument count mismatch");
             if (L.grid.size() + L.inner.size() > 8) throw CompileError("loop nests deeper than 8 are not supported");
+            L.masks = ctx.masks;
+            if (m.schedule.dispatch_key) {
+                SRefs r;
+                scalar_refs(*m.schedule.dispatch_key, r);
+                for (uint64_t id : r.axes) (void)scope_of(ctx, id);
+            }
             plan.launches.push_back(L);
             PlanItem it;
             it.launch = static_cast<int>(plan.launches.size()) - 1;
@@ -60,6 +100,15 @@ void lower(const Module& m, const std::vector<KernelAnalysis>& ka, const Node* n
             if (!ctx.inner.empty()) throw CompileError("internal: P() inside an in-kernel loop");
             if (n->axis.kind == AxisKind::DynTensor)
                 throw CompileError("P() over a tensor-bound extent is not supported (use P.seq)");
+            if (has_slot_ops(n->body.get())) {
+                PlanItem loop;
+                loop.is_loop = true;
+                loop.loop = LoopSpec{n->var, &n->axis};
+                ctx.host.push_back(n->var);
+                lower(m, ka, n->body.get(), ctx, plan, loop.body);
+                out.push_back(std::move(loop));
+                return;
+            }
             ctx.grid.push_back(LoopSpec{n->var, &n->axis});
             lower(m, ka, n->body.get(), ctx, plan, out);
             return;
@@ -75,6 +124,7 @@ void lower(const Module& m, const std::vector<KernelAnalysis>& ka, const Node* n
             PlanItem loop;
             loop.is_loop = true;
             loop.loop = LoopSpec{n->var, &n->axis};
+            ctx.host.push_back(n->var);
             lower(m, ka, n->body.get(), ctx, plan, loop.body);
             out.push_back(std::move(loop));
             return;
@@ -92,12 +142,36 @@ void lower(const Module& m, const std::vector<KernelAnalysis>& ka, const Node* n
             PlanItem loop;
             loop.is_loop = true;
             loop.loop = LoopSpec{n->var, &n->axis};
+            ctx.host.push_back(n->var);
             lower(m, ka, n->body.get(), ctx, plan, loop.body);
             out.push_back(std::move(loop));
             return;
         }
-        case NodeKind::Cond:
-            throw CompileError("P.when / cond is not supported by the HIP target");
+        case NodeKind::Cond: {
+            // src/python/pto_codegen.cpp:2458-2478: the branch the predicate picks.
+            if (reads_grid(ctx, *n->pred)) {
+                Ctx t = ctx, f = ctx;
+                t.masks.push_back(Mask{n->pred.get(), true});
+                f.masks.push_back(Mask{n->pred.get(), false});
+                lower(m, ka, n->kids[0].get(), t, plan, out);
+                lower(m, ka, n->kids[1].get(), f, plan, out);
+                return;
+            }
+            PlanItem c;
+            c.ctl = n;
+            lower(m, ka, n->kids[0].get(), ctx, plan, c.body);
+            lower(m, ka, n->kids[1].get(), ctx, plan, c.alt);
+            out.push_back(std::move(c));
+            return;
+        }
+        case NodeKind::SlotSet:
+        case NodeKind::SlotLoad: {
+            if (!ctx.grid.empty()) throw CompileError("internal: a slot step inside a launch grid");
+            PlanItem c;
+            c.ctl = n;
+            out.push_back(std::move(c));
+            return;
+        }
     }
 }
 
@@ -142,7 +216,51 @@ struct Walker {
     const CycleEnv& env;
     Scheduler s;
     uint64_t tasks = 0;
-    std::vector<std::pair<std::string, int64_t>> vars;
+    VarList vars;
+    std::vector<uint64_t> slots;
+
+    SEnv senv() {
+        return scalar_env(vars, env.symbol_u64, [this](uint32_t i) { return i < slots.size() ? slots[i] : 0; });
+    }
+
+    uint64_t arg_value(const ArgRef& a) {
+        if (a.kind == 'c') return a.u64;
+        if (a.kind == 's') return env.symbol_u64(a.u64);
+        for (auto it = vars.rbegin(); it != vars.rend(); ++it)
+            if (it->first == a.var) return static_cast<uint64_t>(it->second);
+        throw std::runtime_error("unbound loop variable '" + a.var + "'");
+    }
+
+    // The task's argument vector as the reference packs it
+    // (src/python/pto_codegen.cpp:2503-2545): axis args, (rows, cols) of each
+    // tile param in kernel order, scalar args.
+    std::vector<uint64_t> task_args(const Node* n) {
+        std::vector<uint64_t> args;
+        for (const auto& a : n->axis_args) args.push_back(arg_value(a));
+        const KernelAnalysis& a = ka[n->kernel_index];
+        for (const auto& p : a.def->params) {
+            const ValueInfo* v = a.by_id[p.id];
+            if (!v->tile) continue;
+            args.push_back(static_cast<uint64_t>(v->rows));
+            args.push_back(static_cast<uint64_t>(v->cols));
+        }
+        for (const auto& sa : n->scalar_args) args.push_back(arg_value(sa));
+        return args;
+    }
+
+    uint32_t worker_of(const Node* n) {
+        if (!m.schedule.has_dispatch) return 0;
+        if (!m.schedule.dispatch_key) return static_cast<uint32_t>(s.rr++ % s.workers);
+        // src/python/pto_codegen.cpp:2679-2690: key % workers.
+        SEnv e = senv();
+        std::vector<uint64_t> args;
+        bool have = false;
+        e.task_param = [&](uint32_t i) -> uint64_t {
+            if (!have) args = task_args(n), have = true;
+            return i < args.size() ? args[i] : 0;
+        };
+        return static_cast<uint32_t>(eval_u64(*m.schedule.dispatch_key, e) % s.workers);
+    }
 
     int64_t extent(const Axis& a) {
         switch (a.kind) {
@@ -216,8 +334,21 @@ struct Walker {
             }
             case NodeKind::Task: {
                 ++tasks;
-                const uint32_t w = m.schedule.has_dispatch ? static_cast<uint32_t>(s.rr++ % s.workers) : 0u;
+                const uint32_t w = worker_of(n);
                 return s.issue(ka[n->kernel_index].cycles, w, ready);
+            }
+            case NodeKind::Cond:
+                // src/python/pto_codegen.cpp:2458-2478.
+                return eval(n->kids[eval_truth(*n->pred, senv()) ? 0 : 1].get(), ready);
+            case NodeKind::SlotSet:
+                // src/python/pto_codegen.cpp:2248-2253.
+                if (n->slot < slots.size()) slots[n->slot] = n->value;
+                return ready;
+            case NodeKind::SlotLoad: {
+                // src/python/pto_codegen.cpp:2254-2303.
+                const uint64_t v = env.slot_load(*n, vars);
+                if (n->slot < slots.size()) slots[n->slot] = v;
+                return ready;
             }
             default: throw CompileError("cycle model: unsupported node");
         }
@@ -226,11 +357,47 @@ struct Walker {
 
 }  // namespace
 
+SEnv scalar_env(const VarList& vars, std::function<uint64_t(uint64_t)> symbol, std::function<uint64_t(uint32_t)> slot) {
+    SEnv e;
+    e.axis = [&vars](uint64_t id, int64_t& v) {
+        for (auto it = vars.rbegin(); it != vars.rend(); ++it)
+            if (fnv1a_64(it->first) == id) {
+                v = it->second;
+                return true;
+            }
+        return false;
+    };
+    e.symbol = std::move(symbol);
+    e.slot = std::move(slot);
+    return e;
+}
+
+namespace {
+bool any_node(const Node* n, const std::function<bool(const Node*)>& f) {
+    if (!n) return false;
+    if (f(n) || any_node(n->body.get(), f)) return true;
+    for (const auto& k : n->kids)
+        if (any_node(k.get(), f)) return true;
+    return false;
+}
+}  // namespace
+
+bool module_is_dynamic(const Module& m) {
+    if (m.schedule.dispatch_key) return true;
+    return any_node(m.root.get(), [](const Node* n) {
+        return n->kind == NodeKind::Cond || n->kind == NodeKind::SlotSet || n->kind == NodeKind::SlotLoad;
+    });
+}
+
+bool module_loads_slots(const Module& m) {
+    return any_node(m.root.get(), [](const Node* n) { return n->kind == NodeKind::SlotLoad; });
+}
+
 CycleResult run_cycle_model(const Module& m, const std::vector<KernelAnalysis>& ka, const CycleEnv& env) {
     const Schedule& sc = m.schedule;
-    if (sc.has_dispatch && sc.dispatch_policy != "round_robin" && sc.dispatch_policy != "work_steal")
-        throw CompileError("dispatch policy requires ScalarExpr key (not supported by this module format)");
-    Walker w{m, ka, env, {}, 0, {}};
+    Walker w{m, ka, env, {}, 0, {}, std::vector<uint64_t>(256, 0)};
+    if (env.slot_init)
+        for (uint32_t i = 0; i < 256; ++i) w.slots[i] = env.slot_init(i);
     int64_t W = 1;
     if (sc.has_dispatch && sc.num_targets > 0) W = sc.num_targets;
     else if (sc.has_streams && sc.num_streams > 0) W = sc.num_streams;

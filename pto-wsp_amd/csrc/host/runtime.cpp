@@ -5,8 +5,10 @@
 #include <algorithm>
 #include <chrono>
 #include <cstdlib>
+#include <cmath>
 #include <cstring>
 #include <functional>
+#include <limits>
 #include <map>
 #include <set>
 #include <memory>
@@ -100,8 +102,26 @@ struct ptowsp_program {
     std::string precompiled_source;
     void* scratch = nullptr;  // decode: unit counters and partials
     size_t scratch_bytes = 0;
+    // Task lists of masked launches: pinned host chunks copied into device
+    // chunks on the launch stream; reused from the start at every run (the
+    // previous run has been synchronized by then).
+    struct ListChunk {
+        int64_t* host = nullptr;
+        int64_t* dev = nullptr;
+        size_t cap = 0;
+    };
+    std::vector<ListChunk> lists;
+    size_t list_chunk = 0, list_used = 0;
+    uint64_t* slot_stage = nullptr;     // pinned: one element read by a slot load
+    std::vector<uint64_t> slot_log;     // values of the run's slot loads, in order
+    std::vector<uint64_t> slot_start;   // slots when the run started
 
     ~ptowsp_program() {
+        for (auto& c : lists) {
+            if (c.host) (void)hipHostFree(c.host);
+            if (c.dev) (void)hipFree(c.dev);
+        }
+        if (slot_stage) (void)hipHostFree(slot_stage);
         if (scratch) (void)hipFree(scratch);
         for (void* b : stage_buf)
             if (b) (void)hipFree(b);
@@ -174,6 +194,7 @@ struct RunEnv {
     std::vector<std::pair<std::string, int64_t>> host_vars;
     std::map<int, std::vector<int32_t>> idx_host;  // device index tensors read on the host, copied once per run
     bool timing_started = false;                   // ev0 recorded (just before the first kernel)
+    bool replay_slots = false;                     // cycle model: slot loads replay P->slot_log
 };
 
 // Device time starts at the program's first kernel: host work that precedes
@@ -248,6 +269,79 @@ int64_t eval_index_host(RunEnv& E, const IndexExpr& e, const std::vector<std::pa
     return 0;
 }
 
+// The element a slot load reads: the view's indices, then (row, col) within
+// its tile (src/python/pto_codegen.cpp:2254-2303).
+struct SlotElem {
+    int64_t off;  // elements from the tensor's base
+    size_t size;  // bytes
+};
+
+SlotElem slot_elem(RunEnv& E, const Node& n, const std::vector<std::pair<std::string, int64_t>>& vars) {
+    const TensorArg& ta = n.view;
+    const TensorState& T = E.ts[ta.tid];
+    int64_t off = 0;
+    for (size_t d = 0; d < ta.idx.size(); ++d) off += eval_index_host(E, ta.idx[d], vars) * T.stride[d];
+    int64_t s3 = 0, s4 = 1;
+    if (ta.view_rank >= 2) {
+        const int d3 = ta.base_rank - ta.view_rank;
+        s3 = T.stride[d3];
+        s4 = T.stride[d3 + 1];
+    } else if (ta.view_rank == 1) {
+        s4 = T.stride[ta.base_rank - 1];
+    }
+    off += n.row * s3 + n.col * s4;
+    if (off < 0 || off >= T.span) throw std::runtime_error("slot_load_u64: element outside its tensor");
+    return {off, static_cast<size_t>(dtype_size(E.P->m.tensors[ta.tid].dtype))};
+}
+
+float half_bits_to_float(uint16_t h) {
+    const int e = (h >> 10) & 0x1F, m = h & 0x3FF;
+    const float sign = (h & 0x8000) ? -1.0f : 1.0f;
+    if (e == 0) return sign * std::ldexp(static_cast<float>(m), -24);
+    if (e == 31) return m ? std::numeric_limits<float>::quiet_NaN() : sign * std::numeric_limits<float>::infinity();
+    return sign * std::ldexp(static_cast<float>(m + 1024), e - 25);
+}
+
+// `(uint64_t)element` as C++ converts it; a float outside (-1, 2^64) has no
+// defined conversion and is refused.
+uint64_t slot_value(DType dt, const void* p) {
+    auto from_float = [](float f) {
+        if (!(f > -1.0f) || !(f < 18446744073709551616.0f))
+            throw std::runtime_error("slot_load_u64: the element is not representable as u64");
+        return static_cast<uint64_t>(f);
+    };
+    switch (dt) {
+        case DType::F32: {
+            float f;
+            std::memcpy(&f, p, 4);
+            return from_float(f);
+        }
+        case DType::F16: {
+            uint16_t h;
+            std::memcpy(&h, p, 2);
+            return from_float(half_bits_to_float(h));
+        }
+        case DType::I32: {
+            int32_t x;
+            std::memcpy(&x, p, 4);
+            return static_cast<uint64_t>(static_cast<int64_t>(x));
+        }
+        case DType::U32: {
+            uint32_t x;
+            std::memcpy(&x, p, 4);
+            return x;
+        }
+        case DType::I64:
+        case DType::U64: {
+            uint64_t x;
+            std::memcpy(&x, p, 8);
+            return x;
+        }
+        case DType::Bool: return *static_cast<const unsigned char*>(p) != 0;
+        default: throw std::runtime_error("slot_load_u64: unsupported dtype");
+    }
+}
+
 // Affine decomposition: `scale * e` added into (constant, coef per loop var).
 struct Affine {
     int64_t c = 0;
@@ -284,6 +378,7 @@ struct BuiltLaunch {
     EmitSpec spec;
     int64_t ntasks = 0;
     bool host_checked = false;
+    std::vector<int64_t> tasks;  // task-list launches: the grid tasks kept by the masks
 };
 
 // Row-program vector width allowed by the actual strides and alignment.
@@ -497,6 +592,73 @@ bool decode_allowed(const KernelAnalysis& a, const LaunchSpec& L, const LaunchAr
     return true;
 }
 
+uint64_t ctx_slot(RunEnv& E, uint32_t i) { return E.ctx->get_slot_u64 ? E.ctx->get_slot_u64(E.ctx->ctx, i) : 0; }
+
+SEnv host_env(RunEnv& E, const VarList& vars) {
+    return scalar_env(vars, [&E](uint64_t id) { return E.ctx->get_symbol_u64(E.ctx->ctx, id); },
+                      [&E](uint32_t i) { return ctx_slot(E, i); });
+}
+
+// Evaluates the launch's masks for every grid task (mixed radix, innermost
+// grid loop fastest, as the kernels decode it) and keeps those that pass.
+void apply_masks(RunEnv& E, const LaunchSpec& L, BuiltLaunch& B) {
+    const int ng = static_cast<int>(L.grid.size());
+    VarList vars = E.host_vars;
+    const size_t g0 = vars.size();
+    for (int v = 0; v < ng; ++v) vars.emplace_back(L.grid[v].var, 0);
+    const SEnv env = host_env(E, vars);
+    std::vector<int64_t> keep;
+    for (int64_t t = 0; t < B.ntasks; ++t) {
+        int64_t q = t;
+        for (int v = ng - 1; v >= 0; --v) {
+            vars[g0 + v].second = q % B.args.ext[v];
+            q /= B.args.ext[v];
+        }
+        bool ok = true;
+        for (const Mask& mk : L.masks) ok = ok && eval_truth(*mk.pred, env) == mk.want;
+        if (ok) keep.push_back(t);
+    }
+    if (static_cast<int64_t>(keep.size()) == B.ntasks) return;
+    B.ntasks = B.args.ntasks = static_cast<int64_t>(keep.size());
+    if (keep.empty()) return;
+    B.tasks = std::move(keep);
+    B.spec.task_list = true;
+    // The GEMM and decode programs map several tasks or a cost-balanced
+    // split onto a workgroup; a task list runs on the row or tile program.
+    B.spec.gemm = false;
+    B.spec.gemm_pingpong = false;
+    B.spec.gemm_vm = B.spec.gemm_vn = -1;
+    B.spec.decode = false;
+}
+
+// Device copy of a launch's task list (valid until the next run starts).
+const int64_t* upload_task_list(RunEnv& E, const std::vector<int64_t>& tasks, hipStream_t stream) {
+    ptowsp_program* P = E.P;
+    const size_t n = tasks.size();
+    while (P->list_chunk < P->lists.size() && P->lists[P->list_chunk].cap - P->list_used < n) {
+        ++P->list_chunk;
+        P->list_used = 0;
+    }
+    if (P->list_chunk == P->lists.size()) {
+        ptowsp_program::ListChunk c;
+        c.cap = std::max<size_t>(n, size_t(1) << 16);
+        check(hipHostMalloc(reinterpret_cast<void**>(&c.host), c.cap * 8, hipHostMallocDefault), "hipHostMalloc(task list)");
+        if (hipMalloc(reinterpret_cast<void**>(&c.dev), c.cap * 8) != hipSuccess) {
+            (void)hipHostFree(c.host);
+            throw std::runtime_error("hipMalloc(task list) failed");
+        }
+        P->lists.push_back(c);
+        P->list_used = 0;
+    }
+    ptowsp_program::ListChunk& c = P->lists[P->list_chunk];
+    int64_t* h = c.host + P->list_used;
+    int64_t* d = c.dev + P->list_used;
+    std::memcpy(h, tasks.data(), n * 8);
+    check(hipMemcpyAsync(d, h, n * 8, hipMemcpyHostToDevice, stream), "hipMemcpyAsync(task list)");
+    P->list_used += n;
+    return d;
+}
+
 BuiltLaunch build_launch(RunEnv& E, const LaunchSpec& L) {
     ptowsp_program* P = E.P;
     const KernelAnalysis& a = P->ka[L.kernel];
@@ -648,12 +810,13 @@ BuiltLaunch build_launch(RunEnv& E, const LaunchSpec& L) {
     B.spec.decode_ring = tuning().decode_ring;
     B.spec.decode_waves = tuning().decode_waves;
     B.spec.vec_width = a.family == Family::RowProgram ? pick_vec_width(a, A, nvars) : 1;
+    if (!L.masks.empty() && B.ntasks > 0) apply_masks(E, L, B);
     return B;
 }
 
 std::string spec_key(const EmitSpec& s) {
     std::ostringstream o;
-    o << "vw" << s.vec_width << (s.serial ? ";serial" : "") << ";up" << s.row_up << (s.nontemporal ? ";nt" : "")
+    o << "vw" << s.vec_width << (s.serial ? ";serial" : "") << (s.task_list ? ";tl" : "") << ";up" << s.row_up << (s.nontemporal ? ";nt" : "")
       << (s.gemm ? ";gemm" : "") << ";m" << s.gemm_vm << ";n" << s.gemm_vn << (s.gemm_pingpong ? ";pp" : "")
       << (s.decode ? ";dec" : "")
       << (s.decode_norm ? ";norm" : "") << ";r" << s.decode_ring << ";w" << s.decode_waves
@@ -765,6 +928,7 @@ void enqueue_built(RunEnv& E, int li, BuiltLaunch& B, hipStream_t stream, uint64
         enqueue_decode(E, li, B, ek, *jk, stream, launches);
         return;
     }
+    if (B.spec.task_list) B.args.tlist = reinterpret_cast<const i64*>(upload_task_list(E, B.tasks, stream));
     int64_t blocks;
     if (ek.row_program) {
         const KernelAnalysis& a = P->ka[P->plan.launches[li].kernel];
@@ -804,6 +968,7 @@ bool enqueue_decode_folded(RunEnv& E, int li, int lj, hipStream_t stream, uint64
     const LaunchSpec &Li = P->plan.launches[li], &Lj = P->plan.launches[lj];
     const KernelAnalysis &ai = P->ka[Li.kernel], &aj = P->ka[Lj.kernel];
     if (ai.family != Family::Decode || !aj.norm.ok || !Lj.inner.empty() || Lj.grid.size() != Li.grid.size()) return false;
+    if (!Li.masks.empty() || !Lj.masks.empty()) return false;
     if (aj.norm.g != ai.decode.g || aj.norm.d != ai.decode.d) return false;
     const int ntens = static_cast<int>(ai.tensor_param_index.size());
     if (ntens + 2 > kMaxParams) return false;
@@ -845,11 +1010,17 @@ bool enqueue_decode_folded(RunEnv& E, int li, int lj, hipStream_t stream, uint64
     return true;
 }
 
+void run_host_step(RunEnv& E, const PlanItem& it, hipStream_t stream, uint64_t& launches);
+
 void run_items(RunEnv& E, const std::vector<PlanItem>& items, hipStream_t stream, uint64_t& launches) {
     for (size_t i = 0; i < items.size(); ++i) {
         const PlanItem& it = items[i];
+        if (it.ctl) {
+            run_host_step(E, it, stream, launches);
+            continue;
+        }
         if (!it.is_loop) {
-            if (i + 1 < items.size() && !items[i + 1].is_loop &&
+            if (i + 1 < items.size() && !items[i + 1].is_loop && !items[i + 1].ctl &&
                 enqueue_decode_folded(E, it.launch, items[i + 1].launch, stream, launches)) {
                 ++i;
                 continue;
@@ -881,6 +1052,31 @@ void run_items(RunEnv& E, const std::vector<PlanItem>& items, hipStream_t stream
         }
         E.host_vars.pop_back();
     }
+}
+
+// A cond evaluated on the host, a slot set or a slot load
+// (src/python/pto_codegen.cpp:2248-2303, 2458-2478).
+void run_host_step(RunEnv& E, const PlanItem& it, hipStream_t stream, uint64_t& launches) {
+    const Node& n = *it.ctl;
+    if (n.kind == NodeKind::Cond) {
+        run_items(E, eval_truth(*n.pred, host_env(E, E.host_vars)) ? it.body : it.alt, stream, launches);
+        return;
+    }
+    uint64_t v = n.value;
+    if (n.kind == NodeKind::SlotLoad) {
+        // The element as the kernels enqueued so far leave it: read back
+        // after the stream drains.
+        const SlotElem el = slot_elem(E, n, E.host_vars);
+        const TensorState& T = E.ts[n.view.tid];
+        if (!E.P->slot_stage)
+            check(hipHostMalloc(reinterpret_cast<void**>(&E.P->slot_stage), 64, hipHostMallocDefault), "hipHostMalloc(slot)");
+        check(hipMemcpyAsync(E.P->slot_stage, T.dev + el.off * el.size, el.size, hipMemcpyDeviceToHost, stream),
+              "hipMemcpyAsync(slot load)");
+        check(hipStreamSynchronize(stream), "hipStreamSynchronize(slot load)");
+        v = slot_value(E.P->m.tensors[n.view.tid].dtype, E.P->slot_stage);
+        E.P->slot_log.push_back(v);
+    }
+    if (E.ctx->set_slot_u64) E.ctx->set_slot_u64(E.ctx->ctx, n.slot, v);
 }
 
 double ms_since(std::chrono::steady_clock::time_point t0) {
@@ -995,11 +1191,27 @@ CycleResult cycles_for(RunEnv& E) {
         for (const auto& c : n->kids) walk(c.get());
     };
     walk(P->m.root.get());
-    if (P->cycles_valid && P->cycle_key == key.str()) return P->cycles;
+    const bool dynamic = module_is_dynamic(P->m);
+    if (!dynamic && P->cycles_valid && P->cycle_key == key.str()) return P->cycles;
     env.index_value = [&](const IndexExpr& e, const std::vector<std::pair<std::string, int64_t>>& vars) {
         return eval_index_host(E, e, vars);
     };
+    env.slot_init = [&](uint32_t i) { return i < P->slot_start.size() ? P->slot_start[i] : ctx_slot(E, i); };
+    size_t replayed = 0;
+    env.slot_load = [&](const Node& n, const VarList& vars) -> uint64_t {
+        if (E.replay_slots) {
+            if (replayed >= P->slot_log.size()) throw std::runtime_error("internal: more slot loads than the run made");
+            return P->slot_log[replayed++];
+        }
+        const SlotElem el = slot_elem(E, n, vars);
+        const TensorState& T = E.ts[n.view.tid];
+        unsigned char buf[8] = {};
+        if (T.host) std::memcpy(buf, T.host + el.off * el.size, el.size);
+        else check(hipMemcpy(buf, T.dev + el.off * el.size, el.size, hipMemcpyDeviceToHost), "hipMemcpy(slot load)");
+        return slot_value(P->m.tensors[n.view.tid].dtype, buf);
+    };
     CycleResult r = run_cycle_model(P->m, P->ka, env);
+    if (dynamic) return r;
     P->cycle_key = key.str();
     P->cycles = r;
     P->cycles_valid = true;
@@ -1160,6 +1372,7 @@ int ptowsp_hip_cycle_model(ptowsp_program* P, RuntimeContext* ctx, ptowsp_run_in
     try {
         if (!P || !ctx) throw std::runtime_error("null argument");
         RunEnv E{P, ctx, {}, {}, {}};
+        P->slot_start.clear();  // the model starts from the context's slots
         const size_t nt = P->m.tensors.size();
         E.ts.assign(nt, TensorState{});
         for (size_t t = 0; t < nt; ++t) {
@@ -1212,14 +1425,25 @@ int ptowsp_hip_launch(ptowsp_program* P, RuntimeContext* ctx, void* hip_stream, 
         RunEnv E{P, ctx, {}, {}, {}};
         resolve_tensors(E, stream);
         P->cycles_deferred = false;
+        P->list_chunk = P->list_used = 0;
+        P->slot_log.clear();
+        P->slot_start.assign(256, 0);
+        for (uint32_t i = 0; i < 256; ++i) P->slot_start[i] = ctx_slot(E, i);
+        // A slot load reads what the kernels before it wrote: the cycle model
+        // replays the values the run read, after the run.
+        const bool slot_loads = module_loads_slots(P->m);
         const std::vector<int> dev_ext = device_extent_tensors(E);
         CycleResult cyc{};
         bool ext_written = false;
         for (int tid : dev_ext) ext_written |= E.ts[tid].written;
-        if (dev_ext.empty()) cyc = cycles_for(E);
-        else if (ext_written) defer_cycles(E, dev_ext, stream);
+        if (dev_ext.empty() && !slot_loads) cyc = cycles_for(E);
+        else if (!dev_ext.empty() && ext_written) defer_cycles(E, dev_ext, stream);
         uint64_t launches = 0;
         run_items(E, P->plan.items, stream, launches);
+        if (dev_ext.empty() && slot_loads) {
+            E.replay_slots = true;
+            cyc = cycles_for(E);
+        }
         start_timing(E, stream);
         check(hipEventRecord(P->ev1, stream), "hipEventRecord");
         // After the end event: the copy is not device time of the program.
@@ -1248,6 +1472,7 @@ int ptowsp_hip_synchronize(ptowsp_program* P, ptowsp_timing* timing) {
         if (P->cycles_deferred) {
             P->cycles_deferred = false;
             RunEnv E{P, P->deferred_ctx, P->deferred_ts, {}, {}};
+            E.replay_slots = module_loads_slots(P->m);
             for (const auto& [tid, off] : P->deferred_tids) {
                 const size_t n = static_cast<size_t>(std::max<int64_t>(E.ts[tid].span, 0));
                 E.idx_host[tid] = std::vector<int32_t>(P->key_stage + off, P->key_stage + off + n);
@@ -1335,6 +1560,12 @@ int ptowsp_rt_set_symbol_u64(ptowsp_runtime* rt, uint64_t id, uint64_t value) {
 int ptowsp_rt_set_symbol_ptr(ptowsp_runtime* rt, uint64_t id, void* ptr) {
     if (!rt) return -1;
     rt->symp[id] = ptr;
+    return 0;
+}
+
+int ptowsp_rt_reset_slots(ptowsp_runtime* rt) {
+    if (!rt) return -1;
+    std::fill(rt->slots.begin(), rt->slots.end(), 0);
     return 0;
 }
 

@@ -41,6 +41,18 @@ from pto_wsp.builder import (
     get_inner_type,
 )
 from pto_wsp.errors import CompileError, ExecutionError, IRBridgeError, PtoError
+from pto_wsp.primitives import (
+    parallel_for,
+    for_each,
+    select,
+    cond,
+    task,
+    combine,
+    sequential,
+    slot_set_u64,
+    slot_load_u64,
+)
+from pto_wsp import scalar_expr
 
 workload = workload_decorator
 kernel = kernel_decorator
@@ -56,4 +68,6 @@ __all__ = [
     "workload", "kernel", "jit_kernel", "Kernel", "KernelRef", "In", "Out", "InOut", "Constexpr",
     "KernelParam", "extract_kernel_params", "get_direction", "get_inner_type",
     "CompileError", "ExecutionError", "IRBridgeError", "PtoError",
+    "parallel_for", "for_each", "select", "cond", "task", "combine", "sequential", "slot_set_u64", "slot_load_u64",
+    "scalar_expr",
 ]

@@ -69,6 +69,8 @@ _lib.ptowsp_rt_set_axis_size.argtypes = [_vp, ctypes.c_char_p, ctypes.c_int64]
 _lib.ptowsp_rt_set_symbol_u64.argtypes = [_vp, ctypes.c_uint64, ctypes.c_uint64]
 _lib.ptowsp_rt_set_symbol_ptr.argtypes = [_vp, ctypes.c_uint64, _vp]
 _lib.ptowsp_rt_clear.argtypes = [_vp]
+_lib.ptowsp_rt_reset_slots.argtypes = [_vp]
+_lib.ptowsp_rt_reset_slots.restype = ctypes.c_int
 _lib.ptowsp_rt_context.argtypes = [_vp]
 _lib.ptowsp_rt_context.restype = _vp
 
@@ -233,6 +235,7 @@ class NativeProgram:
         if stream is None and any_cuda and torch is not None:
             stream = torch._C._cuda_getCurrentRawStream(torch._C._cuda_getDevice())
         info = RunInfo()
+        _lib.ptowsp_rt_reset_slots(self._rt)  # every run starts with zeroed slots
         ctx = _lib.ptowsp_rt_context(self._rt)
         if _lib.ptowsp_hip_launch(self._h, ctx, _vp(stream) if stream else None, ctypes.byref(info)) != 0:
             raise RuntimeError(_error())
@@ -243,6 +246,7 @@ class NativeProgram:
         """Evaluate only the cycle model (host only, no launch)."""
         live, _ = self._bind(tensors, axis_sizes, symbols_u64, symbols_ptr)
         info = RunInfo()
+        _lib.ptowsp_rt_reset_slots(self._rt)
         rc = _lib.ptowsp_hip_cycle_model(self._h, _lib.ptowsp_rt_context(self._rt), ctypes.byref(info))
         del live
         if rc != 0:

@@ -29,6 +29,7 @@ from typing import Any
 
 from pto_wsp.errors import IRBridgeError
 from pto_wsp.p_namespace import AffineIndex, LoopVar
+from pto_wsp.scalar_expr import as_expr, trace_task_fn
 from pto_wsp.types import DenseDyn, DType, Ragged, Sparse, Symbol, Tensor
 from pto_wsp.workload import Workload, axis_extent
 
@@ -74,6 +75,21 @@ class _Collector:
         self.tensor_ids: dict[int, int] = {}
         self.tensors: list[Tensor] = []
         self.kernels: dict[str, Any] = {}
+        self.bodies: dict[int, tuple] = {}  # id(loop node) -> (node, body workload)
+
+    def body(self, node: Workload) -> Any:
+        """The body workload of a loop node; a callable body (the functional
+        primitives) is called once with the loop variable and the result kept."""
+        kw = node._kwargs
+        b = kw.get("body")
+        if callable(b) and not isinstance(b, Workload):
+            key = id(node)
+            if key not in self.bodies:
+                default = "e" if node._kind == "select" else "i"
+                var = str(kw.get("var_name", default))
+                self.bodies[key] = (node, b(LoopVar(var, kw.get("axis"))))
+            return self.bodies[key][1]
+        return b
 
     def collect(self, node: Any) -> None:
         if not isinstance(node, Workload):
@@ -88,7 +104,7 @@ class _Collector:
                 self._register(v)
         elif kind in ("parallel_for", "for_each"):
             self._register_axis(kw.get("axis"))
-            self.collect(kw.get("body"))
+            self.collect(self.body(node))
         elif kind in ("combine", "sequential"):
             for c in kw.get("workloads", []) or []:
                 self.collect(c)
@@ -96,7 +112,9 @@ class _Collector:
             self.collect(kw.get("then_workload"))
             self.collect(kw.get("else_workload"))
         elif kind == "select":
-            self.collect(kw.get("body"))
+            self.collect(self.body(node))
+        elif kind == "slot_load_u64":
+            self._register(kw.get("tensor"))
 
     def _register(self, t: Any) -> None:
         if not isinstance(t, Tensor):
@@ -195,11 +213,8 @@ class _Writer:
             self.emit("empty")
         elif kind in ("parallel_for", "for_each"):
             var = str(kw.get("var_name", "i"))
-            body = kw.get("body")
-            if callable(body) and not isinstance(body, Workload):
-                body = body(LoopVar(var, kw.get("axis")))
             self.emit("pfor" if kind == "parallel_for" else "each", enc(var), self.axis(kw.get("axis"), var))
-            self.node(body)
+            self.node(self.c.body(w))
         elif kind in ("combine", "sequential"):
             kids = [c for c in (kw.get("workloads", []) or []) if isinstance(c, Workload)]
             self.emit("comb" if kind == "combine" else "seqn", len(kids))
@@ -211,12 +226,27 @@ class _Writer:
             sp = kw.get("sparse")
             self.emit("sel", enc(str(kw.get("var_name", "e"))), enc(f"outer_{id(sp)}"),
                       enc(f"indptr_{id(sp)}"), enc(f"indices_{id(sp)}"))
-            self.node(kw.get("body"))
+            self.node(self.c.body(w))
         elif kind == "cond":
-            self.emit("cond", enc(repr(kw.get("predicate"))))
+            # python/pto_wsp/ir_bridge.py:485-500 of the reference: the predicate
+            # must convert to a ScalarExpr; a missing branch is empty.
+            self.emit("cond", as_expr(kw.get("predicate")).to_text())
             then_w, else_w = kw.get("then_workload"), kw.get("else_workload")
             self.node(then_w if isinstance(then_w, Workload) else Workload("empty"))
             self.node(else_w if isinstance(else_w, Workload) else Workload("empty"))
+        elif kind == "slot_set_u64":
+            self.emit("slotset", int(kw.get("slot", 0)) & 0xFFFFFFFF, int(kw.get("value", 0)) & 0xFFFFFFFFFFFFFFFF)
+        elif kind == "slot_load_u64":
+            # python/pto_wsp/ir_bridge.py:354-375 of the reference.
+            t = kw.get("tensor")
+            if not isinstance(t, Tensor):
+                raise IRBridgeError("slot_load_u64 requires tensor=Tensor view")
+            if len(t.shape) < 2:
+                raise IRBridgeError(f"slot_load_u64 tensor view must be rank>=2 (got shape={t.shape!r})")
+            tid = self.c.tensor_ids[id(t.base)]
+            idx = [self.index_expr(e) for e in t.index_exprs]
+            self.emit("slotld", int(kw.get("slot", 0)) & 0xFFFFFFFF, tid, len(t.base.shape), len(t.shape), len(idx),
+                      *idx, int(kw.get("row", 0)), int(kw.get("col", 0)))
         else:
             raise IRBridgeError(f"workload node kind '{kind}' is not supported by codegen")
 
@@ -317,7 +347,8 @@ class _Writer:
             if sched.dispatch is not None:
                 kind = getattr(sched.dispatch, "_kind", "")
                 kwargs = getattr(sched.dispatch, "_kwargs", {}) or {}
-                directives.append(f"D {kind or 'custom'} {int(kwargs.get('num_aicpus', 0) or 0)}")
+                directives.append(f"D {kind or 'custom'} {int(kwargs.get('num_aicpus', 0) or 0)} "
+                                  + _dispatch_key_text(kind, kwargs))
             tg = w._task_graph_config
             window = getattr(tg, "window", None) if tg is not None else None
             if window is not None:
@@ -331,6 +362,19 @@ class _Writer:
         self.emit("schedule", len(directives))
         for d in directives:
             self.emit(d)
+
+
+def _dispatch_key_text(kind: str, kwargs: dict) -> str:
+    """``1 <expr>`` for a keyed dispatch policy, ``0`` otherwise (the key is
+    traced into a ScalarExpr as python/pto_wsp/ir_bridge.py:619-648 of the
+    reference does)."""
+    fn = kwargs.get("key_fn") if kind in ("affinity", "hash") else kwargs.get("fn") if kind == "dispatch_by" else None
+    if kind in ("affinity", "hash", "dispatch_by") and fn is None:
+        raise IRBridgeError(f"DispatchPolicy.{kind} missing {'fn' if kind == 'dispatch_by' else 'key_fn'}")
+    if fn is None:
+        return "0"
+    expr = trace_task_fn(fn) if callable(fn) else as_expr(fn)
+    return "1 " + expr.to_text()
 
 
 def workload_to_codegen_ir(workload: Workload, module_name: str = "main") -> CodegenIRBuild:

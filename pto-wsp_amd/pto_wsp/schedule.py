@@ -1,9 +1,12 @@
 """Schedule policy objects (``python/pto_wsp/schedule.py`` in the reference).
 
-Only ``DispatchPolicy`` (lane count, round-robin assignment) and a
-``TaskWindow`` in units of tasks with ``STALL`` overflow change anything: they
-feed the analytic cycle model that ``Program.stats.total_cycles`` reports
-(``src/python/pto_codegen.cpp:1527-1607``).  The rest are accepted and carried.
+Only ``DispatchPolicy`` (lane count; round-robin assignment, or a lane of
+``key % lanes`` for ``affinity`` / ``hash`` / ``dispatch_by``, whose key
+function is traced into a ScalarExpr over ``t.params``, ``t.tags`` and
+``t.get(axis)``) and a ``TaskWindow`` in units of tasks with ``STALL``
+overflow change anything: they feed the analytic cycle model that
+``Program.stats.total_cycles`` reports (``src/python/pto_codegen.cpp:1527-1607,
+2679-2690``).  The rest are accepted and carried.
 """
 
 from __future__ import annotations

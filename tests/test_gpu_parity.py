@@ -592,3 +592,148 @@ def test_rebinding_follows_a_swapped_tensor(gpu):
         prog.execute()
         prog.synchronize()
         torch.testing.assert_close(y, x * x, rtol=0, atol=0)
+
+
+# ---------------------------------------------------------------- cond, slots, keyed dispatch
+def _cond_arrays():
+    return {"a0": np.full((4, 1, 2, 2), 1.0, np.float32), "a1": np.full((4, 1, 2, 2), 2.0, np.float32),
+            "c": np.zeros((4, 1, 2, 2), np.float32)}
+
+
+def test_cond_runtime_predicate_by_axis_var(gpu):
+    """tests/test_codegen_cond.py (predicate on the grid variable: a task mask per branch)."""
+    from pto_wsp.scalar_expr import axis
+
+    a = _cond_arrays()
+    prog = run_hip(W.cond_copy(a, axis("b") < 2))
+    np.testing.assert_array_equal(a["c"][:2], a["a0"][:2])
+    np.testing.assert_array_equal(a["c"][2:], a["a1"][2:])
+    ref = run_workload(W.cond_copy(_cond_arrays(), axis("b") < 2))
+    assert (prog.stats.total_cycles, prog.stats.task_count) == (ref.total_cycles, ref.task_count)
+
+
+def test_cond_runtime_predicate_by_symbol_without_rebuild(gpu):
+    from pto_wsp.scalar_expr import axis, fnv1a_64, symbol_u64
+
+    pred = axis("b") < symbol_u64("cut").cast_i64()
+    a = _cond_arrays()
+    prog = W.cond_copy(a, pred).compile(target="hip_gfx950")
+    for cut, split in [(2, 2), (1, 1), (0, 0), (7, 4), (3, 3)]:
+        a["c"].fill(0)
+        prog.set_symbol_u64("cut", cut)
+        prog.execute()
+        prog.synchronize()
+        np.testing.assert_array_equal(a["c"][:split], a["a0"][:split])
+        np.testing.assert_array_equal(a["c"][split:], a["a1"][split:])
+        ref = run_workload(W.cond_copy(_cond_arrays(), pred), symbols_u64={fnv1a_64("cut"): cut})
+        assert (prog.stats.total_cycles, prog.stats.task_count) == (ref.total_cycles, ref.task_count)
+
+
+def test_scalar_expr_dispatch_reads_task_params_tags_and_symbols(gpu):
+    """tests/test_codegen_scalar_expr_eval.py: results and the makespans 6, 3, 5, 6 x per task."""
+    from pto_wsp import DispatchPolicy
+    from pto_wsp.scalar_expr import symbol_u64
+
+    a = np.arange(6 * 4 * 4, dtype=np.float32).reshape(6, 4, 4)
+    arrs = {"a": a, "b": np.zeros_like(a)}
+    p0 = run_hip(W.copy_tiles(arrs, 6).named("scalar_expr_serial"))
+    np.testing.assert_array_equal(arrs["b"], a)
+    per = int(p0.stats.total_cycles) // 6
+    assert int(p0.stats.total_cycles) == 6 * per > 0
+    by_tags = DispatchPolicy.affinity(lambda t: (t.tags["mask"] & t.params[0].cast_u64()), num_aicpus=2)
+    ternary = DispatchPolicy.affinity(
+        lambda t: (t.params[0] == symbol_u64("special").cast_i64()).where(0, 1).cast_u64(), num_aicpus=2)
+    for policy, sym, runs in [(by_tags, "mask", [(0, 6), (1, 3)]), (ternary, "special", [(0, 5), (7, 6)])]:
+        prog = W.copy_tiles(arrs, 6).dispatch(policy).compile(target="hip_gfx950")
+        for value, lanes in runs:
+            arrs["b"][:] = 0
+            prog.set_symbol_u64(sym, value)
+            prog.execute()
+            prog.synchronize()
+            np.testing.assert_array_equal(arrs["b"], a)
+            assert int(prog.stats.total_cycles) == lanes * per
+
+
+@pytest.mark.parametrize("device", [False, True])
+def test_slot_load_from_tensor_drives_cond_without_rebuild(gpu, device):
+    """tests/test_codegen_slots_tensor_predicate.py: a kernel writes the flag, the slot load reads
+    it back from the device in the same run, and the branch follows it."""
+    import torch
+
+    host = {"src": np.zeros((1, 1, 1, 1), np.int32), "flag": np.zeros((1, 1, 1, 1), np.int32),
+            "y": np.zeros((1, 1, 1, 1), np.int32)}
+    arrs = {k: torch.from_numpy(v).to(gpu) for k, v in host.items()} if device else host
+    prog = W.slot_branch(arrs).compile(target="hip_gfx950")
+    for src, want in [(-1, 7), (0, 3), (1, 7), (0, 3)]:
+        for k in ("src", "flag", "y"):
+            if device:
+                arrs[k].fill_(src if k == "src" else 5)
+            else:
+                arrs[k].fill(src if k == "src" else 5)
+        prog.execute()
+        prog.synchronize()
+        flag = int(arrs["flag"].reshape(-1)[0])
+        y = int(arrs["y"].reshape(-1)[0])
+        assert (flag, y) == (src, want)
+        ref_arrs = {"src": np.full((1, 1, 1, 1), src, np.int32), "flag": np.full((1, 1, 1, 1), 5, np.int32),
+                    "y": np.full((1, 1, 1, 1), 5, np.int32)}
+        ref = run_workload(W.slot_branch(ref_arrs))
+        assert (prog.stats.total_cycles, prog.stats.task_count) == (ref.total_cycles, ref.task_count)
+
+
+def test_slot_loads_inside_a_parallel_loop(gpu):
+    rng = np.random.default_rng(5)
+    x = rng.standard_normal((6, 4, 8)).astype(np.float32)
+    src = np.array([3, 0, 8, 5, 1, 2], np.int32).reshape(6, 1, 1)
+    arrs = {"x": x, "y": np.zeros_like(x), "src": src.copy(), "sel": np.zeros_like(src)}
+    prog = run_hip(W.slot_chain(arrs))
+    odd = (src.reshape(6) & 1) == 1
+    np.testing.assert_array_equal(arrs["sel"], src)
+    np.testing.assert_allclose(arrs["y"][odd], x[odd] * 2, rtol=1e-6)
+    np.testing.assert_allclose(arrs["y"][~odd], x[~odd] + 1, rtol=1e-6)
+    ref = run_workload(W.slot_chain({"x": x.copy(), "y": np.zeros_like(x), "src": src.copy(), "sel": np.zeros_like(src)}))
+    assert (prog.stats.total_cycles, prog.stats.task_count) == (ref.total_cycles, ref.task_count)
+
+
+@pytest.mark.parametrize("case", ["mod3", "corner", "none", "all", "symbol"])
+def test_masked_grid_row_program(gpu, case):
+    """A predicate on both grid variables: only the kept tiles are written (task list on the row
+    program); fp32 rtol 1e-5 against the oracle, untouched tiles unchanged, and the symbol case
+    rebinds without a rebuild."""
+    import torch
+    from pto_wsp.scalar_expr import axis, fnv1a_64, symbol_u64
+
+    preds = {"mod3": ((axis("b") + axis("t")) % 3) != 0, "corner": (axis("t") >= 5) & (axis("b") == 1),
+             "none": axis("b") < 0, "all": axis("b") >= 0, "symbol": axis("t") < symbol_u64("n").cast_i64()}
+    x = np.random.default_rng(2).standard_normal((3, 7, 16, 128)).astype(np.float32)
+    y0 = np.full_like(x, -4.0)
+    xd, yd = torch.from_numpy(x).to(gpu), torch.from_numpy(y0).to(gpu)
+    prog = W.masked_rmsnorm({"x": xd, "y": yd}, preds[case]).compile(target="hip_gfx950")
+    for n in ([2, 6, 0] if case == "symbol" else [0]):
+        yd.copy_(torch.from_numpy(y0))
+        prog.set_symbol_u64("n", n)
+        prog.execute()
+        prog.synchronize()
+        ca = {"x": x.copy(), "y": y0.copy()}
+        ref = run_workload(W.masked_rmsnorm(ca, preds[case]), symbols_u64={fnv1a_64("n"): n})
+        np.testing.assert_allclose(yd.cpu().numpy(), ca["y"], rtol=1e-5, atol=1e-6)
+        assert (prog.stats.total_cycles, prog.stats.task_count) == (ref.total_cycles, ref.task_count)
+
+
+def test_masked_grid_tile_program_with_accumulator(gpu):
+    """A mask over bgemm output tiles with the K loop inside the kernel (tile program with a task
+    list): kept tiles get C += A @ B, the others keep C."""
+    from pto_wsp.scalar_expr import axis
+
+    rng = np.random.default_rng(3)
+    a = rng.standard_normal((2, 64, 48)).astype(np.float16)
+    b = rng.standard_normal((2, 48, 32)).astype(np.float16)
+    c = rng.standard_normal((2, 64, 32)).astype(np.float32)
+    pred = ((axis("m") * 2 + axis("n") + axis("b")) % 3) == 1
+    arrs = {"a": a, "b": b, "c": c.copy()}
+    prog = run_hip(W.masked_bgemm(arrs, pred))
+    ca = {"a": a, "b": b, "c": c.copy()}
+    ref = run_workload(W.masked_bgemm(ca, pred))
+    np.testing.assert_allclose(arrs["c"], ca["c"], rtol=1e-5, atol=1e-5)
+    assert not np.array_equal(ca["c"], c) and np.any(ca["c"] == c)
+    assert (prog.stats.total_cycles, prog.stats.task_count) == (ref.total_cycles, ref.task_count)

@@ -5,7 +5,6 @@
   built for gfx950 by hiprtc;
 * the product's cycle model (C++) gives the same total_cycles and task
   count as the oracle (C) on every workload;
-* constructs the HIP target does not lower (P.when / cond) raise CompileError;
 * a CSR select (P.sel) follows its runtime symbols in the cycle model exactly
   as the oracle does.
 """
@@ -168,21 +167,6 @@ def test_ops_without_reference_compute_are_refused():
             k[i](x=X[i], y=Y[i])
 
     _compile_err(wl(), "no compute")
-
-
-def test_cond_is_refused():
-    X = Tensor(data=None, shape=(2, 4, 4), dtype=DType.F32)
-
-    @kernel
-    def k(x: In[Tile[4, 4, DType.F32]], y: Out[Tile[4, 4, DType.F32]]):
-        pto.store(y, x)
-
-    @workload
-    def wl():
-        with P.when(True):
-            k(x=X[0], y=X[1])
-
-    _compile_err(wl(), "cond")
 
 
 def test_ragged_axis_compiles():

@@ -13,7 +13,7 @@ import math
 import numpy as np
 
 from pto_wsp import (DType, Dense, DenseDyn, DispatchPolicy, In, InOut, Out, P, Ragged, Scalar, Symbol,
-                     TaskWindow, Tensor, Tile, WindowMode, kernel, pto, workload)
+                     TaskWindow, Tensor, Tile, WindowMode, Workload, kernel, pto, workload)
 
 F32, F16, BF16, I32 = DType.F32, DType.F16, DType.BF16, DType.I32
 
@@ -560,3 +560,138 @@ def bf16_round(x: np.ndarray) -> np.ndarray:
 
 def bf16_to_f32(b: np.ndarray) -> np.ndarray:
     return (b.astype(np.uint32) << 16).view(np.float32)
+
+
+# ---------------------------------------------------------------- cond / slots / keyed dispatch
+def cond_copy(arrs: dict, pred):
+    """tests/test_codegen_cond.py: C[b] = A0[b] where pred, A1[b] otherwise, over P(Dense[B])."""
+    B = arrs["c"].shape[0]
+    R, C = arrs["c"].shape[2:]
+    A0, A1, Cc = T(arrs["a0"]), T(arrs["a1"]), T(arrs["c"])
+
+    @kernel
+    def copy(src: In[Tile[R, C, F32]], out: Out[Tile[R, C, F32]]):
+        pto.store(out, pto.load(src))
+
+    @workload
+    def wl():
+        for b in P(Dense[B]()):
+            with P.when(pred):
+                copy[b](src=A0[b][0], out=Cc[b][0])
+            with P.otherwise():
+                copy[b](src=A1[b][0], out=Cc[b][0])
+
+    return wl()
+
+
+def slot_branch(arrs: dict):
+    """tests/test_codegen_slots_tensor_predicate.py with compute kernels in place of its cpp_src
+    bodies: flag <- src (a device kernel), slot 0 <- flag[0,0], then y = 7 if slot 0 != 0 else 3."""
+    from pto_wsp.primitives import cond, sequential, slot_load_u64
+    from pto_wsp.scalar_expr import slot_u64
+
+    src, flag, y = T(arrs["src"], I32), T(arrs["flag"], I32), T(arrs["y"], I32)
+
+    @kernel
+    def write_flag(x_in: In[Tile[1, 1, I32]], flag_out: Out[Tile[1, 1, I32]]):
+        pto.store(flag_out, pto.load(x_in))
+
+    @kernel
+    def fill_true(y_out: InOut[Tile[1, 1, I32]]):
+        v = pto.load(y_out)
+        pto.store(y_out, pto.add(pto.mul(v, pto.constant(0.0, I32)), pto.constant(7.0, I32)))
+
+    @kernel
+    def fill_false(y_out: InOut[Tile[1, 1, I32]]):
+        v = pto.load(y_out)
+        pto.store(y_out, pto.add(pto.mul(v, pto.constant(0.0, I32)), pto.constant(3.0, I32)))
+
+    write = Workload("task", kernel=write_flag, params=[0], resources={"x_in": src[0][0], "flag_out": flag[0][0]})
+    load = slot_load_u64(0, flag[0][0], row=0, col=0)
+    t = Workload("task", kernel=fill_true, params=[0], resources={"y_out": y[0][0]})
+    f = Workload("task", kernel=fill_false, params=[0], resources={"y_out": y[0][0]})
+    return sequential(write, load, cond(slot_u64(0) != 0, t, f)).named("slot_tensor_predicate")
+
+
+def masked_rmsnorm(arrs: dict, pred):
+    """Quickstart rmsnorm over X[B, T, R, C] where pred(b, t) holds; other tiles of y are left
+    as they are.  The predicate reads both grid loop variables."""
+    x = arrs["x"]
+    B, NT, R, C = x.shape
+    X, Y = T(arrs["x"]), T(arrs["y"])
+
+    @kernel
+    def rmsnorm_tile(x: In[Tile[R, C, F32]], out: Out[Tile[R, C, F32]]):
+        inv = pto.rsqrt(pto.rowmean(pto.mul(x, x)))
+        pto.store(out, pto.mul(x, inv))
+
+    @workload
+    def wl():
+        for b in P(Dense[B](), names=["b"]):
+            for t in P(Dense[NT](), names=["t"]):
+                with P.when(pred):
+                    rmsnorm_tile[b, t](x=X[b][t], out=Y[b][t])
+
+    return wl()
+
+
+def slot_chain(arrs: dict):
+    """Slot loads inside P(): for each b, slot 1 <- sel[b] (written by a kernel in the same run
+    from src), then y[b] = x[b] * 2 if slot 1 is odd, else y[b] = x[b] + 1.  The P() loop
+    must run as a host loop so each iteration sees its own slot value."""
+    from pto_wsp.primitives import slot_load_u64
+    from pto_wsp.scalar_expr import slot_i64
+
+    n = arrs["x"].shape[0]
+    X, Y, S, SEL = T(arrs["x"]), T(arrs["y"]), T(arrs["src"], I32), T(arrs["sel"], I32)
+
+    @kernel
+    def copy_sel(a: In[Tile[1, 1, I32]], o: Out[Tile[1, 1, I32]]):
+        pto.store(o, pto.load(a))
+
+    @kernel
+    def twice(x: In[Tile[4, 8, F32]], y: Out[Tile[4, 8, F32]]):
+        pto.store(y, pto.mul(x, pto.constant(2.0, F32)))
+
+    @kernel
+    def plus_one(x: In[Tile[4, 8, F32]], y: Out[Tile[4, 8, F32]]):
+        pto.store(y, pto.add(x, pto.constant(1.0, F32)))
+
+    @workload
+    def wl():
+        for b in P(Dense[n]()):
+            copy_sel[b](a=S[b], o=SEL[b])
+            slot_load_u64(1, SEL[b], 0, 0)
+            with P.when((slot_i64(1) % 2) == 1):
+                twice[b](x=X[b], y=Y[b])
+            with P.otherwise():
+                plus_one[b](x=X[b], y=Y[b])
+
+    return wl()
+
+
+def masked_bgemm(arrs: dict, pred, tm: int = 16, tn: int = 16, tk: int = 16, dtype=F16):
+    """bgemm (InOut C, P.seq K loop) on the output tiles (b, m, n) where pred holds."""
+    a, b_, c = arrs["a"], arrs["b"], arrs["c"]
+    B, M, K = a.shape
+    N = b_.shape[2]
+
+    def perm(x, axes):
+        return x.permute(*axes) if hasattr(x, "permute") else x.transpose(*axes)
+
+    A = T(perm(a.reshape(B, M // tm, tm, K // tk, tk), (0, 1, 3, 2, 4)), dtype)
+    Bm = T(perm(b_.reshape(B, K // tk, tk, N // tn, tn), (0, 3, 1, 2, 4)), dtype)
+    C = T(perm(c.reshape(B, M // tm, tm, N // tn, tn), (0, 1, 3, 2, 4)))
+
+    @kernel
+    def gemm_tile(a_tile: In[Tile[tm, tk, dtype]], b_tile: In[Tile[tk, tn, dtype]], c_tile: InOut[Tile[tm, tn, F32]]):
+        pto.store(c_tile, pto.add(c_tile, pto.matmul(a_tile, b_tile)))
+
+    @workload
+    def wl():
+        for b, m, n in P(Dense[B](), Dense[M // tm](), Dense[N // tn](), names=["b", "m", "n"]):
+            with P.when(pred):
+                for k in P.seq(Dense[K // tk](), name="k"):
+                    gemm_tile[b, m, n, k](a_tile=A[b][m][k], b_tile=Bm[b][n][k], c_tile=C[b][m][n])
+
+    return wl()
