@@ -267,6 +267,7 @@ static void parse_kernel(Lex* L, Kernel* k) {
     k->nparams = (int)tok_i64(L);
     k->nops = (int)tok_i64(L);
     k->custom = (int)tok_i64(L);
+    if (k->custom) (void)tok_str(L); /* the cpp_src body: compiled by the caller, reached via get_kernel */
     k->vals = (Val*)alloc(sizeof(Val) * (size_t)(k->nvals + 1));
     k->params = (Param*)alloc(sizeof(Param) * (size_t)(k->nparams + 1));
     k->ops = (Op*)alloc(sizeof(Op) * (size_t)(k->nops + 1));
@@ -1304,6 +1305,31 @@ static uint64_t slot_load_value(Run* R, Node* n) {
     return (uint64_t)f;
 }
 
+/* A task's argument vector: axis args, (rows, cols) per tile param, scalar
+ * args (src/python/pto_codegen.cpp:2503-2545).  Returns the count. */
+static int task_args(Run* R, Node* n, Kernel* k, const uint64_t* scal, uint64_t* args, int cap) {
+    int na = 0;
+    for (int i = 0; i < n->naxis; ++i) {
+        Arg* a = &n->axis[i];
+        if (na >= cap) fail("task %s: too many arguments", k->name);
+        args[na++] = a->kind == 'v' ? (uint64_t)lookup(R, a->var)
+                   : a->kind == 's' ? R->ctx->get_symbol_u64(R->ctx->ctx, a->u64)
+                                    : a->u64;
+    }
+    for (int i = 0; i < k->nparams; ++i) {
+        Val* v = k->by_id[k->params[i].id];
+        if (!v->tile) continue;
+        if (na + 2 > cap) fail("task %s: too many arguments", k->name);
+        args[na++] = (uint64_t)v->rows;
+        args[na++] = (uint64_t)v->cols;
+    }
+    for (int i = 0; i < n->nscal; ++i) {
+        if (na >= cap) fail("task %s: too many arguments", k->name);
+        args[na++] = scal[i];
+    }
+    return na;
+}
+
 static uint64_t eval_node(Run* R, Node* n, uint64_t ready);
 
 static uint64_t run_task(Run* R, Node* n, uint64_t ready) {
@@ -1360,29 +1386,38 @@ static uint64_t run_task(Run* R, Node* n, uint64_t ready) {
         vw->s3 = s3;
         vw->s4 = s4;
     }
-    uint64_t dur = run_kernel(k, s->w, s->views, s->scal);
+    uint64_t dur;
+    if (k->custom) {
+        /* A cpp_src body, called through the runtime's kernel table with the
+         * reference's task descriptor (include/pto/wsp/codegen/abi/kernel_abi.hpp:21-41). */
+        KernelFn fn = R->ctx->get_kernel ? R->ctx->get_kernel(R->ctx->ctx, (uint32_t)kidx) : NULL;
+        if (!fn) fail("kernel %s: no compiled cpp_src body", k->name);
+        uint64_t args[64];
+        void* ptrs[32];
+        uint64_t strides[64];
+        int na = task_args(R, n, k, s->scal, args, 64), nt = 0;
+        for (int i = 0; i < k->nparams; ++i) {
+            if (!k->by_id[k->params[i].id]->tile) continue;
+            if (nt >= 32) fail("kernel %s: too many tile params", k->name);
+            View* vw = &s->views[k->tensor_index[i]];
+            ptrs[nt] = (void*)vw->ptr;
+            strides[2 * nt] = (uint64_t)vw->s3;
+            strides[2 * nt + 1] = (uint64_t)vw->s4;
+            ++nt;
+        }
+        KernelTaskDesc d = {args, (uint32_t)na, (uint32_t)(n->naxis + 2 * nt), ptrs, strides, (uint32_t)nt,
+                            (uint32_t)kidx, (uint32_t)g_tasks};
+        dur = fn(&d, NULL);
+    } else {
+        dur = run_kernel(k, s->w, s->views, s->scal);
+    }
     ++g_tasks;
     uint32_t wid = 0;
     if (R->m->has_dispatch && !R->m->dispatch_key) wid = (uint32_t)(R->rr++ % R->workers);
     if (R->m->dispatch_key) {
-        /* args = axis args, (rows, cols) per tile param, scalar args
-         * (src/python/pto_codegen.cpp:2503-2545); worker = key % workers
-         * (:2679-2690). */
+        /* worker = key % workers (src/python/pto_codegen.cpp:2679-2690). */
         uint64_t args[64];
-        int na = 0;
-        for (int i = 0; i < n->naxis && na < 64; ++i) {
-            Arg* a = &n->axis[i];
-            args[na++] = a->kind == 'v' ? (uint64_t)lookup(R, a->var)
-                       : a->kind == 's' ? R->ctx->get_symbol_u64(R->ctx->ctx, a->u64)
-                                        : a->u64;
-        }
-        for (int i = 0; i < k->nparams && na + 2 <= 64; ++i) {
-            Val* v = k->by_id[k->params[i].id];
-            if (!v->tile) continue;
-            args[na++] = (uint64_t)v->rows;
-            args[na++] = (uint64_t)v->cols;
-        }
-        for (int i = 0; i < n->nscal && na < 64; ++i) args[na++] = s->scal[i];
+        int na = task_args(R, n, k, s->scal, args, 64);
         wid = (uint32_t)(sx_eval(R, R->m->dispatch_key, args, na).v % R->workers);
     }
     return issue(R, dur, wid, ready);

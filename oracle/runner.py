@@ -83,6 +83,80 @@ class OracleResult:
     task_count: int
 
 
+_CUSTOM_WRAPPER = r"""// A cpp_src body wrapped the way the reference wraps it for its cpu_sim
+// artifact (src/python/pto_codegen.cpp:3294-3324), with pto::cpu_sim's
+// cycle counter restated as a thread-local.
+#include <cstddef>
+#include <cstdint>
+#include "ptowsp_abi.h"
+namespace pto { namespace cpu_sim {
+static thread_local uint64_t g_cycles = 0;
+inline void reset_cycles() { g_cycles = 0; }
+inline void add_cycles(uint64_t n) { g_cycles += n; }
+inline uint64_t read_cycles() { return g_cycles; }
+} }
+extern "C" uint64_t ptowsp_oracle_custom(const KernelTaskDesc* task, CSPTContext* cspt) {
+  (void)task;
+  (void)cspt;
+  uint64_t cycles = 0;
+#if defined(__CPU_SIM)
+  pto::cpu_sim::reset_cycles();
+#endif
+@BODY@
+#if defined(__CPU_SIM)
+  if (cycles == 0) cycles = pto::cpu_sim::read_cycles();
+#endif
+  return cycles;
+}
+"""
+_custom_cache: dict = {}
+
+
+def _decode(tok: str) -> str:
+    if tok == "%":
+        return ""
+    out, i = bytearray(), 0
+    while i < len(tok):
+        if tok[i] == "%" and i + 3 <= len(tok) and all(c in "0123456789ABCDEFabcdef" for c in tok[i + 1:i + 3]):
+            out.append(int(tok[i + 1:i + 3], 16))
+            i += 3
+        else:
+            out += tok[i].encode()
+            i += 1
+    return out.decode("utf-8")
+
+
+def custom_kernels(module_text: str) -> dict:
+    """{kernel index: (library, function address)} for the module's cpp_src kernels, each
+    compiled with g++ into oracle/_build/custom/ (cached by content)."""
+    import hashlib
+
+    out = {}
+    kidx = 0
+    for line in module_text.splitlines():
+        toks = line.split()
+        if not toks or toks[0] != "K":
+            continue
+        if len(toks) > 6 and toks[5] == "1":
+            src = _CUSTOM_WRAPPER.replace("@BODY@", _decode(toks[6]))
+            key = hashlib.sha1(src.encode()).hexdigest()[:16]
+            if key not in _custom_cache:
+                d = os.path.join(_HERE, "_build", "custom")
+                os.makedirs(d, exist_ok=True)
+                cpp, so = os.path.join(d, f"k_{key}.cpp"), os.path.join(d, f"k_{key}.so")
+                if not os.path.exists(so):
+                    open(cpp, "w").write(src)
+                    subprocess.run(["g++", "-std=c++17", "-O1", "-D__CPU_SIM=1", "-shared", "-fPIC",
+                                    "-I", os.path.join(os.path.dirname(_HERE), "include"), cpp, "-o", so + ".tmp"],
+                                   check=True)
+                    os.replace(so + ".tmp", so)
+                lib = ctypes.CDLL(so)
+                _custom_cache[key] = (lib, ctypes.cast(lib.ptowsp_oracle_custom, ctypes.c_void_p).value)
+            out[kidx] = _custom_cache[key]
+        kidx += 1
+    return out
+
+
 def run_module(module_text: str, arrays: list, axis_sizes: dict | None = None,
                symbols_u64: dict | None = None, symbols_ptr: dict | None = None) -> OracleResult:
     """Run a serialized module on host numpy arrays (modified in place)."""
@@ -122,8 +196,13 @@ def run_module(module_text: str, arrays: list, axis_sizes: dict | None = None,
         a = arrays[tid]
         return (a.strides[dim] // a.itemsize) & 0xFFFFFFFFFFFFFFFF
 
+    kernels = custom_kernels(module_text)
+
+    def get_kernel(_ctx, k):
+        return kernels[k][1] if k in kernels else None
+
     cbs = (_AXIS(get_axis_size), _SYMU(get_symbol_u64), _SYMP(get_symbol_ptr), _SLOTG(get_slot),
-           _SLOTS(set_slot), _TPTR(get_tensor_ptr), _TSTR(get_tensor_stride), _KERN(lambda _c, _k: None))
+           _SLOTS(set_slot), _TPTR(get_tensor_ptr), _TSTR(get_tensor_stride), _KERN(get_kernel))
     rc = _RuntimeContext(*cbs, None)
     cycles = ctypes.c_uint64(0)
     status = lib.pto_cpusim_run(module_text.encode(), ctypes.byref(rc), ctypes.byref(cycles))

@@ -14,6 +14,7 @@ constexpr int kMaxParams = 12;
 constexpr int kMaxVars = 8;
 constexpr int kMaxScalars = 8;
 constexpr int kMaxIndirect = 4;
+constexpr int kMaxAxisArgs = 8;
 
 // One indirect index term: the element offset of a tensor param gets
 // `stride * idx`, where idx is the int32 element base[c + sum(coef*var)].
@@ -45,6 +46,11 @@ struct LaunchArgs {
     int* err;  // 1: indirect index out of range, 2: tile outside its tensor,
                // 3: a tensor-bound loop extent above its declared maximum
     const i64* tlist;  // task-list launches: grid task index of task t (ascending)
+    // cpp_src kernels: axis arguments known on the host (constants, symbols,
+    // host loop variables), and where each task's reported cycles go (by
+    // grid task index).
+    u64 aarg[kMaxAxisArgs];
+    u64* cyc;
 };
 
 }  // namespace ptowsp

@@ -354,7 +354,6 @@ DecodeInfo classify_decode(const KernelDef& k, const KernelAnalysis& a) {
 KernelAnalysis analyze_kernel(const KernelDef& k) {
     KernelAnalysis a;
     a.def = &k;
-    if (k.custom) refuse(k, "custom C++ kernel bodies (cpp_src / cpp_tu_path) have no HIP lowering");
     for (const auto& v : k.values) a.max_id = std::max(a.max_id, v.id);
     for (const auto& op : k.ops) a.max_id = std::max(a.max_id, op.result);
     const int n = a.max_id + 1;
@@ -383,6 +382,15 @@ KernelAnalysis analyze_kernel(const KernelDef& k) {
     a.stored.assign(nt, false);
     a.read.assign(nt, false);
     a.bin_mode.assign(k.ops.size(), BinMode::Same);
+    if (k.custom) {
+        // A cpp_src body: it may read and write every tile param; its cycles
+        // are what the body reports when it runs.
+        a.family = Family::Custom;
+        a.stored.assign(nt, true);
+        a.read.assign(nt, true);
+        a.cycles = 0;
+        return a;
+    }
 
     auto val = [&](int id) -> const ValueInfo* {
         if (id <= 0 || id >= n || !a.by_id[id]) refuse(k, "op references undefined value " + std::to_string(id));

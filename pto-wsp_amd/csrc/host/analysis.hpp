@@ -14,7 +14,7 @@ namespace ptowsp {
 // How a binary op combines its operands (src/python/pto_codegen.cpp:1078-1107).
 enum class BinMode { Same, RowExpand, ColExpand, ScalarRight, ScalarLeft };
 
-enum class Family { RowProgram, TileProgram, Gemm, Decode };
+enum class Family { RowProgram, TileProgram, Gemm, Decode, Custom };
 
 // Role of a value inside a row program.
 enum class RowClass { None, Full, RowVec, RowVecT, ColVec, ColVecT, Scalar };

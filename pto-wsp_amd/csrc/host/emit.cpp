@@ -815,7 +815,94 @@ EmittedKernel emit_decode(const Module& m, const KernelAnalysis& a, const Launch
 
 }  // namespace
 
+// ---------------------------------------------------------------------------
+// cpp_src kernels
+// ---------------------------------------------------------------------------
+// One thread per task runs the body against the reference's task descriptor
+// (include/pto/wsp/codegen/abi/kernel_abi.hpp:21-41): args = axis args, the
+// (rows, cols) of every tile param, scalar args
+// (src/python/pto_codegen.cpp:2503-2545); tensor_ptrs / tensor_strides
+// (s3, s4 pairs) in tile-param order.  The body is wrapped as the reference
+// wraps it (src/python/pto_codegen.cpp:3294-3324): a `cycles` variable, and
+// pto::cpu_sim::reset_cycles / add_cycles / read_cycles with __CPU_SIM set,
+// counting per thread.  Each task's cycles go to A.cyc[grid task index].
+EmittedKernel emit_custom(const Module& m, const KernelAnalysis& a, const LaunchSpec& L, const EmitSpec& spec) {
+    (void)m;
+    const KernelDef& k = *a.def;
+    const Node& task = *L.task;
+    const int ng = static_cast<int>(L.grid.size());
+    if (!L.inner.empty()) throw CompileError("internal: in-kernel loops around a cpp_src kernel");
+    const int na = static_cast<int>(task.axis_args.size());
+    if (na > kMaxAxisArgs) throw CompileError("kernel " + k.name + ": more than 8 axis arguments");
+    const int ntens = static_cast<int>(a.tensor_param_index.size());
+    const int nscal = static_cast<int>(task.scalar_args.size());
+    EmittedKernel ek;
+    ek.entry = entry_name("custom", k);
+    ek.threads = 64;
+    std::ostringstream o;
+    o << "#include \"ptowsp_device.h\"\nusing namespace ptowsp;\n";
+    o << "#define __CPU_SIM 1\n#define PTO_WSP_KERNEL_ATTR __device__\n";
+    // The <cstdint> names a body uses (hiprtc provides them in __hip_internal).
+    for (const char* t : {"int8_t", "int16_t", "int32_t", "int64_t", "uint8_t", "uint16_t", "uint32_t", "uint64_t"})
+        o << "using " << t << " = __hip_internal::" << t << ";\n";
+    o << "struct KernelTaskDesc { const uint64_t* args; uint32_t num_args; uint32_t num_axis_args; void* const* tensor_ptrs;\n"
+         "  const uint64_t* tensor_strides; uint32_t num_tensors; uint32_t kernel_id; uint32_t task_id; };\n";
+    o << "struct CSPTContext;\n";
+    o << "namespace pto { namespace cpu_sim {\n"
+         "__device__ inline void ptowsp_add_cycles(uint64_t& c, uint64_t n) { c += n; }\n"
+         "__device__ inline void ptowsp_reset_cycles(uint64_t& c) { c = 0; }\n"
+         "__device__ inline uint64_t ptowsp_read_cycles(const uint64_t& c) { return c; }\n"
+         "} }\n";
+    o << "#define add_cycles(n) ptowsp_add_cycles(ptowsp_cyc_, (n))\n#define reset_cycles() ptowsp_reset_cycles(ptowsp_cyc_)\n"
+         "#define read_cycles() ptowsp_read_cycles(ptowsp_cyc_)\n";
+    o << "__device__ __noinline__ uint64_t ptowsp_body(const KernelTaskDesc* task, CSPTContext* cspt) {\n"
+         "  uint64_t ptowsp_cyc_ = 0;\n  (void)ptowsp_cyc_;\n  (void)task;\n  (void)cspt;\n  uint64_t cycles = 0;\n"
+         "#if defined(__CPU_SIM)\n  pto::cpu_sim::reset_cycles();\n#endif\n";
+    o << "#line 1 \"cpp_src of " << k.name << "\"\n" << k.custom_src << "\n";
+    o << "#if defined(__CPU_SIM)\n  if (cycles == 0) cycles = pto::cpu_sim::read_cycles();\n#endif\n  return cycles;\n}\n";
+    o << "#undef add_cycles\n#undef reset_cycles\n#undef read_cycles\n";
+    o << "extern \"C\" __global__ void __launch_bounds__(64) " << ek.entry << "(const LaunchArgs A) {\n";
+    o << "  i64 vars[" << (ng > 0 ? ng : 1) << "];\n  (void)vars;\n";
+    if (spec.serial) o << "  if (blockIdx.x != 0 || threadIdx.x != 0) return;\n  for (i64 t = 0; t < A.ntasks; ++t) {\n";
+    else o << "  for (i64 t = (i64)blockIdx.x * 64 + threadIdx.x; t < A.ntasks; t += (i64)gridDim.x * 64) {\n";
+    o << "    const i64 g = " << (spec.task_list ? "A.tlist[t]" : "t") << ";\n";
+    emit_decode(o, "    ", ng, "g");
+    const int nargs = na + 2 * ntens + nscal;
+    o << "    uint64_t args[" << (nargs > 0 ? nargs : 1) << "];\n";
+    for (int i = 0; i < na; ++i) {
+        const ArgRef& r = task.axis_args[i];
+        int gv = -1;
+        if (r.kind == 'v')
+            for (int v = ng - 1; v >= 0 && gv < 0; --v)
+                if (L.grid[v].var == r.var) gv = v;
+        if (gv >= 0) o << "    args[" << i << "] = (uint64_t)vars[" << gv << "];\n";
+        else o << "    args[" << i << "] = A.aarg[" << i << "];\n";
+    }
+    for (int p = 0; p < ntens; ++p) {
+        const ValueInfo* v = a.by_id[k.params[a.tensor_param_index[p]].id];
+        o << "    args[" << (na + 2 * p) << "] = " << v->rows << "ull; args[" << (na + 2 * p + 1) << "] = " << v->cols << "ull;\n";
+    }
+    for (int i = 0; i < nscal; ++i) o << "    args[" << (na + 2 * ntens + i) << "] = A.scal[" << i << "];\n";
+    o << "    void* ptrs[" << (ntens > 0 ? ntens : 1) << "];\n    uint64_t strides[" << (ntens > 0 ? 2 * ntens : 1) << "];\n";
+    int term = 0;
+    for (int p = 0; p < ntens; ++p) {
+        const ValueInfo* v = a.by_id[k.params[a.tensor_param_index[p]].id];
+        const int nt = spec.indirect_count.size() > static_cast<size_t>(p) ? spec.indirect_count[p] : 0;
+        o << "    { const i64 o_ = " << offset_expr(p, ng, term, nt) << ";\n";
+        o << "      if (o_ < 0 || o_ + (i64)" << (v->rows - 1) << " * A.s3[" << p << "] + (i64)" << (v->cols - 1) << " * A.s4[" << p
+          << "] >= A.span[" << p << "]) { *A.err = 2; continue; }\n";
+        o << "      ptrs[" << p << "] = A.base[" << p << "] + o_ * " << dtype_size(v->dtype) << "; }\n";
+        o << "    strides[" << 2 * p << "] = (uint64_t)A.s3[" << p << "]; strides[" << 2 * p + 1 << "] = (uint64_t)A.s4[" << p << "];\n";
+        term += nt;
+    }
+    o << "    const KernelTaskDesc d = {args, " << nargs << "u, " << (na + 2 * ntens) << "u, ptrs, strides, " << ntens << "u, 0u, (uint32_t)g};\n";
+    o << "    A.cyc[g] = ptowsp_body(&d, nullptr);\n  }\n}\n";
+    ek.source = o.str();
+    return ek;
+}
+
 EmittedKernel emit_launch(const Module& m, const KernelAnalysis& a, const LaunchSpec& L, const EmitSpec& spec) {
+    if (a.family == Family::Custom) return emit_custom(m, a, L, spec);
     if (spec.gemm && a.family == Family::Gemm && !spec.serial) return emit_gemm(m, a, L, spec);
     if (spec.decode && a.family == Family::Decode && !spec.serial) return emit_decode(m, a, L, spec);
     bool indirect = false;

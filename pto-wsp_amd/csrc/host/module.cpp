@@ -129,7 +129,10 @@ KernelDef parse_kernel(Lexer& L) {
     L.expect("K");
     k.name = L.str();
     int64_t nv = L.i64(), np = L.i64(), no = L.i64();
-    k.custom = L.i64() != 0;
+    const int64_t custom = L.i64();
+    k.custom = custom != 0;
+    if (custom == 2) throw CompileError("kernel " + k.name + ": a C++ translation unit (cpp_tu_path) cannot run on the device; give its body as cpp_src");
+    if (k.custom) k.custom_src = L.str();
     for (int64_t i = 0; i < nv; ++i) {
         L.expect("V");
         ValueInfo v;

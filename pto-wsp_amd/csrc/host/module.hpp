@@ -65,6 +65,7 @@ struct KernelDef {
     std::vector<ParamInfo> params;
     std::vector<OpInfo> ops;
     bool custom = false;
+    std::string custom_src;  // cpp_src: a C++ body over the task descriptor
 };
 
 struct IndexExpr {

@@ -21,6 +21,13 @@ struct Ctx {
     std::vector<Mask> masks;
 };
 
+// A P.seq chain whose task runs a cpp_src body: its loops run on the host
+// (the body is one thread's code for one task).
+bool chain_is_custom(const Module& m, const Node* n) {
+    while (n && n->kind == NodeKind::ForEach) n = n->body.get();
+    return n && n->kind == NodeKind::Task && m.kernels[n->kernel_index].custom;
+}
+
 bool has_slot_ops(const Node* n) {
     if (!n) return false;
     if (n->kind == NodeKind::SlotSet || n->kind == NodeKind::SlotLoad) return true;
@@ -114,7 +121,7 @@ void lower(const Module& m, const std::vector<KernelAnalysis>& ka, const Node* n
             return;
         }
         case NodeKind::ForEach: {
-            if (is_seq_chain(n->body.get())) {
+            if (is_seq_chain(n->body.get()) && !chain_is_custom(m, n)) {
                 ctx.inner.push_back(LoopSpec{n->var, &n->axis});
                 lower(m, ka, n->body.get(), ctx, plan, out);
                 return;
@@ -335,7 +342,12 @@ struct Walker {
             case NodeKind::Task: {
                 ++tasks;
                 const uint32_t w = worker_of(n);
-                return s.issue(ka[n->kernel_index].cycles, w, ready);
+                uint64_t dur = ka[n->kernel_index].cycles;
+                if (ka[n->kernel_index].family == Family::Custom) {
+                    if (!env.custom_cycles) throw std::runtime_error("the cycles of a cpp_src kernel are known only after it runs");
+                    dur = env.custom_cycles(*n, vars);
+                }
+                return s.issue(dur, w, ready);
             }
             case NodeKind::Cond:
                 // src/python/pto_codegen.cpp:2458-2478.
@@ -384,6 +396,8 @@ bool any_node(const Node* n, const std::function<bool(const Node*)>& f) {
 
 bool module_is_dynamic(const Module& m) {
     if (m.schedule.dispatch_key) return true;
+    for (const auto& k : m.kernels)
+        if (k.custom) return true;
     return any_node(m.root.get(), [](const Node* n) {
         return n->kind == NodeKind::Cond || n->kind == NodeKind::SlotSet || n->kind == NodeKind::SlotLoad;
     });

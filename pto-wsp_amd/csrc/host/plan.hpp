@@ -79,6 +79,8 @@ struct CycleEnv {
     std::function<int64_t(const IndexExpr&, const VarList&)> index_value;
     std::function<uint64_t(uint32_t)> slot_init;
     std::function<uint64_t(const Node&, const VarList&)> slot_load;
+    // Cycles a cpp_src kernel's task reported when it ran on the device.
+    std::function<uint64_t(const Node&, const VarList&)> custom_cycles;
 };
 
 // The scalar-expression environment over loop variables `vars` (innermost

@@ -3,6 +3,7 @@
 #include <hip/hip_runtime_api.h>
 
 #include <algorithm>
+#include <array>
 #include <chrono>
 #include <cstdlib>
 #include <cmath>
@@ -112,6 +113,17 @@ struct ptowsp_program {
     };
     std::vector<ListChunk> lists;
     size_t list_chunk = 0, list_used = 0;
+    // Per-task cycles of cpp_src kernels: one region of the list arena per
+    // launch (by grid task index), copied back after the run; keyed by task
+    // node and the host loop variables of the launch.
+    struct CustomRun {
+        size_t chunk = 0, off = 0;
+        VarList host;
+        std::vector<std::string> grid;
+        std::vector<int64_t> ext;
+    };
+    std::map<const Node*, std::vector<CustomRun>> custom_runs;
+    std::vector<std::array<size_t, 3>> readback;  // chunk, offset, count
     uint64_t* slot_stage = nullptr;     // pinned: one element read by a slot load
     std::vector<uint64_t> slot_log;     // values of the run's slot loads, in order
     std::vector<uint64_t> slot_start;   // slots when the run started
@@ -631,10 +643,8 @@ void apply_masks(RunEnv& E, const LaunchSpec& L, BuiltLaunch& B) {
     B.spec.decode = false;
 }
 
-// Device copy of a launch's task list (valid until the next run starts).
-const int64_t* upload_task_list(RunEnv& E, const std::vector<int64_t>& tasks, hipStream_t stream) {
-    ptowsp_program* P = E.P;
-    const size_t n = tasks.size();
+// A region of n u64 / i64 words in the per-run arena: (chunk, offset).
+std::pair<size_t, size_t> arena_region(ptowsp_program* P, size_t n) {
     while (P->list_chunk < P->lists.size() && P->lists[P->list_chunk].cap - P->list_used < n) {
         ++P->list_chunk;
         P->list_used = 0;
@@ -642,21 +652,48 @@ const int64_t* upload_task_list(RunEnv& E, const std::vector<int64_t>& tasks, hi
     if (P->list_chunk == P->lists.size()) {
         ptowsp_program::ListChunk c;
         c.cap = std::max<size_t>(n, size_t(1) << 16);
-        check(hipHostMalloc(reinterpret_cast<void**>(&c.host), c.cap * 8, hipHostMallocDefault), "hipHostMalloc(task list)");
+        check(hipHostMalloc(reinterpret_cast<void**>(&c.host), c.cap * 8, hipHostMallocDefault), "hipHostMalloc(arena)");
         if (hipMalloc(reinterpret_cast<void**>(&c.dev), c.cap * 8) != hipSuccess) {
             (void)hipHostFree(c.host);
-            throw std::runtime_error("hipMalloc(task list) failed");
+            throw std::runtime_error("hipMalloc(arena) failed");
         }
         P->lists.push_back(c);
         P->list_used = 0;
     }
-    ptowsp_program::ListChunk& c = P->lists[P->list_chunk];
-    int64_t* h = c.host + P->list_used;
-    int64_t* d = c.dev + P->list_used;
-    std::memcpy(h, tasks.data(), n * 8);
-    check(hipMemcpyAsync(d, h, n * 8, hipMemcpyHostToDevice, stream), "hipMemcpyAsync(task list)");
+    const std::pair<size_t, size_t> r{P->list_chunk, P->list_used};
     P->list_used += n;
-    return d;
+    return r;
+}
+
+// Device copy of a launch's task list (valid until the next run starts).
+const int64_t* upload_task_list(RunEnv& E, const std::vector<int64_t>& tasks, hipStream_t stream) {
+    ptowsp_program* P = E.P;
+    const size_t n = tasks.size();
+    const auto [ci, off] = arena_region(P, n);
+    ptowsp_program::ListChunk& c = P->lists[ci];
+    std::memcpy(c.host + off, tasks.data(), n * 8);
+    check(hipMemcpyAsync(c.dev + off, c.host + off, n * 8, hipMemcpyHostToDevice, stream), "hipMemcpyAsync(task list)");
+    return c.dev + off;
+}
+
+// Host-known axis arguments of a cpp_src task (constants, symbols, host loop
+// variables); grid variables are decoded in the kernel.
+void custom_axis_args(RunEnv& E, const LaunchSpec& L, LaunchArgs& A) {
+    const auto& args = L.task->axis_args;
+    for (size_t i = 0; i < args.size() && i < static_cast<size_t>(kMaxAxisArgs); ++i) {
+        const ArgRef& r = args[i];
+        if (r.kind == 'c') A.aarg[i] = r.u64;
+        else if (r.kind == 's') A.aarg[i] = E.ctx->get_symbol_u64(E.ctx->ctx, r.u64);
+        else {
+            bool grid = false;
+            for (const auto& g : L.grid) grid |= g.var == r.var;
+            if (grid) continue;
+            bool found = false;
+            for (auto h = E.host_vars.rbegin(); h != E.host_vars.rend() && !found; ++h)
+                if (h->first == r.var) A.aarg[i] = static_cast<uint64_t>(h->second), found = true;
+            if (!found) throw std::runtime_error("unbound loop variable '" + r.var + "'");
+        }
+    }
 }
 
 BuiltLaunch build_launch(RunEnv& E, const LaunchSpec& L) {
@@ -810,6 +847,10 @@ BuiltLaunch build_launch(RunEnv& E, const LaunchSpec& L) {
     B.spec.decode_ring = tuning().decode_ring;
     B.spec.decode_waves = tuning().decode_waves;
     B.spec.vec_width = a.family == Family::RowProgram ? pick_vec_width(a, A, nvars) : 1;
+    if (P->ka[L.kernel].family == Family::Custom) {
+        custom_axis_args(E, L, A);
+        B.spec.gemm = B.spec.decode = B.spec.gemm_pingpong = false;
+    }
     if (!L.masks.empty() && B.ntasks > 0) apply_masks(E, L, B);
     return B;
 }
@@ -929,8 +970,25 @@ void enqueue_built(RunEnv& E, int li, BuiltLaunch& B, hipStream_t stream, uint64
         return;
     }
     if (B.spec.task_list) B.args.tlist = reinterpret_cast<const i64*>(upload_task_list(E, B.tasks, stream));
+    const LaunchSpec& L = P->plan.launches[li];
+    if (P->ka[L.kernel].family == Family::Custom) {
+        ptowsp_program::CustomRun run;
+        size_t grid = 1;
+        for (size_t v = 0; v < L.grid.size(); ++v) {
+            run.grid.push_back(L.grid[v].var);
+            run.ext.push_back(B.args.ext[v]);
+            grid *= static_cast<size_t>(B.args.ext[v]);
+        }
+        std::tie(run.chunk, run.off) = arena_region(P, grid);
+        run.host = E.host_vars;
+        B.args.cyc = reinterpret_cast<u64*>(P->lists[run.chunk].dev + run.off);
+        P->readback.push_back({run.chunk, run.off, grid});
+        P->custom_runs[L.task].push_back(std::move(run));
+    }
     int64_t blocks;
-    if (ek.row_program) {
+    if (P->ka[L.kernel].family == Family::Custom) {
+        blocks = B.spec.serial ? 1 : (B.ntasks + 63) / 64;
+    } else if (ek.row_program) {
         const KernelAnalysis& a = P->ka[P->plan.launches[li].kernel];
         const int64_t rows = B.ntasks * a.rows;
         const int64_t chunks = (rows + ek.rows_per_chunk - 1) / ek.rows_per_chunk;
@@ -1210,6 +1268,25 @@ CycleResult cycles_for(RunEnv& E) {
         else check(hipMemcpy(buf, T.dev + el.off * el.size, el.size, hipMemcpyDeviceToHost), "hipMemcpy(slot load)");
         return slot_value(P->m.tensors[n.view.tid].dtype, buf);
     };
+    if (!P->custom_runs.empty())
+        env.custom_cycles = [&](const Node& n, const VarList& vars) -> uint64_t {
+            auto value = [&](const std::string& name) -> int64_t {
+                for (auto it = vars.rbegin(); it != vars.rend(); ++it)
+                    if (it->first == name) return it->second;
+                throw std::runtime_error("internal: loop variable '" + name + "' of a cpp_src task not bound");
+            };
+            auto it = P->custom_runs.find(&n);
+            if (it != P->custom_runs.end())
+                for (const auto& run : it->second) {
+                    bool same = true;
+                    for (const auto& [name, v] : run.host) same = same && value(name) == v;
+                    if (!same) continue;
+                    size_t g = 0;
+                    for (size_t d = 0; d < run.grid.size(); ++d) g = g * static_cast<size_t>(run.ext[d]) + static_cast<size_t>(value(run.grid[d]));
+                    return static_cast<uint64_t>(P->lists[run.chunk].host[run.off + g]);
+                }
+            throw std::runtime_error("internal: no run of cpp_src kernel task");
+        };
     CycleResult r = run_cycle_model(P->m, P->ka, env);
     if (dynamic) return r;
     P->cycle_key = key.str();
@@ -1426,12 +1503,16 @@ int ptowsp_hip_launch(ptowsp_program* P, RuntimeContext* ctx, void* hip_stream, 
         resolve_tensors(E, stream);
         P->cycles_deferred = false;
         P->list_chunk = P->list_used = 0;
+        P->custom_runs.clear();
+        P->readback.clear();
         P->slot_log.clear();
         P->slot_start.assign(256, 0);
         for (uint32_t i = 0; i < 256; ++i) P->slot_start[i] = ctx_slot(E, i);
         // A slot load reads what the kernels before it wrote: the cycle model
         // replays the values the run read, after the run.
-        const bool slot_loads = module_loads_slots(P->m);
+        bool custom = false;
+        for (const auto& k : P->m.kernels) custom |= k.custom;
+        const bool slot_loads = module_loads_slots(P->m) || custom;
         const std::vector<int> dev_ext = device_extent_tensors(E);
         CycleResult cyc{};
         bool ext_written = false;
@@ -1440,7 +1521,20 @@ int ptowsp_hip_launch(ptowsp_program* P, RuntimeContext* ctx, void* hip_stream, 
         else if (!dev_ext.empty() && ext_written) defer_cycles(E, dev_ext, stream);
         uint64_t launches = 0;
         run_items(E, P->plan.items, stream, launches);
-        if (dev_ext.empty() && slot_loads) {
+        if (custom) {
+            // The cpp_src tasks' cycles: copied back after the kernels, the
+            // model runs at synchronize().
+            if (dev_ext.empty()) P->deferred_tids.clear();
+            for (const auto& r : P->readback) {
+                ptowsp_program::ListChunk& c = P->lists[r[0]];
+                if (r[2])
+                    check(hipMemcpyAsync(c.host + r[1], c.dev + r[1], r[2] * 8, hipMemcpyDeviceToHost, stream),
+                          "hipMemcpyAsync(task cycles)");
+            }
+            P->deferred_ts = E.ts;
+            P->deferred_ctx = E.ctx;
+            P->cycles_deferred = true;
+        } else if (dev_ext.empty() && slot_loads) {
             E.replay_slots = true;
             cyc = cycles_for(E);
         }

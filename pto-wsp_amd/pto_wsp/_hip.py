@@ -74,7 +74,7 @@ _lib.ptowsp_rt_reset_slots.restype = ctypes.c_int
 _lib.ptowsp_rt_context.argtypes = [_vp]
 _lib.ptowsp_rt_context.restype = _vp
 
-FAMILIES = {0: "row_program", 1: "tile_program", 2: "gemm", 3: "decode"}
+FAMILIES = {0: "row_program", 1: "tile_program", 2: "gemm", 3: "decode", 4: "custom"}
 
 _NUMPY_DTYPES = {
     DType.F32: np.float32, DType.F16: np.float16, DType.BF16: np.uint16, DType.F64: np.float64,

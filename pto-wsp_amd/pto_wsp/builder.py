@@ -301,8 +301,13 @@ class _KernelCallWithAxes:
 def kernel(func: Callable | None = None, *, num_warps: int = 4, num_stages: int = 2,
            cpp_src: str | None = None, cpp_body_path: str | None = None,
            cpp_tu_path: str | None = None, cpp_includes: Optional[list] = None, **kwargs):
-    """``@kernel`` decorator.  The C++ escape hatches are accepted for API
-    compatibility; the HIP backend refuses kernels that use them."""
+    """``@kernel`` decorator.
+
+    ``cpp_src`` (or ``cpp_body_path``, a file holding one) gives the kernel a
+    C++ body over the reference's task descriptor (``task->args``,
+    ``task->tensor_ptrs``, ``task->tensor_strides``); the HIP backend compiles
+    it as device code run by one thread per task.  ``cpp_tu_path`` (a whole
+    host translation unit) and ``cpp_includes`` are refused by that backend."""
     options = {"num_warps": num_warps, "num_stages": num_stages, **kwargs}
     chosen = [x for x in (cpp_src, cpp_body_path, cpp_tu_path) if x is not None]
     if len(chosen) > 1:

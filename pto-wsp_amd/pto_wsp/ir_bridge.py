@@ -288,7 +288,10 @@ class _Writer:
     # -- kernels ----------------------------------------------------------
     def kernel(self, k: Any) -> None:
         opts = getattr(k, "options", {}) or {}
-        custom = 1 if (opts.get("cpp_src") is not None or opts.get("cpp_file_src") is not None) else 0
+        # 1: a cpp_src body (cpp_body_path reads one), 2: a whole translation unit (cpp_tu_path).
+        custom = 1 if opts.get("cpp_src") is not None else 2 if opts.get("cpp_file_src") is not None else 0
+        if custom and opts.get("cpp_includes"):
+            raise IRBridgeError(f"kernel {k.name}: cpp_includes name host headers; device bodies cannot include them")
         ir = k.trace()
         values: dict[int, Any] = {}
         for _, v in ir.params:
@@ -297,7 +300,9 @@ class _Writer:
             if op.result is not None:
                 values[op.result.id] = op.result
         directions = {p.name: p.direction for p in k._kernel_params}
-        self.emit("K", enc(ir.name), len(values), len(ir.params), len(ir.ops), custom)
+        src = opts.get("cpp_src") if custom == 1 else opts.get("cpp_file_src")
+        self.emit("K", enc(ir.name), len(values), len(ir.params), len(ir.ops), custom,
+                  *([enc(str(src))] if custom else []))
         for vid in sorted(values):
             v = values[vid]
             if v.shape is None:

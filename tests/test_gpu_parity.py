@@ -737,3 +737,41 @@ def test_masked_grid_tile_program_with_accumulator(gpu):
     np.testing.assert_allclose(arrs["c"], ca["c"], rtol=1e-5, atol=1e-5)
     assert not np.array_equal(ca["c"], c) and np.any(ca["c"] == c)
     assert (prog.stats.total_cycles, prog.stats.task_count) == (ref.total_cycles, ref.task_count)
+
+
+# ---------------------------------------------------------------- cpp_src kernels
+@pytest.mark.parametrize("device", [False, True])
+def test_cpp_src_slot_predicate_without_rebuild(gpu, device):
+    """tests/test_codegen_slots_tensor_predicate.py with cpp_src bodies run on the device: the
+    flag a body writes drives the branch through a slot; two cycles per run (one per body)."""
+    import torch
+
+    host = {"x": np.zeros((1, 1, 1, 1), np.float32), "flag": np.zeros((1, 1, 1, 1), np.int32),
+            "y": np.zeros((1, 1, 1, 1), np.int32)}
+    arrs = {k: torch.from_numpy(v).to(gpu) for k, v in host.items()} if device else host
+    prog = W.cpp_slot_branch(arrs).compile(target="hip_gfx950")
+    for x, flag, y in [(-1.0, 0, 3), (1.0, 1, 7), (0.5, 1, 7), (0.0, 0, 3)]:
+        if device:
+            arrs["x"].fill_(x), arrs["flag"].fill_(9), arrs["y"].fill_(0)
+        else:
+            arrs["x"].fill(x), arrs["flag"].fill(9), arrs["y"].fill(0)
+        prog.execute()
+        prog.synchronize()
+        assert (int(arrs["flag"].reshape(-1)[0]), int(arrs["y"].reshape(-1)[0])) == (flag, y)
+        assert (int(prog.stats.total_cycles), int(prog.stats.task_count)) == (2, 2)
+
+
+@pytest.mark.parametrize("masked", [False, True])
+def test_cpp_src_task_descriptor_matches_oracle(gpu, masked):
+    """A body that copies its task descriptor (args, counts, strides, two x elements) into its
+    output and reports per-task cycles: bit-identical to the oracle's g++ build of the same body."""
+    from pto_wsp.scalar_expr import axis
+
+    pred = (axis("b") != 1) if masked else None
+    x = np.arange(3 * 2 * 8, dtype=np.float32).reshape(3, 2, 2, 4)
+    ga = {"x": x.copy(), "o": np.full((2, 3, 2, 2, 16), -1.0, np.float32)}
+    ca = {"x": x.copy(), "o": np.full((2, 3, 2, 2, 16), -1.0, np.float32)}
+    prog = run_hip(W.cpp_probe(ga, pred))
+    ref = run_workload(W.cpp_probe(ca, pred))
+    np.testing.assert_array_equal(ga["o"], ca["o"])
+    assert (int(prog.stats.total_cycles), int(prog.stats.task_count)) == (ref.total_cycles, ref.task_count)

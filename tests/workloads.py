@@ -695,3 +695,94 @@ def masked_bgemm(arrs: dict, pred, tm: int = 16, tn: int = 16, tk: int = 16, dty
                     gemm_tile[b, m, n, k](a_tile=A[b][m][k], b_tile=Bm[b][n][k], c_tile=C[b][m][n])
 
     return wl()
+
+
+# ---------------------------------------------------------------- cpp_src kernels
+_FLAG_BODY = r"""
+  // flag = 1 when x > 0, else 0 (one element each; strides from the descriptor)
+  const float* xv = (const float*)task->tensor_ptrs[0];
+  int32_t* fv = (int32_t*)task->tensor_ptrs[1];
+  fv[0] = xv[0] > 0.0f ? 1 : 0;
+#if defined(__CPU_SIM)
+  pto::cpu_sim::add_cycles(1);
+#endif
+"""
+
+
+def _fill_body(value: int) -> str:
+    return f"""
+  int32_t* yv = (int32_t*)task->tensor_ptrs[0];
+  yv[0 * (int64_t)task->tensor_strides[0] + 0 * (int64_t)task->tensor_strides[1]] = {value};
+#if defined(__CPU_SIM)
+  pto::cpu_sim::add_cycles(1);
+#endif
+"""
+
+
+def cpp_slot_branch(arrs: dict):
+    """tests/test_codegen_slots_tensor_predicate.py with cpp_src bodies of this repository's own:
+    flag <- (x > 0), slot 0 <- flag, y = 7 if slot 0 != 0 else 3; each body adds 1 cycle."""
+    from pto_wsp.primitives import cond, sequential, slot_load_u64
+    from pto_wsp.scalar_expr import slot_u64
+
+    x, flag, y = T(arrs["x"]), T(arrs["flag"], I32), T(arrs["y"], I32)
+
+    @kernel(cpp_src=_FLAG_BODY)
+    def write_flag(x_in: In[Tile[1, 1, F32]], flag_out: Out[Tile[1, 1, I32]]):
+        pass
+
+    @kernel(cpp_src=_fill_body(7))
+    def fill_true(y_out: Out[Tile[1, 1, I32]]):
+        pass
+
+    @kernel(cpp_src=_fill_body(3))
+    def fill_false(y_out: Out[Tile[1, 1, I32]]):
+        pass
+
+    write = Workload("task", kernel=write_flag, params=[0], resources={"x_in": x[0][0], "flag_out": flag[0][0]})
+    load = slot_load_u64(0, flag[0][0], row=0, col=0)
+    t = Workload("task", kernel=fill_true, params=[0], resources={"y_out": y[0][0]})
+    f = Workload("task", kernel=fill_false, params=[0], resources={"y_out": y[0][0]})
+    return sequential(write, load, cond(slot_u64(0) != 0, t, f)).named("slot_tensor_predicate")
+
+
+_PROBE_BODY = r"""
+  // Writes what the task descriptor holds into its output tile (row 0: args;
+  // row 1: num_axis_args, num_tensors, x's strides, x[0,0] + x[1,0]).
+  const float* xv = (const float*)task->tensor_ptrs[0];
+  float* ov = (float*)task->tensor_ptrs[1];
+  const uint64_t os3 = task->tensor_strides[2], os4 = task->tensor_strides[3];
+  for (uint32_t j = 0; j < task->num_args && j < 16; ++j) ov[j * os4] = (float)task->args[j];
+  ov[os3 + 0 * os4] = (float)task->num_axis_args;
+  ov[os3 + 1 * os4] = (float)task->num_tensors;
+  ov[os3 + 2 * os4] = (float)task->tensor_strides[0];
+  ov[os3 + 3 * os4] = (float)task->tensor_strides[1];
+  ov[os3 + 4 * os4] = xv[0] + xv[task->tensor_strides[0]];
+  cycles = 5 + task->args[0] * 3 + task->args[1] + 100 * task->args[2];
+"""
+
+
+def cpp_probe(arrs: dict, pred=None):
+    """A cpp_src kernel over a host P.seq loop (i) around a P() grid (b, h), with a scalar arg;
+    with `pred`, only the grid tasks where it holds run."""
+    from pto_wsp import Scalar
+
+    X, O = T(arrs["x"]), T(arrs["o"])
+    nb, nh = arrs["x"].shape[:2]
+    ni = arrs["o"].shape[0]
+
+    @kernel(cpp_src=_PROBE_BODY)
+    def probe(x: In[Tile[2, 4, F32]], out: Out[Tile[2, 16, F32]], s: Scalar[F32] = 1.5):
+        pass
+
+    @workload
+    def wl():
+        for i in P.seq(Dense[ni](), name="i"):
+            for b, h in P(Dense[nb](), Dense[nh](), names=["b", "h"]):
+                if pred is None:
+                    probe[b, h, i](x=X[b][h], out=O[i][b][h], s=2.5)
+                else:
+                    with P.when(pred):
+                        probe[b, h, i](x=X[b][h], out=O[i][b][h], s=2.5)
+
+    return wl()
