@@ -13,6 +13,11 @@
  *     TMATMUL): include/pto/wsp/codegen/abi/ptoisa_bridge.hpp:54-303
  *   - in-order, window-stall scheduler giving total_cycles (the makespan):
  *       src/python/pto_codegen.cpp:1561-1607
+ *   - ragged / sparse-select loops, cond nodes with ScalarExpr predicates,
+ *     slot set / load, keyed dispatch (key % lanes):
+ *       src/python/pto_codegen.cpp:220-300, 2248-2478, 2679-2690
+ *   - cpp_src kernels: called through ctx->get_kernel with the reference's
+ *     task descriptor; the caller compiles the bodies (oracle/runner.py)
  * The pto-isa submodule that implements the tile instructions is absent
  * from the reference checkout, so reductions are restated as sequential
  * fp32 sums, TEXP as expf, TRSQRT as 1/sqrtf and TMATMUL as a sequential
