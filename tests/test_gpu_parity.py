@@ -775,3 +775,23 @@ def test_cpp_src_task_descriptor_matches_oracle(gpu, masked):
     ref = run_workload(W.cpp_probe(ca, pred))
     np.testing.assert_array_equal(ga["o"], ca["o"])
     assert (int(prog.stats.total_cycles), int(prog.stats.task_count)) == (ref.total_cycles, ref.task_count)
+
+
+def test_cond_on_a_symbol_inside_a_grid(gpu):
+    """A predicate that reads no grid variable is evaluated once on the host and picks the
+    branch launched over the whole grid; nested under it, a grid-variable predicate masks."""
+    from pto_wsp.scalar_expr import axis, fnv1a_64, symbol_u64
+
+    pred = (symbol_u64("flag") != 0) & (axis("b") >= 0)
+    host_only = symbol_u64("flag") != 0
+    for p in (host_only, pred):
+        a = _cond_arrays()
+        prog = W.cond_copy(a, p).compile(target="hip_gfx950")
+        for flag in (0, 1, 0):
+            a["c"].fill(0)
+            prog.set_symbol_u64("flag", flag)
+            prog.execute()
+            prog.synchronize()
+            np.testing.assert_array_equal(a["c"], a["a0"] if flag else a["a1"])
+            ref = run_workload(W.cond_copy(_cond_arrays(), p), symbols_u64={fnv1a_64("flag"): flag})
+            assert (prog.stats.total_cycles, prog.stats.task_count) == (ref.total_cycles, ref.task_count)
