@@ -786,3 +786,134 @@ def cpp_probe(arrs: dict, pred=None):
                         probe[b, h, i](x=X[b][h], out=O[i][b][h], s=2.5)
 
     return wl()
+
+
+# ---------------------------------------------------------------- op variants of the arithmetic contract
+# Broadcast operand shapes for binary(): the rhs tile of out = op(x, y) with x [R, C].
+BIN_SHAPES = {"same": lambda R, C: (R, C), "row": lambda R, C: (R, 1), "row_t": lambda R, C: (1, R),
+              "col": lambda R, C: (1, C), "col_t": lambda R, C: (C, 1)}
+BIN_OPS = {"add": "add", "sub": "sub", "mul": "mul", "div": "div", "max": "max", "min": "min"}
+
+
+def binary(arrs: dict, op: str, out_dtype=F32):
+    """out[b][t] = op(x[b][t], y[b][t]) over X[B, T, R, C] and Y[B, T, yr, yc]: TADD..TMIN on equal
+    shapes, TROWEXPAND* for a [R,1] / [1,R] rhs, TCOLEXPAND{SUB,MUL,DIV} for [1,C] / [C,1]
+    (src/python/pto_codegen.cpp:1078-1107).  out_dtype F16 / BF16 adds the TCVT store cast
+    (:955-976) and moves the kernel onto the tile program."""
+    x, y = arrs["x"], arrs["y"]
+    B, NT, R, C = x.shape
+    yr, yc = y.shape[2:]
+    X, Y, O = T(x), T(y), T(arrs["out"], out_dtype)
+    fn = getattr(pto, BIN_OPS[op])
+
+    @kernel
+    def bin_tile(x_t: In[Tile[R, C, F32]], y_t: In[Tile[yr, yc, F32]], out: Out[Tile[R, C, out_dtype]]):
+        pto.store(out, fn(x_t, y_t))
+
+    @workload
+    def wl():
+        for b in P(Dense[B]()):
+            for t in P(Dense[NT]()):
+                bin_tile[b, t](x_t=X[b][t], y_t=Y[b][t], out=O[b][t])
+
+    return wl()
+
+
+def scalar_binary(arrs: dict, op: str, value: float, left: bool = False, out_dtype=F32):
+    """out = op(x, s) with s = pto.constant(value): TADDS / TSUBS / TMULS / TDIVS / TMAXS / TMINS
+    (src/python/pto_codegen.cpp:1008-1051).  left=True builds op(s, x) with a tile result; the
+    tracer types a binary op by its first operand, so that form is written against the kernel IR
+    directly (the reference's emitter lowers it to TDIVS(dst, s, tile) for Div)."""
+    from pto_wsp.kernel import OpKind, Value, ValueId
+
+    x = arrs["x"]
+    B, NT, R, C = x.shape
+    X, O = T(x), T(arrs["out"], out_dtype)
+    kind = {"add": OpKind.Add, "sub": OpKind.Sub, "mul": OpKind.Mul, "div": OpKind.Div, "max": OpKind.Max,
+            "min": OpKind.Min}[op]
+
+    @kernel
+    def scal_tile(x_t: In[Tile[R, C, F32]], out: Out[Tile[R, C, out_dtype]]):
+        s = pto.constant(value, F32)
+        if left:
+            r = Value(ValueId.next(), F32, (R, C))
+            pto._ir().add_op(kind, [s, x_t], r)
+        else:
+            r = getattr(pto, BIN_OPS[op])(x_t, s)
+        pto.store(out, r)
+
+    @workload
+    def wl():
+        for b in P(Dense[B]()):
+            for t in P(Dense[NT]()):
+                scal_tile[b, t](x_t=X[b][t], out=O[b][t])
+
+    return wl()
+
+
+def store_cast(arrs: dict, out_dtype):
+    """out (F16 / BF16 tile) = x (f32 tile): the TCVT CAST_RINT store (src/python/pto_codegen.cpp:955-976)."""
+    x = arrs["x"]
+    B, NT, R, C = x.shape
+    X, O = T(x), T(arrs["out"], out_dtype)
+
+    @kernel
+    def cast_tile(x_t: In[Tile[R, C, F32]], out: Out[Tile[R, C, out_dtype]]):
+        pto.store(out, x_t)
+
+    @workload
+    def wl():
+        for b in P(Dense[B]()):
+            for t in P(Dense[NT]()):
+                cast_tile[b, t](x_t=X[b][t], out=O[b][t])
+
+    return wl()
+
+
+def f16_from_bits(h: np.ndarray) -> np.ndarray:
+    return np.ascontiguousarray(h).view(np.float16)
+
+
+def bf16_rne_by_distance(x: np.ndarray) -> np.ndarray:
+    """f32 -> bf16 bits by comparing distances to the two neighbouring bf16 values in float64
+    (exact for finite f32 inputs); ties go to the even mantissa.  A restatement independent of
+    the add-and-shift bit trick, for finite inputs whose rounding stays finite."""
+    x = np.ascontiguousarray(x, np.float32)
+    u = x.view(np.uint32)
+    lo = (u >> 16).astype(np.uint32)           # truncation toward zero (same sign)
+    hi = lo + 1                                # next bf16 away from zero
+    vlo = (lo << 16).view(np.float32).astype(np.float64)
+    vhi = (hi.astype(np.uint32) << 16).view(np.float32).astype(np.float64)
+    ax = np.abs(x.astype(np.float64))
+    dlo, dhi = ax - np.abs(vlo), np.abs(vhi) - ax
+    pick_hi = (dhi < dlo) | ((dhi == dlo) & (lo & 1 == 1))
+    return np.where(pick_hi, hi, lo).astype(np.uint16)
+
+
+def rounding_probe_f32(n_random: int, seed: int = 0, for_bf16: bool = False) -> np.ndarray:
+    """f32 values that separate rounding rules: exact halfway cases between neighbours of both
+    parities and both signs, values just either side of a halfway point, signed zeros, f16
+    subnormals and the f16 overflow boundary, then random values over a wide exponent range."""
+    vals = []
+    if for_bf16:
+        for m in range(0, 128, 7):            # bf16 mantissas of both parities
+            base = np.float32(1.0 + m / 128.0)
+            ulp = np.float32(2.0 ** -7)
+            half = np.float32(base + ulp / 2)  # exactly between base and base + ulp
+            vals += [half, -half, np.nextafter(half, np.float32(0)), np.nextafter(half, np.float32(9))]
+            vals += [np.float32(half * 2.0 ** 20), np.float32(half * 2.0 ** -30)]
+    else:
+        for m in range(0, 1024, 37):          # f16 mantissas of both parities
+            base = np.float32(1.0 + m / 1024.0)
+            ulp = np.float32(2.0 ** -10)
+            half = np.float32(base + ulp / 2)
+            vals += [half, -half, np.nextafter(half, np.float32(0)), np.nextafter(half, np.float32(9))]
+            vals += [np.float32(half * 2.0 ** 10), np.float32(half * 2.0 ** -12)]
+        vals += [np.float32(2.0 ** -24), np.float32(2.0 ** -25), np.float32(1.5 * 2.0 ** -25), np.float32(3 * 2.0 ** -26),
+                 np.float32(2.0 ** -14), np.float32(2.0 ** -14 - 2.0 ** -25), np.float32(65504.0), np.float32(65519.0),
+                 np.float32(65520.0), np.float32(-65520.0), np.float32(1e6), np.float32(2.0 ** -30)]
+    vals += [np.float32(0.0), np.float32(-0.0), np.float32(1.0), np.float32(-1.0)]
+    rng = np.random.default_rng(seed)
+    lim = 12 if not for_bf16 else 60
+    rand = (rng.standard_normal(n_random) * np.exp2(rng.integers(-lim, lim, n_random))).astype(np.float32)
+    return np.concatenate([np.asarray(vals, np.float32), rand])
