@@ -67,6 +67,23 @@ uint64_t ptowsp_hip_workload_main(ptowsp_program* prog, RuntimeContext* ctx, CSP
  * the synchronize. */
 int ptowsp_hip_launch(ptowsp_program* prog, RuntimeContext* ctx, void* hip_stream, ptowsp_run_info* info);
 
+/* No counterpart in the reference.  For callers that cannot allocate memory
+ * (code under HIP graph capture, tight serving loops, harnesses that forbid
+ * hipMalloc): the same run as ptowsp_hip_launch, allocating no device or
+ * pinned memory and loading no code objects.  The decode kernels' unit
+ * counters and partials, the kernels' error flag and the copy of
+ * device-resident loop-extent tensors use a fixed device scratch of 16 MiB
+ * per GPU (held until the process ends); a run that needs more is refused
+ * with an error before its decode launch.  Requirements: every tensor is
+ * device memory; each launch's kernel was already built and loaded by an
+ * earlier ptowsp_hip_launch of the same program (same bindings); no cpp_src
+ * kernels, slot loads or masked (cond-on-grid) launches.  All no-allocation
+ * runs on one GPU share its scratch: runs that overlap in time on one GPU
+ * race and must not be issued.  Finish with ptowsp_hip_synchronize as usual;
+ * device time is reported only when an earlier ptowsp_hip_launch created the
+ * program's timing events. */
+int ptowsp_hip_launch_noalloc(ptowsp_program* prog, RuntimeContext* ctx, void* hip_stream, ptowsp_run_info* info);
+
 /* Cycle model result of the last synchronized run (new: pairs with the
  * deferred total_cycles of ptowsp_hip_launch).  -1 while a run is pending. */
 int ptowsp_hip_run_result(const ptowsp_program* prog, ptowsp_run_info* info);

@@ -97,8 +97,21 @@ std::vector<char> jit_compile(const std::string& source) {
     return code;
 }
 
+namespace {
+std::string source_key(const std::string& source) {
+    return hex64(fnv1a_64(source + "\n" + options_key() + "\n" + kDeviceHeader + kLaunchHeader));
+}
+}  // namespace
+
+const JitKernel* jit_loaded(const std::string& source, const std::string& entry) {
+    const std::string key = source_key(source);
+    std::lock_guard<std::mutex> lock(g_mu);
+    auto it = g_loaded.find(key + entry);
+    return it == g_loaded.end() ? nullptr : it->second.get();
+}
+
 const JitKernel& jit_kernel(const std::string& source, const std::string& entry) {
-    const std::string key = hex64(fnv1a_64(source + "\n" + options_key() + "\n" + kDeviceHeader + kLaunchHeader));
+    const std::string key = source_key(source);
     std::lock_guard<std::mutex> lock(g_mu);
     auto it = g_loaded.find(key + entry);
     if (it != g_loaded.end()) return *it->second;

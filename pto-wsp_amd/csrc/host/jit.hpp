@@ -18,6 +18,10 @@ struct JitKernel {
 // named `entry`.  Loaded modules live until the process exits.
 const JitKernel& jit_kernel(const std::string& source, const std::string& entry);
 
+// The kernel if `source` is already loaded in this process, else null
+// (neither compiles nor loads anything).
+const JitKernel* jit_loaded(const std::string& source, const std::string& entry);
+
 // Compiles without loading (no GPU needed); returns the code object bytes.
 std::vector<char> jit_compile(const std::string& source);
 

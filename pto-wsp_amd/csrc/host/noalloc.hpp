@@ -1,0 +1,25 @@
+// Fixed device scratch for the no-allocation launch (noalloc.hip).
+#pragma once
+
+#include <hip/hip_runtime_api.h>
+
+#include <cstddef>
+
+namespace ptowsp {
+
+// Size of the per-device scratch array.  Layout used by a no-allocation run:
+//   [0, 256)            the kernels' error flag (int at offset 0);
+//   [256, 256 + 16 KiB) decode unit counters (kDecodeMaxUnits int32);
+//   then the device-resident loop-extent tensors the cycle model reads;
+//   then the decode partials.
+constexpr size_t kNoAllocScratchBytes = size_t(16) << 20;
+constexpr size_t kNoAllocHeaderBytes = 256;
+
+// Device address of this device's scratch array (looked up once per device
+// with hipGetSymbolAddress, then cached).
+void* noalloc_scratch();
+
+// Zeroes `bytes` (a multiple of 4) at dev_ptr with a small kernel on `stream`.
+void noalloc_zero(void* dev_ptr, size_t bytes, hipStream_t stream);
+
+}  // namespace ptowsp

@@ -23,6 +23,7 @@
 #include "emit.hpp"
 #include "jit.hpp"
 #include "module.hpp"
+#include "noalloc.hpp"
 #include "plan.hpp"
 #include "ptowsp_hip.h"
 
@@ -124,6 +125,12 @@ struct ptowsp_program {
     };
     std::map<const Node*, std::vector<CustomRun>> custom_runs;
     std::vector<std::array<size_t, 3>> readback;  // chunk, offset, count
+    // Run started by ptowsp_hip_launch_noalloc: its error flag and deferred
+    // extent copies live in the device scratch of noalloc.hip.
+    bool noalloc_run = false;
+    int* noalloc_err = nullptr;
+    const int32_t* deferred_dev = nullptr;  // device copy of the deferred extent tensors
+    bool timed = false;                     // the run recorded ev0 / ev1
     uint64_t* slot_stage = nullptr;     // pinned: one element read by a slot load
     std::vector<uint64_t> slot_log;     // values of the run's slot loads, in order
     std::vector<uint64_t> slot_start;   // slots when the run started
@@ -207,12 +214,20 @@ struct RunEnv {
     std::map<int, std::vector<int32_t>> idx_host;  // device index tensors read on the host, copied once per run
     bool timing_started = false;                   // ev0 recorded (just before the first kernel)
     bool replay_slots = false;                     // cycle model: slot loads replay P->slot_log
+    bool timing = true;                            // record ev0 / ev1 (the program's events exist)
+    // No-allocation run: the kernels' error flag, and the device scratch that
+    // replaces the program's hipMalloc'd decode scratch (counters at
+    // nscratch + kNoAllocHeaderBytes, partials after them, nscratch_limit
+    // bytes usable from nscratch).
+    int* err = nullptr;
+    char* nscratch = nullptr;
+    size_t nscratch_limit = 0;
 };
 
 // Device time starts at the program's first kernel: host work that precedes
 // it (building launch arguments, compiling) is not counted.
 void start_timing(RunEnv& E, hipStream_t stream) {
-    if (E.timing_started) return;
+    if (E.timing_started || !E.timing) return;
     check(hipEventRecord(E.P->ev0, stream), "hipEventRecord");
     E.timing_started = true;
 }
@@ -834,7 +849,7 @@ BuiltLaunch build_launch(RunEnv& E, const LaunchSpec& L) {
             if (!found) throw CompileError("a scalar argument bound to a grid or in-kernel loop variable is not supported");
         }
     }
-    A.err = P->d_err;
+    A.err = E.err ? E.err : P->d_err;
     B.spec.serial = grid_write_hazard(a, L, A, B.spec, ng, nvars);
     B.spec.row_up = tuning().row_up;
     B.spec.nontemporal = tuning().nontemporal;
@@ -929,7 +944,19 @@ void enqueue_decode(RunEnv& E, int li, BuiltLaunch& B, const EmittedKernel& ek, 
     const size_t count_bytes = static_cast<size_t>(kDecodeMaxUnits) * sizeof(int32_t);
     const size_t part_bytes = static_cast<size_t>(B.ntasks + waves) * static_cast<size_t>(ek.part_floats) * sizeof(float);
     const size_t need = count_bytes + part_bytes;
-    if (need > P->scratch_bytes) {
+    const int ntens = static_cast<int>(a.tensor_param_index.size());
+    if (ntens >= kMaxParams) throw std::runtime_error("decode launch: no argument slot for its scratch");
+    if (E.nscratch) {
+        // No-allocation run: counters (zeroed at the start of the run) and
+        // partials in the fixed device scratch.
+        char* base = E.nscratch + kNoAllocHeaderBytes;
+        if (kNoAllocHeaderBytes + need > E.nscratch_limit)
+            throw std::runtime_error("ptowsp_hip_launch_noalloc: the decode launch needs " +
+                                     std::to_string(kNoAllocHeaderBytes + need) + " bytes of scratch, more than the " +
+                                     std::to_string(E.nscratch_limit) + " bytes available (the fixed scratch holds " +
+                                     std::to_string(kNoAllocScratchBytes) + " bytes)");
+        B.args.base[ntens] = base;
+    } else if (need > P->scratch_bytes) {
         if (P->scratch) check(hipFree(P->scratch), "hipFree(scratch)");
         P->scratch = nullptr;
         P->scratch_bytes = 0;
@@ -938,9 +965,7 @@ void enqueue_decode(RunEnv& E, int li, BuiltLaunch& B, const EmittedKernel& ek, 
         check(hipDeviceSynchronize(), "hipDeviceSynchronize");
         P->scratch_bytes = need;
     }
-    const int ntens = static_cast<int>(a.tensor_param_index.size());
-    if (ntens >= kMaxParams) throw std::runtime_error("decode launch: no argument slot for its scratch");
-    B.args.base[ntens] = static_cast<char*>(P->scratch);
+    if (!E.nscratch) B.args.base[ntens] = static_cast<char*>(P->scratch);
     B.args.span[ntens] = static_cast<int64_t>(need / sizeof(float));
     B.args.scal[kMaxScalars - 1] = static_cast<uint64_t>(maxp);
     void* params[] = {&B.args};
@@ -960,7 +985,16 @@ void enqueue_built(RunEnv& E, int li, BuiltLaunch& B, hipStream_t stream, uint64
     const JitKernel* jk;
     auto it = c.by_spec.find(key);
     if (it == c.by_spec.end()) {
-        jk = &jit_kernel(ek.source, ek.entry);
+        if (E.nscratch) {
+            // A no-allocation run loads no code objects (loading allocates).
+            jk = jit_loaded(ek.source, ek.entry);
+            if (!jk)
+                throw std::runtime_error("ptowsp_hip_launch_noalloc: the kernel of launch " + std::to_string(li) +
+                                         " is not loaded yet; run the program once through ptowsp_hip_launch, "
+                                         "which builds and loads its kernels");
+        } else {
+            jk = &jit_kernel(ek.source, ek.entry);
+        }
         c.by_spec[key] = jk;
     } else {
         jk = it->second;
@@ -1325,6 +1359,23 @@ void defer_cycles(RunEnv& E, const std::vector<int>& tids, hipStream_t stream) {
         P->deferred_tids.push_back({tid, total});
         total += static_cast<size_t>(std::max<int64_t>(E.ts[tid].span, 0));
     }
+    P->deferred_ts = E.ts;
+    P->deferred_ctx = E.ctx;
+    P->cycles_deferred = true;
+    if (E.nscratch) {
+        // No-allocation run: device-to-device copies into the tail of the
+        // fixed scratch (reserved by the entry point), read back at synchronize.
+        int32_t* dst = reinterpret_cast<int32_t*>(E.nscratch + E.nscratch_limit);
+        for (const auto& [tid, off] : P->deferred_tids) {
+            const size_t n = static_cast<size_t>(std::max<int64_t>(E.ts[tid].span, 0));
+            if (n)
+                check(hipMemcpyAsync(dst + off, E.ts[tid].dev, n * 4, hipMemcpyDeviceToDevice, stream),
+                      "hipMemcpyAsync(extent tensor)");
+        }
+        P->deferred_dev = dst;
+        return;
+    }
+    P->deferred_dev = nullptr;
     if (total > P->key_stage_elems) {
         if (P->key_stage) check(hipHostFree(P->key_stage), "hipHostFree(key stage)");
         P->key_stage = nullptr;
@@ -1338,9 +1389,121 @@ void defer_cycles(RunEnv& E, const std::vector<int>& tids, hipStream_t stream) {
             check(hipMemcpyAsync(P->key_stage + off, E.ts[tid].dev, n * 4, hipMemcpyDeviceToHost, stream),
                   "hipMemcpyAsync(extent tensor)");
     }
-    P->deferred_ts = E.ts;
-    P->deferred_ctx = E.ctx;
-    P->cycles_deferred = true;
+}
+
+// Both launch entry points.  noalloc: the run allocates no device or pinned
+// memory: every tensor must already be in device memory, the kernels' error
+// flag and the decode scratch live in the fixed device scratch of
+// noalloc.hip, the deferred cycle-model input is copied there too, and
+// features whose host steps need staging buffers are refused.
+int launch_impl(ptowsp_program* P, RuntimeContext* ctx, void* hip_stream, ptowsp_run_info* info, bool noalloc) {
+    if (!P || !ctx) throw std::runtime_error("null argument");
+    if (P->pending) throw std::runtime_error("Program already started");
+    hipStream_t stream = static_cast<hipStream_t>(hip_stream);
+    bool custom = false;
+    for (const auto& k : P->m.kernels) custom |= k.custom;
+    RunEnv E{P, ctx, {}, {}, {}};
+    if (noalloc) {
+        const char* who = "ptowsp_hip_launch_noalloc: ";
+        if (custom) throw std::runtime_error(std::string(who) + "cpp_src kernels read their per-task cycles back through staging memory");
+        if (module_loads_slots(P->m)) throw std::runtime_error(std::string(who) + "slot loads read tensors back through staging memory");
+        for (const auto& L : P->plan.launches)
+            if (!L.masks.empty())
+                throw std::runtime_error(std::string(who) + "masked launches upload task lists through staging memory");
+        // Every tensor must be device memory: host tensors would need staging buffers.
+        const size_t nt = P->m.tensors.size();
+        for (size_t t = 0; t < nt; ++t) {
+            bool empty = false;
+            for (int64_t d : P->m.tensors[t].shape) empty |= d == 0;
+            if (empty) continue;
+            const void* ptr = ctx->get_tensor_ptr(ctx->ctx, static_cast<uint32_t>(t));
+            if (ptr && !is_device_pointer(ptr))
+                throw std::runtime_error(std::string(who) + "tensor " + std::to_string(t) +
+                                         " is host memory; this entry point needs device-resident tensors");
+        }
+        E.nscratch = static_cast<char*>(noalloc_scratch());
+        E.err = reinterpret_cast<int*>(E.nscratch);
+        E.timing = P->have_events;
+    } else {
+        if (!P->h_err) {
+            check(hipHostMalloc(reinterpret_cast<void**>(&P->h_err), sizeof(int), hipHostMallocMapped | hipHostMallocCoherent),
+                  "hipHostMalloc(err)");
+            __atomic_store_n(P->h_err, 0, __ATOMIC_RELAXED);
+            check(hipHostGetDevicePointer(reinterpret_cast<void**>(&P->d_err), P->h_err, 0), "hipHostGetDevicePointer(err)");
+        }
+        if (!P->have_events) {
+            // Timing-only events: no system-scope fence (cache writeback) of
+            // their own, which would otherwise be counted as device time.
+            check(hipEventCreateWithFlags(&P->ev0, hipEventDisableSystemFence), "hipEventCreate");
+            check(hipEventCreateWithFlags(&P->ev1, hipEventDisableSystemFence), "hipEventCreate");
+            P->have_events = true;
+        }
+    }
+    resolve_tensors(E, stream);
+    P->cycles_deferred = false;
+    P->deferred_dev = nullptr;
+    P->list_chunk = P->list_used = 0;
+    P->custom_runs.clear();
+    P->readback.clear();
+    P->slot_log.clear();
+    P->slot_start.assign(256, 0);
+    for (uint32_t i = 0; i < 256; ++i) P->slot_start[i] = ctx_slot(E, i);
+    // A slot load reads what the kernels before it wrote: the cycle model
+    // replays the values the run read, after the run.
+    const bool slot_loads = module_loads_slots(P->m) || custom;
+    const std::vector<int> dev_ext = device_extent_tensors(E);
+    if (noalloc) {
+        // The extent copies sit at the tail of the scratch; the decode
+        // launches may use everything before them.
+        size_t ext_bytes = 0;
+        for (int tid : dev_ext) ext_bytes += static_cast<size_t>(std::max<int64_t>(E.ts[tid].span, 0)) * 4;
+        ext_bytes = (ext_bytes + 255) / 256 * 256;
+        if (ext_bytes + kNoAllocHeaderBytes + kDecodeMaxUnits * sizeof(int32_t) > kNoAllocScratchBytes)
+            throw std::runtime_error("ptowsp_hip_launch_noalloc: the loop-extent tensors (" + std::to_string(ext_bytes) +
+                                     " bytes) do not fit in the fixed scratch of " + std::to_string(kNoAllocScratchBytes) +
+                                     " bytes");
+        E.nscratch_limit = kNoAllocScratchBytes - ext_bytes;
+        // The error flag and the decode unit counters start at zero.
+        noalloc_zero(E.nscratch, kNoAllocHeaderBytes + kDecodeMaxUnits * sizeof(int32_t), stream);
+    }
+    CycleResult cyc{};
+    bool ext_written = false;
+    for (int tid : dev_ext) ext_written |= E.ts[tid].written;
+    if (dev_ext.empty() && !slot_loads) cyc = cycles_for(E);
+    else if (!dev_ext.empty() && ext_written) defer_cycles(E, dev_ext, stream);
+    uint64_t launches = 0;
+    run_items(E, P->plan.items, stream, launches);
+    if (custom) {
+        // The cpp_src tasks' cycles: copied back after the kernels, the
+        // model runs at synchronize().
+        if (dev_ext.empty()) P->deferred_tids.clear();
+        for (const auto& r : P->readback) {
+            ptowsp_program::ListChunk& c = P->lists[r[0]];
+            if (r[2])
+                check(hipMemcpyAsync(c.host + r[1], c.dev + r[1], r[2] * 8, hipMemcpyDeviceToHost, stream),
+                      "hipMemcpyAsync(task cycles)");
+        }
+        P->deferred_ts = E.ts;
+        P->deferred_ctx = E.ctx;
+        P->cycles_deferred = true;
+    } else if (dev_ext.empty() && slot_loads) {
+        E.replay_slots = true;
+        cyc = cycles_for(E);
+    }
+    start_timing(E, stream);
+    if (E.timing) check(hipEventRecord(P->ev1, stream), "hipEventRecord");
+    // After the end event: the copy is not device time of the program.
+    if (!dev_ext.empty() && !ext_written) defer_cycles(E, dev_ext, stream);
+    check(hipGetLastError(), "kernel launch");
+    P->stream = stream;
+    P->pending = true;
+    P->timed = E.timing;
+    P->noalloc_run = noalloc;
+    P->noalloc_err = E.err;
+    P->last_run = ptowsp_run_info{cyc.total_cycles, cyc.tasks, static_cast<uint32_t>(launches), 0};
+    if (P->cycles_deferred) P->last_run.total_cycles = P->last_run.task_count = UINT64_MAX;
+    if (info) *info = P->last_run;
+    return 0;
 }
 
 int fail(const std::exception& e) {
@@ -1483,72 +1646,15 @@ int ptowsp_hip_cycle_model(ptowsp_program* P, RuntimeContext* ctx, ptowsp_run_in
 
 int ptowsp_hip_launch(ptowsp_program* P, RuntimeContext* ctx, void* hip_stream, ptowsp_run_info* info) {
     try {
-        if (!P || !ctx) throw std::runtime_error("null argument");
-        if (P->pending) throw std::runtime_error("Program already started");
-        hipStream_t stream = static_cast<hipStream_t>(hip_stream);
-        if (!P->h_err) {
-            check(hipHostMalloc(reinterpret_cast<void**>(&P->h_err), sizeof(int), hipHostMallocMapped | hipHostMallocCoherent),
-                  "hipHostMalloc(err)");
-            __atomic_store_n(P->h_err, 0, __ATOMIC_RELAXED);
-            check(hipHostGetDevicePointer(reinterpret_cast<void**>(&P->d_err), P->h_err, 0), "hipHostGetDevicePointer(err)");
-        }
-        if (!P->have_events) {
-            // Timing-only events: no system-scope fence (cache writeback) of
-            // their own, which would otherwise be counted as device time.
-            check(hipEventCreateWithFlags(&P->ev0, hipEventDisableSystemFence), "hipEventCreate");
-            check(hipEventCreateWithFlags(&P->ev1, hipEventDisableSystemFence), "hipEventCreate");
-            P->have_events = true;
-        }
-        RunEnv E{P, ctx, {}, {}, {}};
-        resolve_tensors(E, stream);
-        P->cycles_deferred = false;
-        P->list_chunk = P->list_used = 0;
-        P->custom_runs.clear();
-        P->readback.clear();
-        P->slot_log.clear();
-        P->slot_start.assign(256, 0);
-        for (uint32_t i = 0; i < 256; ++i) P->slot_start[i] = ctx_slot(E, i);
-        // A slot load reads what the kernels before it wrote: the cycle model
-        // replays the values the run read, after the run.
-        bool custom = false;
-        for (const auto& k : P->m.kernels) custom |= k.custom;
-        const bool slot_loads = module_loads_slots(P->m) || custom;
-        const std::vector<int> dev_ext = device_extent_tensors(E);
-        CycleResult cyc{};
-        bool ext_written = false;
-        for (int tid : dev_ext) ext_written |= E.ts[tid].written;
-        if (dev_ext.empty() && !slot_loads) cyc = cycles_for(E);
-        else if (!dev_ext.empty() && ext_written) defer_cycles(E, dev_ext, stream);
-        uint64_t launches = 0;
-        run_items(E, P->plan.items, stream, launches);
-        if (custom) {
-            // The cpp_src tasks' cycles: copied back after the kernels, the
-            // model runs at synchronize().
-            if (dev_ext.empty()) P->deferred_tids.clear();
-            for (const auto& r : P->readback) {
-                ptowsp_program::ListChunk& c = P->lists[r[0]];
-                if (r[2])
-                    check(hipMemcpyAsync(c.host + r[1], c.dev + r[1], r[2] * 8, hipMemcpyDeviceToHost, stream),
-                          "hipMemcpyAsync(task cycles)");
-            }
-            P->deferred_ts = E.ts;
-            P->deferred_ctx = E.ctx;
-            P->cycles_deferred = true;
-        } else if (dev_ext.empty() && slot_loads) {
-            E.replay_slots = true;
-            cyc = cycles_for(E);
-        }
-        start_timing(E, stream);
-        check(hipEventRecord(P->ev1, stream), "hipEventRecord");
-        // After the end event: the copy is not device time of the program.
-        if (!dev_ext.empty() && !ext_written) defer_cycles(E, dev_ext, stream);
-        check(hipGetLastError(), "kernel launch");
-        P->stream = stream;
-        P->pending = true;
-        P->last_run = ptowsp_run_info{cyc.total_cycles, cyc.tasks, static_cast<uint32_t>(launches), 0};
-        if (P->cycles_deferred) P->last_run.total_cycles = P->last_run.task_count = UINT64_MAX;
-        if (info) *info = P->last_run;
-        return 0;
+        return launch_impl(P, ctx, hip_stream, info, false);
+    } catch (const std::exception& e) {
+        return fail(e);
+    }
+}
+
+int ptowsp_hip_launch_noalloc(ptowsp_program* P, RuntimeContext* ctx, void* hip_stream, ptowsp_run_info* info) {
+    try {
+        return launch_impl(P, ctx, hip_stream, info, true);
     } catch (const std::exception& e) {
         return fail(e);
     }
@@ -1569,21 +1675,29 @@ int ptowsp_hip_synchronize(ptowsp_program* P, ptowsp_timing* timing) {
             E.replay_slots = module_loads_slots(P->m);
             for (const auto& [tid, off] : P->deferred_tids) {
                 const size_t n = static_cast<size_t>(std::max<int64_t>(E.ts[tid].span, 0));
-                E.idx_host[tid] = std::vector<int32_t>(P->key_stage + off, P->key_stage + off + n);
+                if (P->deferred_dev) {
+                    std::vector<int32_t> v(n);
+                    if (n) check(hipMemcpy(v.data(), P->deferred_dev + off, n * 4, hipMemcpyDeviceToHost), "hipMemcpy(extent tensor)");
+                    E.idx_host[tid] = std::move(v);
+                } else {
+                    E.idx_host[tid] = std::vector<int32_t>(P->key_stage + off, P->key_stage + off + n);
+                }
             }
             const CycleResult cyc = cycles_for(E);
             P->last_run.total_cycles = cyc.total_cycles;
             P->last_run.task_count = cyc.tasks;
         }
         float dev_ms = 0.0f;
-        check(hipEventElapsedTime(&dev_ms, P->ev0, P->ev1), "hipEventElapsedTime");
+        if (P->timed) check(hipEventElapsedTime(&dev_ms, P->ev0, P->ev1), "hipEventElapsedTime");
         const auto t0 = std::chrono::steady_clock::now();
         for (const auto& cb : P->copy_back) check(hipMemcpy(cb.host, cb.dev, cb.bytes, hipMemcpyDeviceToHost), "hipMemcpy(D2H)");
         const double d2h = ms_since(t0);
         P->copy_back.clear();
-        const int err = __atomic_load_n(P->h_err, __ATOMIC_ACQUIRE);
+        int err = 0;
+        if (P->noalloc_run) check(hipMemcpy(&err, P->noalloc_err, sizeof(int), hipMemcpyDeviceToHost), "hipMemcpy(error flag)");
+        else err = __atomic_load_n(P->h_err, __ATOMIC_ACQUIRE);
         if (err) {
-            __atomic_store_n(P->h_err, 0, __ATOMIC_RELAXED);
+            if (!P->noalloc_run) __atomic_store_n(P->h_err, 0, __ATOMIC_RELAXED);
             throw std::runtime_error(err == 1   ? "an indirect tensor index was out of range (tasks skipped)"
                                      : err == 3 ? "a loop extent read from a tensor exceeded its declared maximum"
                                                 : "a task's tile fell outside its tensor (tasks skipped)");
