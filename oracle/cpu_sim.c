@@ -71,10 +71,14 @@ static int is_float_dt(int dt) { return dt == DT_F16 || dt == DT_BF16 || dt == D
 typedef struct { int dtype, rank; int64_t shape[8]; } TensorInfo;
 typedef struct { int id, dtype, tile, rows, cols; } Val;
 typedef struct { char* name; int id; } Param;
-typedef struct { int kind; int result; int nopnd; int* opnd; int has_value; double value; } Op;
+typedef struct {
+    int kind; int result; int nopnd; int* opnd; int has_value; double value;
+    int has_k, has_cols, has_cycles; int64_t k, cols, cycles; /* integer attrs */
+} Op;
 
 enum { OP_LOAD, OP_STORE, OP_ADD, OP_SUB, OP_MUL, OP_DIV, OP_MAX, OP_MIN, OP_EXP, OP_RSQRT,
-       OP_ROWSUM, OP_ROWMAX, OP_ROWMEAN, OP_MATMUL, OP_CONSTANT, OP_OTHER };
+       OP_ROWSUM, OP_ROWMAX, OP_ROWMEAN, OP_MATMUL, OP_CONSTANT,
+       OP_IOTA_U32, OP_TSORT32, OP_EXTRACT_TOPK, OP_TMOV, OP_STORE_TOPK, OP_ADD_CYCLES, OP_OTHER };
 
 typedef struct {
     char* name;
@@ -239,8 +243,10 @@ static int tok_dtype(Lex* L) {
 
 static int op_kind(const char* s) {
     static const char* names[] = {"Load", "Store", "Add", "Sub", "Mul", "Div", "Max", "Min", "Exp",
-                                  "Rsqrt", "RowSum", "RowMax", "RowMean", "Matmul", "Constant"};
-    for (int i = 0; i < 15; ++i)
+                                  "Rsqrt", "RowSum", "RowMax", "RowMean", "Matmul", "Constant",
+                                  "IotaU32", "TSort32", "ExtractTopkIndices", "TMov", "StoreTopkIndices",
+                                  "CpuSimAddCycles"};
+    for (int i = 0; i < 21; ++i)
         if (strcmp(s, names[i]) == 0) return i;
     return OP_OTHER;
 }
@@ -250,7 +256,14 @@ static void parse_attr_skip(Lex* L, Op* op) {
     char* ty = tok(L);
     int is_value = strcmp(key, "value") == 0;
     switch (ty[0]) {
-        case 'i': { int64_t v = tok_i64(L); if (is_value) { op->has_value = 1; op->value = (double)v; } break; }
+        case 'i': {
+            int64_t v = tok_i64(L);
+            if (is_value) { op->has_value = 1; op->value = (double)v; }
+            else if (strcmp(key, "k") == 0) { op->has_k = 1; op->k = v; }
+            else if (strcmp(key, "cols") == 0) { op->has_cols = 1; op->cols = v; }
+            else if (strcmp(key, "cycles") == 0) { op->has_cycles = 1; op->cycles = v; }
+            break;
+        }
         case 'd': { double v = tok_f64(L); if (is_value) { op->has_value = 1; op->value = v; } break; }
         case 'b': { int64_t v = tok_i64(L); if (is_value) { op->has_value = 1; op->value = (double)v; } break; }
         case 's': (void)tok_str(L); break;
@@ -505,7 +518,7 @@ static void analyze_kernel(Kernel* k) {
         for (int j = 0; j < op->nopnd; ++j) {
             int id = op->opnd[j];
             if (!k->by_id[id]->tile || k->param_of[id] < 0) continue;
-            if (op->kind == OP_STORE && j == 0) continue;
+            if ((op->kind == OP_STORE || op->kind == OP_STORE_TOPK) && j == 0) continue;
             k->preload[id] = 1;
         }
     }
@@ -872,6 +885,36 @@ static int64_t ew_i(int kind, int64_t a, int64_t b, const char* kname) {
     return 0;
 }
 
+/* TSORT32 of one [1,32] row (ptoisa_jit.py:247-258): (score, (float)index)
+ * pairs in descending score order, NaN after every number, equal scores in
+ * source order.  Stable insertion sort on the key -score (NaN largest). */
+static int tsort_after(float a, float b) { /* a strictly after b */
+    if (b != b) return 0;
+    if (a != a) return 1;
+    return a < b;
+}
+
+static void tsort32_pairs(float* dst, const float* sc, const int64_t* ix) {
+    float key[32];
+    int64_t id[32];
+    for (int i = 0; i < 32; ++i) {
+        float x = sc[i];
+        int64_t xi = ix[i];
+        int j = i;
+        while (j > 0 && tsort_after(key[j - 1], x)) {
+            key[j] = key[j - 1];
+            id[j] = id[j - 1];
+            --j;
+        }
+        key[j] = x;
+        id[j] = xi;
+    }
+    for (int i = 0; i < 32; ++i) {
+        dst[2 * i] = key[i];
+        dst[2 * i + 1] = (float)id[i];
+    }
+}
+
 /* Executes one task; returns its cpu_sim cycle count. */
 static uint64_t run_kernel(Kernel* k, Work* w, View* views, const uint64_t* scalar_args) {
     uint64_t cycles = 0;
@@ -1084,6 +1127,75 @@ static uint64_t run_kernel(Kernel* k, Work* w, View* views, const uint64_t* scal
                 cycles += (uint64_t)res->rows * (op->kind == OP_ROWMEAN ? 2u : 1u);
                 break;
             }
+            case OP_TMOV: { /* TMOV: copy, rows x cols of the destination (ptoisa_bridge.hpp:104-109) */
+                if (op->nopnd != 1 || !res || !res->tile) fail("kernel %s: TMov expects one tile operand", kn);
+                Val* sv = k->by_id[op->opnd[0]];
+                if (!sv->tile || sv->rows != res->rows || sv->cols != res->cols || sv->dtype != res->dtype)
+                    fail("kernel %s: TMov shape/dtype mismatch", kn);
+                Tile* s = &w->tiles[sv->id];
+                Tile* d = &w->tiles[res->id];
+                size_t n = (size_t)res->rows * res->cols;
+                if (d->f) memcpy(d->f, s->f, sizeof(float) * n);
+                else memcpy(d->i, s->i, sizeof(int64_t) * n);
+                cycles += rc(res);
+                break;
+            }
+            case OP_IOTA_U32: { /* 0..C-1 (src/python/pto_codegen.cpp:1132-1150), no cycles */
+                if (!res || !res->tile || res->rows != 1 || res->dtype != DT_U32)
+                    fail("kernel %s: IotaU32 expects a [1,C] u32 result", kn);
+                for (int c = 0; c < res->cols; ++c) w->tiles[res->id].i[c] = c;
+                break;
+            }
+            case OP_TSORT32: { /* (ptoisa_bridge.hpp:280-292): 5 cycles per source element */
+                if (op->nopnd != 2 || !res || !res->tile) fail("kernel %s: TSort32 expects (scores, idx)", kn);
+                Val* sv = k->by_id[op->opnd[0]];
+                Val* iv = k->by_id[op->opnd[1]];
+                if (!sv->tile || sv->rows != 1 || sv->cols != 32 || sv->dtype != DT_F32)
+                    fail("kernel %s: TSort32 requires a [1,32] f32 score tile", kn);
+                if (!iv->tile || iv->rows != 1 || iv->cols != 32 || iv->dtype != DT_U32)
+                    fail("kernel %s: TSort32 requires a [1,32] u32 index tile", kn);
+                if (res->rows != 1 || res->cols != 64 || res->dtype != DT_F32)
+                    fail("kernel %s: TSort32 result must be [1,64] f32", kn);
+                tsort32_pairs(w->tiles[res->id].f, w->tiles[sv->id].f, w->tiles[iv->id].i);
+                cycles += 5u * rc(sv);
+                break;
+            }
+            case OP_EXTRACT_TOPK: { /* (src/python/pto_codegen.cpp:1170-1193), no cycles */
+                if (op->nopnd != 1 || !res || !res->tile) fail("kernel %s: ExtractTopkIndices expects one operand", kn);
+                Val* pv = k->by_id[op->opnd[0]];
+                if (!pv->tile || pv->rows != 1 || pv->cols != 64 || pv->dtype != DT_F32)
+                    fail("kernel %s: ExtractTopkIndices expects [1,64] f32 pairs", kn);
+                int64_t kk = op->has_k && op->k > 0 ? op->k : res->cols;
+                if (res->rows != 1 || res->dtype != DT_I32 || kk != res->cols || kk > 32)
+                    fail("kernel %s: ExtractTopkIndices result must be a [1,k] i32 tile, 1 <= k <= 32", kn);
+                for (int64_t q = 0; q < kk; ++q) w->tiles[res->id].i[q] = (int32_t)w->tiles[pv->id].f[2 * q + 1];
+                break;
+            }
+            case OP_STORE_TOPK: { /* dst[i * s4] = (int)pairs[2i+1] (ptoisa_jit.py:445-456), no cycles */
+                if (op->nopnd != 2 || res) fail("kernel %s: StoreTopkIndices expects (dst, pairs)", kn);
+                int dst = op->opnd[0];
+                int pi = k->param_of[dst];
+                Val* dv = k->by_id[dst];
+                Val* pv = k->by_id[op->opnd[1]];
+                if (pi < 0 || !dv->tile) fail("kernel %s: StoreTopkIndices dst must be a kernel param tile", kn);
+                if (dv->dtype != DT_I32 && dv->dtype != DT_I64) fail("kernel %s: StoreTopkIndices dst must be i32 or i64", kn);
+                if (!pv->tile || pv->rows != 1 || pv->cols != 64 || pv->dtype != DT_F32)
+                    fail("kernel %s: StoreTopkIndices expects [1,64] f32 pairs", kn);
+                if (!op->has_k || op->k < 1 || op->k > 32 || op->k > dv->cols)
+                    fail("kernel %s: StoreTopkIndices k must be in [1, min(32, dst cols)]", kn);
+                View* v = &views[k->tensor_index[pi]];
+                for (int64_t q = 0; q < op->k; ++q) {
+                    int64_t x = (int32_t)w->tiles[pv->id].f[2 * q + 1];
+                    char* p = v->ptr + (q * v->s4) * k_dtype_size[v->dtype];
+                    if (v->dtype == DT_I32) { int32_t y = (int32_t)x; memcpy(p, &y, 4); }
+                    else memcpy(p, &x, 8);
+                }
+                break;
+            }
+            case OP_ADD_CYCLES: /* pto::cpu_sim::add_cycles(n) (ptoisa_jit.py:458-463) */
+                if (!op->has_cycles || op->cycles < 0) fail("kernel %s: CpuSimAddCycles needs a cycles attr", kn);
+                cycles += (uint64_t)op->cycles;
+                break;
             default:
                 /* The emitter adds r*c cycles and computes nothing for other op
                  * kinds (:1223-1231); the oracle refuses them instead. */

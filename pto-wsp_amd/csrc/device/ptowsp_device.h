@@ -269,6 +269,28 @@ __device__ inline void tile_store_i(char* p, const i64* src, i64 s3, i64 s4) {
     }
 }
 
+// TSORT32 of one [1,32] row into [1,64] (score, index) pairs: descending by
+// score, NaN after every number, equal scores (+0 and -0 included) in source
+// order, i.e. a stable ascending sort of -score.  Each lane counts the
+// elements ordered before its own and writes its pair at that rank; the
+// index is the u32 index tile's element converted to float.
+template <int NT>
+__device__ inline void tsort32_rank(float* dst, const float* sc, const i64* ix) {
+    for (int e = threadIdx.x; e < 32; e += NT) {
+        const float x = sc[e];
+        const bool xn = x != x;
+        int rank = 0;
+        for (int j = 0; j < 32; ++j) {
+            const float y = sc[j];
+            const bool yn = y != y;
+            const bool before = xn ? (!yn || j < e) : (!yn && (y > x || (y == x && j < e)));
+            rank += before ? 1 : 0;
+        }
+        dst[2 * rank] = x;
+        dst[2 * rank + 1] = static_cast<float>(ix[e]);
+    }
+}
+
 // ---------------------------------------------------------------------------
 // GEMM blocks: C[BM,BN] (fp32) (+)= sum over K steps of A[BM,BK] x B[BK,BN]
 // (bf16 or f16) on MFMA v_mfma_f32_32x32x16

@@ -37,8 +37,12 @@ bool classify_rows(const KernelDef& k, KernelAnalysis& a) {
         a.not_row_reason = why;
         return false;
     };
-    for (const auto& op : k.ops)
+    for (const auto& op : k.ops) {
         if (op.kind == OpKind::Matmul) return no("matmul");
+        if (op.kind == OpKind::IotaU32 || op.kind == OpKind::TSort32 || op.kind == OpKind::ExtractTopkIndices ||
+            op.kind == OpKind::StoreTopkIndices)
+            return no("top-k ops");
+    }
     int R = 0, C = 0;
     for (const auto& v : k.values) {
         if (!v.tile) continue;
@@ -63,7 +67,8 @@ bool classify_rows(const KernelDef& k, KernelAnalysis& a) {
             int id = op.operands[j];
             if (is_binary(op.kind) && j == 1 && a.bin_mode[i] == BinMode::RowExpand) bcast_row[id]++;
             else if (is_binary(op.kind) && j == 1 && a.bin_mode[i] == BinMode::ColExpand) bcast_col[id]++;
-            else if (!(op.kind == OpKind::Store && j == 0)) other_use[id]++;
+            else if (!(op.kind == OpKind::Store && j == 0) && op.kind != OpKind::TMov && op.kind != OpKind::Load)
+                other_use[id]++;
         }
     }
     auto base_class = [&](const ValueInfo* v) -> RowClass {
@@ -81,6 +86,9 @@ bool classify_rows(const KernelDef& k, KernelAnalysis& a) {
             a.row_class[v.id] = RowClass::Scalar;
             continue;
         }
+        // A param tile read only through Load ops (or only stored to) is no
+        // value of the program: its Load results are.
+        if (a.param_of[v.id] >= 0 && !a.preload[v.id]) continue;
         RowClass c = base_class(&v);
         if (c == RowClass::None)
             return no("tile " + std::to_string(v.id) + " of shape " + std::to_string(v.rows) + "x" +
@@ -112,7 +120,7 @@ GemmInfo classify_gemm(const KernelDef& k, const KernelAnalysis& a) {
     GemmInfo g;
     std::vector<const OpInfo*> ops;
     for (const auto& op : k.ops)
-        if (op.kind != OpKind::Constant) ops.push_back(&op);
+        if (op.kind != OpKind::Constant && op.kind != OpKind::CpuSimAddCycles) ops.push_back(&op);
     if (ops.size() != 2 && ops.size() != 3) return g;
     const OpInfo& mm = *ops[0];
     if (mm.kind != OpKind::Matmul || mm.result <= 0) return g;
@@ -164,6 +172,7 @@ NormInfo classify_norm(const KernelDef& k, const KernelAnalysis& a) {
     size_t div_index = 0;
     for (size_t i = 0; i < k.ops.size(); ++i) {
         const OpInfo& op = k.ops[i];
+        if (op.kind == OpKind::CpuSimAddCycles) continue;
         if (op.kind == OpKind::Div && !div) {
             div = &op;
             div_index = i;
@@ -201,7 +210,7 @@ DecodeInfo classify_decode(const KernelDef& k, const KernelAnalysis& a) {
     std::vector<const OpInfo*> stores;
     for (const auto& op : k.ops) {
         if (op.result > 0) def[op.result] = &op;
-        if (op.kind == OpKind::Constant) continue;
+        if (op.kind == OpKind::Constant || op.kind == OpKind::CpuSimAddCycles) continue;
         ++n_ops;
         if (op.kind == OpKind::Store) stores.push_back(&op);
     }
@@ -421,7 +430,7 @@ KernelAnalysis analyze_kernel(const KernelDef& k) {
         for (size_t j = 0; j < op.operands.size(); ++j) {
             const ValueInfo* v = val(op.operands[j]);
             if (!v->tile || a.param_of[v->id] < 0) continue;
-            if (op.kind == OpKind::Store && j == 0) continue;
+            if ((op.kind == OpKind::Store || op.kind == OpKind::StoreTopkIndices) && j == 0) continue;
             a.preload[v->id] = true;
         }
     }
@@ -434,6 +443,15 @@ KernelAnalysis analyze_kernel(const KernelDef& k) {
                 if (q.kind == OpKind::Matmul && q.result == id) a.acc_vec[id] = true;
         }
     }
+
+    // u32 tiles carry sort indices only: produced by IotaU32 (or a TMov of
+    // one) and read by TSort32 as its index operand.
+    for (const auto& op : k.ops)
+        for (size_t j = 0; j < op.operands.size(); ++j) {
+            const ValueInfo* v = val(op.operands[j]);
+            if (v->tile && v->dtype == DType::U32 && !(op.kind == OpKind::TSort32 && j == 1) && op.kind != OpKind::TMov)
+                refuse(k, "u32 tiles may only feed TSort32 (as its index operand) or TMov");
+        }
 
     uint64_t cycles = 0;
     for (size_t i = 0; i < k.params.size(); ++i) {
@@ -554,6 +572,78 @@ KernelAnalysis analyze_kernel(const KernelDef& k) {
                 if (is_int(s->dtype) != is_int(res->dtype)) refuse(k, "row reduce dtype mismatch");
                 if (dtype_is_float(s->dtype) && s->dtype != DType::F32) refuse(k, "row reduce of non-f32 tiles");
                 cycles += static_cast<uint64_t>(res->rows) * (op.kind == OpKind::RowMean ? 2u : 1u);
+                break;
+            }
+            case OpKind::TMov: {
+                // TMOV: a tile copy; rows x cols of the destination
+                // (ptoisa_bridge.hpp:104-109).
+                if (op.operands.size() != 1 || !res || !res->tile) refuse(k, "TMov expects one tile operand and a tile result");
+                const ValueInfo* s = val(op.operands[0]);
+                if (!s->tile || s->rows != res->rows || s->cols != res->cols || s->dtype != res->dtype)
+                    refuse(k, "TMov shape/dtype mismatch");
+                if (dtype_is_float(res->dtype) && res->dtype != DType::F32)
+                    refuse(k, std::string("TMov of ") + dtype_name(res->dtype) + " tiles is not supported");
+                cycles += rc(res);
+                break;
+            }
+            case OpKind::IotaU32: {
+                // A [1,C] u32 tile holding 0..C-1: a scalar loop in the reference
+                // emitter (src/python/pto_codegen.cpp:1132-1150), no cycles.
+                if (!op.operands.empty() || !res || !res->tile || res->rows != 1 || res->dtype != DType::U32)
+                    refuse(k, "IotaU32 expects a [1,C] u32 result");
+                auto it = op.ints.find("cols");
+                if (it != op.ints.end() && it->second != res->cols) refuse(k, "IotaU32 cols attr does not match its result");
+                break;
+            }
+            case OpKind::TSort32: {
+                // TSORT32 of a [1,32] f32 score tile with a [1,32] u32 index tile into
+                // [1,64] (score, index) pairs; 5 cycles per source element
+                // (ptoisa_bridge.hpp:280-292, ptoisa_jit.py:247-258).
+                if (op.operands.size() != 2 || !res || !res->tile) refuse(k, "TSort32 expects (scores, idx) and a tile result");
+                const ValueInfo* sc = val(op.operands[0]);
+                const ValueInfo* ix = val(op.operands[1]);
+                if (!sc->tile || sc->rows != 1 || sc->cols != 32 || sc->dtype != DType::F32)
+                    refuse(k, "TSort32 requires a [1,32] f32 score tile");
+                if (!ix->tile || ix->rows != 1 || ix->cols != 32 || ix->dtype != DType::U32)
+                    refuse(k, "TSort32 requires a [1,32] u32 index tile");
+                if (res->rows != 1 || res->cols != 64 || res->dtype != DType::F32) refuse(k, "TSort32 result must be [1,64] f32");
+                cycles += 5 * rc(sc);
+                break;
+            }
+            case OpKind::ExtractTopkIndices: {
+                // The first k pair indices as i32 (src/python/pto_codegen.cpp:1170-1193); no cycles.
+                if (op.operands.size() != 1 || !res || !res->tile) refuse(k, "ExtractTopkIndices expects one operand");
+                const ValueInfo* pr = val(op.operands[0]);
+                if (!pr->tile || pr->rows != 1 || pr->cols != 64 || pr->dtype != DType::F32)
+                    refuse(k, "ExtractTopkIndices expects the [1,64] f32 pairs of TSort32");
+                auto it = op.ints.find("k");
+                const int64_t kk = it != op.ints.end() && it->second > 0 ? it->second : res->cols;
+                if (res->rows != 1 || res->dtype != DType::I32 || kk != res->cols || kk > 32)
+                    refuse(k, "ExtractTopkIndices result must be a [1,k] i32 tile with 1 <= k <= 32");
+                break;
+            }
+            case OpKind::StoreTopkIndices: {
+                // dst[i * col_stride] = (int)pairs[2i+1] for i < k, along row 0 of an
+                // output param (ptoisa_jit.py:197-204, 445-456); no cycles.
+                if (op.operands.size() != 2 || res) refuse(k, "StoreTopkIndices expects (dst, pairs)");
+                const ValueInfo* d = val(op.operands[0]);
+                const ValueInfo* pr = val(op.operands[1]);
+                if (a.param_of[d->id] < 0 || !d->tile) refuse(k, "StoreTopkIndices dst must be a kernel param tile");
+                if (d->dtype != DType::I32 && d->dtype != DType::I64) refuse(k, "StoreTopkIndices dst must be i32 or i64");
+                if (!pr->tile || pr->rows != 1 || pr->cols != 64 || pr->dtype != DType::F32)
+                    refuse(k, "StoreTopkIndices expects the [1,64] f32 pairs of TSort32");
+                auto it = op.ints.find("k");
+                const int64_t kk = it != op.ints.end() ? it->second : 0;
+                if (kk < 1 || kk > 32 || kk > d->cols) refuse(k, "StoreTopkIndices k must be in [1, min(32, dst cols)]");
+                a.stored[a.tensor_ordinal[a.param_of[d->id]]] = true;
+                break;
+            }
+            case OpKind::CpuSimAddCycles: {
+                // pto::cpu_sim::add_cycles(n) in the kernel body (ptoisa_jit.py:206-208, 458-463).
+                auto it = op.ints.find("cycles");
+                if (!op.operands.empty() || res || it == op.ints.end() || it->second < 0)
+                    refuse(k, "CpuSimAddCycles expects a non-negative integer 'cycles' attr");
+                cycles += static_cast<uint64_t>(it->second);
                 break;
             }
             default:

@@ -270,6 +270,13 @@ EmittedKernel emit_row(const Module& m, const KernelAnalysis& a, const LaunchSpe
                 }
                 break;
             }
+            case OpKind::CpuSimAddCycles:
+                break;
+            case OpKind::TMov: {
+                const int r = op.result, x = op.operands[0];
+                o << "      const " << (cls(r) == RowClass::Full ? "RS" : "float") << " v" << r << " = " << vname(x) << ";\n";
+                break;
+            }
             case OpKind::Exp:
             case OpKind::Rsqrt: {
                 const int r = op.result, x = op.operands[0];
@@ -461,6 +468,31 @@ EmittedKernel emit_tile(const Module& m, const KernelAnalysis& a, const LaunchSp
                     else o << ind << "  acc = acc / " << s->cols << ";\n";
                 }
                 o << ind << "  L" << res->id << "[r] = acc;\n" << ind << "}\n";
+                break;
+            }
+            case OpKind::CpuSimAddCycles: continue;
+            case OpKind::TMov:
+                o << ind << "for (int e = threadIdx.x; e < " << res->rows * res->cols << "; e += NT) L" << res->id << "[e] = "
+                  << src(op.operands[0], "e") << ";\n";
+                break;
+            case OpKind::IotaU32:
+                o << ind << "for (int e = threadIdx.x; e < " << res->cols << "; e += NT) L" << res->id << "[e] = e;\n";
+                break;
+            case OpKind::TSort32:
+                // Descending by score, NaN last, ties in source order: each of the 32
+                // elements finds its rank and writes its (score, index) pair.
+                o << ind << "tsort32_rank<NT>(L" << res->id << ", L" << op.operands[0] << ", L" << op.operands[1] << ");\n";
+                break;
+            case OpKind::ExtractTopkIndices:
+                o << ind << "for (int e = threadIdx.x; e < " << res->cols << "; e += NT) L" << res->id << "[e] = (i64)(int)L"
+                  << op.operands[0] << "[2 * e + 1];\n";
+                break;
+            case OpKind::StoreTopkIndices: {
+                const ValueInfo* d = a.by_id[op.operands[0]];
+                const int p = tord(d->id);
+                o << ind << "for (int e = threadIdx.x; e < " << op.ints.at("k") << "; e += NT) reinterpret_cast<"
+                  << (d->dtype == DType::I32 ? "int" : "i64") << "*>(p" << p << ")[(i64)e * A.s4[" << p << "]] = (int)L"
+                  << op.operands[1] << "[2 * e + 1];\n";
                 break;
             }
             default: throw CompileError("tile program: unexpected op " + op.kind_name);

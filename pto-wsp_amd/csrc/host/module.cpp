@@ -95,7 +95,10 @@ OpKind op_kind(const std::string& s) {
         {"Sub", OpKind::Sub},       {"Mul", OpKind::Mul},         {"Div", OpKind::Div},
         {"Max", OpKind::Max},       {"Min", OpKind::Min},         {"Exp", OpKind::Exp},
         {"Rsqrt", OpKind::Rsqrt},   {"RowSum", OpKind::RowSum},   {"RowMax", OpKind::RowMax},
-        {"RowMean", OpKind::RowMean}, {"Matmul", OpKind::Matmul}, {"Constant", OpKind::Constant}};
+        {"RowMean", OpKind::RowMean}, {"Matmul", OpKind::Matmul}, {"Constant", OpKind::Constant},
+        {"IotaU32", OpKind::IotaU32}, {"TSort32", OpKind::TSort32}, {"ExtractTopkIndices", OpKind::ExtractTopkIndices},
+        {"TMov", OpKind::TMov}, {"StoreTopkIndices", OpKind::StoreTopkIndices},
+        {"CpuSimAddCycles", OpKind::CpuSimAddCycles}};
     for (const auto& [n, k] : table)
         if (s == n) return k;
     return OpKind::Other;
@@ -108,6 +111,7 @@ void parse_attr(Lexer& L, OpInfo& op) {
     if (ty == "i" || ty == "b") {
         int64_t v = L.i64();
         if (is_value) { op.has_value = true; op.value = static_cast<double>(v); }
+        else if (ty == "i") op.ints[key] = v;
     } else if (ty == "d") {
         double v = L.f64();
         if (is_value) { op.has_value = true; op.value = v; }

@@ -48,7 +48,15 @@ struct ParamInfo {
     std::string direction;
 };
 
-enum class OpKind { Load, Store, Add, Sub, Mul, Div, Max, Min, Exp, Rsqrt, RowSum, RowMax, RowMean, Matmul, Constant, Other };
+enum class OpKind {
+    Load, Store, Add, Sub, Mul, Div, Max, Min, Exp, Rsqrt, RowSum, RowMax, RowMean, Matmul, Constant,
+    // Top-k helpers of the tracer (python/pto_wsp/kernel.py:689-724) and the
+    // PTO-ISA kernel surface (python/pto_wsp/ptoisa_jit.py:187-258): IOTA_U32,
+    // TSORT32, the index extraction, TMOV, store_topk_indices_i32 and
+    // cpu_sim_add_cycles.
+    IotaU32, TSort32, ExtractTopkIndices, TMov, StoreTopkIndices, CpuSimAddCycles,
+    Other
+};
 
 struct OpInfo {
     OpKind kind = OpKind::Other;
@@ -57,6 +65,7 @@ struct OpInfo {
     std::vector<int> operands;
     bool has_value = false;
     double value = 0.0;
+    std::map<std::string, int64_t> ints;  // integer attrs (cols, k, cycles)
 };
 
 struct KernelDef {

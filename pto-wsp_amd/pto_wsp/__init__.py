@@ -53,6 +53,7 @@ from pto_wsp.primitives import (
     slot_load_u64,
 )
 from pto_wsp import scalar_expr
+from pto_wsp.ptoisa_jit import ptoisa, ptoisa_kernel
 
 workload = workload_decorator
 kernel = kernel_decorator
@@ -65,7 +66,7 @@ __all__ = [
     "Program", "ProgramStats", "TraceLevel", "TraceEvent", "ExecutionTrace", "HIP_TARGETS",
     "Workload", "Task", "P", "LoopVar", "AffineIndex",
     "pto", "tl", "Value", "TileType", "ScalarType", "Tile", "Scalar", "KernelIR", "OpKind",
-    "workload", "kernel", "jit_kernel", "Kernel", "KernelRef", "In", "Out", "InOut", "Constexpr",
+    "workload", "kernel", "jit_kernel", "ptoisa", "ptoisa_kernel", "Kernel", "KernelRef", "In", "Out", "InOut", "Constexpr",
     "KernelParam", "extract_kernel_params", "get_direction", "get_inner_type",
     "CompileError", "ExecutionError", "IRBridgeError", "PtoError",
     "parallel_for", "for_each", "select", "cond", "task", "combine", "sequential", "slot_set_u64", "slot_load_u64",

@@ -132,6 +132,11 @@ class OpKind(Enum):
     IotaU32 = auto()
     TSort32 = auto()
     ExtractTopkIndices = auto()
+    # Extensions carrying the PTO-ISA kernels of pto_wsp.ptoisa_jit: TMOV, the
+    # top-k index store and an explicit cycle-model increment.
+    TMov = auto()
+    StoreTopkIndices = auto()
+    CpuSimAddCycles = auto()
 
 
 @dataclass
@@ -343,6 +348,41 @@ class _TileLanguage:
             raise TypeError(f"matmul acc dtype mismatch: acc={acc.dtype} out={out_dtype}")
         out = Value(ValueId.next(), out_dtype, (rows, cols))
         ir.add_op(OpKind.Matmul, [a, b] if acc is None else [a, b, acc], out)
+        return out
+
+    # -- PTO-ISA helpers (reference kernel.py:689-724) ---------------------
+    def iota_u32(self, cols: int) -> Value:
+        """A [1, cols] u32 tile holding 0 .. cols-1."""
+        ir = self._ir()
+        c = int(cols)
+        if c <= 0:
+            raise ValueError("iota_u32: cols must be > 0")
+        out = Value(ValueId.next(), DType.U32, (1, c))
+        ir.add_op(OpKind.IotaU32, [], out, cols=c)
+        return out
+
+    def tsort32(self, scores: Value, idx: Value) -> Value:
+        """TSORT32: the 32 (score, index) pairs sorted by descending score, as an f32 [1, 64]
+        tile of interleaved pairs (index stored as an f32 value)."""
+        ir = self._ir()
+        if scores.shape != (1, 32) or scores.dtype != DType.F32:
+            raise ValueError("tsort32: scores must be Tile[1,32,F32]")
+        if idx.shape != (1, 32) or idx.dtype != DType.U32:
+            raise ValueError("tsort32: idx must be Tile[1,32,U32]")
+        out = Value(ValueId.next(), DType.F32, (1, 64))
+        ir.add_op(OpKind.TSort32, [scores, idx], out)
+        return out
+
+    def extract_topk_indices(self, pairs: Value, k: int) -> Value:
+        """The indices of the first k pairs of a tsort32 result, as an i32 [1, k] tile."""
+        ir = self._ir()
+        kk = int(k)
+        if pairs.shape != (1, 64) or pairs.dtype != DType.F32:
+            raise ValueError("extract_topk_indices: pairs must be Tile[1,64,F32] from tsort32")
+        if kk <= 0 or kk > 32:
+            raise ValueError("extract_topk_indices: k must be in [1,32]")
+        out = Value(ValueId.next(), DType.I32, (1, kk))
+        ir.add_op(OpKind.ExtractTopkIndices, [pairs], out, k=kk)
         return out
 
     # -- scalars -----------------------------------------------------------

@@ -917,3 +917,131 @@ def rounding_probe_f32(n_random: int, seed: int = 0, for_bf16: bool = False) -> 
     lim = 12 if not for_bf16 else 60
     rand = (rng.standard_normal(n_random) * np.exp2(rng.integers(-lim, lim, n_random))).astype(np.float32)
     return np.concatenate([np.asarray(vals, np.float32), rand])
+
+
+# ---------------------------------------------------------------- @ptoisa_kernel
+def rr2(w, window: int):
+    """round_robin(2) + a STALL window: the schedule of tests/test_ptoisa_kernel_jit.py:45-48, 85-88."""
+    return w.dispatch(DispatchPolicy.round_robin(num_aicpus=2)).task_graph(
+        window=TaskWindow(window, "tasks", WindowMode.STALL))
+
+
+def ptoisa_square(arrs: dict):
+    """Y[t][0] = X[t][0] * X[t][0] over X[NT, 1, R, C] with tload / TMUL / tstore
+    (tests/test_ptoisa_kernel_jit.py:22-54)."""
+    from pto_wsp import ptoisa, ptoisa_kernel
+
+    x = arrs["x"]
+    NT, _, R, C = x.shape
+    X, Y = T(x), T(arrs["y"])
+
+    @ptoisa_kernel
+    def square(src: In[Tile[R, C, F32]], dst: Out[Tile[R, C, F32]]):
+        a = ptoisa.tload(src)
+        b = ptoisa.TMUL(a, a)
+        ptoisa.tstore(dst, b)
+
+    @workload
+    def wl():
+        for t in P(Dense[NT]()):
+            square[t](src=X[t][0], dst=Y[t][0])
+
+    return wl()
+
+
+def ptoisa_topk(arrs: dict, k: int = 8):
+    """out[b][t][0, :k] = the indices of the k largest of scores[b][t] ([1,32] f32) with
+    iota_u32 / TSORT32 / store_topk_indices_i32 (tests/test_ptoisa_kernel_jit.py:57-95)."""
+    from pto_wsp import ptoisa, ptoisa_kernel
+
+    s, o = arrs["scores"], arrs["out"]
+    B, NT = s.shape[:2]
+    S, O = T(s), T(o, I32)
+    oc = o.shape[-1]
+
+    @ptoisa_kernel
+    def topk(scores: In[Tile[1, 32, F32]], out_idx: Out[Tile[1, oc, I32]]):
+        sv = ptoisa.tload(scores)
+        idx = ptoisa.iota_u32(32)
+        pairs = ptoisa.TSORT32(sv, idx)
+        ptoisa.store_topk_indices_i32(out_idx, pairs, k)
+
+    @workload
+    def wl():
+        for b in P(Dense[B]()):
+            for t in P(Dense[NT]()):
+                topk[b, t](scores=S[b][t], out_idx=O[b][t])
+
+    return wl()
+
+
+def pto_topk(arrs: dict, k: int = 8):
+    """The same top-k through the pto.* tracer: pto.iota_u32 / pto.tsort32 /
+    pto.extract_topk_indices and a store of the [1,k] i32 tile."""
+    s, o = arrs["scores"], arrs["out"]
+    B, NT = s.shape[:2]
+    S, O = T(s), T(o, I32)
+
+    @kernel
+    def topk_tile(scores: In[Tile[1, 32, F32]], out_idx: Out[Tile[1, k, I32]]):
+        pairs = pto.tsort32(scores, pto.iota_u32(32))
+        pto.store(out_idx, pto.extract_topk_indices(pairs, k))
+
+    @workload
+    def wl():
+        for b in P(Dense[B]()):
+            for t in P(Dense[NT]()):
+                topk_tile[b, t](scores=S[b][t], out_idx=O[b][t])
+
+    return wl()
+
+
+def ptoisa_mix(arrs: dict, extra_cycles: int = 7):
+    """A chain of the other PTO-ISA instructions over X[B, R, C] (f32) with a
+    per-row m[B, R, 1], a per-column g[B, 1, C] and a Scalar[F32] divisor:
+    out = TMAX(TMOV(TDIVS(TCOLEXPANDMUL(TROWEXPANDSUB(x, m), g), s)), TMAXS(x, -0.5)) + TADDS(x, 2)
+    plus cpu_sim_add_cycles(extra_cycles)."""
+    from pto_wsp import ptoisa, ptoisa_kernel
+
+    x = arrs["x"]
+    B, R, C = x.shape
+    X, M, G, O = T(x), T(arrs["m"]), T(arrs["g"]), T(arrs["out"])
+    s_val = float(arrs["s"])
+
+    @ptoisa_kernel
+    def mix(x_t: In[Tile[R, C, F32]], m_t: In[Tile[R, 1, F32]], g_t: In[Tile[1, C, F32]], s: Scalar[F32],
+            out: Out[Tile[R, C, F32]]):
+        a = ptoisa.tload(x_t)
+        m = ptoisa.tload(m_t)
+        g = ptoisa.tload(g_t)
+        y = ptoisa.TMOV(ptoisa.TDIVS(ptoisa.TCOLEXPANDMUL(ptoisa.TROWEXPANDSUB(a, m), g), s))
+        z = ptoisa.TADD(ptoisa.TMAX(y, ptoisa.TMAXS(a, -0.5)), ptoisa.TADDS(a, 2))
+        ptoisa.cpu_sim_add_cycles(extra_cycles)
+        ptoisa.tstore(out, z)
+
+    @workload
+    def wl():
+        for b in P(Dense[B]()):
+            mix[b](x_t=X[b], m_t=M[b], g_t=G[b], s=s_val, out=O[b])
+
+    return wl()
+
+
+def ptoisa_unary(arrs: dict):
+    """out = TRSQRT(TEXP(x)) over X[B, R, C] (f32)."""
+    from pto_wsp import ptoisa, ptoisa_kernel
+
+    x = arrs["x"]
+    B, R, C = x.shape
+    X, O = T(x), T(arrs["out"])
+
+    @ptoisa_kernel
+    def unary(x_t: In[Tile[R, C, F32]], out: Out[Tile[R, C, F32]]):
+        ptoisa.tstore(out, ptoisa.TRSQRT(ptoisa.TEXP(ptoisa.tload(x_t))))
+
+    @workload
+    def wl():
+        for b in P(Dense[B]()):
+            unary[b](x_t=X[b], out=O[b])
+
+    return wl()
