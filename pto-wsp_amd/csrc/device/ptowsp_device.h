@@ -876,11 +876,15 @@ __device__ inline float row16_reduce(float x, Op op) {
 }
 
 // Partials pass between waves of different XCDs (each XCD has its own L2).
-// They are written and read as relaxed agent-scope atomics, which the
-// compiler issues with the sc1 policy (coherent across the XCDs' L2s), so no
-// L2 write-back or invalidate is needed for them; publish() orders a wave's
-// partial stores before its completion count: it waits until the stores are
-// done (vmcnt 0), with compiler barriers on both sides.
+// They are written and read as relaxed agent-scope atomics: global_store /
+// global_load with sc1, the agent-coherent form of the LLVM AMDGPU memory
+// model for gfx942/gfx950, so no L2 write-back (buffer_wbl2) or invalidate
+// (buffer_inv) is needed for them.  What the agent-scope release sequence
+// adds beyond that, s_waitcnt vmcnt(0) before the arrival RMW, publish()
+// does directly (with compiler barriers on both sides) or the deferred
+// arrival of DecodeStream gets from in-order completion: a wave's vector
+// memory operations report completion in issue order, so once a load issued
+// after the partial stores has returned, the stores are complete.
 __device__ inline void coherent_store(float* p, float v) { __hip_atomic_store(p, v, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT); }
 __device__ inline float coherent_load(const float* p) {
     return __hip_atomic_load(const_cast<float*>(p), __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
@@ -890,15 +894,8 @@ __device__ inline void publish() {
     wait_vmcnt<0>();
     __atomic_signal_fence(__ATOMIC_SEQ_CST);
 }
-// Unit completion count: the wave that brings it to `parts` (returned true)
-// folds the unit and sets the count back to zero for the next launch.
-__device__ inline bool arrive(int* cnt, int parts) {
-    int old = 0;
-    if ((threadIdx.x & 63) == 0) old = __hip_atomic_fetch_add(cnt, 1, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
-    old = __builtin_amdgcn_readfirstlane(old);
-    __atomic_signal_fence(__ATOMIC_SEQ_CST);
-    return old == parts - 1;
-}
+// The wave that brings a unit's completion count to `parts` folds the unit
+// and sets the count back to zero for the next launch.
 __device__ inline void reset_count(int* cnt) {
     if ((threadIdx.x & 63) == 0) __hip_atomic_store(cnt, 0, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
 }
@@ -1172,7 +1169,7 @@ __device__ inline DecodeFns<P, B, Q, S, C> decode_fns(P p, B b, Q q, S s, C c) {
 // F provides: page(g, PageOffs&) per lane; bases(PageOffs, kp, vp, mp);
 // q(u) (q tile of unit u, or null when out of range); slot(u) (this wave's
 // partial of unit u); combine(u, parts, first_slot).
-template <class DW, int NB>
+template <class DW, int NB, bool ORDERED>
 struct DecodeStream {
     struct Pending {
         int unit, parts, phase, wait;  // phase 0: none, 1: stores issued, 2: arrival issued
@@ -1180,7 +1177,12 @@ struct DecodeStream {
         int old_v;                     // arrival count before this wave's (lane 0)
     };
 
+    // ORDERED: the whole wave executes an agent-scope release fence before
+    // lane 0's arrival RMW (its partial stores are complete and written back
+    // before the count moves), and the last arriver an agent-scope acquire
+    // fence before it reads the partials.
     __device__ static void arrive_issue(Pending& pd, int* cnt) {
+        if constexpr (ORDERED) __builtin_amdgcn_fence(__ATOMIC_RELEASE, "agent");
         int r = 0;
         if ((threadIdx.x & 63) == 0) r = __hip_atomic_fetch_add(cnt + pd.unit, 1, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
         pd.old_v = r;
@@ -1191,6 +1193,8 @@ struct DecodeStream {
         if (pd.parts > 1) {
             last = __builtin_amdgcn_readfirstlane(pd.old_v) == pd.parts - 1;
             __atomic_signal_fence(__ATOMIC_SEQ_CST);
+            if constexpr (ORDERED)
+                if (last) __builtin_amdgcn_fence(__ATOMIC_ACQUIRE, "agent");
         }
         if (last) {
             f.combine(pd.unit, pd.parts, pd.first);

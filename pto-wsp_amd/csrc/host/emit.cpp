@@ -817,7 +817,7 @@ EmittedKernel emit_decode(const Module& m, const KernelAnalysis& a, const Launch
       << ");\n";
     o << "  };\n";
     o << "  auto fns = decode_fns(f_page, f_bases, f_q, f_slot, f_combine);\n";
-    o << "  DecodeStream<DW, " << spec.decode_ring << ">::run(fns, pre, cpre, U, TC, W, w, s, b, cnt, " << scale.str() << ", A.s4[" << d.kt
+    o << "  DecodeStream<DW, " << spec.decode_ring << ", " << (spec.decode_ordered ? "true" : "false") << ">::run(fns, pre, cpre, U, TC, W, w, s, b, cnt, " << scale.str() << ", A.s4[" << d.kt
       << "], A.s3[" << d.v << "], A.s3[" << d.q << "], lds);\n";
     o << "  }\n";
     o << "  }\n";

@@ -44,6 +44,7 @@ struct EmitSpec {
     // one per SIMD; 8: two per SIMD, 256 VGPRs each).
     int decode_ring = 4;
     int decode_waves = 4;
+    bool decode_ordered = false;  // release / acquire fences around the unit completion count
 };
 
 // Units (grid tasks) of one decode launch at most: every block holds their

@@ -1,5 +1,6 @@
 // C ABI entry points of libptowsp_hip.so: compile, launch, synchronize and
 // the RuntimeContext tables.  See include/ptowsp_hip.h.
+#include <hip/hip_ext.h>
 #include <hip/hip_runtime_api.h>
 
 #include <algorithm>
@@ -213,6 +214,7 @@ struct RunEnv {
     std::vector<std::pair<std::string, int64_t>> host_vars;
     std::map<int, std::vector<int32_t>> idx_host;  // device index tensors read on the host, copied once per run
     bool timing_started = false;                   // ev0 recorded (just before the first kernel)
+    bool timing_ended = false;                     // ev1 is the end of the last kernel launched
     bool replay_slots = false;                     // cycle model: slot loads replay P->slot_log
     bool timing = true;                            // record ev0 / ev1 (the program's events exist)
     // No-allocation run: the kernels' error flag, and the device scratch that
@@ -230,6 +232,30 @@ void start_timing(RunEnv& E, hipStream_t stream) {
     if (E.timing_started || !E.timing) return;
     check(hipEventRecord(E.P->ev0, stream), "hipEventRecord");
     E.timing_started = true;
+}
+
+// Launches one kernel.  With timing on, the launch's own start / stop events
+// bracket it: the first kernel of the run starts the device-time interval at
+// its dispatch and every kernel moves the end to its completion, so the
+// interval is the kernels' execution (and whatever the stream runs between
+// them), without the command processor's latency before the first dispatch.
+void launch_kernel(RunEnv& E, hipFunction_t f, int64_t blocks, int threads, size_t lds, hipStream_t stream, void** params,
+                   const char* what) {
+    const uint64_t work = static_cast<uint64_t>(blocks) * static_cast<uint64_t>(threads);
+    if (E.timing && work <= 0xFFFFFFFFull) {
+        hipEvent_t start = E.timing_started ? nullptr : E.P->ev0;
+        check(hipExtModuleLaunchKernel(f, static_cast<uint32_t>(work), 1, 1, static_cast<uint32_t>(threads), 1, 1, lds, stream,
+                                       params, nullptr, start, E.P->ev1, 0),
+              what);
+        E.timing_started = true;
+        E.timing_ended = true;
+        return;
+    }
+    start_timing(E, stream);
+    check(hipModuleLaunchKernel(f, static_cast<unsigned>(blocks), 1, 1, static_cast<unsigned>(threads), 1, 1,
+                                static_cast<unsigned>(lds), stream, params, nullptr),
+          what);
+    E.timing_ended = false;
 }
 
 int64_t axis_extent(RunEnv& E, const Axis& a) {
@@ -438,6 +464,7 @@ struct Tuning {
     bool gemm_pingpong = true;
     int decode_ring = 4;
     int decode_waves = 4;
+    bool decode_ordered = false;
 };
 
 const Tuning& tuning() {
@@ -448,6 +475,7 @@ const Tuning& tuning() {
         if (const char* s = std::getenv("PTOWSP_GEMM_PINGPONG")) v.gemm_pingpong = std::atoi(s) != 0;
         if (const char* s = std::getenv("PTOWSP_DECODE_RING")) v.decode_ring = std::min(8, std::max(2, std::atoi(s)));
         if (const char* s = std::getenv("PTOWSP_DECODE_WAVES")) v.decode_waves = std::atoi(s) == 8 ? 8 : 4;
+        if (const char* s = std::getenv("PTOWSP_DECODE_ORDERED")) v.decode_ordered = std::atoi(s) != 0;
         return v;
     }();
     return t;
@@ -861,6 +889,7 @@ BuiltLaunch build_launch(RunEnv& E, const LaunchSpec& L) {
     B.spec.decode = decode_allowed(a, L, A, B.spec, ng);
     B.spec.decode_ring = tuning().decode_ring;
     B.spec.decode_waves = tuning().decode_waves;
+    B.spec.decode_ordered = tuning().decode_ordered;
     B.spec.vec_width = a.family == Family::RowProgram ? pick_vec_width(a, A, nvars) : 1;
     if (P->ka[L.kernel].family == Family::Custom) {
         custom_axis_args(E, L, A);
@@ -875,7 +904,7 @@ std::string spec_key(const EmitSpec& s) {
     o << "vw" << s.vec_width << (s.serial ? ";serial" : "") << (s.task_list ? ";tl" : "") << ";up" << s.row_up << (s.nontemporal ? ";nt" : "")
       << (s.gemm ? ";gemm" : "") << ";m" << s.gemm_vm << ";n" << s.gemm_vn << (s.gemm_pingpong ? ";pp" : "")
       << (s.decode ? ";dec" : "")
-      << (s.decode_norm ? ";norm" : "") << ";r" << s.decode_ring << ";w" << s.decode_waves
+      << (s.decode_norm ? ";norm" : "") << ";r" << s.decode_ring << ";w" << s.decode_waves << (s.decode_ordered ? ";ord" : "")
       << ";i";
     for (int c : s.indirect_count) o << c << ",";
     o << ";d";
@@ -969,11 +998,7 @@ void enqueue_decode(RunEnv& E, int li, BuiltLaunch& B, const EmittedKernel& ek, 
     B.args.span[ntens] = static_cast<int64_t>(need / sizeof(float));
     B.args.scal[kMaxScalars - 1] = static_cast<uint64_t>(maxp);
     void* params[] = {&B.args};
-    start_timing(E, stream);
-    check(hipModuleLaunchKernel(jk.function, static_cast<unsigned>(grid), 1, 1, static_cast<unsigned>(ek.threads), 1, 1,
-                                shape.dyn_lds, stream, params,
-                                nullptr),
-          "hipModuleLaunchKernel(decode)");
+    launch_kernel(E, jk.function, grid, ek.threads, shape.dyn_lds, stream, params, "hipModuleLaunchKernel(decode)");
     launches += 1;
 }
 
@@ -1038,10 +1063,7 @@ void enqueue_built(RunEnv& E, int li, BuiltLaunch& B, hipStream_t stream, uint64
     }
     blocks = std::max<int64_t>(1, blocks);
     void* params[] = {&B.args};
-    start_timing(E, stream);
-    check(hipModuleLaunchKernel(jk->function, static_cast<unsigned>(blocks), 1, 1, static_cast<unsigned>(ek.threads), 1, 1,
-                                0, stream, params, nullptr),
-          "hipModuleLaunchKernel");
+    launch_kernel(E, jk->function, blocks, ek.threads, 0, stream, params, "hipModuleLaunchKernel");
     ++launches;
 }
 
@@ -1491,7 +1513,7 @@ int launch_impl(ptowsp_program* P, RuntimeContext* ctx, void* hip_stream, ptowsp
         cyc = cycles_for(E);
     }
     start_timing(E, stream);
-    if (E.timing) check(hipEventRecord(P->ev1, stream), "hipEventRecord");
+    if (E.timing && !E.timing_ended) check(hipEventRecord(P->ev1, stream), "hipEventRecord");
     // After the end event: the copy is not device time of the program.
     if (!dev_ext.empty() && !ext_written) defer_cycles(E, dev_ext, stream);
     check(hipGetLastError(), "kernel launch");
@@ -1570,6 +1592,7 @@ int ptowsp_hip_precompile(ptowsp_program* P, int index, int flags, const char** 
             spec.decode = a.family == Family::Decode && !spec.serial && L.inner.size() == 1;
             spec.decode_ring = tuning().decode_ring;
             spec.decode_waves = tuning().decode_waves;
+            spec.decode_ordered = tuning().decode_ordered;
             spec.indirect_count.assign(L.targs.size(), 0);
             for (size_t p = 0; p < L.targs.size(); ++p)
                 for (const auto& e : L.targs[p]->idx)
