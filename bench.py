@@ -175,6 +175,128 @@ def decode_workload(t, page=16):
     return rr4(paged_decode())
 
 
+def softmax3_workload(lg, pr, rmax, rsum):
+    """examples/softmax/pto_wsp_impl.py:52-105 as written: logits [B,S,V] viewed as
+    [B, S/8, 8, V/64, 64], three launches (running max and exp + running sum with P.seq
+    accumulators over v, then an in-place rescale over P(v)).  Each [8,64] tile view
+    L[b][s][v] starts at row-block v of seq tile s; with V = 512 (8 vocab tiles) the views
+    of a launch are disjoint, with V < 512 neighbouring v overlap."""
+    from pto_wsp import DType, Dense, In, InOut, Out, P, Tensor, Tile, kernel, pto, workload
+
+    f32 = DType.F32
+    B, S, V = tuple(lg.shape)
+    tr, tc = 8, 64
+    st, vt = S // tr, V // tc
+
+    def T(x, shape):
+        v = x.reshape(shape)  # a view of the same memory (numpy or torch, contiguous)
+        return Tensor(data=v, shape=shape, dtype=f32)
+
+    L = T(lg, (B, st, tr, vt, tc))
+    PR = T(pr, (B, st, tr, vt, tc))
+    RM, RS = T(rmax, tuple(rmax.shape)), T(rsum, tuple(rsum.shape))
+
+    @kernel
+    def update_rowmax(x_tile: In[Tile[tr, tc, f32]], m_acc: InOut[Tile[tr, 1, f32]]):
+        pto.store(m_acc, pto.max(m_acc, pto.rowmax(x_tile)))
+
+    @kernel
+    def exp_and_accumulate(x_tile: In[Tile[tr, tc, f32]], m_tile: In[Tile[tr, 1, f32]],
+                           y_tile: Out[Tile[tr, tc, f32]], l_acc: InOut[Tile[tr, 1, f32]]):
+        e = pto.exp(pto.sub(x_tile, m_tile))
+        pto.store(l_acc, pto.add(l_acc, pto.rowsum(e)))
+        pto.store(y_tile, e)
+
+    @kernel
+    def rescale(y_tile: InOut[Tile[tr, tc, f32]], l_tile: In[Tile[tr, 1, f32]]):
+        pto.store(y_tile, pto.div(y_tile, l_tile))
+
+    bb, ss, vv = Dense[B](), Dense[st](), Dense[vt]()
+
+    @workload
+    def softmax_workload():
+        for b in P(bb):
+            for s in P(ss):
+                for v in P.seq(vv):
+                    update_rowmax[b, s, v](x_tile=L[b][s][v], m_acc=RM[b][s])
+        for b in P(bb):
+            for s in P(ss):
+                for v in P.seq(vv):
+                    exp_and_accumulate[b, s, v](x_tile=L[b][s][v], m_tile=RM[b][s], y_tile=PR[b][s][v], l_acc=RS[b][s])
+        for b in P(bb):
+            for s in P(ss):
+                for v in P(vv):
+                    rescale[b, s, v](y_tile=PR[b][s][v], l_tile=RS[b][s])
+
+    return rr4(softmax_workload())
+
+
+class Softmax3Case:
+    """The three-phase softmax example on the tile-program family.  Work = the bytes the
+    tasks' tiles read and write (each task: one [8,64] f32 tile per tile operand, the [8,1]
+    accumulators)."""
+    unit, bound, dtype = "GB/s", "hbm", "f32"
+
+    def __init__(self, name, shape, seed):
+        self.name, self.shape, self.seed = name, shape, seed
+        self.baseline_config = None
+
+    def setup(self, dev):
+        import torch
+
+        g = torch.Generator(device=dev)
+        g.manual_seed(self.seed)
+        B, S, V = self.shape
+        self.lg = torch.randn(self.shape, generator=g, device=dev, dtype=torch.float32) * 0.1
+        self.pr = torch.zeros_like(self.lg)
+        self.rmax = torch.full((B, S // 8, 8, 1), float("-inf"), device=dev)
+        self.rsum = torch.zeros((B, S // 8, 8, 1), device=dev)
+        self.prog = softmax3_workload(self.lg, self.pr, self.rmax, self.rsum).compile(target="hip_gfx950")
+        tasks = B * (S // 8) * (V // 64)
+        tile, acc = 8 * 64 * 4, 8 * 4
+        # phase 1: x + m read, m written; phase 2: x, m, l read, y, l written; phase 3: y, l read, y written
+        self.work = tasks * ((tile + 2 * acc) + (tile + 2 * acc + tile + acc) + (2 * tile + acc))
+
+    def before_step(self):
+        self.rmax.fill_(float("-inf"))
+        self.rsum.zero_()
+
+    def peak(self):
+        return HBM_PEAK_GBS
+
+    def rate(self, seconds):
+        return self.work / seconds / 1e9
+
+    def describe(self):
+        B, S, V = self.shape
+        return (f"{self.name}: examples/softmax three phases over logits [{B},{S},{V}], [8,64] f32 tiles, "
+                f"{'disjoint' if V == 512 else 'overlapping'} views, three launches on the tile-program family")
+
+    def cpu(self, budget_s):
+        """Oracle on a bounded sample: batch 0, seq rows 0-63 (8 seq tiles: groups of tasks that
+        touch no other rows), against the same rows of the GPU result."""
+        import numpy as np
+
+        from oracle.runner import run_workload
+
+        del budget_s
+        self.before_step()
+        self.prog.execute()
+        self.prog.synchronize()
+        B, S, V = self.shape
+        lg = self.lg[:1, :64].cpu().numpy().copy()
+        pr = np.zeros_like(lg)
+        rmax = np.full((1, 8, 8, 1), -np.inf, np.float32)
+        rsum = np.zeros((1, 8, 8, 1), np.float32)
+        t0 = time.perf_counter()
+        run_workload(softmax3_workload(lg, pr, rmax, rsum))
+        sec = time.perf_counter() - t0
+        got = self.pr[:1, :64].cpu().numpy()
+        same = bool(np.allclose(got, pr, rtol=1e-5, atol=1e-9))
+        nbytes = self.work * 64 / (B * S)
+        return nbytes / sec / 1e9, f"batch 0, seq rows 0-63 of [{B},{S},{V}], one oracle run", same
+
+
 class DecodeCase:
     unit, bound, dtype = "GB/s", "hbm", "bf16"
 
@@ -382,7 +504,14 @@ CASES = {
     # out) through the same backend, used to calibrate rocprofv3 traffic
     # counters and as the achievable-bandwidth reference.
     "copy_calib": lambda: RowCase("copy_calib", "copy", (16, 8192, 16, 128), 1.0, 0, None),
+    # Not BASELINE configs: the reference's three-phase softmax example on the
+    # tile-program family, with disjoint views (V = 512) and with overlapping
+    # views (V = 256), whose rescale launch runs as groups of tasks in program
+    # order (PTOWSP_SERIAL_GROUPS=0: the whole launch in one workgroup).
+    "softmax3": lambda: Softmax3Case("softmax3", (8, 4096, 512), 0),
+    "softmax3_overlap": lambda: Softmax3Case("softmax3_overlap", (8, 4096, 256), 0),
 }
+EXTRA = ("copy_calib", "softmax3", "softmax3_overlap")
 
 
 def load_traffic(name):
@@ -456,7 +585,7 @@ def main():
     dev = torch.device("cuda:0")
 
     if args.config == "all":
-        names = [n for n in CASES if n != "copy_calib"]
+        names = [n for n in CASES if n not in EXTRA]
     else:
         names = [args.config]
     head = HEADLINE if HEADLINE in names else names[0]
@@ -472,7 +601,9 @@ def main():
                  "achieved": round(achieved, 2), "unit": case.unit, "peak": case.peak(),
                  "frac": round(achieved / case.peak(), 4), "warmup": case.warmup_done, "steps": args.steps,
                  "tasks": case.prog.stats.task_count,
-                 "total_cycles": case.prog.stats.total_cycles}
+                 "total_cycles": case.prog.stats.total_cycles,
+                 "kernel_us": round(k_ms * 1e3, 2), "step_us": round(ms_step * 1e3, 2),
+                 "tasks_per_s": round(case.prog.stats.task_count / (ms_step * 1e-3), 1)}
         if not args.no_cpu and name != "rmsnorm_quickstart":
             rate, sample, same = case.cpu(12.0 if name == head else 6.0)
             entry["cpu_sim_port"] = round(rate, 6)

@@ -112,7 +112,9 @@ int ptowsp_hip_kernel_family(const ptowsp_program* prog, const char* kernel);
  * touching a GPU (hiprtc only); returns the source of launch `index` through
  * `source`, valid until the next call.  flags bit 0: build the variant that
  * runs all tasks of a launch in program order (used when grid tasks write
- * overlapping memory); bit 1: build GEMM launches with 2x2 neighbouring tasks
+ * overlapping memory), with bits 8-15 the grid variables (bit 8 + v) looped in
+ * program order inside each workgroup while the others are decoded from the
+ * group index (0: all of them, one workgroup); bit 1: build GEMM launches with 2x2 neighbouring tasks
  * of the last two grid loops merged into one workgroup block; bit 2 (with bit
  * 1): build merged 128x128 tasks with K step 32 or 64 as the two-group
  * ping-pong GEMM block. */

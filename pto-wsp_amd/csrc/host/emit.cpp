@@ -349,19 +349,35 @@ EmittedKernel emit_tile(const Module& m, const KernelAnalysis& a, const LaunchSp
     }
     emit_scalars(o, a, true);
     o << "  i64 vars[" << (nvars > 0 ? nvars : 1) << "];\n  (void)vars;\n";
-    // Grid loops are decoded from the task index, or, for a serial launch,
-    // iterated in program order by a single workgroup.
-    // A serial task-list launch decodes each listed task in one workgroup, in
-    // list (program) order.
+    // Grid loops are decoded from the task index.  A serial launch without a
+    // task list runs one group of tasks per workgroup: the grid variables
+    // outside seq_mask are decoded from the group index, those inside are
+    // looped in program order.  A serial task-list launch decodes each listed
+    // task in one workgroup, in list (program) order.
     const bool grid_loops = spec.serial && !spec.task_list;
-    const int decoded = grid_loops ? 0 : ng;
-    const int looped = nvars - decoded;
-    if (grid_loops) o << "  for (i64 t = blockIdx.x; t < 1; t += gridDim.x) {\n";
-    else o << "  for (i64 t = blockIdx.x; t < A.ntasks; t += gridDim.x) {\n";
-    emit_decode(o, "    ", decoded, spec.task_list ? "A.tlist[t]" : "t");
+    const uint32_t all_grid = ng >= 32 ? 0xFFFFFFFFu : ((1u << ng) - 1u);
+    const uint32_t seq = grid_loops ? (spec.seq_mask ? spec.seq_mask : all_grid) : 0u;
+    std::vector<int> par, loops;
+    for (int v = 0; v < ng; ++v) (((seq >> v) & 1u) ? loops : par).push_back(v);
+    for (int v = ng; v < nvars; ++v) loops.push_back(v);
+    const int looped = static_cast<int>(loops.size());
+    if (grid_loops) {
+        o << "  i64 ngroups_ = 1;\n";
+        for (int v : par) o << "  ngroups_ *= A.ext[" << v << "];\n";
+        o << "  for (i64 t = blockIdx.x; t < ngroups_; t += gridDim.x) {\n";
+        if (!par.empty()) {
+            o << "    { i64 q_ = t;\n";
+            for (size_t i = par.size() - 1; i >= 1; --i)
+                o << "      vars[" << par[i] << "] = q_ % A.ext[" << par[i] << "]; q_ /= A.ext[" << par[i] << "];\n";
+            o << "      vars[" << par[0] << "] = q_; }\n";
+        }
+    } else {
+        o << "  for (i64 t = blockIdx.x; t < A.ntasks; t += gridDim.x) {\n";
+        emit_decode(o, "    ", ng, spec.task_list ? "A.tlist[t]" : "t");
+    }
     std::string ind = "    ";
     for (int i = 0; i < looped; ++i) {
-        const int v = decoded + i;
+        const int v = loops[i];
         const int inner_i = v - ng;
         const int term = inner_i >= 0 && spec.inner_dyn_term.size() > static_cast<size_t>(inner_i) ? spec.inner_dyn_term[inner_i] : -1;
         if (term >= 0) o << ind << "const i64 e" << i << " = indirect_index(A, " << term << ", vars, " << v << ");\n";

@@ -19,6 +19,10 @@ struct EmitSpec {
     // when tasks of the grid write overlapping memory (the result then
     // depends on the reference's sequential order).
     bool serial = false;
+    // Serial launches: the grid variables (bit v) iterated in program order
+    // inside a workgroup; the others are decoded from the block index, one
+    // group of tasks per workgroup.  0 means all of them.
+    uint32_t seq_mask = 0;
     // The launch runs the grid tasks listed in A.tlist (ascending), not all
     // of them: a task mask from a cond on grid variables.
     bool task_list = false;

@@ -465,6 +465,7 @@ struct Tuning {
     int decode_ring = 4;
     int decode_waves = 4;
     bool decode_ordered = false;
+    bool serial_groups = true;  // overlapping grids run as parallel groups of in-order tasks
 };
 
 const Tuning& tuning() {
@@ -476,24 +477,37 @@ const Tuning& tuning() {
         if (const char* s = std::getenv("PTOWSP_DECODE_RING")) v.decode_ring = std::min(8, std::max(2, std::atoi(s)));
         if (const char* s = std::getenv("PTOWSP_DECODE_WAVES")) v.decode_waves = std::atoi(s) == 8 ? 8 : 4;
         if (const char* s = std::getenv("PTOWSP_DECODE_ORDERED")) v.decode_ordered = std::atoi(s) != 0;
+        if (const char* s = std::getenv("PTOWSP_SERIAL_GROUPS")) v.serial_groups = std::atoi(s) != 0;
         return v;
     }();
     return t;
 }
 
-// True when two different tasks of the grid may touch the same element of a
-// tensor that the launch writes.  P() promises independent iterations; a
-// workload that breaks the promise (overlapping output views) still gets
-// the reference's result, by running the launch in program order.
-bool grid_write_hazard(const KernelAnalysis& a, const LaunchSpec& L, const LaunchArgs& A, const EmitSpec& spec, int ng,
-                       int nvars) {
-    if (A.ntasks <= 1) return false;
+// Grid variables whose tasks must run in program order (bit v for grid
+// variable v; 0: none).  P() promises independent iterations; a workload
+// that breaks the promise (overlapping output views) still gets the
+// reference's result: the launch is split into groups, one workgroup each,
+// that write disjoint memory, and each group runs its tasks in program order.
+// A group is the set of tasks that agree on the grid variables outside the
+// mask.  The mask is the smallest (most groups) that the footprint analysis
+// below proves safe for every written tensor; all grid variables (one
+// group) when the analysis cannot tell.
+uint32_t grid_write_hazard(const KernelAnalysis& a, const LaunchSpec& L, const LaunchArgs& A, const EmitSpec& spec, int ng,
+                           int nvars) {
+    const uint32_t all = ng >= 32 ? 0xFFFFFFFFu : ((1u << ng) - 1u);
+    if (A.ntasks <= 1) return 0;
     const KernelDef& k = *a.def;
     const size_t np = a.tensor_param_index.size();
+    // Per written tensor: the dims that move one task's footprint (tile rows /
+    // cols, in-kernel loops) and the grid dims, as (|stride|, extent).
+    struct Written {
+        std::vector<std::pair<int64_t, int64_t>> tile_dims, grid_dims;
+    };
+    std::vector<Written> ws;
     for (size_t p = 0; p < np; ++p) {
         if (!a.stored[p]) continue;
         const int tid = L.targs[p]->tid;
-        if (spec.indirect_count[p] > 0) return true;
+        if (spec.indirect_count[p] > 0) return all;
         const ValueInfo* vp = a.by_id[k.params[a.tensor_param_index[p]].id];
         // Every other access to the written tensor must be the very same view.
         for (size_t q = 0; q < np; ++q) {
@@ -501,44 +515,65 @@ bool grid_write_hazard(const KernelAnalysis& a, const LaunchSpec& L, const Launc
             const ValueInfo* vq = a.by_id[k.params[a.tensor_param_index[q]].id];
             if (spec.indirect_count[q] > 0 || A.base[q] != A.base[p] || A.s3[q] != A.s3[p] || A.s4[q] != A.s4[p] ||
                 vq->rows != vp->rows || vq->cols != vp->cols)
-                return true;
+                return all;
             for (int v = 0; v < nvars; ++v)
-                if (A.coef[q][v] != A.coef[p][v]) return true;
+                if (A.coef[q][v] != A.coef[p][v]) return all;
         }
-        // (stride, extent) of every index that moves the written element:
-        // tile rows/cols, in-kernel loops, grid loops.
-        std::vector<std::pair<int64_t, int64_t>> tile_dims, grid_dims;
-        tile_dims.emplace_back(std::llabs(A.s3[p]), vp->rows);
-        tile_dims.emplace_back(std::llabs(A.s4[p]), vp->cols);
+        Written w;
+        w.tile_dims.emplace_back(std::llabs(A.s3[p]), vp->rows);
+        w.tile_dims.emplace_back(std::llabs(A.s4[p]), vp->cols);
         for (size_t i = 0; i < L.inner.size(); ++i) {
             const int v = ng + static_cast<int>(i);
             if (A.coef[p][v] == 0) continue;
-            if (spec.inner_dyn_term[i] >= 0) return true;
-            tile_dims.emplace_back(std::llabs(A.coef[p][v]), A.ext[v]);
+            if (spec.inner_dyn_term[i] >= 0) return all;
+            w.tile_dims.emplace_back(std::llabs(A.coef[p][v]), A.ext[v]);
         }
-        for (int v = 0; v < ng; ++v) grid_dims.emplace_back(std::llabs(A.coef[p][v]), A.ext[v]);
-        // Sufficient condition 1: every index nests like the strides of an
-        // array, so the whole map (grid x task) is injective.
-        auto nests = [](std::vector<std::pair<int64_t, int64_t>> dims, int64_t start) {
-            std::sort(dims.begin(), dims.end());
-            int64_t span = start;
-            for (const auto& [c, e] : dims) {
-                if (e <= 1) continue;
-                if (c < span) return false;
-                span += c * (e - 1);
-            }
-            return true;
-        };
-        std::vector<std::pair<int64_t, int64_t>> all = tile_dims;
-        all.insert(all.end(), grid_dims.begin(), grid_dims.end());
-        if (nests(all, 1)) continue;
-        // Sufficient condition 2: one task's footprint fits in an interval and
-        // the grid steps over whole intervals.
-        int64_t width = 1;
-        for (const auto& [c, e] : tile_dims) width += c * std::max<int64_t>(0, e - 1);
-        if (!nests(grid_dims, width)) return true;
+        for (int v = 0; v < ng; ++v) w.grid_dims.emplace_back(std::llabs(A.coef[p][v]), A.ext[v]);
+        ws.push_back(std::move(w));
     }
-    return false;
+    // True when (stride, extent) dims with offsets from `start` never revisit
+    // an element: every index nests like the strides of an array.
+    auto nests = [](std::vector<std::pair<int64_t, int64_t>> dims, int64_t start) {
+        std::sort(dims.begin(), dims.end());
+        int64_t span = start;
+        for (const auto& [c, e] : dims) {
+            if (e <= 1) continue;
+            if (c < span) return false;
+            span += c * (e - 1);
+        }
+        return true;
+    };
+    // Groups of mask m write disjoint memory when, for every written tensor,
+    // either the whole map (grid x task) is injective or one group's
+    // footprint fits in an interval and the other grid dims step over whole
+    // intervals.
+    auto safe = [&](uint32_t m) {
+        for (const Written& w : ws) {
+            std::vector<std::pair<int64_t, int64_t>> inside = w.tile_dims, across;
+            for (int v = 0; v < ng; ++v) (((m >> v) & 1u) ? inside : across).push_back(w.grid_dims[v]);
+            std::vector<std::pair<int64_t, int64_t>> every = inside;
+            every.insert(every.end(), across.begin(), across.end());
+            if (m == 0 && nests(every, 1)) continue;
+            int64_t width = 1;
+            for (const auto& [c, e] : inside) width += c * std::max<int64_t>(0, e - 1);
+            if (!nests(across, width)) return false;
+        }
+        return true;
+    };
+    if (safe(0)) return 0;
+    if (ng > 16) return all;
+    uint32_t best = all;
+    int64_t best_groups = 1;
+    for (uint32_t m = 1; m < all; ++m) {
+        int64_t groups = 1;
+        for (int v = 0; v < ng; ++v)
+            if (!((m >> v) & 1u)) groups *= std::max<int64_t>(1, A.ext[v]);
+        if (groups > best_groups && safe(m)) {
+            best = m;
+            best_groups = groups;
+        }
+    }
+    return best;
 }
 
 // The MFMA GEMM template needs unit column strides, 16-byte aligned operand
@@ -878,7 +913,9 @@ BuiltLaunch build_launch(RunEnv& E, const LaunchSpec& L) {
         }
     }
     A.err = E.err ? E.err : P->d_err;
-    B.spec.serial = grid_write_hazard(a, L, A, B.spec, ng, nvars);
+    B.spec.seq_mask = grid_write_hazard(a, L, A, B.spec, ng, nvars);
+    B.spec.serial = B.spec.seq_mask != 0;
+    if (B.spec.serial && !tuning().serial_groups) B.spec.seq_mask = 0;  // 0: every grid variable, one workgroup
     B.spec.row_up = tuning().row_up;
     B.spec.nontemporal = tuning().nontemporal;
     B.spec.gemm = gemm_allowed(a, L, A, B.spec, ng, nvars);
@@ -901,7 +938,7 @@ BuiltLaunch build_launch(RunEnv& E, const LaunchSpec& L) {
 
 std::string spec_key(const EmitSpec& s) {
     std::ostringstream o;
-    o << "vw" << s.vec_width << (s.serial ? ";serial" : "") << (s.task_list ? ";tl" : "") << ";up" << s.row_up << (s.nontemporal ? ";nt" : "")
+    o << "vw" << s.vec_width << (s.serial ? ";serial" + std::to_string(s.seq_mask) : "") << (s.task_list ? ";tl" : "") << ";up" << s.row_up << (s.nontemporal ? ";nt" : "")
       << (s.gemm ? ";gemm" : "") << ";m" << s.gemm_vm << ";n" << s.gemm_vn << (s.gemm_pingpong ? ";pp" : "")
       << (s.decode ? ";dec" : "")
       << (s.decode_norm ? ";norm" : "") << ";r" << s.decode_ring << ";w" << s.decode_waves << (s.decode_ordered ? ";ord" : "")
@@ -1052,8 +1089,16 @@ void enqueue_built(RunEnv& E, int li, BuiltLaunch& B, hipStream_t stream, uint64
         const int64_t rows = B.ntasks * a.rows;
         const int64_t chunks = (rows + ek.rows_per_chunk - 1) / ek.rows_per_chunk;
         blocks = (chunks + ek.waves_per_block - 1) / ek.waves_per_block;
+    } else if (B.spec.serial) {
+        // One workgroup per group of tasks (the grid variables outside the
+        // mask); a task list runs in one workgroup.
+        blocks = 1;
+        const uint32_t seq = B.spec.seq_mask ? B.spec.seq_mask : 0xFFFFFFFFu;  // 0: every grid variable
+        if (!B.spec.task_list)
+            for (size_t v = 0; v < L.grid.size(); ++v)
+                if (!((seq >> v) & 1u)) blocks *= std::max<int64_t>(1, B.args.ext[v]);
     } else {
-        blocks = B.spec.serial ? 1 : B.ntasks / ek.tasks_per_block;
+        blocks = B.ntasks / ek.tasks_per_block;
     }
     if (B.spec.gemm && !B.spec.serial) {
         // GEMM kernels run exactly one block per workgroup.
@@ -1586,6 +1631,7 @@ int ptowsp_hip_precompile(ptowsp_program* P, int index, int flags, const char** 
             const KernelAnalysis& a = P->ka[L.kernel];
             EmitSpec spec;
             spec.serial = (flags & 1) != 0;
+            spec.seq_mask = spec.serial ? static_cast<uint32_t>((flags >> 8) & 0xFF) : 0u;
             spec.row_up = tuning().row_up;
             spec.nontemporal = tuning().nontemporal;
             spec.gemm = a.family == Family::Gemm && !spec.serial;

@@ -98,7 +98,21 @@ def test_serial_variants_build_for_gfx950(name):
     make, _ = _cases()[name]
     prog = NativeProgram(workload_to_codegen_ir(make(), name).module)
     src = prog.precompile(0, serial=True)
-    assert "t < 1;" in src
+    # one workgroup: no grid variable is decoded from the group index
+    assert "t < ngroups_;" in src and "ngroups_ *=" not in src
+
+
+def test_grouped_serial_variant_builds_for_gfx950():
+    """The rescale launch of the three-phase softmax with v (grid variable 2) looped in program
+    order inside each workgroup and (b, s) decoded from the group index."""
+    from pto_wsp._hip import NativeProgram
+
+    make, _ = _cases()["softmax3"]
+    prog = NativeProgram(workload_to_codegen_ir(make(), "softmax3").module)
+    src = prog.precompile(2, serial=True, seq_mask=0b100)
+    assert "ngroups_ *= A.ext[0];" in src and "ngroups_ *= A.ext[1];" in src and "ngroups_ *= A.ext[2]" not in src
+    assert "vars[1] = q_ % A.ext[1]" in src and "vars[0] = q_;" in src
+    assert "for (vars[2] = 0; vars[2] < e0; ++vars[2])" in src
 
 
 @pytest.mark.parametrize("name", list(_cases()))

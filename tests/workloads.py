@@ -1045,3 +1045,44 @@ def ptoisa_unary(arrs: dict):
             unary[b](x_t=X[b], out=O[b])
 
     return wl()
+
+
+# ---------------------------------------------------------------- overlapping output views
+def conflict_accumulate(arrs: dict, shared_all: bool = False):
+    """out[b][v] += x[b][s][v] over P(b) x P(s) x P(v) (X[B, S, V, R, C], O[B, V, R, C]):
+    tasks that differ only in s write the same out tile, so the result depends on the
+    program order; the launch runs the groups (b, v) in parallel, s in order within
+    each.  shared_all: every task writes out[0][0] (one group)."""
+    x = arrs["x"]
+    B, S, V, R, C = x.shape
+    X, O = T(x), T(arrs["out"])
+
+    @kernel
+    def acc_tile(x_t: In[Tile[R, C, F32]], o_t: InOut[Tile[R, C, F32]]):
+        pto.store(o_t, pto.add(o_t, x_t))
+
+    @workload
+    def wl():
+        for b in P(Dense[B]()):
+            for s in P(Dense[S]()):
+                for v in P(Dense[V]()):
+                    if shared_all:
+                        acc_tile[b, s, v](x_t=X[b][s][v], o_t=O[0][0])
+                    else:
+                        acc_tile[b, s, v](x_t=X[b][s][v], o_t=O[b][v])
+
+    return wl()
+
+
+def conflict_accumulate_ref(x: np.ndarray, out: np.ndarray, shared_all: bool = False) -> np.ndarray:
+    """The same sums in program order, one float32 add at a time."""
+    r = out.copy()
+    B, S, V = x.shape[:3]
+    for b in range(B):
+        for s in range(S):
+            for v in range(V):
+                if shared_all:
+                    r[0, 0] = r[0, 0] + x[b, s, v]
+                else:
+                    r[b, v] = r[b, v] + x[b, s, v]
+    return r
