@@ -71,9 +71,11 @@ static int is_float_dt(int dt) { return dt == DT_F16 || dt == DT_BF16 || dt == D
 typedef struct { int dtype, rank; int64_t shape[8]; } TensorInfo;
 typedef struct { int id, dtype, tile, rows, cols; } Val;
 typedef struct { char* name; int id; } Param;
+struct SX;
 typedef struct {
     int kind; int result; int nopnd; int* opnd; int has_value; double value;
     int has_k, has_cols, has_cycles; int64_t k, cols, cycles; /* integer attrs */
+    struct SX* cycles_expr; /* CpuSimAddCycles: cycles as an expression of the kernel's scalars */
 } Op;
 
 enum { OP_LOAD, OP_STORE, OP_ADD, OP_SUB, OP_MUL, OP_DIV, OP_MAX, OP_MIN, OP_EXP, OP_RSQRT,
@@ -111,7 +113,8 @@ typedef struct { char kind; char* var; uint64_t u64; } Arg; /* v c s */
 /* Scalar expression (the reference's ScalarExpr, include/pto/wsp/ir/ as
  * emitted by src/python/pto_codegen.cpp:220-300). ty: 'b' bool, 'i' int64_t,
  * 'u' uint64_t. kind: L literal, P task param, G task tag, A axis var,
- * Y symbol, S slot, U unary, B binary, T ternary, C cast. */
+ * Y symbol, S slot, U unary, B binary, T ternary, C cast, K kernel scalar
+ * parameter (cycle expressions of PTO-ISA kernels). */
 typedef struct SX {
     char kind, ty;
     uint64_t u;
@@ -251,6 +254,15 @@ static int op_kind(const char* s) {
     return OP_OTHER;
 }
 
+static SX* parse_sx(Lex* L);
+
+/* True when the expression reads nothing but literals and kernel scalars. */
+static int sx_kernel_only(const SX* e) {
+    if (!e) return 1;
+    if (e->kind == 'P' || e->kind == 'G' || e->kind == 'A' || e->kind == 'Y' || e->kind == 'S') return 0;
+    return sx_kernel_only(e->a) && sx_kernel_only(e->b) && sx_kernel_only(e->c);
+}
+
 static void parse_attr_skip(Lex* L, Op* op) {
     char* key = tok_str(L);
     char* ty = tok(L);
@@ -266,7 +278,18 @@ static void parse_attr_skip(Lex* L, Op* op) {
         }
         case 'd': { double v = tok_f64(L); if (is_value) { op->has_value = 1; op->value = v; } break; }
         case 'b': { int64_t v = tok_i64(L); if (is_value) { op->has_value = 1; op->value = (double)v; } break; }
-        case 's': (void)tok_str(L); break;
+        case 's': {
+            char* v = tok_str(L);
+            if (strcmp(key, "cycles_expr") == 0) {
+                Lex sub = {v};
+                op->cycles_expr = parse_sx(&sub);
+                while (*sub.p == ' ') sub.p++;
+                if (*sub.p) fail("module text: trailing tokens in a cycles expression");
+                if (!sx_kernel_only(op->cycles_expr))
+                    fail("a cycles expression may read only the kernel's scalar parameters");
+            }
+            break;
+        }
         case 'I': { int64_t n = tok_i64(L); for (int64_t i = 0; i < n; ++i) (void)tok_i64(L); break; }
         case 'S': { int64_t n = tok_i64(L); for (int64_t i = 0; i < n; ++i) (void)tok_str(L); break; }
         default: fail("module text: bad attr type '%s'", ty);
@@ -377,7 +400,8 @@ static SX* parse_sx(Lex* L) {
         e->ty = k[1] == 'b' ? 'b' : k[1] == 'i' ? 'i' : 'u';
         e->u = e->ty == 'i' ? (uint64_t)tok_i64(L) : tok_u64(L);
         if (e->ty == 'b') e->u = e->u != 0;
-    } else if (strcmp(k, "P") == 0 || strcmp(k, "S") == 0 || strcmp(k, "A") == 0 || strcmp(k, "C") == 0) {
+    } else if (strcmp(k, "P") == 0 || strcmp(k, "S") == 0 || strcmp(k, "A") == 0 || strcmp(k, "C") == 0 ||
+               strcmp(k, "K") == 0) {
         e->kind = k[0];
         char* t = tok(L);
         if (strcmp(t, "b") != 0 && strcmp(t, "i") != 0 && strcmp(t, "u") != 0) fail("scalar expression: bad type '%s'", t);
@@ -915,6 +939,8 @@ static void tsort32_pairs(float* dst, const float* sc, const int64_t* ix) {
     }
 }
 
+static uint64_t cycles_expr_value(const SX* e, const uint64_t* kscal, int nk);
+
 /* Executes one task; returns its cpu_sim cycle count. */
 static uint64_t run_kernel(Kernel* k, Work* w, View* views, const uint64_t* scalar_args) {
     uint64_t cycles = 0;
@@ -1193,6 +1219,13 @@ static uint64_t run_kernel(Kernel* k, Work* w, View* views, const uint64_t* scal
                 break;
             }
             case OP_ADD_CYCLES: /* pto::cpu_sim::add_cycles(n) (ptoisa_jit.py:458-463) */
+                if (op->cycles_expr) {
+                    int nscal = 0;
+                    for (int i = 0; i < k->nparams; ++i)
+                        if (!k->by_id[k->params[i].id]->tile) ++nscal;
+                    cycles += cycles_expr_value(op->cycles_expr, scalar_args, nscal);
+                    break;
+                }
                 if (!op->has_cycles || op->cycles < 0) fail("kernel %s: CpuSimAddCycles needs a cycles attr", kn);
                 cycles += (uint64_t)op->cycles;
                 break;
@@ -1262,7 +1295,7 @@ static int sx_is_cmp(const char* op) {
 
 static char sx_type(const SX* e) {
     switch (e->kind) {
-        case 'L': case 'P': case 'A': case 'S': case 'C': return e->ty;
+        case 'L': case 'P': case 'A': case 'S': case 'C': case 'K': return e->ty;
         case 'G': case 'Y': return 'u';
         case 'U': return e->op[0] == '!' ? 'b' : sx_promo(sx_type(e->a));
         case 'B':
@@ -1282,6 +1315,10 @@ static SV sx_read(uint64_t raw, char ty) {
     return r;
 }
 
+/* The scalar arguments of the task whose cycle expressions are evaluated. */
+static const uint64_t* g_kscal = NULL;
+static int g_nkscal = 0;
+
 static SV sx_eval(Run* R, const SX* e, const uint64_t* args, int nargs) {
     SV r = {'i', 0};
     switch (e->kind) {
@@ -1289,6 +1326,9 @@ static SV sx_eval(Run* R, const SX* e, const uint64_t* args, int nargs) {
         case 'P':
             if (!args) fail("emit_scalar_expr_cpp: task_param() requires task_param_expr callback");
             return sx_read(e->u < (uint64_t)nargs ? args[e->u] : 0, e->ty);
+        case 'K':
+            if (!g_kscal) fail("kernel scalar parameter read outside a task");
+            return sx_read(e->u < (uint64_t)g_nkscal ? g_kscal[e->u] : 0, e->ty);
         case 'G':
         case 'Y': r.t = 'u'; r.v = R->ctx->get_symbol_u64(R->ctx->ctx, e->u); return r;
         case 'S':
@@ -1382,6 +1422,17 @@ static SV sx_eval(Run* R, const SX* e, const uint64_t* args, int nargs) {
     }
     fail("scalar expression: bad node");
     return r;
+}
+
+/* (uint64_t)(e) with the task's kernel scalar arguments (the expression reads
+ * nothing else, checked when it is parsed). */
+static uint64_t cycles_expr_value(const SX* e, const uint64_t* kscal, int nk) {
+    g_kscal = kscal;
+    g_nkscal = nk;
+    SV v = sx_eval(NULL, e, NULL, 0);
+    g_kscal = NULL;
+    g_nkscal = 0;
+    return v.v;
 }
 
 /* `(uint64_t)element` of a slot load (src/python/pto_codegen.cpp:2254-2303). */

@@ -8,6 +8,7 @@
 // (src/python/pto_codegen.cpp:2507-2545).
 #include "analysis.hpp"
 
+#include <functional>
 #include <map>
 #include <set>
 
@@ -639,10 +640,28 @@ KernelAnalysis analyze_kernel(const KernelDef& k) {
                 break;
             }
             case OpKind::CpuSimAddCycles: {
-                // pto::cpu_sim::add_cycles(n) in the kernel body (ptoisa_jit.py:206-208, 458-463).
+                // pto::cpu_sim::add_cycles(n) in the kernel body (ptoisa_jit.py:206-208, 458-463):
+                // an integer, or an expression of the kernel's scalar parameters.
+                if (!op.operands.empty() || res) refuse(k, "CpuSimAddCycles takes no operands");
+                if (op.cycles_expr) {
+                    SRefs refs;
+                    scalar_refs(*op.cycles_expr, refs);
+                    if (!refs.axes.empty() || refs.slots || refs.task_params || refs.symbols)
+                        refuse(k, "a cycles expression may read only the kernel's scalar parameters");
+                    std::function<void(const SExpr&)> check = [&](const SExpr& e) {
+                        if (e.kind == SExpr::Kind::KernelScalar && static_cast<int>(e.u) >= ns)
+                            refuse(k, "a cycles expression reads scalar parameter " + std::to_string(e.u) + " of " +
+                                          std::to_string(ns));
+                        for (const SExpr* c : {e.a.get(), e.b.get(), e.c.get()})
+                            if (c) check(*c);
+                    };
+                    check(*op.cycles_expr);
+                    a.cycle_exprs.push_back(op.cycles_expr);
+                    break;
+                }
                 auto it = op.ints.find("cycles");
-                if (!op.operands.empty() || res || it == op.ints.end() || it->second < 0)
-                    refuse(k, "CpuSimAddCycles expects a non-negative integer 'cycles' attr");
+                if (it == op.ints.end() || it->second < 0)
+                    refuse(k, "CpuSimAddCycles expects a non-negative integer 'cycles' attr or a cycles expression");
                 cycles += static_cast<uint64_t>(it->second);
                 break;
             }

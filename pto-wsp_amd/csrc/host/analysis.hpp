@@ -4,6 +4,7 @@
 #pragma once
 
 #include <cstdint>
+#include <memory>
 #include <string>
 #include <vector>
 
@@ -67,6 +68,10 @@ struct KernelAnalysis {
     std::vector<bool> read;                // tensor ordinal: read (preload, Load, Matmul operand)
     std::vector<BinMode> bin_mode;         // per op (binary ops only)
     uint64_t cycles = 0;                   // cpu_sim cycles of one task
+    // Cycles added per task by expressions of the kernel's scalar parameters
+    // (cpu_sim_add_cycles with an expression), evaluated with each task's
+    // scalar arguments.
+    std::vector<std::shared_ptr<const SExpr>> cycle_exprs;
 
     Family family = Family::TileProgram;
     // Row-program shape: every Full value is [rows, cols].

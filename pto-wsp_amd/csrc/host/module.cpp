@@ -116,7 +116,19 @@ void parse_attr(Lexer& L, OpInfo& op) {
         double v = L.f64();
         if (is_value) { op.has_value = true; op.value = v; }
     } else if (ty == "s") {
-        (void)L.str();
+        const std::string v = L.str();
+        if (key == "cycles_expr") {
+            // A scalar expression in the prefix token form, as one string.
+            size_t pos = 0;
+            auto next = [&]() -> std::string {
+                while (pos < v.size() && v[pos] == ' ') ++pos;
+                const size_t b = pos;
+                while (pos < v.size() && v[pos] != ' ') ++pos;
+                return v.substr(b, pos - b);
+            };
+            op.cycles_expr = std::shared_ptr<const SExpr>(parse_scalar(next));
+            if (!next().empty()) throw CompileError("module text: trailing tokens in a cycles expression");
+        }
     } else if (ty == "I") {
         int64_t n = L.i64();
         for (int64_t i = 0; i < n; ++i) (void)L.i64();

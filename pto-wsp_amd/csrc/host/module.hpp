@@ -66,6 +66,7 @@ struct OpInfo {
     bool has_value = false;
     double value = 0.0;
     std::map<std::string, int64_t> ints;  // integer attrs (cols, k, cycles)
+    std::shared_ptr<const SExpr> cycles_expr;  // CpuSimAddCycles: cycles as an expression of the kernel's scalars
 };
 
 struct KernelDef {

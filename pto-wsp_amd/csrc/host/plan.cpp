@@ -342,10 +342,19 @@ struct Walker {
             case NodeKind::Task: {
                 ++tasks;
                 const uint32_t w = worker_of(n);
-                uint64_t dur = ka[n->kernel_index].cycles;
-                if (ka[n->kernel_index].family == Family::Custom) {
+                const KernelAnalysis& kn = ka[n->kernel_index];
+                uint64_t dur = kn.cycles;
+                if (kn.family == Family::Custom) {
                     if (!env.custom_cycles) throw std::runtime_error("the cycles of a cpp_src kernel are known only after it runs");
                     dur = env.custom_cycles(*n, vars);
+                }
+                if (!kn.cycle_exprs.empty()) {
+                    // add_cycles((uint64_t)(expr)) with the task's scalar arguments.
+                    SEnv e = senv();
+                    e.kernel_scalar = [&](uint32_t i) -> uint64_t {
+                        return i < n->scalar_args.size() ? arg_value(n->scalar_args[i]) : 0;
+                    };
+                    for (const auto& x : kn.cycle_exprs) dur += eval_u64(*x, e);
                 }
                 return s.issue(dur, w, ready);
             }
@@ -396,8 +405,11 @@ bool any_node(const Node* n, const std::function<bool(const Node*)>& f) {
 
 bool module_is_dynamic(const Module& m) {
     if (m.schedule.dispatch_key) return true;
-    for (const auto& k : m.kernels)
+    for (const auto& k : m.kernels) {
         if (k.custom) return true;
+        for (const auto& op : k.ops)
+            if (op.cycles_expr) return true;  // per-task cycles read the scalar arguments
+    }
     return any_node(m.root.get(), [](const Node* n) {
         return n->kind == NodeKind::Cond || n->kind == NodeKind::SlotSet || n->kind == NodeKind::SlotLoad;
     });

@@ -38,6 +38,7 @@ SType static_type(const SExpr& e) {
         case K::TaskTag:
         case K::Symbol: return SType::U64;
         case K::TaskParam:
+        case K::KernelScalar:
         case K::AxisVar:
         case K::Slot:
         case K::Cast: return e.type;
@@ -123,6 +124,10 @@ SValue eval_scalar(const SExpr& e, const SEnv& env) {
             if (!env.task_param) fail("task_param() outside a task");
             return typed_read(env.task_param(static_cast<uint32_t>(e.u)), e.type);
         }
+        case K::KernelScalar: {
+            if (!env.kernel_scalar) fail("kernel scalar parameter read outside a task");
+            return typed_read(env.kernel_scalar(static_cast<uint32_t>(e.u)), e.type);
+        }
         case K::TaskTag: return {SType::U64, env.symbol(e.u)};
         case K::AxisVar: {
             int64_t v = 0;
@@ -160,6 +165,7 @@ void scalar_refs(const SExpr& e, SRefs& out) {
     if (e.kind == K::AxisVar) out.axes.push_back(e.u);
     if (e.kind == K::Slot) out.slots = true;
     if (e.kind == K::TaskParam) out.task_params = true;
+    if (e.kind == K::KernelScalar) out.kernel_scalars = true;
     if (e.kind == K::Symbol || e.kind == K::TaskTag) out.symbols = true;
     for (const SExpr* k : {e.a.get(), e.b.get(), e.c.get()})
         if (k) scalar_refs(*k, out);
@@ -198,8 +204,8 @@ std::unique_ptr<SExpr> parse_scalar(const std::function<std::string()>& next) {
         e->kind = K::LitU64;
         e->type = SType::U64;
         e->u = num_u("u64 literal");
-    } else if (k == "P" || k == "S") {
-        e->kind = k == "P" ? K::TaskParam : K::Slot;
+    } else if (k == "P" || k == "S" || k == "K") {
+        e->kind = k == "P" ? K::TaskParam : k == "S" ? K::Slot : K::KernelScalar;
         e->type = type();
         e->u = num_u("index");
     } else if (k == "A") {

@@ -22,7 +22,9 @@ namespace ptowsp {
 enum class SType { Bool, I64, U64 };
 
 struct SExpr {
-    enum class Kind { LitBool, LitI64, LitU64, TaskParam, TaskTag, AxisVar, Symbol, Slot, Unary, Binary, Ternary, Cast };
+    // KernelScalar: the task's value of the kernel's scalar parameter with
+    // that ordinal (cycle expressions of PTO-ISA kernels).
+    enum class Kind { LitBool, LitI64, LitU64, TaskParam, TaskTag, AxisVar, Symbol, Slot, Unary, Binary, Ternary, Cast, KernelScalar };
     Kind kind = Kind::LitI64;
     SType type = SType::I64;   // declared type (reads of params/axes/slots, casts)
     uint64_t u = 0;            // literal bits, id, slot or parameter index
@@ -42,6 +44,7 @@ struct SEnv {
     std::function<uint64_t(uint64_t id)> symbol;
     std::function<uint64_t(uint32_t slot)> slot;
     std::function<uint64_t(uint32_t index)> task_param;
+    std::function<uint64_t(uint32_t ordinal)> kernel_scalar;
 };
 
 SValue eval_scalar(const SExpr& e, const SEnv& env);
@@ -53,7 +56,7 @@ uint64_t eval_u64(const SExpr& e, const SEnv& env);
 // What an expression reads.
 struct SRefs {
     std::vector<uint64_t> axes;
-    bool slots = false, task_params = false, symbols = false;
+    bool slots = false, task_params = false, symbols = false, kernel_scalars = false;
 };
 void scalar_refs(const SExpr& e, SRefs& out);
 

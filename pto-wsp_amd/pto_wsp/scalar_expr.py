@@ -69,6 +69,8 @@ class Expr:
             return repr(self.a)
         if k == "task_param":
             return f"task.params[{self.a}]"
+        if k == "kernel_scalar":
+            return f"scalar[{self.a}]"
         if k == "axis_var":
             return f"axis({self.a:#x})"
         if k == "task_tag_u64":
@@ -199,7 +201,7 @@ class Expr:
 def _emit(e: Expr, out: list[str]) -> None:
     """Token grammar (one token per field, operands in prefix order):
 
-    Lb 0|1 | Li <i64> | Lu <u64> | P <ty> <index> | G <tag id> | A <ty> <axis id> |
+    Lb 0|1 | Li <i64> | Lu <u64> | P <ty> <index> | K <ty> <scalar ordinal> | G <tag id> | A <ty> <axis id> |
     Y <symbol id> | S <ty> <slot> | U <op> <e> | B <op> <e> <e> | T <e> <e> <e> | C <ty> <e>
     with <ty> one of b, i, u.
     """
@@ -215,6 +217,8 @@ def _emit(e: Expr, out: list[str]) -> None:
         out += ["Lu", str(int(e.a) & _MASK)]
     elif k == "task_param":
         out += ["P", _TYPE_CODE[e.type], str(int(e.a))]
+    elif k == "kernel_scalar":
+        out += ["K", _TYPE_CODE[e.type], str(int(e.a))]
     elif k == "task_tag_u64":
         out += ["G", str(int(e.a) & _MASK)]
     elif k == "axis_var":

@@ -89,3 +89,26 @@ def test_ptoisa_exp_rsqrt(gpu):
     x = np.random.default_rng(5).uniform(-4, 4, (3, 8, 64)).astype(np.float32)
     ga, ca, _ = _pair(W.ptoisa_unary, {"x": x, "out": np.zeros_like(x)}, 64)
     np.testing.assert_allclose(ga["out"], ca["out"], rtol=2.4e-7, atol=0)
+
+
+@pytest.mark.parametrize("impl,cycles", [("pto", 800), ("ptoisa", 1319680)])
+def test_lightning_indexer_example(gpu, impl, cycles):
+    """examples/deepseek_lightning_indexer (its seed-0 inputs): golden top-8 indices and the
+    cycles the example records for its pto / ptoisa kernels."""
+    scores, eff = W.lightning_inputs()
+    out = np.zeros((2, 4, 1, 8), np.int32)
+    prog = _hip(W.lightning_indexer(scores, eff, out, impl))
+    np.testing.assert_array_equal(out.reshape(2, 4, 8), W.stable_topk_desc(scores, 8))
+    assert prog.stats.total_cycles == cycles
+
+
+@pytest.mark.parametrize("impl", ["pto", "ptoisa"])
+def test_lightning_indexer_larger(gpu, impl):
+    scores, eff = W.lightning_inputs(seed=3, bsz=8, tiles=64)
+    out = np.zeros((8, 64, 1, 8), np.int32)
+    prog = _hip(W.lightning_indexer(scores, eff, out, impl))
+    ref_out = np.zeros_like(out)
+    ref = run_workload(W.lightning_indexer(scores, eff, ref_out, impl))
+    np.testing.assert_array_equal(out.reshape(8, 64, 8), W.stable_topk_desc(scores, 8))
+    np.testing.assert_array_equal(out, ref_out)
+    assert prog.stats.total_cycles == ref.total_cycles

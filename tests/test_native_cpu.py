@@ -76,6 +76,9 @@ def _cases():
                                               "c": np.zeros((4, 4, 4), np.float32)}), {"b": 3}),
         "paged_decode": (lambda: W.paged_decode(W.paged_decode_arrays([37, 16, 200], 2, 4, 128, seed=1)), {}),
         "paged_decode_p8": (lambda: W.paged_decode(W.paged_decode_arrays([37, 9], 1, 4, 64, page=8, seed=1)), {}),
+        "lightning_pto": (lambda: W.lightning_indexer(*W.lightning_inputs(), np.zeros((2, 4, 1, 8), np.int32), "pto"), {}),
+        "lightning_ptoisa": (lambda: W.lightning_indexer(*W.lightning_inputs(), np.zeros((2, 4, 1, 8), np.int32),
+                                                         "ptoisa"), {}),
     }
 
 

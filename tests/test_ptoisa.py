@@ -158,10 +158,16 @@ def test_tracer_refusals_match_reference_messages():
         def with_includes(a: In[Tile[1, 32, F32]], o: Out[Tile[1, 32, F32]]):
             ptoisa.tstore(o, ptoisa.tload(a))
 
-    with pytest.raises(TypeError, match="integer cycle count"):
+    with pytest.raises(ValueError, match="is not a scalar parameter"):
         @ptoisa_kernel
         def string_cycles(a: In[Tile[1, 32, F32]], o: Out[Tile[1, 32, F32]]):
             ptoisa.cpu_sim_add_cycles("n * 3")
+            ptoisa.tstore(o, ptoisa.tload(a))
+
+    with pytest.raises(TypeError, match="an int, a Scalar parameter or a C expression"):
+        @ptoisa_kernel
+        def float_cycles(a: In[Tile[1, 32, F32]], o: Out[Tile[1, 32, F32]]):
+            ptoisa.cpu_sim_add_cycles(1.5)
             ptoisa.tstore(o, ptoisa.tload(a))
 
     with pytest.raises(ValueError, match="broadcast operand"):
@@ -205,3 +211,37 @@ def test_native_compile_selects_families():
     assert "row program" in mix.precompile(0)
     topk = NativeProgram(workload_to_codegen_ir(W.pto_topk({"scores": sc, "out": oi}), "pto_topk").module)
     assert "tsort32_rank" in topk.precompile(0)
+
+
+# ------------------------------------------------------------------ the reference's PTO-ISA example
+@pytest.mark.parametrize("impl,cycles", [("pto", 800), ("ptoisa", 1319680)])
+def test_lightning_indexer_example(impl, cycles):
+    """examples/deepseek_lightning_indexer: the top-8 indices equal the example's golden
+    (descending score, lower index first) and the cycles equal the values the example records
+    for its "pto" and "ptoisa" kernels (deepseek_lightning_indexer_example.py:41-45).  The
+    ptoisa kernel charges each tier ((pad_to > 32) ? pad_to / 32 * 128 : 0) cycles through
+    cpu_sim_add_cycles of a C expression; by hand, worker 0 (b = 0, tiers 65536, 131072,
+    131072, 2048) runs 4 x (32 + 160) + 262144 + 2 x 524288 + 8192 = 1319680."""
+    scores, eff = W.lightning_inputs()
+    out = np.zeros((2, 4, 1, 8), np.int32)
+    r = run_workload(W.lightning_indexer(scores, eff, out, impl))
+    np.testing.assert_array_equal(out.reshape(2, 4, 8), W.stable_topk_desc(scores, 8))
+    assert r.total_cycles == cycles
+    assert 4 * (32 + 160) + 262144 + 2 * 524288 + 8192 == 1319680
+
+
+def test_cycle_expression_parser():
+    from pto_wsp.ptoisa_jit import parse_c_expr
+    from pto_wsp.scalar_expr import Expr
+
+    env = {"n": Expr("kernel_scalar", "i64", 0), "m": Expr("kernel_scalar", "u64", 1)}
+    e = parse_c_expr("((n > 32) ? ((uint64_t)(n / 32) * 128ull) : 0ull)", env)
+    assert e.to_text() == "T B > K i 0 Li 32 B * C u B / K i 0 Li 32 Lu 128 Lu 0"
+    # precedence: * before +, << below +, && below ==
+    assert parse_c_expr("1 + 2 * n", env).to_text() == "B + Li 1 B * Li 2 K i 0"
+    assert parse_c_expr("m << 1 + 1", env).to_text() == "B << K u 1 B + Li 1 Li 1"
+    assert parse_c_expr("n == 1 && m != 2u", env).to_text() == "B && B == K i 0 Li 1 B != K u 1 Lu 2"
+    assert parse_c_expr("-(int64_t)m", env).to_text() == "U - C i K u 1"
+    for bad in ["n +", "x + 1", "(uint32_t)n", "n ? 1", "1.5 * n"]:
+        with pytest.raises(ValueError):
+            parse_c_expr(bad, env)

@@ -1086,3 +1086,74 @@ def conflict_accumulate_ref(x: np.ndarray, out: np.ndarray, shared_all: bool = F
                 else:
                     r[b, v] = r[b, v] + x[b, s, v]
     return r
+
+
+# ---------------------------------------------------------------- deepseek lightning indexer
+def lightning_inputs(seed: int = 0, bsz: int = 2, tiles: int = 4, cand: int = 32):
+    """examples/deepseek_lightning_indexer/golden.py:28-38: N(0,1) scores and one effective
+    sequence length per (b, s) drawn from the four tiers."""
+    rng = np.random.default_rng(seed)
+    scores = rng.standard_normal((bsz, tiles, cand), dtype=np.float32)
+    eff_seq = rng.choice(np.array([512, 4096, 16384, 131072], dtype=np.uint64), size=(bsz, tiles, 1, 1), replace=True)
+    return scores, eff_seq
+
+
+def stable_topk_desc(scores: np.ndarray, k: int) -> np.ndarray:
+    """examples/deepseek_lightning_indexer/golden.py:6-25: per row, descending score with the
+    lower index first on ties."""
+    B, S, C = scores.shape
+    out = np.empty((B, S, k), np.int32)
+    idx = np.arange(C)
+    for b in range(B):
+        for s in range(S):
+            out[b, s] = np.lexsort((idx, -scores[b, s].astype(np.float64)))[:k]
+    return out
+
+
+def lightning_indexer(scores: np.ndarray, eff_seq: np.ndarray, out_idx: np.ndarray, impl: str):
+    """examples/deepseek_lightning_indexer/pto_wsp_impl.py:30-150: a slot loaded from EffSeq[b][s]
+    picks one of four tiers (pad_to 2048 / 8192 / 65536 / 131072) and the top-8 of the 32
+    candidates is taken with TSORT32; impl "pto" traces pto.* ops, "ptoisa" the PTO-ISA calls
+    with the tier cost as cpu_sim_add_cycles of a C expression of pad_to."""
+    from pto_wsp import ptoisa, ptoisa_kernel
+    from pto_wsp.primitives import slot_load_u64
+    from pto_wsp.scalar_expr import slot_u64
+
+    bsz, tiles, cand = scores.shape
+    Scores = Tensor(data=scores.reshape(bsz, tiles, 1, cand), shape=(bsz, tiles, 1, cand), dtype=F32)
+    EffSeq = Tensor(data=eff_seq, shape=eff_seq.shape, dtype=DType.U64)
+    OutIdx = Tensor(data=out_idx, shape=out_idx.shape, dtype=I32)
+
+    @kernel
+    def topk8_sort32_pto(scores_tile: In[Tile[1, 32, F32]], out_idx_tile: Out[Tile[1, 8, I32]], pad_to: Scalar[I32]):
+        idx = pto.iota_u32(32)
+        pairs = pto.tsort32(scores_tile, idx)
+        pto.store(out_idx_tile, pto.extract_topk_indices(pairs, 8))
+
+    @ptoisa_kernel
+    def topk8_sort32(scores_tile: In[Tile[1, 32, F32]], out_idx_tile: Out[Tile[1, 8, I32]], pad_to: Scalar[I32]):
+        s = ptoisa.tload(scores_tile)
+        pairs = ptoisa.TSORT32(s, ptoisa.iota_u32(32))
+        ptoisa.store_topk_indices_i32(out_idx_tile, pairs, 8)
+        ptoisa.cpu_sim_add_cycles(f"(({pad_to.debug_name} > 32) ? ((uint64_t)({pad_to.debug_name} / 32) * 128ull) : 0ull)")
+
+    topk = topk8_sort32_pto if impl == "pto" else topk8_sort32
+
+    @workload
+    def wl():
+        for b in P(Dense[bsz]()):
+            for s in P(Dense[tiles]()):
+                slot_load_u64(0, EffSeq[b][s], row=0, col=0)
+                with P.when(slot_u64(0) <= 2048):
+                    topk[b, s](scores_tile=Scores[b][s], out_idx_tile=OutIdx[b][s], pad_to=2048)
+                with P.otherwise():
+                    with P.when(slot_u64(0) <= 8192):
+                        topk[b, s](scores_tile=Scores[b][s], out_idx_tile=OutIdx[b][s], pad_to=8192)
+                    with P.otherwise():
+                        with P.when(slot_u64(0) <= 65536):
+                            topk[b, s](scores_tile=Scores[b][s], out_idx_tile=OutIdx[b][s], pad_to=65536)
+                        with P.otherwise():
+                            topk[b, s](scores_tile=Scores[b][s], out_idx_tile=OutIdx[b][s], pad_to=131072)
+
+    return (wl().dispatch(DispatchPolicy.affinity(lambda t: t.get("b"), num_aicpus=4))
+            .task_graph(window=TaskWindow(1024, "tasks", WindowMode.STALL)))
