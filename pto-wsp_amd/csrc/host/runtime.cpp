@@ -466,6 +466,7 @@ struct Tuning {
     int decode_waves = 4;
     bool decode_ordered = false;
     bool serial_groups = true;  // overlapping grids run as parallel groups of in-order tasks
+    int tile_threads = 256;     // threads of a tile-program workgroup
 };
 
 const Tuning& tuning() {
@@ -478,6 +479,10 @@ const Tuning& tuning() {
         if (const char* s = std::getenv("PTOWSP_DECODE_WAVES")) v.decode_waves = std::atoi(s) == 8 ? 8 : 4;
         if (const char* s = std::getenv("PTOWSP_DECODE_ORDERED")) v.decode_ordered = std::atoi(s) != 0;
         if (const char* s = std::getenv("PTOWSP_SERIAL_GROUPS")) v.serial_groups = std::atoi(s) != 0;
+        if (const char* s = std::getenv("PTOWSP_TILE_THREADS")) {
+            const int t = std::atoi(s);
+            v.tile_threads = t == 64 || t == 128 || t == 256 || t == 512 ? t : 256;
+        }
         return v;
     }();
     return t;
@@ -928,6 +933,7 @@ BuiltLaunch build_launch(RunEnv& E, const LaunchSpec& L) {
     B.spec.decode_waves = tuning().decode_waves;
     B.spec.decode_ordered = tuning().decode_ordered;
     B.spec.vec_width = a.family == Family::RowProgram ? pick_vec_width(a, A, nvars) : 1;
+    B.spec.threads = tuning().tile_threads;
     if (P->ka[L.kernel].family == Family::Custom) {
         custom_axis_args(E, L, A);
         B.spec.gemm = B.spec.decode = B.spec.gemm_pingpong = false;
@@ -941,7 +947,7 @@ std::string spec_key(const EmitSpec& s) {
     o << "vw" << s.vec_width << (s.serial ? ";serial" + std::to_string(s.seq_mask) : "") << (s.task_list ? ";tl" : "") << ";up" << s.row_up << (s.nontemporal ? ";nt" : "")
       << (s.gemm ? ";gemm" : "") << ";m" << s.gemm_vm << ";n" << s.gemm_vn << (s.gemm_pingpong ? ";pp" : "")
       << (s.decode ? ";dec" : "")
-      << (s.decode_norm ? ";norm" : "") << ";r" << s.decode_ring << ";w" << s.decode_waves << (s.decode_ordered ? ";ord" : "")
+      << (s.decode_norm ? ";norm" : "") << ";t" << s.threads << ";r" << s.decode_ring << ";w" << s.decode_waves << (s.decode_ordered ? ";ord" : "")
       << ";i";
     for (int c : s.indirect_count) o << c << ",";
     o << ";d";

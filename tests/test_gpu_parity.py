@@ -795,3 +795,44 @@ def test_cond_on_a_symbol_inside_a_grid(gpu):
             np.testing.assert_array_equal(a["c"], a["a0"] if flag else a["a1"])
             ref = run_workload(W.cond_copy(_cond_arrays(), p), symbols_u64={fnv1a_64("flag"): flag})
             assert (prog.stats.total_cycles, prog.stats.task_count) == (ref.total_cycles, ref.task_count)
+
+
+def test_example_llama(gpu):
+    """examples/llama: five kernels per seq tile (attention, residual, rmsnorm, MLP, residual)."""
+    from test_oracle_golden import CYC, _llama_inputs
+
+    x, w1, w2 = _llama_inputs()
+    out, ref_out = np.zeros_like(x), np.zeros_like(x)
+    prog = run_hip(W.llama_block(x, w1, w2, out, 8, 1e-6))
+    ref = run_workload(W.llama_block(x, w1, w2, ref_out, 8, 1e-6))
+    np.testing.assert_allclose(out, ref_out, rtol=1e-5, atol=1e-6)
+    np.testing.assert_allclose(out, W.llama_block_ref(x, w1, w2, 8, 1e-6), rtol=1e-5, atol=1e-6)
+    assert prog.stats.total_cycles == ref.total_cycles == CYC["llama"]["total_cycles"]
+
+
+def test_example_deepseek_v3(gpu):
+    """examples/deepseek_v3: two expert matmuls and the gated mix per 8-row tile."""
+    from test_oracle_golden import CYC, _moe_inputs
+
+    x, w0, w1, g = _moe_inputs()
+    y, ref_y = np.zeros_like(x), np.zeros_like(x)
+    prog = run_hip(W.moe_block(x, w0, w1, g, y))
+    ref = run_workload(W.moe_block(x, w0, w1, g, ref_y))
+    np.testing.assert_allclose(y, ref_y, rtol=1e-5, atol=1e-6)
+    assert prog.stats.total_cycles == ref.total_cycles == CYC["deepseek_v3"]["total_cycles"]
+
+
+def test_example_tensor_data(gpu):
+    from test_oracle_golden import CYC
+
+    rng = np.random.default_rng(0)
+    a = rng.standard_normal((2, 2, 2, 32, 32), dtype=np.float32)
+    b = rng.standard_normal((2, 2, 2, 32, 32), dtype=np.float32)
+    x = rng.standard_normal((2, 4, 32, 32), dtype=np.float32)
+    c, y = np.zeros_like(a), np.zeros_like(x)
+    p1 = run_hip(W.add_tiles5(a, b, c))
+    p2 = run_hip(W.square_tiles4(x, y))
+    np.testing.assert_array_equal(c, a + b)
+    np.testing.assert_array_equal(y, x * x)
+    assert p1.stats.total_cycles == CYC["tensor_data_add"]["total_cycles"]
+    assert p2.stats.total_cycles == CYC["tensor_data_square"]["total_cycles"]

@@ -256,3 +256,56 @@ def test_ragged_axis_flattens_lengths():
         run_workload(W.ragged_mark({"y": y}, r), symbols_u64={fnv1a_64(f"outer_{id(r)}"): 2},
                      symbols_ptr={fnv1a_64(f"lengths_{id(r)}"): np.asarray(lengths, np.int32)})
         np.testing.assert_array_equal(y.reshape(3), want)
+
+
+def _llama_inputs():
+    rng = np.random.default_rng(0)  # examples/llama/llama_example.py:19-28
+    x = rng.standard_normal((16, 8), dtype=np.float32)
+    w1 = rng.standard_normal((8, 16), dtype=np.float32)
+    w2 = rng.standard_normal((16, 8), dtype=np.float32)
+    return x, w1, w2
+
+
+def test_llama_example():
+    g = CYC["llama"]
+    x, w1, w2 = _llama_inputs()
+    out = np.zeros_like(x)
+    r = run_workload(W.llama_block(x, w1, w2, out, 8, 1e-6))
+    assert r.total_cycles == g["total_cycles"]
+    ref = W.llama_block_ref(x, w1, w2, 8, 1e-6)
+    assert _close(out, ref, g["rtol"], g["atol"])
+    # attention over the whole sequence instead of per 8-row tile is another result
+    assert not _close(out, W.llama_block_ref(x, w1, w2, 16, 1e-6), g["rtol"], g["atol"])
+
+
+def _moe_inputs():
+    rng = np.random.default_rng(0)  # examples/deepseek_v3/deepseek_v3_example.py:19-28
+    x = rng.standard_normal((16, 8), dtype=np.float32)
+    w0 = rng.standard_normal((8, 8), dtype=np.float32)
+    w1 = rng.standard_normal((8, 8), dtype=np.float32)
+    g = rng.random((16, 1), dtype=np.float32)
+    return x, w0, w1, g
+
+
+def test_deepseek_v3_example():
+    gold = CYC["deepseek_v3"]
+    x, w0, w1, g = _moe_inputs()
+    y = np.zeros_like(x)
+    r = run_workload(W.moe_block(x, w0, w1, g, y))
+    assert r.total_cycles == gold["total_cycles"]
+    x64, g64 = x.astype(np.float64), g.astype(np.float64)
+    ref = g64 * (x64 @ w0) + (1.0 - g64) * (x64 @ w1)  # examples/deepseek_v3/golden.py:6-9
+    assert _close(y, ref, gold["rtol"], gold["atol"])
+    assert not _close(y, (1.0 - g64) * (x64 @ w0) + g64 * (x64 @ w1), gold["rtol"], gold["atol"])
+
+
+def test_tensor_data_examples():
+    rng = np.random.default_rng(0)  # examples/tensor_data/tensor_data_example.py:19-29
+    a = rng.standard_normal((2, 2, 2, 32, 32), dtype=np.float32)
+    b = rng.standard_normal((2, 2, 2, 32, 32), dtype=np.float32)
+    x = rng.standard_normal((2, 4, 32, 32), dtype=np.float32)
+    c, y = np.zeros_like(a), np.zeros_like(x)
+    assert run_workload(W.add_tiles5(a, b, c)).total_cycles == CYC["tensor_data_add"]["total_cycles"]
+    assert run_workload(W.square_tiles4(x, y)).total_cycles == CYC["tensor_data_square"]["total_cycles"]
+    np.testing.assert_array_equal(c, a + b)
+    np.testing.assert_array_equal(y, x * x)

@@ -1157,3 +1157,131 @@ def lightning_indexer(scores: np.ndarray, eff_seq: np.ndarray, out_idx: np.ndarr
 
     return (wl().dispatch(DispatchPolicy.affinity(lambda t: t.get("b"), num_aicpus=4))
             .task_graph(window=TaskWindow(1024, "tasks", WindowMode.STALL)))
+
+
+# ---------------------------------------------------------------- llama / deepseek_v3 / tensor_data examples
+def llama_block(x: np.ndarray, w1: np.ndarray, w2: np.ndarray, out: np.ndarray, tile_seq: int, eps: float):
+    """examples/llama/pto_wsp_impl.py:21-118: per seq tile, attention (q = k = v = x), residual
+    add, rmsnorm (eps), ReLU MLP, residual add, as five kernels in one P() body."""
+    seq, d = x.shape
+    st = seq // tile_seq
+    mlp = w1.shape[1]
+    xt = x.reshape(st, tile_seq, d).astype(np.float32)
+    X, KT = T(xt), T(xt.transpose(0, 2, 1))
+    W1, W2 = T(w1.astype(np.float32)), T(w2.astype(np.float32))
+    O = T(out.reshape(st, tile_seq, d))
+    Xn, Attn, Res1, Mlp = (T(np.zeros_like(xt)) for _ in range(4))
+
+    @kernel
+    def rmsnorm_tile(x: In[Tile[tile_seq, d, F32]], out: Out[Tile[tile_seq, d, F32]]):
+        inv = pto.rsqrt(pto.add(pto.rowmean(pto.mul(x, x)), pto.constant(eps, F32)))
+        pto.store(out, pto.mul(x, inv))
+
+    @kernel
+    def attn_tile(q: In[Tile[tile_seq, d, F32]], k_t: In[Tile[d, tile_seq, F32]], v: In[Tile[tile_seq, d, F32]],
+                  out: Out[Tile[tile_seq, d, F32]]):
+        s = pto.mul(pto.matmul(q, k_t), pto.constant(1.0 / math.sqrt(d), F32))
+        e = pto.exp(pto.sub(s, pto.rowmax(s)))
+        pto.store(out, pto.matmul(pto.div(e, pto.rowsum(e)), v))
+
+    @kernel
+    def add_tile(a: In[Tile[tile_seq, d, F32]], b: In[Tile[tile_seq, d, F32]], out: Out[Tile[tile_seq, d, F32]]):
+        pto.store(out, pto.add(a, b))
+
+    @kernel
+    def mlp_tile(x: In[Tile[tile_seq, d, F32]], w1: In[Tile[d, mlp, F32]], w2: In[Tile[mlp, d, F32]],
+                 out: Out[Tile[tile_seq, d, F32]]):
+        h = pto.matmul(x, w1)
+        pto.store(out, pto.matmul(pto.max(h, pto.constant(0.0, F32)), w2))
+
+    @workload
+    def wl():
+        for s in P(Dense[st]()):
+            attn_tile[s](q=X[s], k_t=KT[s], v=X[s], out=Attn[s])
+            add_tile[s](a=X[s], b=Attn[s], out=Res1[s])
+            rmsnorm_tile[s](x=Res1[s], out=Xn[s])
+            mlp_tile[s](x=Xn[s], w1=W1, w2=W2, out=Mlp[s])
+            add_tile[s](a=Res1[s], b=Mlp[s], out=O[s])
+
+    return rr4(wl())
+
+
+def llama_block_ref(x, w1, w2, tile_seq, eps):
+    """examples/llama/golden.py:7-35 in float64."""
+    out = np.zeros(x.shape, np.float64)
+    d = x.shape[1]
+    for t in range(x.shape[0] // tile_seq):
+        xt = x[t * tile_seq:(t + 1) * tile_seq].astype(np.float64)
+        s = (xt @ xt.T) / math.sqrt(d)
+        e = np.exp(s - s.max(-1, keepdims=True))
+        res1 = xt + (e / e.sum(-1, keepdims=True)) @ xt
+        xn = res1 / np.sqrt((res1 * res1).mean(-1, keepdims=True) + eps)
+        out[t * tile_seq:(t + 1) * tile_seq] = res1 + np.maximum(xn @ w1, 0.0) @ w2
+    return out
+
+
+def moe_block(x: np.ndarray, w0: np.ndarray, w1: np.ndarray, g: np.ndarray, y: np.ndarray):
+    """examples/deepseek_v3/pto_wsp_impl.py:20-95: two expert matmuls and a gated mix
+    y = g * (x @ w0) + (1 - g) * (x @ w1) per 8-row seq tile."""
+    seq, d = x.shape
+    ts = 8
+    st = seq // ts
+    xt = x.reshape(st, ts, d).astype(np.float32)
+    X, G = T(xt), T(g.reshape(st, ts, 1).astype(np.float32))
+    W0, W1, Y = T(w0.astype(np.float32)), T(w1.astype(np.float32)), T(y.reshape(st, ts, d))
+    E0, E1 = T(np.zeros_like(xt)), T(np.zeros_like(xt))
+
+    @kernel
+    def expert_linear(x: In[Tile[ts, d, F32]], w: In[Tile[d, d, F32]], out: Out[Tile[ts, d, F32]]):
+        pto.store(out, pto.matmul(x, w))
+
+    @kernel
+    def moe_mix(e0: In[Tile[ts, d, F32]], e1: In[Tile[ts, d, F32]], g: In[Tile[ts, 1, F32]], out: Out[Tile[ts, d, F32]]):
+        g1 = pto.add(pto.mul(g, pto.constant(-1.0, F32)), pto.constant(1.0, F32))
+        pto.store(out, pto.add(pto.mul(e0, g), pto.mul(e1, g1)))
+
+    @workload
+    def wl():
+        for s in P(Dense[st]()):
+            expert_linear[s](x=X[s], w=W0, out=E0[s])
+            expert_linear[s](x=X[s], w=W1, out=E1[s])
+            moe_mix[s](e0=E0[s], e1=E1[s], g=G[s], out=Y[s])
+
+    return rr4(wl())
+
+
+def add_tiles5(a: np.ndarray, b: np.ndarray, c: np.ndarray):
+    """examples/tensor_data/pto_wsp_impl.py:20-66: C = A + B over [B, TM, TN, R, C] tiles."""
+    nb, tm, tn, r, cc = a.shape
+    A, B, C = T(a), T(b), T(c)
+
+    @kernel
+    def add_tiles(a_tile: In[Tile[r, cc, F32]], b_tile: In[Tile[r, cc, F32]], c_tile: Out[Tile[r, cc, F32]]):
+        pto.store(c_tile, pto.add(a_tile, b_tile))
+
+    @workload
+    def wl():
+        for bb in P(Dense[nb]()):
+            for i in P(Dense[tm]()):
+                for j in P(Dense[tn]()):
+                    add_tiles[bb, i, j](a_tile=A[bb][i][j], b_tile=B[bb][i][j], c_tile=C[bb][i][j])
+
+    return rr4(wl())
+
+
+def square_tiles4(x: np.ndarray, y: np.ndarray):
+    """examples/tensor_data/pto_wsp_impl.py:69-107: Y = X * X over [B, T, R, C] tiles."""
+    nb, nt, r, cc = x.shape
+    X, Y = T(x), T(y)
+
+    @kernel
+    def square_tile(in_tile: In[Tile[r, cc, F32]], out_tile: Out[Tile[r, cc, F32]]):
+        pto.store(out_tile, pto.mul(in_tile, in_tile))
+
+    @workload
+    def wl():
+        for bb in P(Dense[nb]()):
+            for t in P(Dense[nt]()):
+                square_tile[bb, t](in_tile=X[bb][t], out_tile=Y[bb][t])
+
+    return rr4(wl())
