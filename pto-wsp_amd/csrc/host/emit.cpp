@@ -80,6 +80,22 @@ void emit_decode(std::ostringstream& o, const std::string& ind, int ng, const st
     o << ind << "  vars[0] = q_; }\n";
 }
 
+// True when an index expression reads loop variable `var`.
+bool reads_var(const IndexExpr& e, const std::string& var) {
+    switch (e.kind) {
+        case 'v': return e.var == var;
+        case 'a':
+            for (const auto& [n, c] : e.terms)
+                if (n == var && c != 0) return true;
+            return false;
+        case 't':
+            for (const auto& x : e.idx)
+                if (reads_var(x, var)) return true;
+            return false;
+        default: return false;
+    }
+}
+
 // Element offset expression of tensor ordinal p: affine part + indirect terms.
 std::string offset_expr(int p, int nvars, int first_term, int nterms) {
     std::ostringstream e;
@@ -321,14 +337,96 @@ EmittedKernel emit_tile(const Module& m, const KernelAnalysis& a, const LaunchSp
     auto is_int_v = [&](int id) { return !dtype_is_float(a.by_id[id]->dtype); };
     auto tord = [&](int id) { return a.param_of[id] >= 0 ? a.tensor_ordinal[a.param_of[id]] : -1; };
 
-    // LDS tiles: op results, preloaded params.
+    // Params resident in LDS across the in-kernel loops of a task: views that
+    // no in-kernel loop moves, on a tensor that no other param of the launch
+    // names, read (preloaded or loaded) and / or stored without a cast, and
+    // not read from global by a matmul.  They are loaded once before the
+    // in-kernel loops and stored once after them, instead of every iteration
+    // (the in-order iterations of one task see the same values either way).
+    std::vector<bool> resident(ntens, false);
+    if (ni > 0) {
+        for (int p = 0; p < ntens; ++p) {
+            const int pid = k.params[a.tensor_param_index[p]].id;
+            const ValueInfo* v = a.by_id[pid];
+            bool ok = v->dtype == DType::F32 || v->dtype == DType::I32 || v->dtype == DType::I64;
+            for (int q = 0; q < ntens && ok; ++q)
+                if (q != p && L.targs[q]->tid == L.targs[p]->tid) ok = false;
+            for (const auto& li : L.inner)
+                for (const auto& e : L.targs[p]->idx)
+                    if (ok && reads_var(e, li.var)) ok = false;
+            if (ok && spec.indirect_count.size() > static_cast<size_t>(p) && spec.indirect_count[p] > 0) ok = false;
+            bool used = a.preload[pid], stored = false;
+            for (const auto& op : k.ops) {
+                if (!ok) break;
+                for (size_t j = 0; j < op.operands.size(); ++j) {
+                    if (op.operands[j] != pid) continue;
+                    if (op.kind == OpKind::Matmul || op.kind == OpKind::StoreTopkIndices) ok = false;
+                    const bool is_store = op.kind == OpKind::Store && j == 0;
+                    // A read after a store in the same iteration sees the preloaded value,
+                    // which the resident tile no longer holds.
+                    if (!is_store && stored) ok = false;
+                    if (op.kind == OpKind::Load) used = true;
+                    if (is_store) {
+                        used = stored = true;
+                        if (a.by_id[op.operands[1]]->dtype != v->dtype) ok = false;
+                    }
+                }
+            }
+            resident[p] = ok && used;
+        }
+    }
+    auto resident_id = [&](int id) { const int p = tord(id); return p >= 0 && resident[p]; };
+
+    // Params staged ahead through the (single) in-kernel loop: views that the
+    // loop moves, read (preloaded, loaded or a matmul operand), with no
+    // indirect terms, on tensors that no param of the launch stores (so that
+    // reading later iterations early sees the same data).  Chunks of SB
+    // iterations are loaded into SB LDS slots at once, then the chunk's
+    // iterations run from LDS: one memory latency per chunk instead of one per
+    // iteration.
+    std::vector<bool> staged(ntens, false);
+    int SB = 0;
+    if (ni == 1) {
+        size_t stage_bytes = 0;
+        for (int p = 0; p < ntens; ++p) {
+            const int pid = k.params[a.tensor_param_index[p]].id;
+            const ValueInfo* v = a.by_id[pid];
+            bool moves = false;
+            for (const auto& e : L.targs[p]->idx) moves = moves || reads_var(e, L.inner[0].var);
+            if (!moves || resident[p] || a.stored[p]) continue;
+            if (spec.indirect_count.size() > static_cast<size_t>(p) && spec.indirect_count[p] > 0) continue;
+            bool written = false;
+            for (int q = 0; q < ntens; ++q) written = written || (a.stored[q] && L.targs[q]->tid == L.targs[p]->tid);
+            if (written) continue;
+            bool read = a.preload[pid];
+            for (const auto& op : k.ops)
+                if ((op.kind == OpKind::Load || op.kind == OpKind::Matmul) && !op.operands.empty() &&
+                    (op.operands[0] == pid || (op.kind == OpKind::Matmul && op.operands.size() > 1 && op.operands[1] == pid)))
+                    read = true;
+            if (!read) continue;
+            staged[p] = true;
+            stage_bytes += static_cast<size_t>(v->rows) * v->cols * (is_int_v(pid) ? 8 : 4);
+        }
+        if (stage_bytes > 0) {
+            SB = static_cast<int>(std::min<size_t>(8, (48 * 1024) / stage_bytes));
+            if (SB < 2) {
+                SB = 0;
+                staged.assign(ntens, false);
+            }
+        }
+    }
+    auto staged_id = [&](int id) { const int p = tord(id); return p >= 0 && staged[p]; };
+
+    // LDS tiles: op results, preloaded and resident params.
     std::set<int> lds_vals;
     for (const auto& op : k.ops)
         if (op.result > 0 && a.by_id[op.result]->tile) lds_vals.insert(op.result);
     for (const auto& p : k.params)
-        if (a.by_id[p.id]->tile && a.preload[p.id]) lds_vals.insert(p.id);
+        if (a.by_id[p.id]->tile && (a.preload[p.id] || resident_id(p.id)) && !staged_id(p.id)) lds_vals.insert(p.id);
     size_t lds = 0;
     for (int id : lds_vals) lds += static_cast<size_t>(a.by_id[id]->rows) * a.by_id[id]->cols * (is_int_v(id) ? 8 : 4);
+    for (const auto& p : k.params)
+        if (staged_id(p.id)) lds += static_cast<size_t>(SB) * a.by_id[p.id]->rows * a.by_id[p.id]->cols * (is_int_v(p.id) ? 8 : 4);
     if (lds > 160 * 1024)
         throw CompileError("kernel " + k.name + ": tiles need " + std::to_string(lds) +
                            " bytes of LDS, more than the 160 KiB of a gfx950 workgroup");
@@ -345,8 +443,15 @@ EmittedKernel emit_tile(const Module& m, const KernelAnalysis& a, const LaunchSp
     o << "  constexpr int NT = " << spec.threads << ";\n";
     for (int id : lds_vals) {
         const ValueInfo* v = a.by_id[id];
-        o << "  __shared__ " << (is_int_v(id) ? "i64" : "float") << " L" << id << "[" << v->rows * v->cols << "];\n";
+        o << "  __shared__ __attribute__((aligned(16))) " << (is_int_v(id) ? "i64" : "float") << " L" << id << "[" << v->rows * v->cols
+          << "];\n";
     }
+    for (const auto& p : k.params)
+        if (staged_id(p.id)) {
+            const ValueInfo* v = a.by_id[p.id];
+            o << "  __shared__ __attribute__((aligned(16))) " << (is_int_v(p.id) ? "i64" : "float") << " LP" << p.id << "["
+              << SB * v->rows * v->cols << "];\n";
+        }
     emit_scalars(o, a, true);
     o << "  i64 vars[" << (nvars > 0 ? nvars : 1) << "];\n  (void)vars;\n";
     // Grid loops are decoded from the task index.  A serial launch without a
@@ -376,31 +481,90 @@ EmittedKernel emit_tile(const Module& m, const KernelAnalysis& a, const LaunchSp
         emit_decode(o, "    ", ng, spec.task_list ? "A.tlist[t]" : "t");
     }
     std::string ind = "    ";
-    for (int i = 0; i < looped; ++i) {
-        const int v = loops[i];
-        const int inner_i = v - ng;
-        const int term = inner_i >= 0 && spec.inner_dyn_term.size() > static_cast<size_t>(inner_i) ? spec.inner_dyn_term[inner_i] : -1;
-        if (term >= 0) o << ind << "const i64 e" << i << " = indirect_index(A, " << term << ", vars, " << v << ");\n";
-        else o << ind << "const i64 e" << i << " = A.ext[" << v << "];\n";
-        o << ind << "for (vars[" << v << "] = 0; vars[" << v << "] < e" << i << "; ++vars[" << v << "]) {\n";
-        ind += "  ";
-    }
-    // Tile pointers with a per-task bounds check (indirect and run-time extents
-    // cannot all be checked on the host).
-    int term = 0;
-    for (int p = 0; p < ntens; ++p) {
+    bool any_resident = false;
+    for (int p = 0; p < ntens; ++p) any_resident = any_resident || resident[p];
+    // Tile pointer of tensor ordinal p with a per-task bounds check (indirect
+    // and run-time extents cannot all be checked on the host).
+    std::vector<int> first_term(ntens, 0);
+    for (int p = 1; p < ntens; ++p)
+        first_term[p] = first_term[p - 1] + (spec.indirect_count.size() > static_cast<size_t>(p - 1) ? spec.indirect_count[p - 1] : 0);
+    auto pointer = [&](int p) {
         const ValueInfo* v = a.by_id[k.params[a.tensor_param_index[p]].id];
         const int nt = spec.indirect_count.size() > static_cast<size_t>(p) ? spec.indirect_count[p] : 0;
-        o << ind << "const i64 o" << p << " = " << offset_expr(p, nvars, term, nt) << ";\n";
-        term += nt;
+        o << ind << "const i64 o" << p << " = " << offset_expr(p, nvars, first_term[p], nt) << ";\n";
         o << ind << "if (o" << p << " < 0 || o" << p << " + (i64)" << (v->rows - 1) << " * A.s3[" << p << "] + (i64)" << (v->cols - 1)
           << " * A.s4[" << p << "] >= A.span[" << p << "]) { if (threadIdx.x == 0) *A.err = 2; continue; }\n";
         o << ind << "char* p" << p << " = A.base[" << p << "] + o" << p << " * " << dtype_size(v->dtype) << ";\n";
+    };
+    auto load_tile = [&](int id, int dst, int p) {
+        const ValueInfo* v = a.by_id[id];
+        o << ind << "tile_load_" << (is_int_v(id) ? "i" : "f") << "<" << dt_code(v->dtype) << ", " << v->rows << ", " << v->cols
+          << ", NT>(L" << dst << ", p" << p << ", A.s3[" << p << "], A.s4[" << p << "]);\n";
+    };
+    for (int i = 0; i < looped; ++i) {
+        const int v = loops[i];
+        const int inner_i = v - ng;
+        if (inner_i == 0 && any_resident) {
+            // Task prologue: the resident params' pointers and first loads (the
+            // in-kernel variables do not move them).
+            for (int j = 0; j < ni; ++j) o << ind << "vars[" << ng + j << "] = 0;\n";
+            for (int p = 0; p < ntens; ++p) {
+                if (!resident[p]) continue;
+                pointer(p);
+                const int pid = k.params[a.tensor_param_index[p]].id;
+                bool read = a.preload[pid];
+                for (const auto& op : k.ops)
+                    if (op.kind == OpKind::Load && op.operands[0] == pid) read = true;
+                if (read) load_tile(pid, pid, p);
+            }
+            o << ind << "bool ran_ = false;\n";
+            o << ind << "__syncthreads();\n";
+        }
+        const int term = inner_i >= 0 && spec.inner_dyn_term.size() > static_cast<size_t>(inner_i) ? spec.inner_dyn_term[inner_i] : -1;
+        if (term >= 0) o << ind << "const i64 e" << i << " = indirect_index(A, " << term << ", vars, " << v << ");\n";
+        else o << ind << "const i64 e" << i << " = A.ext[" << v << "];\n";
+        if (inner_i == 0 && SB > 0) {
+            // Chunks of SB iterations: the staged params' tiles of the whole
+            // chunk are loaded first, then the iterations run.
+            o << ind << "for (i64 c0_ = 0; c0_ < e" << i << "; c0_ += " << SB << ") {\n";
+            o << ind << "  const i64 nb_ = e" << i << " - c0_ < " << SB << " ? e" << i << " - c0_ : " << SB << ";\n";
+            o << ind << "  for (i64 j_ = 0; j_ < nb_; ++j_) {\n";
+            o << ind << "    vars[" << v << "] = c0_ + j_;\n";
+            for (int p = 0; p < ntens; ++p) {
+                if (!staged[p]) continue;
+                const int pid = k.params[a.tensor_param_index[p]].id;
+                const ValueInfo* pv = a.by_id[pid];
+                o << ind << "    { const i64 o_ = " << offset_expr(p, nvars, first_term[p], 0) << ";\n";
+                o << ind << "      if (o_ >= 0 && o_ + (i64)" << (pv->rows - 1) << " * A.s3[" << p << "] + (i64)" << (pv->cols - 1)
+                  << " * A.s4[" << p << "] < A.span[" << p << "])\n";
+                o << ind << "        tile_load_" << (is_int_v(pid) ? "i" : "f") << "<" << dt_code(pv->dtype) << ", " << pv->rows << ", "
+                  << pv->cols << ", NT>(LP" << pid << " + j_ * " << pv->rows * pv->cols << ", A.base[" << p << "] + o_ * "
+                  << dtype_size(pv->dtype) << ", A.s3[" << p << "], A.s4[" << p << "]); }\n";
+            }
+            o << ind << "  }\n";
+            o << ind << "  __syncthreads();\n";
+            o << ind << "  for (i64 j_ = 0; j_ < nb_; ++j_) {\n";
+            ind += "    ";
+            o << ind << "vars[" << v << "] = c0_ + j_;\n";
+            for (int p = 0; p < ntens; ++p) {
+                if (!staged[p]) continue;
+                const int pid = k.params[a.tensor_param_index[p]].id;
+                const ValueInfo* pv = a.by_id[pid];
+                o << ind << (is_int_v(pid) ? "i64" : "float") << "* const L" << pid << " = LP" << pid << " + j_ * "
+                  << pv->rows * pv->cols << ";\n";
+            }
+            continue;
+        }
+        o << ind << "for (vars[" << v << "] = 0; vars[" << v << "] < e" << i << "; ++vars[" << v << "]) {\n";
+        ind += "  ";
     }
+    for (int p = 0; p < ntens; ++p)
+        if (!resident[p]) pointer(p);
+    if (any_resident) o << ind << "ran_ = true;\n";
     // Preloads (:764-779).
     for (size_t i = 0; i < k.params.size(); ++i) {
         const ValueInfo* v = a.by_id[k.params[i].id];
-        if (!v->tile || !a.preload[v->id]) continue;
+        if (!v->tile || !a.preload[v->id] || resident_id(v->id) || staged_id(v->id)) continue;
         const int p = a.tensor_ordinal[i];
         o << ind << "tile_load_" << (is_int_v(v->id) ? "i" : "f") << "<" << dt_code(v->dtype) << ", " << v->rows << ", " << v->cols
           << ", NT>(L" << v->id << ", p" << p << ", A.s3[" << p << "], A.s4[" << p << "]);\n";
@@ -417,16 +581,27 @@ EmittedKernel emit_tile(const Module& m, const KernelAnalysis& a, const LaunchSp
             case OpKind::Load: {
                 const ValueInfo* s = a.by_id[op.operands[0]];
                 const int p = tord(s->id);
-                o << ind << "tile_load_" << (is_int_v(s->id) ? "i" : "f") << "<" << dt_code(s->dtype) << ", " << s->rows << ", "
-                  << s->cols << ", NT>(L" << res->id << ", p" << p << ", A.s3[" << p << "], A.s4[" << p << "]);\n";
+                if (resident[p] || staged[p])
+                    o << ind << "for (int e = threadIdx.x; e < " << s->rows * s->cols << "; e += NT) L" << res->id << "[e] = L" << s->id
+                      << "[e];\n";
+                else
+                    o << ind << "tile_load_" << (is_int_v(s->id) ? "i" : "f") << "<" << dt_code(s->dtype) << ", " << s->rows << ", "
+                      << s->cols << ", NT>(L" << res->id << ", p" << p << ", A.s3[" << p << "], A.s4[" << p << "]);\n";
                 break;
             }
             case OpKind::Store: {
                 const ValueInfo* d = a.by_id[op.operands[0]];
                 const ValueInfo* s = a.by_id[op.operands[1]];
                 const int p = tord(d->id);
-                o << ind << "tile_store_" << (is_int_v(s->id) ? "i" : "f") << "<" << dt_code(d->dtype) << ", " << d->rows << ", "
-                  << d->cols << ", NT>(p" << p << ", L" << s->id << ", A.s3[" << p << "], A.s4[" << p << "]);\n";
+                if (resident[p]) {
+                    // The param's LDS tile holds its value until the loops end (same dtype: no cast).
+                    if (s->id != d->id)
+                        o << ind << "for (int e = threadIdx.x; e < " << d->rows * d->cols << "; e += NT) L" << d->id << "[e] = L"
+                          << s->id << "[e];\n";
+                } else {
+                    o << ind << "tile_store_" << (is_int_v(s->id) ? "i" : "f") << "<" << dt_code(d->dtype) << ", " << d->rows << ", "
+                      << d->cols << ", NT>(p" << p << ", L" << s->id << ", A.s3[" << p << "], A.s4[" << p << "]);\n";
+                }
                 break;
             }
             case OpKind::Matmul: {
@@ -435,7 +610,7 @@ EmittedKernel emit_tile(const Module& m, const KernelAnalysis& a, const LaunchSp
                 const int M = av->rows, K = av->cols, N = bv->cols;
                 auto elem = [&](const ValueInfo* v, const std::string& r, const std::string& c, int ld) {
                     const int p = tord(v->id);
-                    if (p >= 0)
+                    if (p >= 0 && !staged[p])
                         return "gload_f<" + std::to_string(dt_code(v->dtype)) + ">(p" + std::to_string(p) + ", (i64)(" + r + ") * A.s3[" +
                                std::to_string(p) + "] + (i64)(" + c + ") * A.s4[" + std::to_string(p) + "])";
                     return "L" + std::to_string(v->id) + "[(" + r + ") * " + std::to_string(ld) + " + (" + c + ")]";
@@ -475,10 +650,23 @@ EmittedKernel emit_tile(const Module& m, const KernelAnalysis& a, const LaunchSp
             case OpKind::RowMean: {
                 const ValueInfo* s = a.by_id[op.operands[0]];
                 const std::string ty = is_int_v(s->id) ? "i64" : "float";
+                const char* fold = op.kind == OpKind::RowMax ? "acc = x > acc ? x : acc;" : "acc = acc + x;";
                 o << ind << "for (int r = threadIdx.x; r < " << s->rows << "; r += NT) {\n";
-                o << ind << "  " << ty << " acc = L" << s->id << "[r * " << s->cols << "];\n";
-                o << ind << "  for (int c = 1; c < " << s->cols << "; ++c) { const " << ty << " x = L" << s->id << "[r * " << s->cols
-                  << " + c]; acc = " << (op.kind == OpKind::RowMax ? "x > acc ? x : acc" : "acc + x") << "; }\n";
+                if (ty == "float" && s->cols % 4 == 0 && s->cols >= 8) {
+                    // The oracle's left-to-right order, read 16 bytes at a time and
+                    // unrolled so that the loads do not wait on the fold chain.
+                    o << ind << "  const float4* row_ = reinterpret_cast<const float4*>(L" << s->id << " + r * " << s->cols << ");\n";
+                    o << ind << "  float acc = row_[0].x;\n";
+                    o << ind << "  { float x = row_[0].y; " << fold << " x = row_[0].z; " << fold << " x = row_[0].w; " << fold
+                      << " }\n";
+                    o << ind << "#pragma unroll 8\n";
+                    o << ind << "  for (int c4 = 1; c4 < " << s->cols / 4 << "; ++c4) { const float4 v4 = row_[c4]; float x = v4.x; "
+                      << fold << " x = v4.y; " << fold << " x = v4.z; " << fold << " x = v4.w; " << fold << " }\n";
+                } else {
+                    o << ind << "  " << ty << " acc = L" << s->id << "[r * " << s->cols << "];\n";
+                    o << ind << "  for (int c = 1; c < " << s->cols << "; ++c) { const " << ty << " x = L" << s->id << "[r * "
+                      << s->cols << " + c]; " << fold << " }\n";
+                }
                 if (op.kind == OpKind::RowMean) {
                     if (ty == "float") o << ind << "  acc = acc / " << flt(static_cast<double>(s->cols)) << ";\n";
                     else o << ind << "  acc = acc / " << s->cols << ";\n";
@@ -516,8 +704,26 @@ EmittedKernel emit_tile(const Module& m, const KernelAnalysis& a, const LaunchSp
         o << ind << "__syncthreads();\n";
     }
     for (int i = looped - 1; i >= 0; --i) {
-        ind.resize(ind.size() - 2);
-        o << ind << "}\n";
+        if (loops[i] == ng && SB > 0) {
+            ind.resize(ind.size() - 4);
+            o << ind << "  }\n" << ind << "}\n";
+        } else {
+            ind.resize(ind.size() - 2);
+            o << ind << "}\n";
+        }
+        if (loops[i] == ng && any_resident) {
+            // Task epilogue: the stored resident params go back to global
+            // memory (when the in-kernel loops ran at least once).
+            o << ind << "if (ran_) {\n";
+            for (int p = 0; p < ntens; ++p) {
+                if (!resident[p] || !a.stored[p]) continue;
+                const int pid = k.params[a.tensor_param_index[p]].id;
+                const ValueInfo* v = a.by_id[pid];
+                o << ind << "  tile_store_" << (is_int_v(pid) ? "i" : "f") << "<" << dt_code(v->dtype) << ", " << v->rows << ", "
+                  << v->cols << ", NT>(p" << p << ", L" << pid << ", A.s3[" << p << "], A.s4[" << p << "]);\n";
+            }
+            o << ind << "}\n";
+        }
     }
     o << "  }\n}\n";
     ek.source = o.str();
