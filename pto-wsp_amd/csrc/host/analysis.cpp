@@ -87,10 +87,14 @@ bool classify_rows(const KernelDef& k, KernelAnalysis& a) {
             a.row_class[v.id] = RowClass::Scalar;
             continue;
         }
-        // A param tile read only through Load ops (or only stored to) is no
-        // value of the program: its Load results are.
-        if (a.param_of[v.id] >= 0 && !a.preload[v.id]) continue;
         RowClass c = base_class(&v);
+        // A param tile read only through Load ops (or only stored to) is no
+        // value of the program (its Load results are): its class only
+        // records its shape, and one that fits no class is no obstacle.
+        if (a.param_of[v.id] >= 0 && !a.preload[v.id]) {
+            a.row_class[v.id] = c;
+            continue;
+        }
         if (c == RowClass::None)
             return no("tile " + std::to_string(v.id) + " of shape " + std::to_string(v.rows) + "x" +
                       std::to_string(v.cols) + " does not fit rows of " + std::to_string(R) + "x" + std::to_string(C));

@@ -441,7 +441,12 @@ int pick_vec_width(const KernelAnalysis& a, const LaunchArgs& A, int nvars) {
         bool ok = true;
         for (size_t p = 0; p < a.tensor_param_index.size() && ok; ++p) {
             const int id = a.def->params[a.tensor_param_index[p]].id;
-            const RowClass c = a.row_class[id];
+            // The param's own class, or that of a Load of it, decides how it is accessed.
+            RowClass c = a.row_class[id];
+            for (const auto& op : a.def->ops)
+                if (op.kind == OpKind::Load && op.operands[0] == id && op.result > 0 &&
+                    (a.row_class[op.result] == RowClass::Full || a.row_class[op.result] == RowClass::ColVec))
+                    c = a.row_class[op.result];
             if (c != RowClass::Full && c != RowClass::ColVec) continue;
             if (A.s4[p] != 1) ok = false;
             if (reinterpret_cast<uintptr_t>(A.base[p]) % (vw * 4)) ok = false;

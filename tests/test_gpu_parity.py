@@ -836,3 +836,29 @@ def test_example_tensor_data(gpu):
     np.testing.assert_array_equal(y, x * x)
     assert p1.stats.total_cycles == CYC["tensor_data_add"]["total_cycles"]
     assert p2.stats.total_cycles == CYC["tensor_data_square"]["total_cycles"]
+
+
+def test_row_program_store_into_a_transposed_view(gpu):
+    """The row program's vector width must follow the strides of the params that are only
+    stored: out is a transposed view (column stride R), so its rows are written element by
+    element while x's are read 16 bytes at a time."""
+    from pto_wsp import In, Out, P, Dense, Tensor, Tile, kernel, pto, workload
+
+    x = np.random.default_rng(8).standard_normal((2, 3, 16, 64)).astype(np.float32)
+    y_base = np.zeros((2, 3, 64, 16), np.float32)
+    y_view = y_base.transpose(0, 1, 3, 2)
+    X = Tensor(data=x, shape=x.shape, dtype=W.F32)
+    Y = Tensor(data=y_view, shape=y_view.shape, dtype=W.F32)
+
+    @kernel
+    def scale_tile(x_t: In[Tile[16, 64, W.F32]], out: Out[Tile[16, 64, W.F32]]):
+        pto.store(out, pto.mul(x_t, pto.constant(2.0, W.F32)))
+
+    @workload
+    def wl():
+        for b in P(Dense[2]()):
+            for t in P(Dense[3]()):
+                scale_tile[b, t](x_t=X[b][t], out=Y[b][t])
+
+    run_hip(W.rr4(wl()))
+    np.testing.assert_array_equal(y_base.transpose(0, 1, 3, 2), x * np.float32(2.0))
