@@ -138,6 +138,17 @@ EmittedKernel emit_row(const Module& m, const KernelAnalysis& a, const LaunchSpe
     auto cls = [&](int id) { return a.row_class[id]; };
     auto vname = [&](int id) { return (a.by_id[id]->tile ? "v" : "s") + std::to_string(id); };
     auto tord = [&](int id) { return a.tensor_ordinal[a.param_of[id]]; };
+    // Row loops: the in-kernel loops run inside each row's lane team; params
+    // they do not move are read once / accumulated in registers.
+    const int ni = spec.row_loops ? static_cast<int>(L.inner.size()) : 0;
+    const int nvars = ng + ni;
+    std::vector<bool> moving(ntens, false);
+    for (int p = 0; p < ntens; ++p)
+        for (int i = 0; i < ni; ++i)
+            for (const auto& e : L.targs[p]->idx) moving[p] = moving[p] || reads_var(e, L.inner[i].var);
+    auto base = [&](int p) {
+        return moving[p] ? "(tb" + std::to_string(p) + "[u] + io" + std::to_string(p) + ")" : "tb" + std::to_string(p) + "[u]";
+    };
 
     // Values loaded up front: preloaded params and Load results.
     std::vector<std::pair<int, int>> loads;  // value id, tensor ordinal
@@ -150,9 +161,10 @@ EmittedKernel emit_row(const Module& m, const KernelAnalysis& a, const LaunchSpe
 
     // A stored tensor that is also read: wait for outstanding loads before stores.
     std::set<int> read_t, stored_t;
-    for (const auto& [id, p] : loads) read_t.insert(L.targs[p]->tid);
+    for (const auto& [id, p] : loads)
+        if (!ni || moving[p]) read_t.insert(L.targs[p]->tid);
     for (int p = 0; p < ntens; ++p)
-        if (a.stored[p]) stored_t.insert(L.targs[p]->tid);
+        if (a.stored[p] && (!ni || moving[p])) stored_t.insert(L.targs[p]->tid);
     bool rw_alias = false;
     for (int t : stored_t)
         if (read_t.count(t)) rw_alias = true;
@@ -176,7 +188,7 @@ EmittedKernel emit_row(const Module& m, const KernelAnalysis& a, const LaunchSpe
     emit_scalars(o, a, false);
     o << "  const i64 total = A.ntasks * R;\n";
     o << "  const i64 nch = (total + CH - 1) / CH;\n";
-    o << "  i64 vars[" << (ng > 0 ? ng : 1) << "];\n  (void)vars;\n";
+    o << "  i64 vars[" << (nvars > 0 ? nvars : 1) << "];\n  (void)vars;\n";
     o << "  for (i64 ch = (i64)blockIdx.x * WPB + wave; ch < nch; ch += (i64)gridDim.x * WPB) {\n";
     o << "    int rr[UP]; bool ok[UP];\n";
     for (int p = 0; p < ntens; ++p) o << "    char* tb" << p << "[UP];\n";
@@ -202,30 +214,59 @@ EmittedKernel emit_row(const Module& m, const KernelAnalysis& a, const LaunchSpe
         o << "    }\n";
     }
     // Phase 1: every load of the chunk, so UP*NV vector loads per value are in flight.
+    std::string ind1 = "    ";
+    auto phase1 = [&](bool want_moving) {
     for (const auto& [id, p] : loads) {
+        if (ni && moving[p] != want_moving) continue;
+        const std::string tbp = base(p);
         switch (cls(id)) {
             case RowClass::Full:
-                o << "    RS ld" << id << "[UP];\n#pragma unroll\n    for (int u = 0; u < UP; ++u) row_load<NV, VW, G" << nt << ">(ld" << id
-                  << "[u], (const float*)tb" << p << "[u] + (i64)rr[u] * A.s3[" << p << "], A.s4[" << p << "], j);\n";
+                o << ind1 << "RS ld" << id << "[UP];\n#pragma unroll\n" << ind1 << "for (int u = 0; u < UP; ++u) row_load<NV, VW, G" << nt << ">(ld" << id
+                  << "[u], (const float*)" << tbp << " + (i64)rr[u] * A.s3[" << p << "], A.s4[" << p << "], j);\n";
                 break;
             case RowClass::RowVec:
-                o << "    float ld" << id << "[UP];\n#pragma unroll\n    for (int u = 0; u < UP; ++u) ld" << id
-                  << "[u] = ((const float*)tb" << p << "[u])[(i64)rr[u] * A.s3[" << p << "]];\n";
+                o << ind1 << "float ld" << id << "[UP];\n#pragma unroll\n" << ind1 << "for (int u = 0; u < UP; ++u) ld" << id
+                  << "[u] = ((const float*)" << tbp << ")[(i64)rr[u] * A.s3[" << p << "]];\n";
                 break;
             case RowClass::RowVecT:
-                o << "    float ld" << id << "[UP];\n#pragma unroll\n    for (int u = 0; u < UP; ++u) ld" << id
-                  << "[u] = ((const float*)tb" << p << "[u])[(i64)rr[u] * A.s4[" << p << "]];\n";
+                o << ind1 << "float ld" << id << "[UP];\n#pragma unroll\n" << ind1 << "for (int u = 0; u < UP; ++u) ld" << id
+                  << "[u] = ((const float*)" << tbp << ")[(i64)rr[u] * A.s4[" << p << "]];\n";
                 break;
             case RowClass::ColVec:
-                o << "    RS ld" << id << "[UP];\n#pragma unroll\n    for (int u = 0; u < UP; ++u) row_load<NV, VW, G>(ld" << id
-                  << "[u], (const float*)tb" << p << "[u], A.s4[" << p << "], j);\n";
+                o << ind1 << "RS ld" << id << "[UP];\n#pragma unroll\n" << ind1 << "for (int u = 0; u < UP; ++u) row_load<NV, VW, G>(ld" << id
+                  << "[u], (const float*)" << tbp << ", A.s4[" << p << "], j);\n";
                 break;
             case RowClass::ColVecT:
-                o << "    RS ld" << id << "[UP];\n#pragma unroll\n    for (int u = 0; u < UP; ++u) row_load_strided<NV, VW, G>(ld"
-                  << id << "[u], (const float*)tb" << p << "[u], A.s3[" << p << "], j);\n";
+                o << ind1 << "RS ld" << id << "[UP];\n#pragma unroll\n" << ind1 << "for (int u = 0; u < UP; ++u) row_load_strided<NV, VW, G>(ld"
+                  << id << "[u], (const float*)" << tbp << ", A.s3[" << p << "], j);\n";
                 break;
             default: throw CompileError("row program: bad load class");
         }
+    }
+    };
+    phase1(false);
+    if (ni) {
+        // Accumulators that are stored but never read: their registers.
+        for (int p = 0; p < ntens; ++p) {
+            const int pid = k.params[a.tensor_param_index[p]].id;
+            if (moving[p] || !a.stored[p] || a.preload[pid]) continue;
+            o << "    " << (cls(pid) == RowClass::Full ? "RS" : "float") << " ld" << pid << "[UP];\n";
+        }
+        o << "    i64 iters_ = 1;\n";
+        for (int i = 0; i < ni; ++i) o << "    iters_ *= A.ext[" << ng + i << "];\n";
+        o << "    for (i64 it_ = 0; it_ < iters_; ++it_) {\n";
+        o << "    { i64 q_ = it_;\n";
+        for (int i = ni - 1; i >= 0; --i)
+            o << "      vars[" << ng + i << "] = q_ % A.ext[" << ng + i << "]; q_ /= A.ext[" << ng + i << "];\n";
+        o << "    }\n";
+        for (int p = 0; p < ntens; ++p) {
+            if (!moving[p]) continue;
+            const int es = dtype_size(a.by_id[k.params[a.tensor_param_index[p]].id]->dtype);
+            o << "    const i64 io" << p << " = ((i64)0";
+            for (int i = 0; i < ni; ++i) o << " + A.coef[" << p << "][" << ng + i << "] * vars[" << ng + i << "]";
+            o << ") * " << es << ";\n";
+        }
+        phase1(true);
     }
     // Phase 2: compute and store each pass.
     o << "#pragma unroll\n    for (int u = 0; u < UP; ++u) {\n";
@@ -248,11 +289,16 @@ EmittedKernel emit_row(const Module& m, const KernelAnalysis& a, const LaunchSpe
                     o << "      __builtin_amdgcn_s_waitcnt(0);\n";
                     waited = true;
                 }
+                if (ni && !moving[p]) {
+                    // An accumulator: the register copy, written back after the loops.
+                    if (s != d) o << "      ld" << d << "[u] = " << vname(s) << ";\n";
+                    break;
+                }
                 if (cls(s) == RowClass::Full)
-                    o << "      if (ok[u]) row_store<NV, VW, G" << nt << ">((float*)tb" << p << "[u] + (i64)rr[u] * A.s3[" << p << "], "
+                    o << "      if (ok[u]) row_store<NV, VW, G" << nt << ">((float*)" << base(p) << " + (i64)rr[u] * A.s3[" << p << "], "
                       << vname(s) << ", A.s4[" << p << "], j);\n";
                 else
-                    o << "      if (ok[u] && j == 0) ((float*)tb" << p << "[u])[(i64)rr[u] * A.s3[" << p << "]] = " << vname(s)
+                    o << "      if (ok[u] && j == 0) ((float*)" << base(p) << ")[(i64)rr[u] * A.s3[" << p << "]] = " << vname(s)
                       << ";\n";
                 break;
             }
@@ -320,7 +366,23 @@ EmittedKernel emit_row(const Module& m, const KernelAnalysis& a, const LaunchSpe
             default: throw CompileError("row program: unexpected op " + op.kind_name);
         }
     }
-    o << "    }\n  }\n}\n";
+    o << "    }\n";
+    if (ni) {
+        o << "    }\n";  // in-kernel loops
+        // Accumulators back to memory.
+        for (int p = 0; p < ntens; ++p) {
+            const int pid = k.params[a.tensor_param_index[p]].id;
+            if (moving[p] || !a.stored[p]) continue;
+            o << "#pragma unroll\n    for (int u = 0; u < UP; ++u) {\n";
+            if (cls(pid) == RowClass::Full)
+                o << "      if (ok[u]) row_store<NV, VW, G" << nt << ">((float*)tb" << p << "[u] + (i64)rr[u] * A.s3[" << p << "], ld" << pid
+                  << "[u], A.s4[" << p << "], j);\n";
+            else
+                o << "      if (ok[u] && j == 0) ((float*)tb" << p << "[u])[(i64)rr[u] * A.s3[" << p << "]] = ld" << pid << "[u];\n";
+            o << "    }\n";
+        }
+    }
+    o << "  }\n}\n";
     ek.source = o.str();
     return ek;
 }
@@ -1161,7 +1223,8 @@ EmittedKernel emit_launch(const Module& m, const KernelAnalysis& a, const Launch
     if (spec.decode && a.family == Family::Decode && !spec.serial) return emit_decode(m, a, L, spec);
     bool indirect = false;
     for (int c : spec.indirect_count) indirect = indirect || c > 0;
-    if (a.family == Family::RowProgram && L.inner.empty() && !indirect && !spec.serial) return emit_row(m, a, L, spec);
+    if (a.family == Family::RowProgram && (L.inner.empty() || spec.row_loops) && !indirect && !spec.serial)
+        return emit_row(m, a, L, spec);
     return emit_tile(m, a, L, spec);
 }
 

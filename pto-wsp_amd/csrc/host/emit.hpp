@@ -19,6 +19,9 @@ struct EmitSpec {
     // when tasks of the grid write overlapping memory (the result then
     // depends on the reference's sequential order).
     bool serial = false;
+    // Row programs: the kernel's in-kernel (P.seq) loops run inside each row's
+    // lane team (the host has checked that rows do not depend on each other).
+    bool row_loops = false;
     // Serial launches: the grid variables (bit v) iterated in program order
     // inside a workgroup; the others are decoded from the block index, one
     // group of tasks per workgroup.  0 means all of them.

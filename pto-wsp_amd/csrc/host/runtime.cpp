@@ -472,6 +472,7 @@ struct Tuning {
     bool decode_ordered = false;
     bool serial_groups = true;  // overlapping grids run as parallel groups of in-order tasks
     int tile_threads = 256;     // threads of a tile-program workgroup
+    bool row_loops = true;      // row programs over in-kernel loops
 };
 
 const Tuning& tuning() {
@@ -484,6 +485,7 @@ const Tuning& tuning() {
         if (const char* s = std::getenv("PTOWSP_DECODE_WAVES")) v.decode_waves = std::atoi(s) == 8 ? 8 : 4;
         if (const char* s = std::getenv("PTOWSP_DECODE_ORDERED")) v.decode_ordered = std::atoi(s) != 0;
         if (const char* s = std::getenv("PTOWSP_SERIAL_GROUPS")) v.serial_groups = std::atoi(s) != 0;
+        if (const char* s = std::getenv("PTOWSP_ROW_LOOPS")) v.row_loops = std::atoi(s) != 0;
         if (const char* s = std::getenv("PTOWSP_TILE_THREADS")) {
             const int t = std::atoi(s);
             v.tile_threads = t == 64 || t == 128 || t == 256 || t == 512 ? t : 256;
@@ -641,6 +643,76 @@ bool gemm_allowed(const KernelAnalysis& a, const LaunchSpec& L, const LaunchArgs
     if (((bm - 1) * A.s3[g.c] + bn) * 4 >= lim) return false;
     spec.gemm_pingpong = tuning().gemm_pingpong && bm == 256 && bn == 256 && (g.k == 64 || g.k == 32) &&
                          A.s3[g.a] % 64 == 0 && A.s3[g.b] % 64 == 0;
+    return true;
+}
+
+// Row programs over in-kernel (P.seq) loops: every row of a task runs the
+// whole loop in one lane team, params that the loop does not move stay in
+// registers (read once; stored ones are accumulators written back after the
+// loop), and the others are loaded / stored every iteration.  Rows of one
+// task then run concurrently, so the launch must have no memory dependence
+// between two (row, iteration) pairs except through those accumulators:
+// - an accumulator's tensor is named by no other param, it is stored without
+//   a cast, and no op reads it after its store in an iteration;
+// - a param read every iteration is on a tensor that no param stores;
+// - a param stored every iteration is on a tensor no other param names, and
+//   its elements over (row, column, in-kernel iterations, grid) never repeat.
+// Static in-kernel extents, no indirect indices, not serial.
+bool row_loops_allowed(const KernelAnalysis& a, const LaunchSpec& L, const LaunchArgs& A, const EmitSpec& spec, int ng,
+                       int nvars) {
+    if (a.family != Family::RowProgram || L.inner.empty() || spec.serial || spec.task_list) return false;
+    for (int c : spec.indirect_count)
+        if (c > 0) return false;
+    for (int t : spec.inner_dyn_term)
+        if (t >= 0) return false;
+    const KernelDef& k = *a.def;
+    const size_t np = a.tensor_param_index.size();
+    auto nests = [](std::vector<std::pair<int64_t, int64_t>> dims) {
+        std::sort(dims.begin(), dims.end());
+        int64_t span = 1;
+        for (const auto& [c, e] : dims) {
+            if (e <= 1) continue;
+            if (c < span) return false;
+            span += c * (e - 1);
+        }
+        return true;
+    };
+    for (size_t p = 0; p < np; ++p) {
+        const int pid = k.params[a.tensor_param_index[p]].id;
+        const ValueInfo* vp = a.by_id[pid];
+        bool moves = false;
+        for (int v = ng; v < nvars; ++v) moves = moves || A.coef[p][v] != 0;
+        bool alone = true, stored_elsewhere = false;
+        for (size_t q = 0; q < np; ++q) {
+            if (q == p || L.targs[q]->tid != L.targs[p]->tid) continue;
+            alone = false;
+            if (a.stored[q]) stored_elsewhere = true;
+        }
+        if (!a.stored[p]) {
+            if (stored_elsewhere) return false;  // read while another param writes the tensor
+            continue;
+        }
+        if (!alone) return false;
+        // Stores of the same dtype (row programs are f32), no read after a store.
+        bool stored = false;
+        for (const auto& op : k.ops)
+            for (size_t j = 0; j < op.operands.size(); ++j) {
+                if (op.operands[j] != pid) continue;
+                const bool is_store = op.kind == OpKind::Store && j == 0;
+                if (!is_store && stored) return false;
+                if (is_store) {
+                    stored = true;
+                    if (a.by_id[op.operands[1]]->dtype != vp->dtype) return false;
+                }
+            }
+        if (moves) {
+            std::vector<std::pair<int64_t, int64_t>> dims;
+            dims.emplace_back(std::llabs(A.s3[p]), vp->rows);
+            dims.emplace_back(std::llabs(A.s4[p]), vp->cols);
+            for (int v = 0; v < nvars; ++v) dims.emplace_back(std::llabs(A.coef[p][v]), A.ext[v]);
+            if (!nests(dims)) return false;
+        }
+    }
     return true;
 }
 
@@ -934,6 +1006,7 @@ BuiltLaunch build_launch(RunEnv& E, const LaunchSpec& L) {
         B.spec.gemm_pingpong = false;
     }
     B.spec.decode = decode_allowed(a, L, A, B.spec, ng);
+    B.spec.row_loops = tuning().row_loops && row_loops_allowed(a, L, A, B.spec, ng, nvars);
     B.spec.decode_ring = tuning().decode_ring;
     B.spec.decode_waves = tuning().decode_waves;
     B.spec.decode_ordered = tuning().decode_ordered;
@@ -950,7 +1023,7 @@ BuiltLaunch build_launch(RunEnv& E, const LaunchSpec& L) {
 std::string spec_key(const EmitSpec& s) {
     std::ostringstream o;
     o << "vw" << s.vec_width << (s.serial ? ";serial" + std::to_string(s.seq_mask) : "") << (s.task_list ? ";tl" : "") << ";up" << s.row_up << (s.nontemporal ? ";nt" : "")
-      << (s.gemm ? ";gemm" : "") << ";m" << s.gemm_vm << ";n" << s.gemm_vn << (s.gemm_pingpong ? ";pp" : "")
+      << (s.row_loops ? ";rl" : "") << (s.gemm ? ";gemm" : "") << ";m" << s.gemm_vm << ";n" << s.gemm_vn << (s.gemm_pingpong ? ";pp" : "")
       << (s.decode ? ";dec" : "")
       << (s.decode_norm ? ";norm" : "") << ";t" << s.threads << ";r" << s.decode_ring << ";w" << s.decode_waves << (s.decode_ordered ? ";ord" : "")
       << ";i";
@@ -1643,6 +1716,7 @@ int ptowsp_hip_precompile(ptowsp_program* P, int index, int flags, const char** 
             EmitSpec spec;
             spec.serial = (flags & 1) != 0;
             spec.seq_mask = spec.serial ? static_cast<uint32_t>((flags >> 8) & 0xFF) : 0u;
+            spec.row_loops = (flags & 16) && !spec.serial && a.family == Family::RowProgram && !L.inner.empty();
             spec.row_up = tuning().row_up;
             spec.nontemporal = tuning().nontemporal;
             spec.gemm = a.family == Family::Gemm && !spec.serial;

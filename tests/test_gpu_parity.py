@@ -862,3 +862,17 @@ def test_row_program_store_into_a_transposed_view(gpu):
 
     run_hip(W.rr4(wl()))
     np.testing.assert_array_equal(y_base.transpose(0, 1, 3, 2), x * np.float32(2.0))
+
+
+def test_softmax_three_phase_row_loops(gpu):
+    """examples/softmax with 8 vocab tiles (disjoint views): the two launches with P.seq
+    accumulators run as row programs over their in-kernel loop (accumulators in registers,
+    butterfly reductions), within rtol 1e-5 of the oracle's sequential order."""
+    lg = (0.1 * np.random.default_rng(2).standard_normal((2, 64, 512), dtype=np.float32)).astype(np.float32)
+    ga, ca = W.softmax3_arrays(lg), W.softmax3_arrays(lg)
+    prog = run_hip(W.rr4(W.softmax3(ga)))
+    ref = run_workload(W.rr4(W.softmax3(ca)))
+    for k in ("probs", "rmax", "rsum"):
+        np.testing.assert_allclose(ga[k], ca[k], rtol=1e-5, atol=1e-7)
+    np.testing.assert_array_equal(ga["rmax"], ca["rmax"])  # max is exact in any order
+    assert prog.stats.total_cycles == ref.total_cycles

@@ -238,3 +238,17 @@ def test_select_without_bound_symbols_runs_nothing():
     build = workload_to_codegen_ir(w, "s")
     got = NativeProgram(build.module).cycle_model(build.tensors, {}, {}, {})
     assert got.task_count == 0
+
+
+def test_row_loop_variant_builds_for_gfx950():
+    """exp_and_accumulate (launch 1 of the three-phase softmax) as a row program over its
+    in-kernel loop: the fixed running max and running sum stay in registers, the x tile is
+    loaded and the y tile stored every iteration, the sum is written back after the loop."""
+    from pto_wsp._hip import NativeProgram
+
+    lg = np.zeros((1, 32, 512), np.float32)
+    prog = NativeProgram(workload_to_codegen_ir(W.rr4(W.softmax3(W.softmax3_arrays(lg))), "s3").module)
+    src = prog.precompile(1, row_loops=True)
+    assert "row program" in src and "for (i64 it_ = 0; it_ < iters_; ++it_)" in src
+    assert "(tb0[u] + io0)" in src and "(tb2[u] + io2)" in src and "io1" not in src and "io3" not in src
+    assert "ld4[u] = v8;" in src
