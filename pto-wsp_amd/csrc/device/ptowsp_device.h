@@ -204,13 +204,48 @@ __device__ inline RowSlice<NV, VW> ew_rsqrt(const RowSlice<NV, VW>& a) {
 __device__ inline float half_bits_to_f32(u16 h) { return static_cast<float>(__builtin_bit_cast(_Float16, h)); }
 __device__ inline float bf16_bits_to_f32(u16 b) { return __uint_as_float(static_cast<u32>(b) << 16); }
 
-__device__ inline u16 f32_to_half_bits(float f) { return __builtin_bit_cast(u16, static_cast<_Float16>(f)); }
+// f32 -> f16, round to nearest even.  The empty asm makes f an opaque f32
+// register value: without it the compiler folds a producing f32 multiply
+// into the conversion (v_fma_mixlo_f16: one rounding of the exact product,
+// where the oracle rounds the product to f32 and then to f16).
+__device__ inline u16 f32_to_half_bits(float f) {
+    asm("" : "+v"(f));
+    return __builtin_bit_cast(u16, static_cast<_Float16>(f));
+}
 
 // Round-to-nearest-even f32 -> bf16 (NaN stays NaN).
 __device__ inline u16 f32_to_bf16_bits(float f) {
     const u32 x = __float_as_uint(f);
     if ((x & 0x7FFFFFFFu) > 0x7F800000u) return static_cast<u16>((x >> 16) | 0x40u);
     return static_cast<u16>((x + 0x7FFFu + ((x >> 16) & 1u)) >> 16);
+}
+
+// Row store into a 16-bit float tile (DT 0: f16, 1: bf16), each element
+// rounded to nearest even as tile_store_f does; the same lane layout as
+// row_store, VW 16-bit values per chunk.
+template <int DT>
+__device__ inline u16 f32_to_h16_bits(float f) {
+    if constexpr (DT == 0) return f32_to_half_bits(f);
+    else return f32_to_bf16_bits(f);
+}
+template <int NV, int VW, int G, int DT>
+__device__ inline void row_store_h(u16* p, const RowSlice<NV, VW>& r, i64 s4, int j) {
+    if constexpr (VW == 4) {
+#pragma unroll
+        for (int k = 0; k < NV; ++k) {
+            const u32 lo = f32_to_h16_bits<DT>(r.v[k * 4 + 0]) | (static_cast<u32>(f32_to_h16_bits<DT>(r.v[k * 4 + 1])) << 16);
+            const u32 hi = f32_to_h16_bits<DT>(r.v[k * 4 + 2]) | (static_cast<u32>(f32_to_h16_bits<DT>(r.v[k * 4 + 3])) << 16);
+            *reinterpret_cast<uint2*>(p + (k * G + j) * 4) = make_uint2(lo, hi);
+        }
+    } else if constexpr (VW == 2) {
+#pragma unroll
+        for (int k = 0; k < NV; ++k)
+            *reinterpret_cast<u32*>(p + (k * G + j) * 2) =
+                f32_to_h16_bits<DT>(r.v[k * 2 + 0]) | (static_cast<u32>(f32_to_h16_bits<DT>(r.v[k * 2 + 1])) << 16);
+    } else {
+#pragma unroll
+        for (int k = 0; k < NV; ++k) p[static_cast<i64>(k * G + j) * s4] = f32_to_h16_bits<DT>(r.v[k]);
+    }
 }
 
 // Element loaders from global memory, widened to float (or int).

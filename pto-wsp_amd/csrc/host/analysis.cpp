@@ -44,10 +44,19 @@ bool classify_rows(const KernelDef& k, KernelAnalysis& a) {
             op.kind == OpKind::StoreTopkIndices)
             return no("top-k ops");
     }
+    // A 16-bit float param that is only ever a Store destination receives
+    // the store cast; every value of the program stays f32.
+    auto cast_out = [&](const ValueInfo& v) {
+        if ((v.dtype != DType::F16 && v.dtype != DType::BF16) || a.param_of[v.id] < 0 || a.preload[v.id]) return false;
+        for (const auto& op : k.ops)
+            for (size_t j = 0; j < op.operands.size(); ++j)
+                if (op.operands[j] == v.id && !(op.kind == OpKind::Store && j == 0)) return false;
+        return true;
+    };
     int R = 0, C = 0;
     for (const auto& v : k.values) {
         if (!v.tile) continue;
-        if (v.dtype != DType::F32) return no("non-f32 tile");
+        if (v.dtype != DType::F32 && !cast_out(v)) return no("non-f32 tile");
         if (v.cols > C || (v.cols == C && v.rows > R)) {
             C = v.cols;
             R = v.rows;

@@ -5,7 +5,9 @@
 // 1/sqrt, Matmul as an fp32 accumulation that ignores a third operand.
 #include "emit.hpp"
 
+#include <algorithm>
 #include <cstdio>
+#include <map>
 #include <set>
 #include <sstream>
 
@@ -213,6 +215,23 @@ EmittedKernel emit_row(const Module& m, const KernelAnalysis& a, const LaunchSpe
         }
         o << "    }\n";
     }
+    // Store of value `val` (f32) into param `dparam` (tensor ordinal p) at
+    // base pointer `basep`, with the f16 / bf16 store cast for a 16-bit param.
+    auto store_row = [&](const std::string& ind, int p, int dparam, const std::string& basep, const std::string& val, bool full) {
+        const DType dt = a.by_id[dparam]->dtype;
+        const std::string ps = std::to_string(p);
+        if (full && dt == DType::F32)
+            o << ind << "if (ok[u]) row_store<NV, VW, G" << nt << ">((float*)" << basep << " + (i64)rr[u] * A.s3[" << ps << "], " << val
+              << ", A.s4[" << ps << "], j);\n";
+        else if (full)
+            o << ind << "if (ok[u]) row_store_h<NV, VW, G, " << dt_code(dt) << ">((u16*)" << basep << " + (i64)rr[u] * A.s3[" << ps
+              << "], " << val << ", A.s4[" << ps << "], j);\n";
+        else if (dt == DType::F32)
+            o << ind << "if (ok[u] && j == 0) ((float*)" << basep << ")[(i64)rr[u] * A.s3[" << ps << "]] = " << val << ";\n";
+        else
+            o << ind << "if (ok[u] && j == 0) ((u16*)" << basep << ")[(i64)rr[u] * A.s3[" << ps << "]] = f32_to_h16_bits<" << dt_code(dt)
+              << ">(" << val << ");\n";
+    };
     // Phase 1: every load of the chunk, so UP*NV vector loads per value are in flight.
     std::string ind1 = "    ";
     auto phase1 = [&](bool want_moving) {
@@ -294,12 +313,7 @@ EmittedKernel emit_row(const Module& m, const KernelAnalysis& a, const LaunchSpe
                     if (s != d) o << "      ld" << d << "[u] = " << vname(s) << ";\n";
                     break;
                 }
-                if (cls(s) == RowClass::Full)
-                    o << "      if (ok[u]) row_store<NV, VW, G" << nt << ">((float*)" << base(p) << " + (i64)rr[u] * A.s3[" << p << "], "
-                      << vname(s) << ", A.s4[" << p << "], j);\n";
-                else
-                    o << "      if (ok[u] && j == 0) ((float*)" << base(p) << ")[(i64)rr[u] * A.s3[" << p << "]] = " << vname(s)
-                      << ";\n";
+                store_row("      ", p, d, base(p), vname(s), cls(s) == RowClass::Full);
                 break;
             }
             case OpKind::Add: case OpKind::Sub: case OpKind::Mul: case OpKind::Div: case OpKind::Max: case OpKind::Min: {
@@ -374,11 +388,7 @@ EmittedKernel emit_row(const Module& m, const KernelAnalysis& a, const LaunchSpe
             const int pid = k.params[a.tensor_param_index[p]].id;
             if (moving[p] || !a.stored[p]) continue;
             o << "#pragma unroll\n    for (int u = 0; u < UP; ++u) {\n";
-            if (cls(pid) == RowClass::Full)
-                o << "      if (ok[u]) row_store<NV, VW, G" << nt << ">((float*)tb" << p << "[u] + (i64)rr[u] * A.s3[" << p << "], ld" << pid
-                  << "[u], A.s4[" << p << "], j);\n";
-            else
-                o << "      if (ok[u] && j == 0) ((float*)tb" << p << "[u])[(i64)rr[u] * A.s3[" << p << "]] = ld" << pid << "[u];\n";
+            store_row("      ", p, pid, "tb" + std::to_string(p) + "[u]", "ld" + std::to_string(pid) + "[u]", cls(pid) == RowClass::Full);
             o << "    }\n";
         }
     }
@@ -479,14 +489,52 @@ EmittedKernel emit_tile(const Module& m, const KernelAnalysis& a, const LaunchSp
     }
     auto staged_id = [&](int id) { const int p = tord(id); return p >= 0 && staged[p]; };
 
-    // LDS tiles: op results, preloaded and resident params.
+    // LDS tiles: op results, preloaded and resident params, placed in one pool
+    // by lifetime.  Every op ends with a workgroup barrier, so a tile whose
+    // last reader is op i can share bytes with a tile first written by an op
+    // after i; a tile written or read by op i does not share with another
+    // tile live at op i.  Preloaded params are live from before op 0,
+    // resident params for the whole task (prologue to epilogue).
     std::set<int> lds_vals;
     for (const auto& op : k.ops)
         if (op.result > 0 && a.by_id[op.result]->tile) lds_vals.insert(op.result);
     for (const auto& p : k.params)
         if (a.by_id[p.id]->tile && (a.preload[p.id] || resident_id(p.id)) && !staged_id(p.id)) lds_vals.insert(p.id);
-    size_t lds = 0;
-    for (int id : lds_vals) lds += static_cast<size_t>(a.by_id[id]->rows) * a.by_id[id]->cols * (is_int_v(id) ? 8 : 4);
+    const int nops = static_cast<int>(k.ops.size());
+    std::map<int, std::pair<int, int>> life;  // tile -> [first op, last op] (-1: before op 0)
+    for (int id : lds_vals) life[id] = resident_id(id) ? std::make_pair(-1, nops) : std::make_pair(a.param_of[id] >= 0 ? -1 : nops, -1);
+    for (int oi = 0; oi < nops; ++oi) {
+        const auto& op = k.ops[oi];
+        if (op.result > 0 && life.count(op.result)) {
+            auto& l = life[op.result];
+            l.first = std::min(l.first, oi);
+            l.second = std::max(l.second, oi);
+        }
+        for (int id : op.operands)
+            if (life.count(id)) {
+                auto& l = life[id];
+                l.first = std::min(l.first, oi);
+                l.second = std::max(l.second, oi);
+            }
+    }
+    auto tile_bytes = [&](int id) { return static_cast<size_t>(a.by_id[id]->rows) * a.by_id[id]->cols * (is_int_v(id) ? 8 : 4); };
+    std::vector<int> order(lds_vals.begin(), lds_vals.end());
+    std::stable_sort(order.begin(), order.end(), [&](int x, int y) { return tile_bytes(x) > tile_bytes(y); });
+    std::map<int, size_t> lds_off;
+    size_t pool = 0;
+    for (int id : order) {
+        const size_t sz = (tile_bytes(id) + 15) & ~static_cast<size_t>(15);
+        std::vector<std::pair<size_t, size_t>> busy;
+        for (const auto& [q, off] : lds_off)
+            if (life[q].first <= life[id].second && life[id].first <= life[q].second) busy.push_back({off, off + ((tile_bytes(q) + 15) & ~static_cast<size_t>(15))});
+        std::sort(busy.begin(), busy.end());
+        size_t off = 0;
+        for (const auto& [lo, hi] : busy)
+            if (off + sz > lo && off < hi) off = hi;
+        lds_off[id] = off;
+        pool = std::max(pool, off + sz);
+    }
+    size_t lds = pool;
     for (const auto& p : k.params)
         if (staged_id(p.id)) lds += static_cast<size_t>(SB) * a.by_id[p.id]->rows * a.by_id[p.id]->cols * (is_int_v(p.id) ? 8 : 4);
     if (lds > 160 * 1024)
@@ -499,14 +547,16 @@ EmittedKernel emit_tile(const Module& m, const KernelAnalysis& a, const LaunchSp
     ek.lds_bytes = lds;
     std::ostringstream o;
     o << "#include \"ptowsp_device.h\"\nusing namespace ptowsp;\n";
-    o << "// tile program: kernel " << k.name << "\n";
+    o << "// tile program: kernel " << k.name;
+    if (!a.not_row_reason.empty()) o << " (not a row program: " << a.not_row_reason << ")";
+    o << "\n";
     ek.entry = entry_name("tile", k);
     o << "extern \"C\" __global__ void __launch_bounds__(" << spec.threads << ") " << ek.entry << "(const LaunchArgs A) {\n";
     o << "  constexpr int NT = " << spec.threads << ";\n";
+    if (pool > 0) o << "  __shared__ __attribute__((aligned(16))) char pool_[" << pool << "];\n";
     for (int id : lds_vals) {
-        const ValueInfo* v = a.by_id[id];
-        o << "  __shared__ __attribute__((aligned(16))) " << (is_int_v(id) ? "i64" : "float") << " L" << id << "[" << v->rows * v->cols
-          << "];\n";
+        const char* ty = is_int_v(id) ? "i64" : "float";
+        o << "  " << ty << "* const L" << id << " = reinterpret_cast<" << ty << "*>(pool_ + " << lds_off[id] << ");\n";
     }
     for (const auto& p : k.params)
         if (staged_id(p.id)) {

@@ -652,8 +652,8 @@ bool gemm_allowed(const KernelAnalysis& a, const LaunchSpec& L, const LaunchArgs
 // loop), and the others are loaded / stored every iteration.  Rows of one
 // task then run concurrently, so the launch must have no memory dependence
 // between two (row, iteration) pairs except through those accumulators:
-// - an accumulator's tensor is named by no other param, it is stored without
-//   a cast, and no op reads it after its store in an iteration;
+// - an accumulator's tensor is named by no other param, and no op reads it
+//   after its store in an iteration;
 // - a param read every iteration is on a tensor that no param stores;
 // - a param stored every iteration is on a tensor no other param names, and
 //   its elements over (row, column, in-kernel iterations, grid) never repeat.
@@ -693,17 +693,15 @@ bool row_loops_allowed(const KernelAnalysis& a, const LaunchSpec& L, const Launc
             continue;
         }
         if (!alone) return false;
-        // Stores of the same dtype (row programs are f32), no read after a store.
+        // No read after a store (a 16-bit param is never read: it only takes
+        // the store cast, at every store or when written back).
         bool stored = false;
         for (const auto& op : k.ops)
             for (size_t j = 0; j < op.operands.size(); ++j) {
                 if (op.operands[j] != pid) continue;
                 const bool is_store = op.kind == OpKind::Store && j == 0;
                 if (!is_store && stored) return false;
-                if (is_store) {
-                    stored = true;
-                    if (a.by_id[op.operands[1]]->dtype != vp->dtype) return false;
-                }
+                stored = stored || is_store;
             }
         if (moves) {
             std::vector<std::pair<int64_t, int64_t>> dims;

@@ -4,8 +4,9 @@ Each case runs the same seeded workload on the HIP target and on the CPU
 oracle (whose results tests/test_oracle_ops.py pins bit for bit against
 float64 arithmetic and numpy's float16 cast) and requires identical bits:
 every op here is one correctly rounded fp32 operation or an exact min / max,
-and the casts round to nearest even.  f32 outputs run on the row program;
-F16 / BF16 outputs move the same kernel onto the tile program.
+and the casts round to nearest even.  These kernels run as row programs (the
+F16 / BF16 outputs through row_store_h); the rounding probe also runs through
+the tile program's cast (tile_store_f).
 """
 
 import numpy as np
@@ -73,14 +74,15 @@ def test_scalar_left_variant(gpu, op, out_dtype):
     np.testing.assert_array_equal(ga["out"].view(np.uint8), ca["out"].view(np.uint8))
 
 
+@pytest.mark.parametrize("family", ["row", "tile"])
 @pytest.mark.parametrize("out_dtype", [F16, BF16], ids=["f16", "bf16"])
-def test_store_cast_rounding_probe(gpu, out_dtype):
+def test_store_cast_rounding_probe(gpu, out_dtype, family):
     vals = W.rounding_probe_f32(6000, seed=13, for_bf16=out_dtype == BF16)
     R, C = 16, 32
     reps = -(-len(vals) // (R * C))
     x = np.resize(vals, reps * R * C).astype(np.float32).reshape(1, reps, R, C)
     arrs = {"x": x, "out": np.zeros(x.shape, NP_OUT[out_dtype])}
-    ga, ca = _pair(lambda a: W.store_cast(a, out_dtype), arrs)
+    ga, ca = _pair(lambda a: W.store_cast(a, out_dtype, via_tile=family == "tile"), arrs)
     np.testing.assert_array_equal(ga["out"].view(np.uint16), ca["out"].view(np.uint16))
     if out_dtype == F16:
         with np.errstate(over="ignore"):

@@ -851,11 +851,30 @@ def scalar_binary(arrs: dict, op: str, value: float, left: bool = False, out_dty
     return wl()
 
 
-def store_cast(arrs: dict, out_dtype):
-    """out (F16 / BF16 tile) = x (f32 tile): the TCVT CAST_RINT store (src/python/pto_codegen.cpp:955-976)."""
+def store_cast(arrs: dict, out_dtype, via_tile: bool = False):
+    """out (F16 / BF16 tile) = x (f32 tile): the TCVT CAST_RINT store (src/python/pto_codegen.cpp:955-976).
+    via_tile=True adds a [R, 2C] input and an op on it whose result nothing reads: the kernel's
+    tiles then share no row shape, so the cast runs on the tile program instead of a row program."""
     x = arrs["x"]
     B, NT, R, C = x.shape
     X, O = T(x), T(arrs["out"], out_dtype)
+
+    if via_tile:
+        WD = T(np.zeros((B, NT, R, 2 * C), np.float32) if isinstance(x, np.ndarray) else
+               __import__("torch").zeros((B, NT, R, 2 * C), device=x.device))
+
+        @kernel
+        def cast_tile(x_t: In[Tile[R, C, F32]], wide: In[Tile[R, 2 * C, F32]], out: Out[Tile[R, C, out_dtype]]):
+            pto.max(wide, wide)
+            pto.store(out, x_t)
+
+        @workload
+        def wl():
+            for b in P(Dense[B]()):
+                for t in P(Dense[NT]()):
+                    cast_tile[b, t](x_t=X[b][t], wide=WD[b][t], out=O[b][t])
+
+        return wl()
 
     @kernel
     def cast_tile(x_t: In[Tile[R, C, F32]], out: Out[Tile[R, C, out_dtype]]):
