@@ -303,7 +303,8 @@ static void parse_kernel(Lex* L, Kernel* k) {
     k->nparams = (int)tok_i64(L);
     k->nops = (int)tok_i64(L);
     k->custom = (int)tok_i64(L);
-    if (k->custom) (void)tok_str(L); /* the cpp_src body: compiled by the caller, reached via get_kernel */
+    if (k->custom) (void)tok_str(L); /* the cpp_src body (1) or cpp_tu_path file (2): compiled by the caller,
+                                        reached via get_kernel */
     k->vals = (Val*)alloc(sizeof(Val) * (size_t)(k->nvals + 1));
     k->params = (Param*)alloc(sizeof(Param) * (size_t)(k->nparams + 1));
     k->ops = (Op*)alloc(sizeof(Op) * (size_t)(k->nops + 1));
@@ -1551,10 +1552,10 @@ static uint64_t run_task(Run* R, Node* n, uint64_t ready) {
     }
     uint64_t dur;
     if (k->custom) {
-        /* A cpp_src body, called through the runtime's kernel table with the
+        /* A cpp_src body or cpp_tu_path file, called through the runtime's kernel table with the
          * reference's task descriptor (include/pto/wsp/codegen/abi/kernel_abi.hpp:21-41). */
         KernelFn fn = R->ctx->get_kernel ? R->ctx->get_kernel(R->ctx->ctx, (uint32_t)kidx) : NULL;
-        if (!fn) fail("kernel %s: no compiled cpp_src body", k->name);
+        if (!fn) fail("kernel %s: no compiled custom kernel", k->name);
         uint64_t args[64];
         void* ptrs[32];
         uint64_t strides[64];
@@ -1568,8 +1569,9 @@ static uint64_t run_task(Run* R, Node* n, uint64_t ready) {
             strides[2 * nt + 1] = (uint64_t)vw->s4;
             ++nt;
         }
-        KernelTaskDesc d = {args, (uint32_t)na, (uint32_t)(n->naxis + 2 * nt), ptrs, strides, (uint32_t)nt,
-                            (uint32_t)kidx, (uint32_t)g_tasks};
+        /* kernel_id and task_id are 0, as the reference's artifact passes them
+         * (src/python/pto_codegen.cpp:2645-2649). */
+        KernelTaskDesc d = {args, (uint32_t)na, (uint32_t)(n->naxis + 2 * nt), ptrs, strides, (uint32_t)nt, 0u, 0u};
         dur = fn(&d, NULL);
     } else {
         dur = run_kernel(k, s->w, s->views, s->scal);

@@ -127,8 +127,11 @@ def _decode(tok: str) -> str:
 
 
 def custom_kernels(module_text: str) -> dict:
-    """{kernel index: (library, function address)} for the module's cpp_src kernels, each
-    compiled with g++ into oracle/_build/custom/ (cached by content)."""
+    """{kernel index: (library, function address)} for the module's custom kernels, each
+    compiled with g++ into oracle/_build/custom/ (cached by content): a cpp_src body inside
+    the reference's wrapper (entry ptowsp_oracle_custom), or a cpp_tu_path translation unit
+    as it is, against the ABI headers in oracle/abi/ (entry: the kernel's name, the symbol
+    the reference's workload loop calls, src/python/pto_codegen.cpp:2645-2651)."""
     import hashlib
 
     out = {}
@@ -137,9 +140,11 @@ def custom_kernels(module_text: str) -> dict:
         toks = line.split()
         if not toks or toks[0] != "K":
             continue
-        if len(toks) > 6 and toks[5] == "1":
-            src = _CUSTOM_WRAPPER.replace("@BODY@", _decode(toks[6]))
-            key = hashlib.sha1(src.encode()).hexdigest()[:16]
+        if len(toks) > 6 and toks[5] in ("1", "2"):
+            tu = toks[5] == "2"
+            src = _decode(toks[6]) if tu else _CUSTOM_WRAPPER.replace("@BODY@", _decode(toks[6]))
+            entry = _decode(toks[1]) if tu else "ptowsp_oracle_custom"
+            key = hashlib.sha1((entry + "\n" + src).encode()).hexdigest()[:16]
             if key not in _custom_cache:
                 d = os.path.join(_HERE, "_build", "custom")
                 os.makedirs(d, exist_ok=True)
@@ -147,11 +152,11 @@ def custom_kernels(module_text: str) -> dict:
                 if not os.path.exists(so):
                     open(cpp, "w").write(src)
                     subprocess.run(["g++", "-std=c++17", "-O1", "-D__CPU_SIM=1", "-shared", "-fPIC",
-                                    "-I", os.path.join(os.path.dirname(_HERE), "include"), cpp, "-o", so + ".tmp"],
-                                   check=True)
+                                    "-I", os.path.join(os.path.dirname(_HERE), "include"),
+                                    "-I", os.path.join(_HERE, "abi"), cpp, "-o", so + ".tmp"], check=True)
                     os.replace(so + ".tmp", so)
                 lib = ctypes.CDLL(so)
-                _custom_cache[key] = (lib, ctypes.cast(lib.ptowsp_oracle_custom, ctypes.c_void_p).value)
+                _custom_cache[key] = (lib, ctypes.cast(getattr(lib, entry), ctypes.c_void_p).value)
             out[kidx] = _custom_cache[key]
         kidx += 1
     return out

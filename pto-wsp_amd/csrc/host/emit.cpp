@@ -1206,6 +1206,20 @@ EmittedKernel emit_custom(const Module& m, const KernelAnalysis& a, const Launch
     ek.entry = entry_name("custom", k);
     ek.threads = 64;
     std::ostringstream o;
+    if (k.custom_tu) {
+        // cpp_tu_path: the file itself, compiled as device code against the
+        // ABI headers (kernel_abi.hpp, ptoisa_bridge.hpp: layouts and cycle
+        // counters; no PTO-ISA tile API), defines extern "C" <name>(task,
+        // cspt); the launcher below calls it once per task.
+        o << "// ptowsp: cpp_tu\n#include \"ptowsp_device.h\"\n#define __CPU_SIM 1\n"
+             "#include \"pto/wsp/codegen/abi/kernel_abi.hpp\"\n#include \"pto/wsp/codegen/abi/ptoisa_bridge.hpp\"\n";
+        // Every function of the file without an execution space becomes host
+        // and device code, so its helpers need no annotation.
+        o << "#pragma clang force_cuda_host_device begin\n";
+        o << "#line 1 \"cpp_tu of " << k.name << "\"\n" << k.custom_src << "\n";
+        o << "#pragma clang force_cuda_host_device end\n";
+        o << "using namespace ptowsp;\n";
+    } else {
     o << "#include \"ptowsp_device.h\"\nusing namespace ptowsp;\n";
     o << "#define __CPU_SIM 1\n#define PTO_WSP_KERNEL_ATTR __device__\n";
     // The <cstdint> names a body uses (hiprtc provides them in __hip_internal).
@@ -1227,8 +1241,10 @@ EmittedKernel emit_custom(const Module& m, const KernelAnalysis& a, const Launch
     o << "#line 1 \"cpp_src of " << k.name << "\"\n" << k.custom_src << "\n";
     o << "#if defined(__CPU_SIM)\n  if (cycles == 0) cycles = pto::cpu_sim::read_cycles();\n#endif\n  return cycles;\n}\n";
     o << "#undef add_cycles\n#undef reset_cycles\n#undef read_cycles\n";
+    }
     o << "extern \"C\" __global__ void __launch_bounds__(64) " << ek.entry << "(const LaunchArgs A) {\n";
     o << "  i64 vars[" << (ng > 0 ? ng : 1) << "];\n  (void)vars;\n";
+    if (k.custom_tu) o << "  pto::cpu_sim::reset_cycles();\n";
     if (spec.serial) o << "  if (blockIdx.x != 0 || threadIdx.x != 0) return;\n  for (i64 t = 0; t < A.ntasks; ++t) {\n";
     else o << "  for (i64 t = (i64)blockIdx.x * 64 + threadIdx.x; t < A.ntasks; t += (i64)gridDim.x * 64) {\n";
     o << "    const i64 g = " << (spec.task_list ? "A.tlist[t]" : "t") << ";\n";
@@ -1261,8 +1277,10 @@ EmittedKernel emit_custom(const Module& m, const KernelAnalysis& a, const Launch
         o << "    strides[" << 2 * p << "] = (uint64_t)A.s3[" << p << "]; strides[" << 2 * p + 1 << "] = (uint64_t)A.s4[" << p << "];\n";
         term += nt;
     }
-    o << "    const KernelTaskDesc d = {args, " << nargs << "u, " << (na + 2 * ntens) << "u, ptrs, strides, " << ntens << "u, 0u, (uint32_t)g};\n";
-    o << "    A.cyc[g] = ptowsp_body(&d, nullptr);\n  }\n}\n";
+    // kernel_id and task_id are 0, as the reference's cpu_sim artifact passes
+    // them (src/python/pto_codegen.cpp:2645-2649); cspt is null.
+    o << "    const KernelTaskDesc d = {args, " << nargs << "u, " << (na + 2 * ntens) << "u, ptrs, strides, " << ntens << "u, 0u, 0u};\n";
+    o << "    A.cyc[g] = " << (k.custom_tu ? k.name : std::string("ptowsp_body")) << "(&d, nullptr);\n  }\n}\n";
     ek.source = o.str();
     return ek;
 }

@@ -29,6 +29,72 @@ const char* kOptions[] = {
     "-Xclang", "-target-feature", "-Xclang", "-packed-fp32-ops",
 };
 
+// Headers a cpp_tu_path translation unit includes, as device code: the task
+// descriptor and timing context of the reference's
+// include/pto/wsp/codegen/abi/kernel_abi.hpp:21-71 (same layouts; the file
+// is compiled with every unannotated function as host and device code, so
+// PTO_WSP_KERNEL_ATTR stays empty), the
+// PTO_WSP_ADVANCE macro and pto::cpu_sim cycle counter of
+// include/pto/wsp/codegen/abi/ptoisa_bridge.hpp:33-64 (one counter per
+// launcher thread, zeroed when the launch starts; the PTO-ISA tile API that
+// header also pulls in is not provided), and the <cstdint> / <cstddef> names.
+const char kStdTypes[] = R"(#pragma once
+typedef __hip_internal::int8_t int8_t; typedef __hip_internal::int16_t int16_t;
+typedef __hip_internal::int32_t int32_t; typedef __hip_internal::int64_t int64_t;
+typedef __hip_internal::uint8_t uint8_t; typedef __hip_internal::uint16_t uint16_t;
+typedef __hip_internal::uint32_t uint32_t; typedef __hip_internal::uint64_t uint64_t;
+typedef __SIZE_TYPE__ size_t; typedef __PTRDIFF_TYPE__ ptrdiff_t;
+namespace std { using ::int8_t; using ::int16_t; using ::int32_t; using ::int64_t; using ::uint8_t; using ::uint16_t;
+                using ::uint32_t; using ::uint64_t; using ::size_t; using ::ptrdiff_t; }
+)";
+const char kKernelAbi[] = R"(#pragma once
+#include <cstdint>
+#include <cstddef>
+#define PTO_WSP_KERNEL_ATTR
+extern "C" {
+struct KernelTaskDesc {
+    const uint64_t* args;
+    uint32_t num_args;
+    uint32_t num_axis_args;
+    void* const* tensor_ptrs;
+    const uint64_t* tensor_strides;
+    uint32_t num_tensors;
+    uint32_t kernel_id;
+    uint32_t task_id;
+};
+struct TimingConfig {
+    uint64_t loop_overhead;
+    uint64_t dispatch_overhead;
+    uint64_t channel_latency;
+};
+struct CSPTContext {
+    void* ctx;
+    void (*advance_cycles)(void* ctx, uint64_t cycles);
+    uint64_t (*get_time)(void* ctx);
+    const TimingConfig* timing;
+};
+typedef uint64_t (*KernelFn)(const KernelTaskDesc* task, CSPTContext* cspt);
+}
+)";
+const char kPtoisaBridge[] = R"(#pragma once
+#include "pto/wsp/codegen/abi/kernel_abi.hpp"
+#define PTO_WSP_ADVANCE(cspt_ptr, cycles_expr) \
+    do { \
+        if ((cspt_ptr) && (cspt_ptr)->advance_cycles && (cycles_expr) != 0) \
+            (cspt_ptr)->advance_cycles((cspt_ptr)->ctx, static_cast<uint64_t>(cycles_expr)); \
+    } while (0)
+namespace pto { namespace cpu_sim {
+__device__ inline uint64_t& ptowsp_cycle_counter() {
+    __shared__ uint64_t c[64];
+    return c[threadIdx.x & 63];
+}
+__device__ inline void reset_cycles() { ptowsp_cycle_counter() = 0; }
+__device__ inline void add_cycles(uint64_t cycles) { ptowsp_cycle_counter() += cycles; }
+__device__ inline uint64_t read_cycles() { return ptowsp_cycle_counter(); }
+} }
+)";
+constexpr const char* kTuMarker = "// ptowsp: cpp_tu\n";
+
 std::string options_key() {
     std::string s;
     for (const char* o : kOptions) s += std::string(o) + " ";
@@ -75,9 +141,11 @@ std::string jit_cache_dir() {
 
 std::vector<char> jit_compile(const std::string& source) {
     hiprtcProgram prog = nullptr;
-    const char* headers[] = {kDeviceHeader, kLaunchHeader};
-    const char* names[] = {"ptowsp_device.h", "ptowsp_launch.h"};
-    if (hiprtcCreateProgram(&prog, source.c_str(), "ptowsp_kernel.hip", 2, headers, names) != HIPRTC_SUCCESS)
+    const char* headers[] = {kDeviceHeader, kLaunchHeader, kKernelAbi, kPtoisaBridge, kStdTypes, kStdTypes, kStdTypes, kStdTypes};
+    const char* names[] = {"ptowsp_device.h", "ptowsp_launch.h", "pto/wsp/codegen/abi/kernel_abi.hpp",
+                           "pto/wsp/codegen/abi/ptoisa_bridge.hpp", "cstdint", "cstddef", "stdint.h", "stddef.h"};
+    const int nh = source.rfind(kTuMarker, 0) == 0 ? 8 : 2;
+    if (hiprtcCreateProgram(&prog, source.c_str(), "ptowsp_kernel.hip", nh, headers, names) != HIPRTC_SUCCESS)
         throw CompileError("hiprtcCreateProgram failed");
     const int nopt = static_cast<int>(sizeof(kOptions) / sizeof(kOptions[0]));
     hiprtcResult rc = hiprtcCompileProgram(prog, nopt, kOptions);
@@ -99,7 +167,9 @@ std::vector<char> jit_compile(const std::string& source) {
 
 namespace {
 std::string source_key(const std::string& source) {
-    return hex64(fnv1a_64(source + "\n" + options_key() + "\n" + kDeviceHeader + kLaunchHeader));
+    std::string h = source + "\n" + options_key() + "\n" + kDeviceHeader + kLaunchHeader;
+    if (source.rfind(kTuMarker, 0) == 0) h += std::string(kKernelAbi) + kPtoisaBridge + kStdTypes;
+    return hex64(fnv1a_64(h));
 }
 }  // namespace
 

@@ -146,8 +146,9 @@ KernelDef parse_kernel(Lexer& L) {
     k.name = L.str();
     int64_t nv = L.i64(), np = L.i64(), no = L.i64();
     const int64_t custom = L.i64();
+    if (custom < 0 || custom > 2) throw CompileError("kernel " + k.name + ": unknown custom-kernel kind " + std::to_string(custom));
     k.custom = custom != 0;
-    if (custom == 2) throw CompileError("kernel " + k.name + ": a C++ translation unit (cpp_tu_path) cannot run on the device; give its body as cpp_src");
+    k.custom_tu = custom == 2;
     if (k.custom) k.custom_src = L.str();
     for (int64_t i = 0; i < nv; ++i) {
         L.expect("V");

@@ -75,7 +75,8 @@ struct KernelDef {
     std::vector<ParamInfo> params;
     std::vector<OpInfo> ops;
     bool custom = false;
-    std::string custom_src;  // cpp_src: a C++ body over the task descriptor
+    std::string custom_src;  // cpp_src: a C++ body over the task descriptor; cpp_tu_path: a whole file
+    bool custom_tu = false;  // custom_src is a translation unit defining extern "C" <name>(task, cspt)
 };
 
 struct IndexExpr {

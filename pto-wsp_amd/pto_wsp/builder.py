@@ -306,8 +306,13 @@ def kernel(func: Callable | None = None, *, num_warps: int = 4, num_stages: int 
     ``cpp_src`` (or ``cpp_body_path``, a file holding one) gives the kernel a
     C++ body over the reference's task descriptor (``task->args``,
     ``task->tensor_ptrs``, ``task->tensor_strides``); the HIP backend compiles
-    it as device code run by one thread per task.  ``cpp_tu_path`` (a whole
-    host translation unit) and ``cpp_includes`` are refused by that backend."""
+    it as device code run by one thread per task.  ``cpp_tu_path`` names a
+    whole translation unit that defines ``extern "C" uint64_t <kernel name>(
+    const KernelTaskDesc*, CSPTContext*)`` against the reference's ABI headers
+    (``pto/wsp/codegen/abi/kernel_abi.hpp``, ``ptoisa_bridge.hpp`` without the
+    PTO-ISA tile API); the HIP backend compiles the file as device code and
+    calls that function once per task.  ``cpp_includes`` (host include
+    directories) is refused by that backend."""
     options = {"num_warps": num_warps, "num_stages": num_stages, **kwargs}
     chosen = [x for x in (cpp_src, cpp_body_path, cpp_tu_path) if x is not None]
     if len(chosen) > 1:

@@ -761,20 +761,44 @@ def test_cpp_src_slot_predicate_without_rebuild(gpu, device):
         assert (int(prog.stats.total_cycles), int(prog.stats.task_count)) == (2, 2)
 
 
+@pytest.mark.parametrize("tu", [False, True], ids=["cpp_src", "cpp_tu_path"])
 @pytest.mark.parametrize("masked", [False, True])
-def test_cpp_src_task_descriptor_matches_oracle(gpu, masked):
+def test_cpp_src_task_descriptor_matches_oracle(gpu, masked, tu, tmp_path):
     """A body that copies its task descriptor (args, counts, strides, two x elements) into its
-    output and reports per-task cycles: bit-identical to the oracle's g++ build of the same body."""
+    output and reports per-task cycles: bit-identical to the oracle's g++ build of the same body.
+    tu: the same probe as a whole translation unit (a helper function, pto::cpu_sim's counter)."""
     from pto_wsp.scalar_expr import axis
 
+    path = None
+    if tu:
+        path = str(tmp_path / "probe.cpp")
+        with open(path, "w") as f:
+            f.write(W.PROBE_TU)
     pred = (axis("b") != 1) if masked else None
     x = np.arange(3 * 2 * 8, dtype=np.float32).reshape(3, 2, 2, 4)
     ga = {"x": x.copy(), "o": np.full((2, 3, 2, 2, 16), -1.0, np.float32)}
     ca = {"x": x.copy(), "o": np.full((2, 3, 2, 2, 16), -1.0, np.float32)}
-    prog = run_hip(W.cpp_probe(ga, pred))
-    ref = run_workload(W.cpp_probe(ca, pred))
+    prog = run_hip(W.cpp_probe(ga, pred, tu_path=path))
+    ref = run_workload(W.cpp_probe(ca, pred, tu_path=path))
     np.testing.assert_array_equal(ga["o"], ca["o"])
     assert (int(prog.stats.total_cycles), int(prog.stats.task_count)) == (ref.total_cycles, ref.task_count)
+
+
+def test_cpp_tu_path_copy_like_the_reference(gpu, tmp_path):
+    """The reference's tu_copy translation unit (tests/test_npu_codegen_emit.py:155-206) on the
+    device: an exact 4x4 copy, 0 cycles, also through a transposed output view."""
+    from test_custom_kernels import TU_COPY, tu_copy_workload
+
+    p = tmp_path / "tu_copy.cpp"
+    p.write_text(TU_COPY)
+    x = np.arange(16, dtype=np.float32).reshape(4, 4)
+    y = np.zeros((4, 4), np.float32)
+    prog = run_hip(tu_copy_workload(x, y, p))
+    np.testing.assert_array_equal(y, x)
+    assert (int(prog.stats.total_cycles), int(prog.stats.task_count)) == (0, 1)
+    yt = np.zeros((4, 4), np.float32)
+    run_hip(tu_copy_workload(x, yt.T, p))
+    np.testing.assert_array_equal(yt.T, x)
 
 
 def test_cond_on_a_symbol_inside_a_grid(gpu):

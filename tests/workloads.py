@@ -762,16 +762,48 @@ _PROBE_BODY = r"""
 """
 
 
-def cpp_probe(arrs: dict, pred=None):
+# The same probe as a whole translation unit (@kernel(cpp_tu_path=...)): the entry has the
+# kernel's name, a helper function without annotations computes the sum, and the cycles go
+# through pto::cpu_sim's counter.
+PROBE_TU = r"""
+#include "pto/wsp/codegen/abi/kernel_abi.hpp"
+#include "pto/wsp/codegen/abi/ptoisa_bridge.hpp"
+#include <cstdint>
+#include <cstddef>
+
+static float column_pair(const float* x, uint64_t s3) { return x[0] + x[s3]; }
+
+extern "C" PTO_WSP_KERNEL_ATTR uint64_t probe(const KernelTaskDesc* task, CSPTContext* cspt) {
+  (void)cspt;
+  const float* xv = (const float*)task->tensor_ptrs[0];
+  float* ov = (float*)task->tensor_ptrs[1];
+  const uint64_t os3 = task->tensor_strides[2], os4 = task->tensor_strides[3];
+  for (uint32_t j = 0; j < task->num_args && j < 16; ++j) ov[j * os4] = (float)task->args[j];
+  ov[os3 + 0 * os4] = (float)task->num_axis_args;
+  ov[os3 + 1 * os4] = (float)task->num_tensors;
+  ov[os3 + 2 * os4] = (float)task->tensor_strides[0];
+  ov[os3 + 3 * os4] = (float)task->tensor_strides[1];
+  ov[os3 + 4 * os4] = column_pair(xv, task->tensor_strides[0]);
+  pto::cpu_sim::reset_cycles();
+  pto::cpu_sim::add_cycles(5 + task->args[0] * 3);
+  pto::cpu_sim::add_cycles(task->args[1] + 100 * task->args[2]);
+  return pto::cpu_sim::read_cycles();
+}
+"""
+
+
+def cpp_probe(arrs: dict, pred=None, tu_path: str | None = None):
     """A cpp_src kernel over a host P.seq loop (i) around a P() grid (b, h), with a scalar arg;
-    with `pred`, only the grid tasks where it holds run."""
+    with `pred`, only the grid tasks where it holds run; with `tu_path` (a file holding
+    PROBE_TU) the kernel is that translation unit instead."""
     from pto_wsp import Scalar
 
     X, O = T(arrs["x"]), T(arrs["o"])
     nb, nh = arrs["x"].shape[:2]
     ni = arrs["o"].shape[0]
+    opts = {"cpp_tu_path": tu_path} if tu_path else {"cpp_src": _PROBE_BODY}
 
-    @kernel(cpp_src=_PROBE_BODY)
+    @kernel(**opts)
     def probe(x: In[Tile[2, 4, F32]], out: Out[Tile[2, 16, F32]], s: Scalar[F32] = 1.5):
         pass
 
