@@ -703,31 +703,59 @@ struct GemmPingPong {
         for (int q = 0; q < BQ; ++q) dma16(rb, vb ^ ((q & 1) << 6), sob + q * BRPB * ldb * 2, base + ASZ * 2 + (w * BQ + q) * 1024);
     }
 
-    // All fragments of one stage (the address math of GemmBlock::mma).
-    __device__ static void read(Frag& f, const u16* stage, int wm, int wn) {
+    struct NoDma {
+        __device__ void operator()(int) const {}
+    };
+
+    // All fragments of one stage (the address math of GemmBlock::mma); dma(k)
+    // is issued after the wave's (4k+4)-th LDS read, k = 0 .. KS*(FI+2*FJ)/4-1.
+    template <class Dma = NoDma>
+    __device__ static void read(Frag& f, const u16* stage, int wm, int wn, Dma dma = Dma()) {
         const int lane = threadIdx.x & 63;
         const int r = lane & 31, kc = lane >> 5;
         const int g = lane >> 4, a4 = lane & 3, e = (lane >> 2) & 3;
         const u16* as = stage + (wm * TM + r) * BK;
         const u16* bs = stage + ASZ;
+        int nl = 0;
+        auto tick = [&]() {
+            if (++nl % 4 == 0) {
+                __builtin_amdgcn_sched_barrier(0);
+                dma(nl / 4 - 1);
+                __builtin_amdgcn_sched_barrier(0);
+            }
+        };
 #pragma unroll
         for (int s = 0; s < KS; ++s) {
             const int kk = s * 16;
 #pragma unroll
-            for (int i = 0; i < FI; ++i)
+            for (int i = 0; i < FI; ++i) {
                 f.a[s][i] = *reinterpret_cast<const u32x4*>(as + i * 32 * BK + ((((kk >> 3) + kc) ^ GB::swa(wm * TM + i * 32 + r)) << 3));
+                tick();
+            }
 #pragma unroll
             for (int j = 0; j < FJ; ++j) {
                 const int n = wn * TN + j * 32 + 16 * (g & 1) + 4 * a4;
                 const int pn = (((n >> 4) ^ e) << 4) | (n & 15);
                 const int k = kk + 8 * (g >> 1) + e;
                 const s16x4 lo = __builtin_amdgcn_ds_read_tr16_b64_v4i16((__attribute__((address_space(3))) s16x4*)(bs + k * 256 + pn));
+                tick();
                 const s16x4 hi =
                     __builtin_amdgcn_ds_read_tr16_b64_v4i16((__attribute__((address_space(3))) s16x4*)(bs + (k + 4) * 256 + pn));
+                tick();
                 const u32x2 l2 = __builtin_bit_cast(u32x2, lo), h2 = __builtin_bit_cast(u32x2, hi);
                 f.b[s][j] = u32x4{l2.x, l2.y, h2.x, h2.y};
             }
         }
+    }
+
+    // BK = 64: A chunk c of a stage (rows 8c..8c+7) and B chunk c (K rows 2c,
+    // 2c+1), from the lane offsets va0 / vb0 of chunk 0 (offsets(.., 0, ..)):
+    // chunk c flips A's 16-byte column bits by c & 7 and B's bit 6 by c & 1.
+    __device__ static void achunk(u32 base, int c, int va0, u32x4 ra, int soa, int lda) {
+        dma16(ra, va0 ^ ((c & 7) << 4), soa + c * ARPB * lda * 2, base + c * 1024);
+    }
+    __device__ static void bchunk(u32 base, int c, int vb0, u32x4 rb, int sob, int ldb) {
+        dma16(rb, vb0 ^ ((c & 1) << 6), sob + c * BRPB * ldb * 2, base + ASZ * 2 + c * 1024);
     }
 
     __device__ static void mma(Acc& acc, const Frag& f) {
@@ -783,6 +811,114 @@ struct GemmPingPong {
         }
     }
 
+    // BK = 64 schedule.  A wave's DMA instructions block its issue until the
+    // texture path drains them (64 B/clk per CU), so a read slot that also
+    // issues a whole 64 KiB stage outlasts the compute slot beside it.  The
+    // stage DMA is therefore split by consumer, 32 KiB per read slot, and
+    // interleaved with that slot's LDS reads:
+    //   group 0 (A rows 0-127), slot 2j: B of stage j+1 (8 chunks per wave);
+    //   group 1 (A rows 128-255), slot 2j+1: A rows 128-255 of stage j+1 and
+    //     A rows 0-127 of stage j+2 (4 + 4 chunks per wave).
+    // Buffer reuse: B of stage j+1 replaces B of stage j-1 (read in slots
+    // 2j-2 / 2j-1); A rows 128-255 of stage j+1 replace those of stage j-1
+    // (read by group 1 in slot 2j-1); A rows 0-127 of stage j+2 replace those
+    // of stage j (read by group 0 in slot 2j).  Waits: group 0 waits for its
+    // B of stage j+1 at the end of slot 2j+1; group 1 waits for A rows 0-127
+    // of stage j+1 at the end of slot 2j+1 and for rows 128-255 of stage j+1
+    // at the end of slot 2j+2, each before the barrier that precedes the read.
+    template <bool ACC, class Off>
+    __device__ static void run_split(u16* lds, const u16* pa, int lda, const u16* pb, int ldb, float* pc, int ldc, i64 it0,
+                                     i64 iters, Off off, int pfa_row, int pfb_row) {
+        const int w = wave_index(), grp = w >> 2, wq = w & 3, wm = w / WN, wn = w % WN;
+        const int lane = threadIdx.x & 63;
+        const u32x4 ra = buffer_words(pa), rb = buffer_words(pb);
+        const buf_rsrc rc = __builtin_amdgcn_make_buffer_rsrc(pc, 0, -1, 0x00020000);
+        const int nst = static_cast<int>(iters - it0);
+        const u32 scratch = lds_address(lds + NS * STAGE);
+        int va0, vb0;
+        offsets(va0, vb0, 0, lda, ldb);
+        const int pfa_v = (pfa_row + (lane & 31)) * lda * 2, pfb_v = ((pfb_row + (lane >> 2)) * ldb + (lane & 3) * 64) * 2;
+        const bool touch = w == 0 && pfa_row >= 0 && pfb_row >= 0;
+        Acc acc;
+#pragma unroll
+        for (int i = 0; i < FI; ++i)
+#pragma unroll
+            for (int j = 0; j < FJ; ++j) acc.v[i][j] = f32x16{};
+        Frag f;
+        auto sbase = [&](int st) { return lds_address(lds + (st % NS) * STAGE); };
+        // group 0 wave wq: B chunks 8wq..8wq+7 of stage st
+        auto issue_b = [&](int st, int k) {
+            int soa, sob;
+            off(it0 + st, soa, sob);
+            bchunk(sbase(st), wq * 8 + k, vb0, rb, sob, ldb);
+        };
+        // group 1 wave wq: A chunk 16*half + 4wq + k of stage st (half 0: rows 0-127, 1: rows 128-255)
+        auto issue_a = [&](int st, int half, int k) {
+            int soa, sob;
+            off(it0 + st, soa, sob);
+            achunk(sbase(st), half * 16 + wq * 4 + k, va0, ra, soa, lda);
+        };
+        wait_vmcnt<0>();
+        block_barrier();  // the previous block's last stage reads are done
+        // stage 0, and A rows 0-127 of stage 1
+        if (grp == 0) {
+            for (int k = 0; k < 8; ++k) issue_b(0, k);
+        } else {
+            for (int k = 0; k < 4; ++k) issue_a(0, 0, k);
+            for (int k = 0; k < 4; ++k) issue_a(0, 1, k);
+            if (nst > 1)
+                for (int k = 0; k < 4; ++k) issue_a(1, 0, k);
+        }
+        wait_vmcnt<0>();
+        block_barrier();
+        if (grp == 1) block_barrier();  // group 1 runs one slot behind
+        for (int j = 0; j < nst; ++j) {
+            const bool t = touch && j + PF < nst;
+            if (grp == 0) {
+                const bool h1 = j + 1 < nst;
+                read(f, lds + (j % NS) * STAGE, wm, wn, [&](int k) {
+                    if (h1 && k < 8) issue_b(j + 1, k);
+                });
+                if (t) {
+                    int soa, sob;
+                    off(it0 + j + PF, soa, sob);
+                    dma4(ra, pfa_v, soa, scratch);
+                    dma4(rb, pfb_v, sob, scratch);
+                }
+            } else {
+                const bool h1 = j + 1 < nst, h2 = j + 2 < nst;
+                read(f, lds + (j % NS) * STAGE, wm, wn, [&](int k) {
+                    if (k < 4) {
+                        if (h1) issue_a(j + 1, 1, k);
+                    } else if (k < 8 && h2) {
+                        issue_a(j + 2, 0, k - 4);
+                    }
+                });
+                // A rows 0-127 of stage j+1 (issued in this group's previous read slot) have landed
+                const int pending = (h1 ? 4 : 0) + (h2 ? 4 : 0);
+                if (pending == 8) wait_vmcnt<8>();
+                else if (pending == 4) wait_vmcnt<4>();
+                else wait_vmcnt<0>();
+            }
+            wait_lgkm0();
+            block_barrier();
+            mma(acc, f);
+            if (grp == 0) {
+                // own B of stage j+1 landed (wave 0's two touches may stay in flight)
+                if (t) wait_vmcnt<2>();
+                else wait_vmcnt<0>();
+            } else {
+                // own A rows 128-255 of stage j+1 landed (rows 0-127 of stage j+2 may stay in flight)
+                if (j + 2 < nst) wait_vmcnt<4>();
+                else wait_vmcnt<0>();
+            }
+            block_barrier();
+        }
+        wait_vmcnt<0>();
+        c_out<ACC>(acc, rc, ldc);
+        if (grp == 0) block_barrier();
+    }
+
     // Task K steps it0 .. iters-1 (off(it, soa, sob): step it's byte offsets
     // from the step-0 origins pa / pb).  The block sums A x B from zero; ACC:
     // then adds C, as c + sum.  pfa_row / pfb_row (< 0: no L2 touches): the
@@ -791,6 +927,10 @@ struct GemmPingPong {
     template <bool ACC, class Off>
     __device__ static void run(u16* lds, const u16* pa, int lda, const u16* pb, int ldb, float* pc, int ldc, i64 it0, i64 iters,
                                Off off, int pfa_row, int pfb_row) {
+        if constexpr (BK == 64) {
+            run_split<ACC>(lds, pa, lda, pb, ldb, pc, ldc, it0, iters, off, pfa_row, pfb_row);
+            return;
+        }
         const int w = wave_index(), grp = w >> 2, wm = w / WN, wn = w % WN;
         const int lane = threadIdx.x & 63;
         const u32x4 ra = buffer_words(pa), rb = buffer_words(pb);
