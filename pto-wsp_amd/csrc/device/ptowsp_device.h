@@ -1158,6 +1158,7 @@ struct DecodeWave {
         // Online softmax, one (query row, token) per lane and pass.
         auto fmax_ = [](float a, float b) { return fmaxf(a, b); };
         auto fadd_ = [](float a, float b) { return a + b; };
+        bool moved = false;  // some query row's running max changed (its a != 1)
 #pragma unroll
         for (int r = 0; r < NP; ++r) {
             const int h = 4 * r + grp;
@@ -1168,20 +1169,27 @@ struct DecodeWave {
             st.l[r] = st.l[r] * a + row16_reduce(e, fadd_);
             st.m[r] = mn;
             if (h < G) {
+                moved = moved || a != 1.0f;
                 lds[h * 16 + t] = e;
                 if (t == 0) lds[G * 16 + h] = a;
             }
         }
         wave_lds_fence();
         // o <- o * a + p @ v over this lane's 4 tokens (token by token, each
-        // unpacked v value used by every query row at once).
+        // unpacked v value used by every query row at once).  Once the
+        // running maxima settle, a == 1 for every row and o * a == o exactly,
+        // so the rescale is skipped for the whole wave.
+        const bool rescale = __builtin_amdgcn_ballot_w64(moved) != 0;
         f32x4v_t p4[G];
 #pragma unroll
-        for (int g = 0; g < G; ++g) {
-            const float ag = lds[G * 16 + g];
-            p4[g] = *reinterpret_cast<const f32x4v_t*>(lds + g * 16 + 4 * grp);
+        for (int g = 0; g < G; ++g) p4[g] = *reinterpret_cast<const f32x4v_t*>(lds + g * 16 + 4 * grp);
+        if (rescale) {
 #pragma unroll
-            for (int e = 0; e < DV; ++e) st.o[g][e] = st.o[g][e] * ag;
+            for (int g = 0; g < G; ++g) {
+                const float ag = lds[G * 16 + g];
+#pragma unroll
+                for (int e = 0; e < DV; ++e) st.o[g][e] = st.o[g][e] * ag;
+            }
         }
         wave_lds_fence();
 #pragma unroll
@@ -1419,15 +1427,23 @@ struct DecodeStream {
         PageOffs rc, rn;
         f.page(s + lane < b ? s + lane : b - 1, rc);
         rn = rc;
+        // Page g's offsets are read from the current run only: the run moves
+        // on just before the first page past it is loaded, so the next run's
+        // registers are read 64 pages after their load was issued.  (A select
+        // between the two runs here would make every page load wait for the
+        // most recent page-table read, i.e. for the whole ring.)
         auto load = [&](typename DW::Page& pg, i64 g) {
             const bool real = g < b;
-            const int i = static_cast<int>((real ? g : b - 1) - r0);
-            const PageOffs& src = i < 64 ? rc : rn;
-            const int li = i & 63;
+            if (real && g - r0 == 64) {
+                r0 += 64;
+                rc = rn;
+                if (r0 + 64 < b) f.page(r0 + 64 + lane < b ? r0 + 64 + lane : b - 1, rn);
+            }
+            const int li = static_cast<int>((real ? g : b - 1) - r0);
             PageOffs po;
-            po.k = readlane64(src.k, li);
-            po.v = readlane64(src.v, li);
-            po.m = readlane64(src.m, li);
+            po.k = readlane64(rc.k, li);
+            po.v = readlane64(rc.v, li);
+            po.m = readlane64(rc.m, li);
             const u16 *kp, *vp;
             const float* mp;
             f.bases(po, kp, vp, mp);
@@ -1501,11 +1517,6 @@ struct DecodeStream {
                         un = next_unit(pre, u);
                         get_q(qn, un);
                     }
-                }
-                if (gi + 1 - r0 == 64) {
-                    r0 += 64;
-                    rc = rn;
-                    if (r0 + 64 < b) f.page(r0 + 64 + lane < b ? r0 + 64 + lane : b - 1, rn);
                 }
             }
         }
