@@ -1000,9 +1000,10 @@ struct GemmPingPong {
 //    then holds query rows 4*(l/16)..+3 for token l%16;
 //  * the scores pass through LDS so that each pass holds one (query row,
 //    token) per lane; row max and row sum over a 16-lane DPP row;
-//  * p and the rescale factor pass through LDS; p @ v runs in fp32 FMAs on
-//    the VALU, lane l owning tokens 4*(l/16)..+3 of every page and head dims
-//    (D/16)*(l%16)..; the four token groups are summed once per partial.
+//  * p and the rescale factor pass through LDS; p @ v runs on the matrix
+//    cores (v_mfma_f32_16x16x16, p split into two 16-bit parts), lane l
+//    supplying tokens 4*(l/16)..+3 of every page for head dims (D/16)*(l%16)+e
+//    and accumulating query rows 4*(l/16)..+3 of them.
 
 typedef float f32x4v_t __attribute__((ext_vector_type(4)));
 
@@ -1013,18 +1014,6 @@ __device__ inline f32x4v_t mfma_16x16x32(u32x4 a, u32x4 b, f32x4v_t c) {
     else
         return __builtin_amdgcn_mfma_f32_16x16x32_bf16(__builtin_bit_cast(bf16x8, a), __builtin_bit_cast(bf16x8, b), c, 0, 0,
                                                        0);
-}
-
-// 16-bit float (bf16 or f16) in the low / high half of a dword, as f32.
-template <bool F16>
-__device__ inline float h16_lo(u32 w) {
-    if constexpr (F16) return static_cast<float>(__builtin_bit_cast(_Float16, static_cast<u16>(w & 0xFFFFu)));
-    else return __uint_as_float(w << 16);
-}
-template <bool F16>
-__device__ inline float h16_hi(u32 w) {
-    if constexpr (F16) return static_cast<float>(__builtin_bit_cast(_Float16, static_cast<u16>(w >> 16)));
-    else return __uint_as_float(w & 0xFFFF0000u);
 }
 
 // Orders LDS traffic between the lanes of one wave (LDS executes a wave's
@@ -1138,8 +1127,42 @@ struct DecodeWave {
 
     struct State {
         float m[NP], l[NP];    // query row 4*pass + l/16, replicated over its 16 lanes
-        float o[G][DV];        // partial over this lane's 4 tokens of every page
+        f32x4v_t o[DV];        // o[e][j]: query row 4*(l/16) + j, head dim DV*(l%16) + e
     };
+
+    typedef float f32x2_t __attribute__((ext_vector_type(2)));
+    // hi + lo == x for four fp32 values x to about 2^-17 (bf16) / 2^-22 (f16)
+    // relative: hi = x rounded to 16 bits, lo = (x - hi) rounded (x - hi is
+    // exact in fp32).  Packed two per dword, element 0 in the low half.
+    __device__ static void split4(f32x4v_t x, u32x2& hi, u32x2& lo) {
+        if constexpr (F16) {
+            typedef _Float16 h2_t __attribute__((ext_vector_type(2)));
+            const h2_t a = __builtin_convertvector((f32x2_t{x[0], x[1]}), h2_t);
+            const h2_t b = __builtin_convertvector((f32x2_t{x[2], x[3]}), h2_t);
+            const f32x2_t ra = f32x2_t{x[0], x[1]} - __builtin_convertvector(a, f32x2_t);
+            const f32x2_t rb = f32x2_t{x[2], x[3]} - __builtin_convertvector(b, f32x2_t);
+            hi = u32x2{__builtin_bit_cast(u32, a), __builtin_bit_cast(u32, b)};
+            lo = u32x2{__builtin_bit_cast(u32, __builtin_convertvector(ra, h2_t)), __builtin_bit_cast(u32, __builtin_convertvector(rb, h2_t))};
+        } else {
+            typedef __bf16 h2_t __attribute__((ext_vector_type(2)));
+            const h2_t a = __builtin_convertvector((f32x2_t{x[0], x[1]}), h2_t);
+            const h2_t b = __builtin_convertvector((f32x2_t{x[2], x[3]}), h2_t);
+            const f32x2_t ra = f32x2_t{x[0], x[1]} - __builtin_convertvector(a, f32x2_t);
+            const f32x2_t rb = f32x2_t{x[2], x[3]} - __builtin_convertvector(b, f32x2_t);
+            hi = u32x2{__builtin_bit_cast(u32, a), __builtin_bit_cast(u32, b)};
+            lo = u32x2{__builtin_bit_cast(u32, __builtin_convertvector(ra, h2_t)), __builtin_bit_cast(u32, __builtin_convertvector(rb, h2_t))};
+        }
+    }
+    // v_mfma_f32_16x16x16 (bf16 / f16): lane l holds A[l%16][4*(l/16)..+3],
+    // B[4*(l/16)..+3][l%16] and D[4*(l/16)..+3][l%16].
+    __device__ static f32x4v_t mfma16(u32x2 a, u32x2 b, f32x4v_t c) {
+        if constexpr (F16) {
+            typedef _Float16 h4_t __attribute__((ext_vector_type(4)));
+            return __builtin_amdgcn_mfma_f32_16x16x16f16(__builtin_bit_cast(h4_t, a), __builtin_bit_cast(h4_t, b), c, 0, 0, 0);
+        } else {
+            return __builtin_amdgcn_mfma_f32_16x16x16bf16_1k(__builtin_bit_cast(s16x4, a), __builtin_bit_cast(s16x4, b), c, 0, 0, 0);
+        }
+    }
 
     __device__ static void step(State& st, const Page& pg, const u32x4* qa, float scale, float* lds) {
         const int lane = threadIdx.x & 63, t = lane & 15, grp = lane >> 4;
@@ -1175,34 +1198,39 @@ struct DecodeWave {
             }
         }
         wave_lds_fence();
-        // o <- o * a + p @ v over this lane's 4 tokens (token by token, each
-        // unpacked v value used by every query row at once).  Once the
-        // running maxima settle, a == 1 for every row and o * a == o exactly,
-        // so the rescale is skipped for the whole wave.
+        // o <- o * a + p @ v on the matrix cores: v_mfma_f32_16x16x16 with
+        // M = query rows, K = the page's 16 tokens, N = 16 head dims.  p is
+        // fp32 and enters as hi + lo (split4), two products per MFMA step.
+        // MFMA e covers head dims DV*n + e (n = l%16): lane (n, l/16)
+        // supplies V[tokens 4*(l/16)..+3][DV*n + e] straight from its page
+        // registers (one 16-bit half of pg.v[i][e/2] per token) and
+        // accumulates o rows 4*(l/16)..+3.  Once the running maxima settle,
+        // a == 1 for every row and o * a == o exactly, so the rescale is
+        // skipped for the whole wave.
         const bool rescale = __builtin_amdgcn_ballot_w64(moved) != 0;
-        f32x4v_t p4[G];
-#pragma unroll
-        for (int g = 0; g < G; ++g) p4[g] = *reinterpret_cast<const f32x4v_t*>(lds + g * 16 + 4 * grp);
-        if (rescale) {
-#pragma unroll
-            for (int g = 0; g < G; ++g) {
-                const float ag = lds[G * 16 + g];
-#pragma unroll
-                for (int e = 0; e < DV; ++e) st.o[g][e] = st.o[g][e] * ag;
-            }
-        }
+        f32x4v_t pr = {0.0f, 0.0f, 0.0f, 0.0f};
+        if (t < G) pr = *reinterpret_cast<const f32x4v_t*>(lds + t * 16 + 4 * grp);
+        f32x4v_t a4 = {1.0f, 1.0f, 1.0f, 1.0f};
+        if (rescale) a4 = *reinterpret_cast<const f32x4v_t*>(lds + G * 16 + 4 * grp);
         wave_lds_fence();
+        u32x2 ph, pl;
+        split4(pr, ph, pl);
+        if (rescale) {
+            // A real branch (the empty asm keeps it from being turned into
+            // selects): the multiply is rare, and o stays in the matrix
+            // cores' accumulator registers otherwise.
+            asm volatile("");
 #pragma unroll
-        for (int i = 0; i < 4; ++i)
+            for (int e = 0; e < DV; ++e) st.o[e] = st.o[e] * a4;
+        }
 #pragma unroll
-            for (int w = 0; w < DV / 2; ++w) {
-                const float lo = h16_lo<F16>(pg.v[i][w]), hi = h16_hi<F16>(pg.v[i][w]);
-#pragma unroll
-                for (int g = 0; g < G; ++g) {
-                    st.o[g][2 * w] = __builtin_fmaf(p4[g][i], lo, st.o[g][2 * w]);
-                    st.o[g][2 * w + 1] = __builtin_fmaf(p4[g][i], hi, st.o[g][2 * w + 1]);
-                }
-            }
+        for (int e = 0; e < DV; ++e) {
+            const u32 sel = (e & 1) ? 0x07060302u : 0x05040100u;
+            const u32x2 bv = {__builtin_amdgcn_perm(pg.v[1][e >> 1], pg.v[0][e >> 1], sel),
+                              __builtin_amdgcn_perm(pg.v[3][e >> 1], pg.v[2][e >> 1], sel)};
+            st.o[e] = mfma16(ph, bv, st.o[e]);
+            st.o[e] = mfma16(pl, bv, st.o[e]);
+        }
     }
 
     // q rows as the MFMA's A operand (rows >= G are zero).
@@ -1222,18 +1250,14 @@ struct DecodeWave {
             st.l[r] = 0.0f;
         }
 #pragma unroll
-        for (int g = 0; g < G; ++g)
-#pragma unroll
-            for (int e = 0; e < DV; ++e) st.o[g][e] = 0.0f;
+        for (int e = 0; e < DV; ++e) st.o[e] = f32x4v_t{0.0f, 0.0f, 0.0f, 0.0f};
     }
 
-    // Writes st as a partial (m[G], l[G], o[G][D]) after summing the four
-    // token groups (lanes l, l^16, l^32, l^48).  o is kept in lane order:
-    // head dim DV*t + e sits at position 16*e + t (part_dim maps back), so
-    // store i of every lane l writes position 64*i + l (e = 4*i + l/16) and
-    // each store instruction covers 256 contiguous bytes.
+    // Writes st as a partial (m[G], l[G], o[G][D]).  o is kept in lane
+    // order: head dim DV*n + e sits at position 16*e + n (part_dim maps
+    // back), so the 16 lanes of a row group write 64 contiguous bytes per
+    // (row, e).
     __device__ static void store(const State& st, float* part) {
-        static_assert(DV % 4 == 0, "lane-order partial");
         const int lane = threadIdx.x & 63, t = lane & 15, grp = lane >> 4;
         if (t == 0) {
 #pragma unroll
@@ -1246,18 +1270,11 @@ struct DecodeWave {
             }
         }
 #pragma unroll
-        for (int g = 0; g < G; ++g) {
-            float x[DV];
+        for (int j = 0; j < 4; ++j) {
+            const int g = 4 * grp + j;
+            if (g < G) {
 #pragma unroll
-            for (int e = 0; e < DV; ++e) {
-                x[e] = st.o[g][e];
-                x[e] = x[e] + __shfl_xor(x[e], 16);
-                x[e] = x[e] + __shfl_xor(x[e], 32);
-            }
-#pragma unroll
-            for (int i = 0; i < DV / 4; ++i) {
-                const float y = grp == 0 ? x[4 * i] : grp == 1 ? x[4 * i + 1] : grp == 2 ? x[4 * i + 2] : x[4 * i + 3];
-                coherent_store(part + 2 * G + g * D + 64 * i + lane, y);
+                for (int e = 0; e < DV; ++e) coherent_store(part + 2 * G + g * D + 16 * e + t, st.o[e][j]);
             }
         }
     }
