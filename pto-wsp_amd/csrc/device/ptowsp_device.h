@@ -1134,24 +1134,16 @@ struct DecodeWave {
     // hi + lo == x for four fp32 values x to about 2^-17 (bf16) / 2^-22 (f16)
     // relative: hi = x rounded to 16 bits, lo = (x - hi) rounded (x - hi is
     // exact in fp32).  Packed two per dword, element 0 in the low half.
+    template <bool H, class A, class B> struct Pick { typedef B type; };
+    template <class A, class B> struct Pick<true, A, B> { typedef A type; };
     __device__ static void split4(f32x4v_t x, u32x2& hi, u32x2& lo) {
-        if constexpr (F16) {
-            typedef _Float16 h2_t __attribute__((ext_vector_type(2)));
-            const h2_t a = __builtin_convertvector((f32x2_t{x[0], x[1]}), h2_t);
-            const h2_t b = __builtin_convertvector((f32x2_t{x[2], x[3]}), h2_t);
-            const f32x2_t ra = f32x2_t{x[0], x[1]} - __builtin_convertvector(a, f32x2_t);
-            const f32x2_t rb = f32x2_t{x[2], x[3]} - __builtin_convertvector(b, f32x2_t);
-            hi = u32x2{__builtin_bit_cast(u32, a), __builtin_bit_cast(u32, b)};
-            lo = u32x2{__builtin_bit_cast(u32, __builtin_convertvector(ra, h2_t)), __builtin_bit_cast(u32, __builtin_convertvector(rb, h2_t))};
-        } else {
-            typedef __bf16 h2_t __attribute__((ext_vector_type(2)));
-            const h2_t a = __builtin_convertvector((f32x2_t{x[0], x[1]}), h2_t);
-            const h2_t b = __builtin_convertvector((f32x2_t{x[2], x[3]}), h2_t);
-            const f32x2_t ra = f32x2_t{x[0], x[1]} - __builtin_convertvector(a, f32x2_t);
-            const f32x2_t rb = f32x2_t{x[2], x[3]} - __builtin_convertvector(b, f32x2_t);
-            hi = u32x2{__builtin_bit_cast(u32, a), __builtin_bit_cast(u32, b)};
-            lo = u32x2{__builtin_bit_cast(u32, __builtin_convertvector(ra, h2_t)), __builtin_bit_cast(u32, __builtin_convertvector(rb, h2_t))};
-        }
+        typedef typename Pick<F16, _Float16, __bf16>::type h_t;
+        typedef h_t h2_t __attribute__((ext_vector_type(2)));
+        const f32x2_t x0 = {x[0], x[1]}, x1 = {x[2], x[3]};
+        const h2_t a = __builtin_convertvector(x0, h2_t), b = __builtin_convertvector(x1, h2_t);
+        const f32x2_t r0 = x0 - __builtin_convertvector(a, f32x2_t), r1 = x1 - __builtin_convertvector(b, f32x2_t);
+        hi = u32x2{__builtin_bit_cast(u32, a), __builtin_bit_cast(u32, b)};
+        lo = u32x2{__builtin_bit_cast(u32, __builtin_convertvector(r0, h2_t)), __builtin_bit_cast(u32, __builtin_convertvector(r1, h2_t))};
     }
     // v_mfma_f32_16x16x16 (bf16 / f16): lane l holds A[l%16][4*(l/16)..+3],
     // B[4*(l/16)..+3][l%16] and D[4*(l/16)..+3][l%16].
