@@ -341,8 +341,16 @@ __device__ inline void tsort32_rank(float* dst, const float* sc, const i64* ix) 
 //   A stage [BM][BK]: 16-byte chunk c of row m lives at chunk c ^ swa(m), so
 //     the 32 rows of an MFMA operand read hit distinct banks;
 //   B stage [BK][BN] (k-major, as in memory): 32-byte segment g of row k lives
-//     at g ^ (k & 3); the MFMA B operand is read with ds_read_b64_tr_b16,
-//     which transposes 16-bit elements across each group of 16 lanes.
+//     at g ^ swb(k); the MFMA B operand is read with ds_read_b64_tr_b16,
+//     which transposes 16-bit elements across each group of 16 lanes.  A
+//     transpose read serves 32 lanes per LDS cycle (256 bytes): lanes 0-15
+//     read 4 rows of segment s, lanes 16-31 the same rows of segment s+1.
+//     For rows of 256 bytes or more (BN >= 128) the banks repeat every 8
+//     segments, and swb(k) = 2*(k & 3) puts the two 16-lane groups on
+//     disjoint bank halves (s ^ {0,2,4,6} and (s+1) ^ {0,2,4,6}, s even);
+//     with k & 3 the two groups hit the same 32 banks and each read takes
+//     twice the cycles.  128-byte rows (BN = 64) alternate bank halves by
+//     row parity, and k & 3 is conflict-free there.
 // MFMA 32x32x16 lane l holds A row / B column (l % 32) with k = 8*(l/32)..+7;
 // accumulator element e sits at row (e/4)*8 + (l/32)*4 + e%4, column l % 32.
 // ds_read_b64_tr_b16: in each 16-lane group, lane l receives element (l % 4)
@@ -443,6 +451,7 @@ struct GemmBlock {
     };
 
     __device__ static int swa(int m) { return ((m / RPL) ^ (m >> 3)) & SWM; }
+    __device__ static int swb(int k) { return BN >= 128 ? (k & 3) << 1 : k & 3; }
 
     // Per-lane byte offsets, from the block's A / B origin at the first K step,
     // of the chunks this wave moves (lda / ldb: row pitch in elements).
@@ -456,7 +465,7 @@ struct GemmBlock {
 #pragma unroll
         for (int q = 0; q < BQ; ++q) {
             const int k = (w * BQ + q) * BRPB + lane / BCPR, p = lane % BCPR;
-            const int c = (((p >> 1) ^ (k & 3)) << 1) | (p & 1);
+            const int c = (((p >> 1) ^ swb(k)) << 1) | (p & 1);
             o.b[q] = (k * ldb + c * 8) * 2;
         }
     }
@@ -489,7 +498,7 @@ struct GemmBlock {
 #pragma unroll
             for (int j = 0; j < FJ; ++j) {
                 const int n = wn * TN + j * 32 + 16 * (g & 1) + 4 * a4;
-                const int pn = (((n >> 4) ^ e) << 4) | (n & 15);
+                const int pn = (((n >> 4) ^ swb(e)) << 4) | (n & 15);
                 const int k = kk + 8 * (g >> 1) + e;
                 const s16x4 lo = __builtin_amdgcn_ds_read_tr16_b64_v4i16((__attribute__((address_space(3))) s16x4*)(bs + k * BN + pn));
                 const s16x4 hi =
@@ -683,24 +692,26 @@ struct GemmPingPong {
     // DMA lane offsets of loader wave w (0..3) for its first A / B chunk.
     // With row pitches that are multiples of 64 elements (checked on the
     // host), chunk q of A sits at va with its 16-byte column bits flipped by
-    // q (BK = 64) or by bit 1 of q (BK = 32), and chunk q of B at vb with bit
-    // 6 flipped by q & 1; the row steps q*ARPB / q*BRPB go into the uniform
-    // offset.
-    __device__ static void offsets(int& va, int& vb, int w, int lda, int ldb) {
+    // q (BK = 64) or by bit 1 of q (BK = 32).  Chunk q of B (K rows 2q, 2q+1
+    // after the wave's first) uses vb[q & 1]: the rows' swizzle GB::swb
+    // depends on k & 3, which moves by 2 with each chunk.  The row steps
+    // q*ARPB / q*BRPB go into the uniform offset.
+    __device__ static void offsets(int& va, int (&vb)[2], int w, int lda, int ldb) {
         const int lane = threadIdx.x & 63;
         const int m = w * AQ * ARPB + lane / CH, p = lane % CH;
         va = (m * lda + ((p ^ GB::swa(m)) << 3)) * 2;
         const int k = w * BQ * BRPB + lane / BCPR, pb = lane % BCPR;
-        vb = (k * ldb + (((((pb >> 1) ^ (k & 3)) << 1) | (pb & 1)) * 8)) * 2;
+#pragma unroll
+        for (int h = 0; h < 2; ++h) vb[h] = (k * ldb + (((((pb >> 1) ^ GB::swb(k + 2 * h)) << 1) | (pb & 1)) * 8)) * 2;
     }
     __device__ static int a_voff(int va, int q) { return BK == 64 ? va ^ (q << 4) : va ^ ((q & 1) << 5); }
 
-    __device__ static void load(u16* stage, int w, int va, int vb, u32x4 ra, int soa, u32x4 rb, int sob, int lda, int ldb) {
+    __device__ static void load(u16* stage, int w, int va, const int (&vb)[2], u32x4 ra, int soa, u32x4 rb, int sob, int lda, int ldb) {
         const u32 base = lds_address(stage);
 #pragma unroll
         for (int q = 0; q < AQ; ++q) dma16(ra, a_voff(va, q), soa + q * ARPB * lda * 2, base + (w * AQ + q) * 1024);
 #pragma unroll
-        for (int q = 0; q < BQ; ++q) dma16(rb, vb ^ ((q & 1) << 6), sob + q * BRPB * ldb * 2, base + ASZ * 2 + (w * BQ + q) * 1024);
+        for (int q = 0; q < BQ; ++q) dma16(rb, vb[q & 1], sob + q * BRPB * ldb * 2, base + ASZ * 2 + (w * BQ + q) * 1024);
     }
 
     struct NoDma {
@@ -735,7 +746,7 @@ struct GemmPingPong {
 #pragma unroll
             for (int j = 0; j < FJ; ++j) {
                 const int n = wn * TN + j * 32 + 16 * (g & 1) + 4 * a4;
-                const int pn = (((n >> 4) ^ e) << 4) | (n & 15);
+                const int pn = (((n >> 4) ^ GB::swb(e)) << 4) | (n & 15);
                 const int k = kk + 8 * (g >> 1) + e;
                 const s16x4 lo = __builtin_amdgcn_ds_read_tr16_b64_v4i16((__attribute__((address_space(3))) s16x4*)(bs + k * 256 + pn));
                 tick();
@@ -750,12 +761,13 @@ struct GemmPingPong {
 
     // BK = 64: A chunk c of a stage (rows 8c..8c+7) and B chunk c (K rows 2c,
     // 2c+1), from the lane offsets va0 / vb0 of chunk 0 (offsets(.., 0, ..)):
-    // chunk c flips A's 16-byte column bits by c & 7 and B's bit 6 by c & 1.
+    // chunk c flips A's 16-byte column bits by c & 7 and takes B's offset
+    // for its parity.
     __device__ static void achunk(u32 base, int c, int va0, u32x4 ra, int soa, int lda) {
         dma16(ra, va0 ^ ((c & 7) << 4), soa + c * ARPB * lda * 2, base + c * 1024);
     }
-    __device__ static void bchunk(u32 base, int c, int vb0, u32x4 rb, int sob, int ldb) {
-        dma16(rb, vb0 ^ ((c & 1) << 6), sob + c * BRPB * ldb * 2, base + ASZ * 2 + c * 1024);
+    __device__ static void bchunk(u32 base, int c, const int (&vb0)[2], u32x4 rb, int sob, int ldb) {
+        dma16(rb, vb0[c & 1], sob + c * BRPB * ldb * 2, base + ASZ * 2 + c * 1024);
     }
 
     __device__ static void mma(Acc& acc, const Frag& f) {
@@ -778,36 +790,54 @@ struct GemmPingPong {
         }
     }
 
-    // C block (plus C when ACC) written in the accumulator layout; for ACC the
-    // C reads run NB accumulators ahead of the adds.
+    // C block (plus C when ACC) through LDS, with 128-bit global accesses.
+    // The accumulator layout gives each lane 4 rows of one column, so moving
+    // C straight from it takes 32-bit accesses, and the texture path
+    // addresses 4 lanes per clock: 16 B/clk per CU against 64 B/clk for
+    // 16-byte lanes.  Instead each wave writes one 32-row slab of its
+    // quadrant (accumulators (i, 0) and (i, 1)) into a private LDS region in
+    // row-major order (32-bit writes; the row pitch of 72 floats puts the two
+    // 32-lane halves of a write on disjoint banks), reads it back as 16-byte
+    // pieces (lane l: row 4q + l/16, columns 4*(l%16)..+3) and stores them
+    // with buffer_store_dwordx4; for ACC the slab's C is read ahead with
+    // buffer_load_dwordx4, one slab in advance, and added as c + sum.  A
+    // wave's LDS operations complete in order, so one region serves all four
+    // slabs.  The stage buffers are free here: group 0 runs this after group
+    // 1's last stage read (the barrier before group 0's last compute slot
+    // waits for it), group 1 after the barrier that ends group 0's epilogue.
     template <bool ACC>
-    __device__ static void c_out(Acc& acc, buf_rsrc rc, int ldc) {
-        if constexpr (!ACC) {
-            GB::template c_out<false>(acc, rc, ldc);
-        } else {
-            constexpr int NF = FI * FJ, NB = 6;
-            const int lane = threadIdx.x & 63, wave = wave_index();
-            const int wm = wave / WN, wn = wave % WN;
-            const int vc = ((lane >> 5) * 4 * ldc + (lane & 31)) * 4;
-            const int so = (wm * TM * ldc + wn * TN) * 4;
-            auto row = [&](int i, int e) { return so + (i * 32 + (e >> 2) * 8 + (e & 3)) * ldc * 4; };
-            float t[NF][16];
-            auto fetch = [&](int n) {
-                const int i = n / FJ, j = n % FJ;
+    __device__ static void c_out(Acc& acc, u16* lds, buf_rsrc rc, int ldc) {
+        constexpr int P = 72;
+        const int lane = threadIdx.x & 63, wave = wave_index();
+        const int wm = wave / WN, wn = wave % WN;
+        float* reg = reinterpret_cast<float*>(lds) + (wave & 3) * 32 * P;
+        const int so = (wm * TM * ldc + wn * TN) * 4;
+        const int vg = ((lane >> 4) * ldc + (lane & 15) * 4) * 4;
+        const int wr = (lane >> 5) * 4 * P + (lane & 31), rd = (lane >> 4) * P + (lane & 15) * 4;
+        f32x4v c[2][8];
+        auto fetch = [&](int i, f32x4v(&d)[8]) {
 #pragma unroll
-                for (int e = 0; e < 16; ++e) t[n][e] = __uint_as_float(__builtin_amdgcn_raw_buffer_load_b32(rc, vc + j * 128, row(i, e), 2));
-            };
+            for (int q = 0; q < 8; ++q)
+                d[q] = __builtin_bit_cast(f32x4v, __builtin_amdgcn_raw_buffer_load_b128(rc, vg, so + (i * 32 + q * 4) * ldc * 4, 2));
+        };
+        if constexpr (ACC) fetch(0, c[0]);
 #pragma unroll
-            for (int n = 0; n < NB; ++n) fetch(n);
-#pragma unroll
-            for (int n = 0; n < NF; ++n) {
-                const int i = n / FJ, j = n % FJ;
-                if (n + NB < NF) fetch(n + NB);
-#pragma unroll
-                for (int e = 0; e < 16; ++e)
-                    __builtin_amdgcn_raw_buffer_store_b32(__float_as_uint(t[n][e] + acc.v[i][j][e]), rc, vc + j * 128, row(i, e), 2);
-                __builtin_amdgcn_sched_barrier(0);
+        for (int i = 0; i < FI; ++i) {
+            if constexpr (ACC) {
+                if (i + 1 < FI) fetch(i + 1, c[(i + 1) & 1]);
             }
+#pragma unroll
+            for (int j = 0; j < FJ; ++j)
+#pragma unroll
+                for (int e = 0; e < 16; ++e) reg[wr + ((e >> 2) * 8 + (e & 3)) * P + j * 32] = acc.v[i][j][e];
+            __builtin_amdgcn_wave_barrier();
+#pragma unroll
+            for (int q = 0; q < 8; ++q) {
+                f32x4v x = *reinterpret_cast<const f32x4v*>(reg + rd + q * 4 * P);
+                if constexpr (ACC) x = c[i & 1][q] + x;
+                __builtin_amdgcn_raw_buffer_store_b128(__builtin_bit_cast(u32x4, x), rc, vg, so + (i * 32 + q * 4) * ldc * 4, 2);
+            }
+            __builtin_amdgcn_wave_barrier();
         }
     }
 
@@ -835,7 +865,7 @@ struct GemmPingPong {
         const buf_rsrc rc = __builtin_amdgcn_make_buffer_rsrc(pc, 0, -1, 0x00020000);
         const int nst = static_cast<int>(iters - it0);
         const u32 scratch = lds_address(lds + NS * STAGE);
-        int va0, vb0;
+        int va0, vb0[2];
         offsets(va0, vb0, 0, lda, ldb);
         const int pfa_v = (pfa_row + (lane & 31)) * lda * 2, pfb_v = ((pfb_row + (lane >> 2)) * ldb + (lane & 3) * 64) * 2;
         const bool touch = w == 0 && pfa_row >= 0 && pfb_row >= 0;
@@ -915,7 +945,7 @@ struct GemmPingPong {
             block_barrier();
         }
         wait_vmcnt<0>();
-        c_out<ACC>(acc, rc, ldc);
+        c_out<ACC>(acc, lds, rc, ldc);
         if (grp == 0) block_barrier();
     }
 
@@ -937,7 +967,7 @@ struct GemmPingPong {
         const buf_rsrc rc = __builtin_amdgcn_make_buffer_rsrc(pc, 0, -1, 0x00020000);
         const int nst = static_cast<int>(iters - it0);
         const u32 scratch = lds_address(lds + NS * STAGE);
-        int va, vb;
+        int va, vb[2];
         offsets(va, vb, w & 3, lda, ldb);
         const int pfa_v = (pfa_row + (lane & 31)) * lda * 2, pfb_v = ((pfb_row + (lane >> 2)) * ldb + (lane & 3) * 64) * 2;
         const bool touch = w == 0 && pfa_row >= 0 && pfb_row >= 0;
@@ -981,7 +1011,7 @@ struct GemmPingPong {
             }
             block_barrier();
         }
-        c_out<ACC>(acc, rc, ldc);
+        c_out<ACC>(acc, lds, rc, ldc);
         if (grp == 0) block_barrier();
     }
 };
