@@ -152,14 +152,29 @@ EmittedKernel emit_row(const Module& m, const KernelAnalysis& a, const LaunchSpe
         return moving[p] ? "(tb" + std::to_string(p) + "[u] + io" + std::to_string(p) + ")" : "tb" + std::to_string(p) + "[u]";
     };
 
-    // Values loaded up front: preloaded params and Load results.
+    // Accumulators under row loops (params that the loops do not move and
+    // that are stored) live in the register ld<param id> across the
+    // iterations.  A Load op of such a param reads that register: its result
+    // is a copy taken at the start of each iteration (before the iteration's
+    // store, which the admission check guarantees), not a load from memory.
+    auto is_acc = [&](int p) { return ni > 0 && !moving[p] && a.stored[p]; };
+    std::vector<std::pair<int, int>> acc_loads;  // Load result id, param id
+    std::vector<bool> acc_read(ntens, false);
+    for (const auto& op : k.ops)
+        if (op.kind == OpKind::Load && is_acc(tord(op.operands[0]))) {
+            acc_loads.emplace_back(op.result, op.operands[0]);
+            acc_read[tord(op.operands[0])] = true;
+        }
+
+    // Values loaded up front: preloaded params, accumulators read through a
+    // Load op, and the other Load results.
     std::vector<std::pair<int, int>> loads;  // value id, tensor ordinal
     for (size_t i = 0; i < k.params.size(); ++i) {
         const ValueInfo* v = a.by_id[k.params[i].id];
-        if (v->tile && a.preload[v->id]) loads.emplace_back(v->id, a.tensor_ordinal[i]);
+        if (v->tile && (a.preload[v->id] || acc_read[a.tensor_ordinal[i]])) loads.emplace_back(v->id, a.tensor_ordinal[i]);
     }
     for (const auto& op : k.ops)
-        if (op.kind == OpKind::Load) loads.emplace_back(op.result, tord(op.operands[0]));
+        if (op.kind == OpKind::Load && !is_acc(tord(op.operands[0]))) loads.emplace_back(op.result, tord(op.operands[0]));
 
     // A stored tensor that is also read: wait for outstanding loads before stores.
     std::set<int> read_t, stored_t;
@@ -268,7 +283,7 @@ EmittedKernel emit_row(const Module& m, const KernelAnalysis& a, const LaunchSpe
         // Accumulators that are stored but never read: their registers.
         for (int p = 0; p < ntens; ++p) {
             const int pid = k.params[a.tensor_param_index[p]].id;
-            if (moving[p] || !a.stored[p] || a.preload[pid]) continue;
+            if (moving[p] || !a.stored[p] || a.preload[pid] || acc_read[p]) continue;
             o << "    " << (cls(pid) == RowClass::Full ? "RS" : "float") << " ld" << pid << "[UP];\n";
         }
         o << "    i64 iters_ = 1;\n";
@@ -294,6 +309,8 @@ EmittedKernel emit_row(const Module& m, const KernelAnalysis& a, const LaunchSpe
         if (c == RowClass::RowVec || c == RowClass::RowVecT) o << "      const float v" << id << " = ld" << id << "[u];\n";
         else o << "      const RS& v" << id << " = ld" << id << "[u];\n";
     }
+    for (const auto& [id, pid] : acc_loads)
+        o << "      const " << (cls(pid) == RowClass::Full ? "RS" : "float") << " v" << id << " = ld" << pid << "[u];\n";
     bool waited = false;
     for (size_t oi = 0; oi < k.ops.size(); ++oi) {
         const auto& op = k.ops[oi];
@@ -383,7 +400,10 @@ EmittedKernel emit_row(const Module& m, const KernelAnalysis& a, const LaunchSpe
     o << "    }\n";
     if (ni) {
         o << "    }\n";  // in-kernel loops
-        // Accumulators back to memory.
+        // Accumulators back to memory, only when the loops ran: with an empty
+        // in-kernel extent no store executes, as in the reference, and the
+        // registers of an accumulator that is never read hold nothing.
+        o << "    if (iters_ > 0) {\n";
         for (int p = 0; p < ntens; ++p) {
             const int pid = k.params[a.tensor_param_index[p]].id;
             if (moving[p] || !a.stored[p]) continue;
@@ -391,6 +411,7 @@ EmittedKernel emit_row(const Module& m, const KernelAnalysis& a, const LaunchSpe
             store_row("      ", p, pid, "tb" + std::to_string(p) + "[u]", "ld" + std::to_string(pid) + "[u]", cls(pid) == RowClass::Full);
             o << "    }\n";
         }
+        o << "    }\n";
     }
     o << "  }\n}\n";
     ek.source = o.str();
