@@ -294,6 +294,42 @@ class _TileLanguage:
     def cos(self, x: Value) -> Value:
         return self._elementwise(OpKind.Cos, x)
 
+    # -- slice / interleave / broadcast (RoPE helpers) ----------------------
+    # The reference traces these as Constant ops that carry their operands
+    # and a marker attr (python/pto_wsp/kernel.py:631-685); its lowering gives
+    # a tile-shaped Constant no compute, so compiling a kernel that uses them
+    # raises CompileError here.  The result shapes follow the reference,
+    # including its (32, 64) / (32, 128) default for a scalar operand.
+    def slice_even(self, x: Value) -> Value:
+        """x[:, 0::2]: even-indexed elements along the last dimension."""
+        return self._half_slice(x, "even")
+
+    def slice_odd(self, x: Value) -> Value:
+        """x[:, 1::2]: odd-indexed elements along the last dimension."""
+        return self._half_slice(x, "odd")
+
+    def _half_slice(self, x: Value, which: str) -> Value:
+        ir = self._ir()
+        shape = (x.shape[0], x.shape[1] // 2) if x.shape else (32, 64)
+        out = Value(ValueId.next(), x.dtype, shape)
+        ir.add_op(OpKind.Constant, [x], out, slice_type=which)
+        return out
+
+    def interleave(self, a: Value, b: Value) -> Value:
+        """Even elements from a, odd elements from b, along the last dimension."""
+        ir = self._ir()
+        shape = (a.shape[0], a.shape[1] * 2) if a.shape else (32, 128)
+        out = Value(ValueId.next(), a.dtype, shape)
+        ir.add_op(OpKind.Constant, [a, b], out, op_type="interleave")
+        return out
+
+    def broadcast(self, x: Value, shape: tuple) -> Value:
+        """x broadcast to `shape`."""
+        ir = self._ir()
+        out = Value(ValueId.next(), x.dtype, tuple(shape))
+        ir.add_op(OpKind.Constant, [x], out, broadcast_shape=tuple(shape))
+        return out
+
     # -- reductions --------------------------------------------------------
     def rowsum(self, x: Value) -> Value:
         return self._row_reduce(OpKind.RowSum, x)

@@ -186,6 +186,47 @@ def test_ops_without_reference_compute_are_refused():
     _compile_err(wl(), "no compute")
 
 
+@pytest.mark.parametrize("op", ["slice_even", "slice_odd", "interleave", "broadcast"])
+def test_rope_helpers_trace_then_refuse(op):
+    """The reference traces these as tile-shaped Constant ops carrying their operands
+    (python/pto_wsp/kernel.py:631-685), which its lowering gives no compute; the trace
+    succeeds here with the same shapes and markers, and compiling refuses it."""
+    from pto_wsp.kernel import OpKind
+
+    X = Tensor(data=None, shape=(2, 8, 16), dtype=DType.F32)
+    Y = Tensor(data=None, shape=(2, 8, 16), dtype=DType.F32)
+
+    @kernel
+    def k(x: In[Tile[8, 16, DType.F32]], y: Out[Tile[8, 16, DType.F32]]):
+        if op == "slice_even":
+            r = pto.interleave(pto.slice_even(x), pto.slice_even(x))
+        elif op == "slice_odd":
+            r = pto.interleave(pto.slice_odd(x), pto.slice_odd(x))
+        elif op == "interleave":
+            r = pto.interleave(pto.slice_even(x), pto.slice_odd(x))
+        else:
+            r = pto.broadcast(pto.rowsum(x), (8, 16))
+        pto.store(y, r)
+
+    ir = k.trace()
+    consts = [o for o in ir.ops if o.kind == OpKind.Constant]
+    assert consts and all(o.result.shape is not None for o in consts)
+    if op == "broadcast":
+        assert consts[0].result.shape == (8, 16) and consts[0].attrs["broadcast_shape"] == (8, 16)
+    else:
+        halves = [o for o in consts if "slice_type" in o.attrs]
+        assert {o.result.shape for o in halves} == {(8, 8)}
+        assert consts[-1].attrs["op_type"] == "interleave" and consts[-1].result.shape == (8, 16)
+        assert len(consts[-1].operands) == 2
+
+    @workload
+    def wl():
+        for i in P(Dense[2]()):
+            k[i](x=X[i], y=Y[i])
+
+    _compile_err(wl(), "no compute")
+
+
 def test_ragged_axis_compiles():
     y = np.zeros((3, 1, 1), np.int32)
     r = Ragged(2, [1, 1])
