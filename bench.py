@@ -419,22 +419,33 @@ class RowCase:
                 f"P(batch={self.shape[0]}) x P(tiles={self.shape[1]}), round_robin(4), TaskWindow(8192, STALL)")
 
     def cpu(self, budget_s):
-        """Oracle over the whole workload (repeated within the budget) + parity of the GPU output."""
+        """Oracle over the whole workload (repeated within the budget) + parity of the GPU output.
+        The module is serialized once, as the reference compiles its artifact once; each timed
+        run is the oracle's execution of the whole workload (wall clock around the call, like the
+        reference's execute() + synchronize()).  Small workloads repeat up to 5000 times."""
         import numpy as np
 
-        from oracle.runner import run_workload
+        from oracle.runner import run_module
+        from pto_wsp.ir_bridge import workload_to_codegen_ir
+        from pto_wsp.program import Program
 
         xh = self.x.detach().cpu().numpy()
         yh = np.zeros_like(xh)
+        wl = row_workload(self.kind, xh, yh)
+        build = workload_to_codegen_ir(wl, module_name="bench_cpu")
+        arrays = [t.data for t in build.tensors]
+        sizes = Program._infer_axis_sizes(wl)
         times = []
         t_start = time.perf_counter()
-        while len(times) < 8 and (time.perf_counter() - t_start) < budget_s:
+        while len(times) < 5000 and (len(times) < 8 or self.x.numel() < (1 << 20)) and (time.perf_counter() - t_start) < budget_s:
             t0 = time.perf_counter()
-            run_workload(row_workload(self.kind, xh, yh))
+            res = run_module(build.module, arrays, sizes)
             times.append(time.perf_counter() - t0)
         sec = sum(times) / len(times)
+        self.cpu_us_per_run = sec * 1e6
+        self.cpu_tasks_per_s = res.task_count / sec
         same = bool(np.allclose(self.y.cpu().numpy(), yh, rtol=1e-5, atol=1e-6 if self.kind != "softmax" else 0.0))
-        sample = (f"the full {self.name} workload X{list(self.shape)}, {len(times)} run(s) of {sec:.2f} s each, "
+        sample = (f"the full {self.name} workload X{list(self.shape)}, {len(times)} run(s) of {sec * 1e3:.4g} ms each, "
                   f"wall clock around the oracle call")
         return self.work / sec / 1e9, sample, same
 
@@ -604,10 +615,15 @@ def main():
                  "total_cycles": case.prog.stats.total_cycles,
                  "kernel_us": round(k_ms * 1e3, 2), "step_us": round(ms_step * 1e3, 2),
                  "tasks_per_s": round(case.prog.stats.task_count / (ms_step * 1e-3), 1)}
-        if not args.no_cpu and name != "rmsnorm_quickstart":
-            rate, sample, same = case.cpu(12.0 if name == head else 6.0)
+        if not args.no_cpu:
+            rate, sample, same = case.cpu(12.0 if name == head else (2.0 if name == "rmsnorm_quickstart" else 6.0))
             entry["cpu_sim_port"] = round(rate, 6)
             entry["matches_cpu_sim"] = same
+            entry["cpu_sample"] = sample
+            entry["cpu_cores"] = f"1 of {len(os.sched_getaffinity(0))}"
+            if hasattr(case, "cpu_us_per_run"):
+                entry["cpu_us_per_run"] = round(case.cpu_us_per_run, 2)
+                entry["cpu_tasks_per_s"] = round(case.cpu_tasks_per_s, 1)
             if name == head:
                 cpu = {"value": round(rate, 4), "unit": case.unit, "cores": 1, "kind": "port",
                        "sample": sample + f", 1 of {len(os.sched_getaffinity(0))} cores"}

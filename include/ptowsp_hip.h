@@ -68,20 +68,23 @@ uint64_t ptowsp_hip_workload_main(ptowsp_program* prog, RuntimeContext* ctx, CSP
 int ptowsp_hip_launch(ptowsp_program* prog, RuntimeContext* ctx, void* hip_stream, ptowsp_run_info* info);
 
 /* No counterpart in the reference.  For callers that cannot allocate memory
- * (code under HIP graph capture, tight serving loops, harnesses that forbid
- * hipMalloc): the same run as ptowsp_hip_launch, allocating no device or
- * pinned memory and loading no code objects.  The decode kernels' unit
- * counters and partials, the kernels' error flag and the copy of
- * device-resident loop-extent tensors use a fixed device scratch of 16 MiB
- * per GPU (held until the process ends); a run that needs more is refused
- * with an error before its decode launch.  Requirements: every tensor is
- * device memory; each launch's kernel was already built and loaded by an
- * earlier ptowsp_hip_launch of the same program (same bindings); no cpp_src
- * kernels, slot loads or masked (cond-on-grid) launches.  All no-allocation
- * runs on one GPU share its scratch: runs that overlap in time on one GPU
- * race and must not be issued.  Finish with ptowsp_hip_synchronize as usual;
- * device time is reported only when an earlier ptowsp_hip_launch created the
- * program's timing events. */
+ * (tight serving loops, harnesses that forbid hipMalloc): the same run as
+ * ptowsp_hip_launch, allocating no device or pinned memory and loading no
+ * code objects.  The decode kernels' unit counters and partials, the
+ * kernels' error flag and the copy of device-resident loop-extent tensors
+ * use a fixed device scratch of 16 MiB per GPU (held until the process
+ * ends); a run that needs more is refused with an error before its decode
+ * launch.  Requirements: every tensor is device memory; each launch's
+ * kernel was already built and loaded by an earlier ptowsp_hip_launch of
+ * the same program (same bindings), which also resolves the device's
+ * scratch and loads the kernel that clears it (without one on this device
+ * the call is refused); no cpp_src kernels, slot loads or masked
+ * (cond-on-grid) launches.  It is not made for HIP stream capture: it
+ * records timing events and may read index tensors with synchronous
+ * copies.  All no-allocation runs on one GPU share its scratch: runs that
+ * overlap in time on one GPU race and must not be issued.  Finish with
+ * ptowsp_hip_synchronize as usual; device time is reported only when an
+ * earlier ptowsp_hip_launch created the program's timing events. */
 int ptowsp_hip_launch_noalloc(ptowsp_program* prog, RuntimeContext* ctx, void* hip_stream, ptowsp_run_info* info);
 
 /* Cycle model result of the last synchronized run (new: pairs with the

@@ -9,6 +9,7 @@
 // shares it and finds whatever the previous run left there.
 #include <hip/hip_runtime.h>
 
+#include <atomic>
 #include <mutex>
 #include <stdexcept>
 #include <string>
@@ -22,6 +23,7 @@ static __device__ __align__(256) unsigned char scratch[ptowsp::kNoAllocScratchBy
 constexpr int kMaxDevices = 64;
 std::mutex g_mu;
 void* g_ptr[kMaxDevices] = {};
+std::atomic<bool> g_ready[kMaxDevices] = {};
 
 // Sets n 32-bit words to zero (a kernel rather than hipMemsetAsync, so that a
 // caller may capture the run into a HIP graph).
@@ -39,17 +41,36 @@ void check(hipError_t e, const char* what) {
 
 namespace ptowsp {
 
-void* noalloc_scratch() {
+namespace {
+int current_device() {
     int dev = 0;
     check(hipGetDevice(&dev), "hipGetDevice");
     if (dev < 0 || dev >= kMaxDevices) throw std::runtime_error("no-allocation scratch: device index out of range");
+    return dev;
+}
+}  // namespace
+
+void noalloc_prepare(hipStream_t stream) {
+    const int dev = current_device();
+    if (g_ready[dev].load(std::memory_order_acquire)) return;
     std::lock_guard<std::mutex> lock(g_mu);
-    if (!g_ptr[dev]) {
-        void* p = nullptr;
-        check(hipGetSymbolAddress(&p, HIP_SYMBOL(scratch)), "hipGetSymbolAddress(no-allocation scratch)");
-        if (!p) throw std::runtime_error("hipGetSymbolAddress(no-allocation scratch) returned a null address");
-        g_ptr[dev] = p;
-    }
+    if (g_ready[dev].load(std::memory_order_relaxed)) return;
+    void* p = nullptr;
+    check(hipGetSymbolAddress(&p, HIP_SYMBOL(scratch)), "hipGetSymbolAddress(no-allocation scratch)");
+    if (!p) throw std::runtime_error("hipGetSymbolAddress(no-allocation scratch) returned a null address");
+    // The zeroing kernel's first launch loads the code object; every
+    // no-allocation run clears the words it needs again before use.
+    noalloc_zero(p, 256, stream);
+    g_ptr[dev] = p;
+    g_ready[dev].store(true, std::memory_order_release);
+}
+
+void* noalloc_scratch() {
+    const int dev = current_device();
+    if (!g_ready[dev].load(std::memory_order_acquire))
+        throw std::runtime_error(
+            "ptowsp_hip_launch_noalloc: no ptowsp_hip_launch has run on this device yet (it resolves the fixed scratch and "
+            "loads its kernel, which this entry point does not)");
     return g_ptr[dev];
 }
 

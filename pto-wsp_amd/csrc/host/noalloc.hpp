@@ -15,8 +15,14 @@ namespace ptowsp {
 constexpr size_t kNoAllocScratchBytes = size_t(16) << 20;
 constexpr size_t kNoAllocHeaderBytes = 256;
 
-// Device address of this device's scratch array (looked up once per device
-// with hipGetSymbolAddress, then cached).
+// Set-up, run by every allocating launch (cheap after the first on a
+// device): looks up this device's scratch address with hipGetSymbolAddress
+// and runs the zeroing kernel once on it, so that the library's code object
+// is loaded and the array is resident before any no-allocation run.
+void noalloc_prepare(hipStream_t stream);
+
+// Device address of this device's scratch array, as found by
+// noalloc_prepare; throws when no allocating launch has prepared it.
 void* noalloc_scratch();
 
 // Zeroes `bytes` (a multiple of 4) at dev_ptr with a small kernel on `stream`.

@@ -214,7 +214,6 @@ struct RunEnv {
     std::vector<std::pair<std::string, int64_t>> host_vars;
     std::map<int, std::vector<int32_t>> idx_host;  // device index tensors read on the host, copied once per run
     bool timing_started = false;                   // ev0 recorded (just before the first kernel)
-    bool timing_ended = false;                     // ev1 is the end of the last kernel launched
     bool replay_slots = false;                     // cycle model: slot loads replay P->slot_log
     bool timing = true;                            // record ev0 / ev1 (the program's events exist)
     // No-allocation run: the kernels' error flag, and the device scratch that
@@ -234,28 +233,19 @@ void start_timing(RunEnv& E, hipStream_t stream) {
     E.timing_started = true;
 }
 
-// Launches one kernel.  With timing on, the launch's own start / stop events
-// bracket it: the first kernel of the run starts the device-time interval at
-// its dispatch and every kernel moves the end to its completion, so the
-// interval is the kernels' execution (and whatever the stream runs between
-// them), without the command processor's latency before the first dispatch.
+// Launches one kernel.  Device time runs from the start event, recorded on
+// the stream just before the run's first kernel, to the end event recorded
+// after its last one.  Events attached to the dispatch itself
+// (hipExtModuleLaunchKernel's start / stop events) would leave out the
+// command processor's latency before the first dispatch (about 1 us), but
+// measured 15 us more host time per launch on the MI355X box; the separate
+// records cost about 2.5 us each.
 void launch_kernel(RunEnv& E, hipFunction_t f, int64_t blocks, int threads, size_t lds, hipStream_t stream, void** params,
                    const char* what) {
-    const uint64_t work = static_cast<uint64_t>(blocks) * static_cast<uint64_t>(threads);
-    if (E.timing && work <= 0xFFFFFFFFull) {
-        hipEvent_t start = E.timing_started ? nullptr : E.P->ev0;
-        check(hipExtModuleLaunchKernel(f, static_cast<uint32_t>(work), 1, 1, static_cast<uint32_t>(threads), 1, 1, lds, stream,
-                                       params, nullptr, start, E.P->ev1, 0),
-              what);
-        E.timing_started = true;
-        E.timing_ended = true;
-        return;
-    }
     start_timing(E, stream);
     check(hipModuleLaunchKernel(f, static_cast<unsigned>(blocks), 1, 1, static_cast<unsigned>(threads), 1, 1,
                                 static_cast<unsigned>(lds), stream, params, nullptr),
           what);
-    E.timing_ended = false;
 }
 
 int64_t axis_extent(RunEnv& E, const Axis& a) {
@@ -1574,6 +1564,7 @@ int launch_impl(ptowsp_program* P, RuntimeContext* ctx, void* hip_stream, ptowsp
         E.err = reinterpret_cast<int*>(E.nscratch);
         E.timing = P->have_events;
     } else {
+        noalloc_prepare(stream);
         if (!P->h_err) {
             check(hipHostMalloc(reinterpret_cast<void**>(&P->h_err), sizeof(int), hipHostMallocMapped | hipHostMallocCoherent),
                   "hipHostMalloc(err)");
@@ -1640,7 +1631,7 @@ int launch_impl(ptowsp_program* P, RuntimeContext* ctx, void* hip_stream, ptowsp
         cyc = cycles_for(E);
     }
     start_timing(E, stream);
-    if (E.timing && !E.timing_ended) check(hipEventRecord(P->ev1, stream), "hipEventRecord");
+    if (E.timing) check(hipEventRecord(P->ev1, stream), "hipEventRecord");
     // After the end event: the copy is not device time of the program.
     if (!dev_ext.empty() && !ext_written) defer_cycles(E, dev_ext, stream);
     check(hipGetLastError(), "kernel launch");

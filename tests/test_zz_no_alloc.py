@@ -4,9 +4,11 @@ The no-allocation entry point must give the same results as
 ptowsp_hip_launch: the paged decode (whose kernels use the scratch buffer:
 unit counters and partials) is run through both on the same program and
 bindings, twice in a row with a smaller second input, and the outputs must be
-identical bit for bit, with identical cycle-model results.  Also checked: a
-decode launch that needs more than the fixed scratch is refused with an error,
-and host-resident tensors are refused.
+identical bit for bit, with identical cycle-model results, and the device's
+free memory (hipMemGetInfo) must be the same before and after the
+no-allocation run.  Also checked: a decode launch that needs more than the
+fixed scratch is refused with an error, and host-resident tensors are
+refused.
 """
 
 import ctypes
@@ -78,8 +80,12 @@ def test_noalloc_decode_matches_launch_twice(gpu):
         # Leave garbage in the outputs and accumulators' neighbours: the run must not depend on them.
         _reset(t)
         t["out"].fill_(123.0)
+        torch.cuda.synchronize()
+        free_before = torch.cuda.mem_get_info(gpu)[0]
         got_cycles = p.run(_lib.ptowsp_hip_launch_noalloc)
         torch.cuda.synchronize()
+        free_after = torch.cuda.mem_get_info(gpu)[0]
+        assert free_after == free_before, (free_before, free_after)
         assert torch.equal(t["out"], ref)
         assert got_cycles == ref_cycles
         # The existing entry point is unaffected by the no-allocation run in between.
