@@ -1054,7 +1054,9 @@ EmittedKernel emit_decode(const Module& m, const KernelAnalysis& a, const Launch
     }
     o << "        if (npg < 0) npg = 0;\n";
     o << "        if (npg > maxp) { npg = maxp; if (blockIdx.x == 0) *A.err = 3; }\n";
-    o << "        n_[i] = static_cast<int>(npg);\n";
+    // Pages of more than 16 tokens are folded as 16-token sub-pages: the
+    // prefixes, the split and the stream count sub-pages.
+    o << "        n_[i] = static_cast<int>(npg) * " << d.pg / 16 << ";\n";
     o << "        run += n_[i];\n";
     o << "        crun += DecodeSplit::cost(n_[i]);\n";
     o << "      }\n";
@@ -1114,23 +1116,34 @@ EmittedKernel emit_decode(const Module& m, const KernelAnalysis& a, const Launch
     o << "  int* cnt = reinterpret_cast<int*>(A.base[" << ntens << "]);\n";
     o << "  float* partials = reinterpret_cast<float*>(A.base[" << ntens << "] + DecodeSplit::kMaxUnits * 4);\n";
     o << "  float* lds = lds_all[wave];\n";
-    // Offsets of global page g (per lane): its unit, the page index within
-    // the unit, the affine and page-table terms; an out-of-range page raises
-    // the error flag and reads the tensor's first page instead.
+    // Offsets of global (sub-)page g (per lane): its unit, the page index
+    // within the unit, the affine and page-table terms, and for pages of
+    // more than 16 tokens the sub-page's first token (its token stride: s4
+    // of the K^T and mask tiles, s3 of the V tile).  The 16-token tile that
+    // is loaded is bounds-checked; an out-of-range one raises the error flag
+    // and reads the tensor's first tile instead.
+    const int sub = d.pg / 16;
     o << "  auto f_page = [&](i64 g, PageOffs& po) {\n";
     o << "    const int uu = DecodeSplit::unit_of(pre, U, g);\n";
     o << "    i64 vars[" << nvars << "];\n";
     decode_vars("uu", "    ");
-    o << "    vars[" << ng << "] = g - pre[uu];\n";
-    auto checked = [&](int p, int rows, int cols, const std::string& field) {
-        o << "    { i64 o_ = " << offset_expr(p, nvars, first_term[p], nterms(p)) << ";\n";
+    if (sub == 1) {
+        o << "    vars[" << ng << "] = g - pre[uu];\n";
+        o << "    const i64 t0_ = 0;\n";
+    } else {
+        o << "    const i64 vp_ = g - pre[uu];\n";
+        o << "    vars[" << ng << "] = vp_ / " << sub << ";\n";
+        o << "    const i64 t0_ = (vp_ % " << sub << ") * 16;\n";
+    }
+    auto checked = [&](int p, int rows, int cols, const std::string& field, const std::string& tstride) {
+        o << "    { i64 o_ = " << offset_expr(p, nvars, first_term[p], nterms(p)) << " + t0_ * " << tstride << ";\n";
         o << "      if (o_ < 0 || o_ + (i64)" << rows - 1 << " * A.s3[" << p << "] + (i64)" << cols - 1 << " * A.s4[" << p
           << "] >= A.span[" << p << "]) { *A.err = 2; o_ = 0; }\n";
         o << "      po." << field << " = o_; }\n";
     };
-    checked(d.kt, d.d, d.pg, "k");
-    checked(d.v, d.pg, d.d, "v");
-    if (d.mask >= 0) checked(d.mask, 1, d.pg, "m");
+    checked(d.kt, d.d, 16, "k", "A.s4[" + std::to_string(d.kt) + "]");
+    checked(d.v, 16, d.d, "v", "A.s3[" + std::to_string(d.v) + "]");
+    if (d.mask >= 0) checked(d.mask, 1, 16, "m", "A.s4[" + std::to_string(d.mask) + "]");
     else o << "    po.m = 0;\n";
     o << "  };\n";
     o << "  auto f_bases = [&](const PageOffs& po, const u16*& kp, const u16*& vp, const float*& mp) {\n";

@@ -718,9 +718,12 @@ bool decode_allowed(const KernelAnalysis& a, const LaunchSpec& L, const LaunchAr
     const int64_t maxp = ax.kind == AxisKind::DynTensor ? ax.max : A.ext[ng];
     int64_t units = 1;
     for (int v = 0; v < ng; ++v) units *= A.ext[v];
-    // Page and cost prefixes (pages + kDecodeUnitCost per unit) stay below 2^31.
-    if (units < 1 || units > kDecodeMaxUnits || maxp < 0 || maxp + kDecodeUnitCost >= (int64_t(1) << 31) / units) return false;
+    // Page and cost prefixes (16-token sub-pages + kDecodeUnitCost per unit) stay below 2^31.
     const DecodeInfo& d = a.decode;
+    const int64_t sub = d.pg / 16;
+    if (units < 1 || units > kDecodeMaxUnits || maxp < 0 || maxp > (int64_t(1) << 31) / sub ||
+        maxp * sub + kDecodeUnitCost >= (int64_t(1) << 31) / units)
+        return false;
     const int nvars = ng + 1;
     const int ntens = static_cast<int>(a.tensor_param_index.size());
     if (ntens + 1 > kMaxParams) return false;  // one extra slot: counters and partials

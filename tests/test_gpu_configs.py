@@ -171,3 +171,35 @@ def test_config4_paged_decode_full(gpu):
     np.testing.assert_allclose(got, h["out"], rtol=2e-5, atol=2e-5 * float(np.abs(h["out"]).max()))
     del t
     torch.cuda.empty_cache()
+
+
+def test_paged_decode_32_token_pages_full(gpu):
+    """Config 5's shape with 32-token pages (folded as two 16-token sub-pages by the
+    decode family): every sequence and KV head against float64 attention."""
+    import torch
+
+    dev = torch.device("cuda:0")
+    t = W.paged_decode_torch(dev, 64, 32, 8, 128, 512, 8192, seed=1, page=32)
+    prog = W.rr4(W.paged_decode(t)).compile(target="hip_gfx950")
+    assert prog._native.kernel_family("decode_page") == "decode"
+    prog.execute()
+    prog.synchronize()
+    lengths = t["lengths"]
+    npg = (lengths + 31) // 32
+    assert prog.stats.task_count == 8 * int(npg.sum()) + 64 * 8
+    out = t["out"]
+    for b in range(64):
+        L, n = int(lengths[b]), int(npg[b])
+        pages = t["page_table"][b, :n].long()
+        k = t["k_cache"][pages].double().permute(1, 0, 2, 3).reshape(8, n * 32, 128)[:, :L]
+        v = t["v_cache"][pages].double().permute(1, 0, 2, 3).reshape(8, n * 32, 128)[:, :L]
+        q = t["q"][b].double()
+        s = torch.matmul(q, k.transpose(1, 2).contiguous()) / (128 ** 0.5)
+        ref = torch.matmul(torch.softmax(s, dim=-1), v)
+        got = out[b].double()
+        for g in range(8):
+            rel = float((got[g] - ref[g]).norm() / ref[g].norm())
+            assert rel <= 1e-5, (b, g, rel)
+        del k, v, s, ref, got
+    del t
+    torch.cuda.empty_cache()

@@ -3,7 +3,8 @@
 Each seed draws the query rows per KV head (1..16), the head dim (64, 128,
 256, with rows x dim <= 1024), the KV heads, 1..24 sequences whose lengths
 mix empty, sub-page, exact-page and multi-thousand-token sequences, the page
-size (16: the streaming decode family; 8: the tile program), the mask, and
+size (16, 32, 64: the streaming decode family, which folds pages of more
+than 16 tokens as 16-token sub-pages; 8: the tile program), the mask, and
 the input dtype (bf16 / f16).  The GPU accumulators and output must equal
 the oracle's within rtol 2e-5 (with an atol of 2e-5 of each tensor's largest
 magnitude: both fold the pages in fp32, split differently), sequences with
@@ -26,17 +27,18 @@ def _case(seed):
         group, d = int(rng.integers(1, 17)), int(rng.choice([64, 128, 256]))
         if group * d <= 1024:
             break
+    page = int(rng.choice([8, 16, 16, 16, 32, 32, 64]))
     n = int(rng.integers(1, 25))
     kinds = rng.integers(0, 4, n)
-    lengths = [0 if k == 0 else int(rng.integers(1, 17)) if k == 1 else 16 * int(rng.integers(1, 9)) if k == 2
-               else int(rng.integers(17, 3000)) for k in kinds]
+    lengths = [0 if k == 0 else int(rng.integers(1, page + 1)) if k == 1 else page * int(rng.integers(1, 9)) if k == 2
+               else int(rng.integers(page + 1, 3000)) for k in kinds]
     if max(lengths) == 0:
         lengths[0] = 5
-    return dict(lengths=lengths, hkv=int(rng.integers(1, 5)), group=group, d=d, page=16 if rng.random() < 0.8 else 8,
+    return dict(lengths=lengths, hkv=int(rng.integers(1, 5)), group=group, d=d, page=page,
                 masked=bool(rng.random() < 0.8), f16=bool(rng.random() < 0.3))
 
 
-@pytest.mark.parametrize("seed", range(16))
+@pytest.mark.parametrize("seed", range(24))
 def test_random_decode_matches_oracle(gpu, seed):
     c = _case(seed)
     print(c, flush=True)
@@ -44,6 +46,9 @@ def test_random_decode_matches_oracle(gpu, seed):
     ca = {k: v.copy() for k, v in ga.items()}
     dt = W.F16 if c["f16"] else W.BF16
     prog = W.paged_decode(ga, masked=c["masked"], dtype=dt).compile(target="hip_gfx950")
+    # (a [1, page] mask with as many query rows as page tokens is a row broadcast, see below)
+    want_family = "tile_program" if c["page"] == 8 or (c["masked"] and c["group"] == c["page"]) else "decode"
+    assert prog._native.kernel_family("decode_page") == want_family
     prog.execute()
     prog.synchronize()
     ref = run_workload(W.paged_decode(ca, masked=c["masked"], dtype=dt))

@@ -159,6 +159,24 @@ def test_family_selection():
     assert prog.kernel_family("decode_page") == "tile_program"
 
 
+@pytest.mark.parametrize("page, family", [(16, "decode"), (32, "decode"), (64, "decode"), (128, "decode"),
+                                          (8, "tile_program"), (48, "tile_program")])
+def test_decode_family_page_sizes(page, family):
+    """Pages of 16, 32, 64 or 128 tokens take the decode family (pages of more than 16
+    tokens are folded as 16-token sub-pages: each sub-page's offset is the page's plus
+    16 tokens times the token stride); other sizes stay on the tile program."""
+    from pto_wsp._hip import NativeProgram
+
+    arrs = W.paged_decode_arrays([40, 300, 0, 17], 2, 4, 128, page=page)
+    prog = NativeProgram(workload_to_codegen_ir(W.rr4(W.paged_decode(arrs)), "d").module)
+    assert prog.kernel_family("decode_page") == family
+    if family == "decode":
+        src = prog.precompile(0)
+        assert "decode program" in src
+        assert f"n_[i] = static_cast<int>(npg) * {page // 16};" in src  # sub-page counts in the prefixes
+        assert ("vp_ %" in src) == (page > 16)
+
+
 def _compile_err(w, match):
     with pytest.raises(CompileError, match=match):
         Program(w, "hip_gfx950", {})
