@@ -25,8 +25,8 @@ std::mutex g_mu;
 void* g_ptr[kMaxDevices] = {};
 std::atomic<bool> g_ready[kMaxDevices] = {};
 
-// Sets n 32-bit words to zero (a kernel rather than hipMemsetAsync, so that a
-// caller may capture the run into a HIP graph).
+// Sets n 32-bit words to zero (a kernel rather than hipMemsetAsync: it
+// allocates nothing and records no memset node if the stream is captured).
 __global__ void zero_words(unsigned int* p, unsigned long long n) {
     for (unsigned long long i = blockIdx.x * static_cast<unsigned long long>(blockDim.x) + threadIdx.x; i < n;
          i += static_cast<unsigned long long>(gridDim.x) * blockDim.x)
