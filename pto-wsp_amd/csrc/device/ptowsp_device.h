@@ -373,6 +373,12 @@ __device__ inline f32x16 mfma_32x32x16(u32x4 a, u32x4 b, f32x16 c) {
                                                        0);
 }
 
+// Compile-time bool carried as a type (for generic lambdas under C++17).
+template <bool B>
+struct BoolC {
+    static constexpr bool value = B;
+};
+
 __device__ inline int wave_index() { return __builtin_amdgcn_readfirstlane(static_cast<int>(threadIdx.x >> 6)); }
 
 // Raw dword buffer descriptor for p (no range check: offsets are bounded on the host).
@@ -902,47 +908,70 @@ struct GemmPingPong {
         wait_vmcnt<0>();
         block_barrier();
         if (grp == 1) block_barrier();  // group 1 runs one slot behind
-        for (int j = 0; j < nst; ++j) {
-            const bool t = touch && j + PF < nst;
-            if (grp == 0) {
-                const bool h1 = j + 1 < nst;
+        // One iteration (stage j) of group G.  H1 / H2: stages j+1 / j+2
+        // exist (their DMA is issued here); T: wave 0's L2 touches of stage
+        // j+PF.  The conditions are compile-time: a branch on them inside
+        // the loop delays the computing group's barrier arrival and the
+        // reading group's reads (measured without DMA: 36.7 cycles per MFMA
+        // with the branches against 34.6 without, 32.4 for the bare
+        // alternation).
+        auto step = [&](auto g_, auto h1_, auto h2_, auto t_, int j) {
+            constexpr bool G1 = decltype(g_)::value, H1 = decltype(h1_)::value, H2 = decltype(h2_)::value;
+            constexpr bool T = decltype(t_)::value;
+            if constexpr (!G1) {
                 read(f, lds + (j % NS) * STAGE, wm, wn, [&](int k) {
-                    if (h1 && k < 8) issue_b(j + 1, k);
+                    if constexpr (H1) {
+                        if (k < 8) issue_b(j + 1, k);
+                    }
                 });
-                if (t) {
+                if constexpr (T) {
                     int soa, sob;
                     off(it0 + j + PF, soa, sob);
                     dma4(ra, pfa_v, soa, scratch);
                     dma4(rb, pfb_v, sob, scratch);
                 }
             } else {
-                const bool h1 = j + 1 < nst, h2 = j + 2 < nst;
                 read(f, lds + (j % NS) * STAGE, wm, wn, [&](int k) {
                     if (k < 4) {
-                        if (h1) issue_a(j + 1, 1, k);
-                    } else if (k < 8 && h2) {
-                        issue_a(j + 2, 0, k - 4);
+                        if constexpr (H1) issue_a(j + 1, 1, k);
+                    } else if (k < 8) {
+                        if constexpr (H2) issue_a(j + 2, 0, k - 4);
                     }
                 });
                 // A rows 0-127 of stage j+1 (issued in this group's previous read slot) have landed
-                const int pending = (h1 ? 4 : 0) + (h2 ? 4 : 0);
-                if (pending == 8) wait_vmcnt<8>();
-                else if (pending == 4) wait_vmcnt<4>();
+                if constexpr (H1 && H2) wait_vmcnt<8>();
+                else if constexpr (H1 || H2) wait_vmcnt<4>();
                 else wait_vmcnt<0>();
             }
             wait_lgkm0();
             block_barrier();
             mma(acc, f);
-            if (grp == 0) {
+            if constexpr (!G1) {
                 // own B of stage j+1 landed (wave 0's two touches may stay in flight)
-                if (t) wait_vmcnt<2>();
+                if constexpr (T) wait_vmcnt<2>();
                 else wait_vmcnt<0>();
             } else {
                 // own A rows 128-255 of stage j+1 landed (rows 0-127 of stage j+2 may stay in flight)
-                if (j + 2 < nst) wait_vmcnt<4>();
+                if constexpr (H2) wait_vmcnt<4>();
                 else wait_vmcnt<0>();
             }
             block_barrier();
+        };
+        // Stages 0 .. nst-PF-1 in the steady loop (every condition holds),
+        // then the last three with their own conditions.
+        static_assert(PF == 3, "the peeled tail covers the stages without L2 touches");
+        auto run_group = [&](auto g_, auto t_) {
+            int j = 0;
+            for (; j + PF < nst; ++j) step(g_, BoolC<true>{}, BoolC<true>{}, t_, j);
+            if (j + 2 < nst) step(g_, BoolC<true>{}, BoolC<true>{}, BoolC<false>{}, j++);
+            if (j + 1 < nst) step(g_, BoolC<true>{}, BoolC<false>{}, BoolC<false>{}, j++);
+            if (j < nst) step(g_, BoolC<false>{}, BoolC<false>{}, BoolC<false>{}, j);
+        };
+        if (grp == 0) {
+            if (touch) run_group(BoolC<false>{}, BoolC<true>{});
+            else run_group(BoolC<false>{}, BoolC<false>{});
+        } else {
+            run_group(BoolC<true>{}, BoolC<false>{});
         }
         wait_vmcnt<0>();
         c_out<ACC>(acc, lds, rc, ldc);
