@@ -1053,16 +1053,17 @@ struct GemmPingPong {
 // waves (DecodeSplit); each wave folds its pages into a partial (m, l, o) for
 // the unit's G query rows, starting from (-inf, 0, 0), and DecodeCombine folds
 // the unit's partials in page order into the accumulators.  Per page:
-//  * scores on MFMA v_mfma_f32_16x16x32 (one per 32-wide head-dim slice):
-//    A = q (lane l: query row l%16, zero for rows >= G, head dims
-//    8*(l/16)..+7 of the slice), B = the K page (lane l: token l%16); lane l
-//    then holds query rows 4*(l/16)..+3 for token l%16;
-//  * the scores pass through LDS so that each pass holds one (query row,
-//    token) per lane; row max and row sum over a 16-lane DPP row;
-//  * p and the rescale factor pass through LDS; p @ v runs on the matrix
-//    cores (v_mfma_f32_16x16x16, p split into two 16-bit parts), lane l
-//    supplying tokens 4*(l/16)..+3 of every page for head dims (D/16)*(l%16)+e
-//    and accumulating query rows 4*(l/16)..+3 of them.
+//  * scores transposed, S^T = K q^T, on v_mfma_f32_16x16x32 (one per 32-wide
+//    head-dim slice): A = the K page (lane l: token l%16, head dims
+//    8*(l/16)..+7 of the slice), B = q^T (lane l: query row l%16, zero for
+//    rows >= G); lane l then holds tokens 4*(l/16)..+3 of query row l%16,
+//    which is the A operand layout of p @ v, so p never leaves the lane;
+//  * a query row's max and sum: over the lane's 4 tokens, then over the 4
+//    lanes l%16 + 16*i with two lane swaps (v_permlane32_swap,
+//    v_permlane16_swap), so every lane of the row ends with the result;
+//  * p @ v on the matrix cores (v_mfma_f32_16x16x16, p split into two
+//    16-bit parts), lane l supplying tokens 4*(l/16)..+3 of every page for
+//    head dims (D/16)*(l%16)+e and accumulating query rows 4*(l/16)..+3.
 
 typedef float f32x4v_t __attribute__((ext_vector_type(4)));
 
@@ -1075,27 +1076,18 @@ __device__ inline f32x4v_t mfma_16x16x32(u32x4 a, u32x4 b, f32x4v_t c) {
                                                        0);
 }
 
-// Orders LDS traffic between the lanes of one wave (LDS executes a wave's
-// instructions in order; this keeps the compiler from reordering them).
-__device__ inline void wave_lds_fence() { __builtin_amdgcn_fence(__ATOMIC_SEQ_CST, "wavefront"); }
-
-// Reduction over the 16 lanes of a DPP row (xor 1, xor 2, then the half-row
-// and row mirrors); every lane of the row ends with the row's result.
+// Reduction over the lanes l%16 + 16*i (i = 0..3), the four lanes that hold
+// one query row of the transposed scores: a swap of the wave's halves, then
+// of its odd and even 16-lane rows.  Every lane ends with the result, and
+// computes it with the same operand order (lower lane's value first).
 template <class Op>
-__device__ inline float row16_reduce(float x, Op op) {
-    auto dpp = [](float v, int ctrl) {
-        switch (ctrl) {
-            case 0: return __int_as_float(__builtin_amdgcn_update_dpp(0, __float_as_int(v), 0xB1, 0xF, 0xF, false));
-            case 1: return __int_as_float(__builtin_amdgcn_update_dpp(0, __float_as_int(v), 0x4E, 0xF, 0xF, false));
-            case 2: return __int_as_float(__builtin_amdgcn_update_dpp(0, __float_as_int(v), 0x141, 0xF, 0xF, false));
-            default: return __int_as_float(__builtin_amdgcn_update_dpp(0, __float_as_int(v), 0x140, 0xF, 0xF, false));
-        }
-    };
-    x = op(x, dpp(x, 0));
-    x = op(x, dpp(x, 1));
-    x = op(x, dpp(x, 2));
-    x = op(x, dpp(x, 3));
-    return x;
+__device__ inline float cross4_reduce(float x, Op op) {
+    const u32 b = __float_as_uint(x);
+    const auto h = __builtin_amdgcn_permlane32_swap(b, b, false, false);
+    x = op(__uint_as_float(h[0]), __uint_as_float(h[1]));
+    const u32 c = __float_as_uint(x);
+    const auto r = __builtin_amdgcn_permlane16_swap(c, c, false, false);
+    return op(__uint_as_float(r[0]), __uint_as_float(r[1]));
 }
 
 // Partials pass between waves of different XCDs (each XCD has its own L2).
@@ -1128,19 +1120,18 @@ struct DecodeWave {
     static_assert(G >= 1 && G <= 16 && (D == 64 || D == 128 || D == 256) && G * D <= 1024, "decode shape");
     static constexpr int NS = D / 32;          // head-dim slices of the score MFMA
     static constexpr int DV = D / 16;          // head-dim columns per lane in p @ v
-    static constexpr int NP = (G + 3) / 4;     // softmax passes of 4 query rows x 16 tokens
-    static constexpr int kLdsFloats = G * 16 + 16;  // scores / p rows, then the rescale factors
     // Chunk partial layout: m[G], l[G], o[G][D].
     static constexpr int kPartFloats = 2 * G + G * D;
 
     struct Page {
         u32x4 k[NS];           // lane l: token l%16, head dims 32*j + 8*(l/16) .. +7
         u32 v[4][DV / 2];      // lane l: tokens 4*(l/16) + i, head dims DV*(l%16) .. +DV-1
-        float mask;            // token l%16
+        float mask[4];         // lane l: tokens 4*(l/16) .. +3
     };
 
     // Per-lane byte offsets within a page, fixed for a launch: K (token t at
-    // t*ks elements, head dims contiguous), V (token t at t*vs), mask (token t).
+    // t*ks elements, head dims contiguous), V (token t at t*vs), mask (token t
+    // at t, four tokens per lane).
     struct Lanes {
         u32 k, v, m;
         u32 vrow;  // bytes between consecutive V tokens
@@ -1150,15 +1141,18 @@ struct DecodeWave {
         Lanes r;
         r.k = static_cast<u32>((t * ks + 8 * grp) * 2);
         r.v = static_cast<u32>((4 * grp * vs + DV * t) * 2);
-        r.m = static_cast<u32>(t * 4);
+        r.m = static_cast<u32>(grp * 16);
         r.vrow = static_cast<u32>(vs * 2);
         return r;
     }
 
-    // kp, vp, mp: wave-uniform page bases (buffer loads, streaming).
-    __device__ static void load_page(Page& pg, const u16* kp, const u16* vp, const float* mp, const Lanes& ln) {
-        const buf_rsrc rk = __builtin_amdgcn_make_buffer_rsrc(const_cast<u16*>(kp), 0, -1, 0x00020000);
-        const buf_rsrc rv = __builtin_amdgcn_make_buffer_rsrc(const_cast<u16*>(vp), 0, -1, 0x00020000);
+    // kp, vp, mp: wave-uniform page bases (buffer loads, streaming).  With
+    // real false every load is out of range of its buffer (no records): it
+    // reads no memory and returns zeros, and it still counts as a load.
+    __device__ static void load_page(Page& pg, const u16* kp, const u16* vp, const float* mp, const Lanes& ln, bool real) {
+        const int nrec = __builtin_amdgcn_readfirstlane(real ? -1 : 0);  // real is wave-uniform
+        const buf_rsrc rk = __builtin_amdgcn_make_buffer_rsrc(const_cast<u16*>(kp), 0, nrec, 0x00020000);
+        const buf_rsrc rv = __builtin_amdgcn_make_buffer_rsrc(const_cast<u16*>(vp), 0, nrec, 0x00020000);
 #pragma unroll
         for (int j = 0; j < NS; ++j)
             pg.k[j] = __builtin_bit_cast(u32x4, __builtin_amdgcn_raw_buffer_load_b128(rk, ln.k + 64 * j, 0, 2));
@@ -1179,13 +1173,17 @@ struct DecodeWave {
             }
         }
         if constexpr (MASK) {
-            const buf_rsrc rm = __builtin_amdgcn_make_buffer_rsrc(const_cast<float*>(mp), 0, -1, 0x00020000);
-            pg.mask = __uint_as_float(__builtin_amdgcn_raw_buffer_load_b32(rm, ln.m, 0, 2));
+            const buf_rsrc rm = __builtin_amdgcn_make_buffer_rsrc(const_cast<float*>(mp), 0, nrec, 0x00020000);
+            const u32x4 mk = __builtin_bit_cast(u32x4, __builtin_amdgcn_raw_buffer_load_b128(rm, ln.m, 0, 2));
+            pg.mask[0] = __uint_as_float(mk.x);
+            pg.mask[1] = __uint_as_float(mk.y);
+            pg.mask[2] = __uint_as_float(mk.z);
+            pg.mask[3] = __uint_as_float(mk.w);
         }
     }
 
     struct State {
-        float m[NP], l[NP];    // query row 4*pass + l/16, replicated over its 16 lanes
+        float m, l;            // query row l%16, replicated over its 4 lanes
         f32x4v_t o[DV];        // o[e][j]: query row 4*(l/16) + j, head dim DV*(l%16) + e
     };
 
@@ -1215,62 +1213,54 @@ struct DecodeWave {
         }
     }
 
-    __device__ static void step(State& st, const Page& pg, const u32x4* qa, float scale, float* lds) {
+    __device__ static void step(State& st, const Page& pg, const u32x4* qa, float scale) {
         const int lane = threadIdx.x & 63, t = lane & 15, grp = lane >> 4;
-        // Scores: A = q (query rows), B = K^T; lane l holds rows 4*(l/16) + j, token l%16.
+        // Scores S^T: A = the K page, B = q^T; lane l holds tokens 4*(l/16) + i
+        // of query row l%16.
         f32x4v_t acc = {0.0f, 0.0f, 0.0f, 0.0f};
 #pragma unroll
-        for (int j = 0; j < NS; ++j) acc = mfma_16x16x32<F16>(qa[j], pg.k[j], acc);
+        for (int j = 0; j < NS; ++j) acc = mfma_16x16x32<F16>(pg.k[j], qa[j], acc);
+        float sc[4];
 #pragma unroll
-        for (int j = 0; j < 4; ++j) {
-            const int h = 4 * grp + j;
-            float sc = acc[j] * scale;
-            if constexpr (MASK) sc = sc - pg.mask;
-            if (h < G) lds[h * 16 + t] = sc;
+        for (int i = 0; i < 4; ++i) {
+            sc[i] = acc[i] * scale;
+            if constexpr (MASK) sc[i] = sc[i] - pg.mask[i];
         }
-        wave_lds_fence();
-        // Online softmax, one (query row, token) per lane and pass.
-        auto fmax_ = [](float a, float b) { return fmaxf(a, b); };
-        auto fadd_ = [](float a, float b) { return a + b; };
-        bool moved = false;  // some query row's running max changed (its a != 1)
+        // Online softmax of query row l%16 (rows >= G are q = 0 rows whose
+        // results are never stored; p @ v keeps MFMA rows apart).
+        auto fmax_ = [](float x, float y) { return fmaxf(x, y); };
+        auto fadd_ = [](float x, float y) { return x + y; };
+        const float mx = cross4_reduce(fmaxf(fmaxf(sc[0], sc[1]), fmaxf(sc[2], sc[3])), fmax_);
+        const float mn = fmaxf(st.m, mx);
+        const float a = expf(st.m - mn);
+        f32x4v_t pr;
 #pragma unroll
-        for (int r = 0; r < NP; ++r) {
-            const int h = 4 * r + grp;
-            const float sc = h < G ? lds[h * 16 + t] : 0.0f;
-            const float mn = fmaxf(st.m[r], row16_reduce(sc, fmax_));
-            const float a = expf(st.m[r] - mn);
-            const float e = expf(sc - mn);
-            st.l[r] = st.l[r] * a + row16_reduce(e, fadd_);
-            st.m[r] = mn;
-            if (h < G) {
-                moved = moved || a != 1.0f;
-                lds[h * 16 + t] = e;
-                if (t == 0) lds[G * 16 + h] = a;
-            }
-        }
-        wave_lds_fence();
+        for (int i = 0; i < 4; ++i) pr[i] = expf(sc[i] - mn);
+        st.l = st.l * a + cross4_reduce((pr[0] + pr[1]) + (pr[2] + pr[3]), fadd_);
+        st.m = mn;
         // o <- o * a + p @ v on the matrix cores: v_mfma_f32_16x16x16 with
         // M = query rows, K = the page's 16 tokens, N = 16 head dims.  p is
-        // fp32 and enters as hi + lo (split4), two products per MFMA step.
-        // MFMA e covers head dims DV*n + e (n = l%16): lane (n, l/16)
-        // supplies V[tokens 4*(l/16)..+3][DV*n + e] straight from its page
-        // registers (one 16-bit half of pg.v[i][e/2] per token) and
-        // accumulates o rows 4*(l/16)..+3.  Once the running maxima settle,
-        // a == 1 for every row and o * a == o exactly, so the rescale is
-        // skipped for the whole wave.
-        const bool rescale = __builtin_amdgcn_ballot_w64(moved) != 0;
-        f32x4v_t pr = {0.0f, 0.0f, 0.0f, 0.0f};
-        if (t < G) pr = *reinterpret_cast<const f32x4v_t*>(lds + t * 16 + 4 * grp);
-        f32x4v_t a4 = {1.0f, 1.0f, 1.0f, 1.0f};
-        if (rescale) a4 = *reinterpret_cast<const f32x4v_t*>(lds + G * 16 + 4 * grp);
-        wave_lds_fence();
+        // fp32 and enters as hi + lo (split4), two products per MFMA step;
+        // the lane's scores are already its A operand (query row l%16,
+        // tokens 4*(l/16)..+3).  MFMA e covers head dims DV*n + e (n = l%16):
+        // lane (n, l/16) supplies V[tokens 4*(l/16)..+3][DV*n + e] straight
+        // from its page registers (one 16-bit half of pg.v[i][e/2] per token)
+        // and accumulates o rows 4*(l/16)..+3.  Once the running maxima
+        // settle, a == 1 for every row and o * a == o exactly, so the rescale
+        // is skipped for the whole wave.
+        const bool rescale = __builtin_amdgcn_ballot_w64(t < G && a != 1.0f) != 0;
         u32x2 ph, pl;
         split4(pr, ph, pl);
         if (rescale) {
             // A real branch (the empty asm keeps it from being turned into
             // selects): the multiply is rare, and o stays in the matrix
-            // cores' accumulator registers otherwise.
+            // cores' accumulator registers otherwise.  o row 4*(l/16) + j
+            // takes the factor of query row 4*(l/16) + j, held by lane
+            // 4*(l/16) + j.
             asm volatile("");
+            f32x4v_t a4;
+#pragma unroll
+            for (int j = 0; j < 4; ++j) a4[j] = __int_as_float(__builtin_amdgcn_ds_bpermute((4 * grp + j) * 4, __float_as_int(a)));
 #pragma unroll
             for (int e = 0; e < DV; ++e) st.o[e] = st.o[e] * a4;
         }
@@ -1284,7 +1274,7 @@ struct DecodeWave {
         }
     }
 
-    // q rows as the MFMA's A operand (rows >= G are zero).
+    // q rows as the score MFMA's B operand (rows >= G are zero).
     __device__ static void load_q(u32x4 (&qa)[NS], const u16* q, i64 qs) {
         const int lane = threadIdx.x & 63, t = lane & 15, grp = lane >> 4;
 #pragma unroll
@@ -1295,11 +1285,8 @@ struct DecodeWave {
     }
 
     __device__ static void init(State& st) {
-#pragma unroll
-        for (int r = 0; r < NP; ++r) {
-            st.m[r] = -__builtin_inff();
-            st.l[r] = 0.0f;
-        }
+        st.m = -__builtin_inff();
+        st.l = 0.0f;
 #pragma unroll
         for (int e = 0; e < DV; ++e) st.o[e] = f32x4v_t{0.0f, 0.0f, 0.0f, 0.0f};
     }
@@ -1310,15 +1297,9 @@ struct DecodeWave {
     // (row, e).
     __device__ static void store(const State& st, float* part) {
         const int lane = threadIdx.x & 63, t = lane & 15, grp = lane >> 4;
-        if (t == 0) {
-#pragma unroll
-            for (int r = 0; r < NP; ++r) {
-                const int h = 4 * r + grp;
-                if (h < G) {
-                    coherent_store(part + h, st.m[r]);
-                    coherent_store(part + G + h, st.l[r]);
-                }
-            }
+        if (grp == 0 && t < G) {
+            coherent_store(part + t, st.m);
+            coherent_store(part + G + t, st.l);
         }
 #pragma unroll
         for (int j = 0; j < 4; ++j) {
@@ -1486,10 +1467,9 @@ struct DecodeStream {
 
     template <class F>
     __device__ static void run(F& f, const int* pre, const int* cpre, int U, i64 TC, i64 W, i64 w, i64 s, i64 b, int* cnt,
-                               float scale, i64 ks, i64 vs, i64 qs, float* lds) {
+                               float scale, i64 ks, i64 vs, i64 qs) {
         const int lane = threadIdx.x & 63;
         const typename DW::Lanes ln = DW::lanes(ks, vs);
-        const typename DW::Lanes dummy = {0u, 0u, 0u, ln.vrow};
         // Page-table runs.
         i64 r0 = s;
         PageOffs rc, rn;
@@ -1516,8 +1496,12 @@ struct DecodeStream {
             const float* mp;
             f.bases(po, kp, vp, mp);
             // Past the stream's end the ring is still filled (so that every
-            // step waits for the same number of loads), from one 16-byte line.
-            DW::load_page(pg, kp, vp, mp, real ? ln : dummy);
+            // step waits for the same number of loads) with loads that read
+            // nothing.  The lane offsets stay the same registers on every
+            // path: a lane-offset temporary could share registers with a
+            // page load in flight, and the wait for that write would drain
+            // the ring.
+            DW::load_page(pg, kp, vp, mp, ln, real);
         };
         // The first pages go out before anything else is read.
         typename DW::Page pg[NB];
@@ -1544,6 +1528,10 @@ struct DecodeStream {
             }
         };
         get_q(qa, u);
+        // The first pages and q are waited for here, once: a load into q's
+        // registers still in flight where the stream loop begins would make
+        // the compiler's wait counts drain the ring at every loop iteration.
+        wait_vmcnt<0>();
         int un = u;
         if (eu < b) {
             un = next_unit(pre, u);
@@ -1556,7 +1544,7 @@ struct DecodeStream {
             for (int i = 0; i < NB; ++i) {
                 const i64 gi = g + i;
                 load(pg[(i + NB - 1) % NB], gi + NB - 1);
-                DW::step(st, pg[i], qa, scale, lds);
+                DW::step(st, pg[i], qa, scale);
                 tick(pd, cnt, f);
                 if (gi + 1 == eu) {
                     // Unit u's pages in this wave are folded.

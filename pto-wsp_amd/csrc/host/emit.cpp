@@ -1027,7 +1027,6 @@ EmittedKernel emit_decode(const Module& m, const KernelAnalysis& a, const Launch
     o << "  typedef " << tmpl << " DW;\n";
     o << "  static_assert(DecodeSplit::kMaxUnits == " << kDecodeMaxUnits << ", \"unit limit\");\n";
     o << "  static_assert(DecodeSplit::kUnitCost == " << kDecodeUnitCost << ", \"unit cost\");\n";
-    o << "  __shared__ __attribute__((aligned(16))) float lds_all[" << nw << "][DW::kLdsFloats];\n";
     o << "  __shared__ int pre[DecodeSplit::kMaxUnits + 1], cpre[DecodeSplit::kMaxUnits + 1];\n";
     o << "  __shared__ int wsum[" << nw << "], cwsum[" << nw << "];\n";
     o << "  const int tid = threadIdx.x, lane = tid & 63;\n";
@@ -1115,7 +1114,6 @@ EmittedKernel emit_decode(const Module& m, const KernelAnalysis& a, const Launch
     o << "  if (s < b) {\n";
     o << "  int* cnt = reinterpret_cast<int*>(A.base[" << ntens << "]);\n";
     o << "  float* partials = reinterpret_cast<float*>(A.base[" << ntens << "] + DecodeSplit::kMaxUnits * 4);\n";
-    o << "  float* lds = lds_all[wave];\n";
     // Offsets of global (sub-)page g (per lane): its unit, the page index
     // within the unit, the affine and page-table terms, and for pages of
     // more than 16 tokens the sub-page's first token (its token stride: s4
@@ -1186,7 +1184,7 @@ EmittedKernel emit_decode(const Module& m, const KernelAnalysis& a, const Launch
     o << "  };\n";
     o << "  auto fns = decode_fns(f_page, f_bases, f_q, f_slot, f_combine);\n";
     o << "  DecodeStream<DW, " << spec.decode_ring << ", " << (spec.decode_ordered ? "true" : "false") << ">::run(fns, pre, cpre, U, TC, W, w, s, b, cnt, " << scale.str() << ", A.s4[" << d.kt
-      << "], A.s3[" << d.v << "], A.s3[" << d.q << "], lds);\n";
+      << "], A.s3[" << d.v << "], A.s3[" << d.q << "]);\n";
     o << "  }\n";
     o << "  }\n";
     if (spec.decode_norm) {
@@ -1209,7 +1207,7 @@ EmittedKernel emit_decode(const Module& m, const KernelAnalysis& a, const Launch
     }
     o << "}\n";
     ek.source = o.str();
-    ek.lds_bytes = static_cast<size_t>(4 * (d.g * 16 + 16) * 4 + (kDecodeMaxUnits + 1 + 4) * 4);
+    ek.lds_bytes = static_cast<size_t>((2 * (kDecodeMaxUnits + 1) + 2 * nw) * 4);
     return ek;
 }
 
