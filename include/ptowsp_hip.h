@@ -121,7 +121,9 @@ int ptowsp_hip_kernel_family(const ptowsp_program* prog, const char* kernel);
  * of the last two grid loops merged into one workgroup block; bit 2 (with bit
  * 1): build merged 128x128 tasks with K step 32 or 64 as the two-group
  * ping-pong GEMM block; bit 4: build row-program launches with in-kernel
- * loops as row programs that run the loops inside each row's lane team. */
+ * loops as row programs that run the loops inside each row's lane team;
+ * bit 5: build decode launches with the following `out = o / l` launch
+ * folded into them (the form a run uses when that launch follows). */
 int ptowsp_hip_precompile(ptowsp_program* prog, int index, int flags, const char** source);
 
 /* Evaluates only the cpu_sim cycle model (total_cycles, task_count) for the

@@ -1716,6 +1716,7 @@ int ptowsp_hip_precompile(ptowsp_program* P, int index, int flags, const char** 
             spec.decode_ring = tuning().decode_ring;
             spec.decode_waves = tuning().decode_waves;
             spec.decode_ordered = tuning().decode_ordered;
+            spec.decode_norm = spec.decode && (flags & 32) != 0;
             spec.indirect_count.assign(L.targs.size(), 0);
             for (size_t p = 0; p < L.targs.size(); ++p)
                 for (const auto& e : L.targs[p]->idx)

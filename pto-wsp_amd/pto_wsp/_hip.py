@@ -169,7 +169,7 @@ class NativeProgram:
         return FAMILIES.get(int(_lib.ptowsp_hip_kernel_family(self._h, name.encode())), "unknown")
 
     def precompile(self, index: int = 0, serial: bool = False, merged: bool = False, pingpong: bool = False,
-                   seq_mask: int = 0, row_loops: bool = False) -> str:
+                   seq_mask: int = 0, row_loops: bool = False, decode_norm: bool = False) -> str:
         """Emits and builds every launch; returns the source of launch `index`.
 
         serial: the in-order variant used when grid tasks overlap, with seq_mask the grid
@@ -178,11 +178,12 @@ class NativeProgram:
         loops run inside each row's lane team;
         merged: GEMM launches with the last two grid loops merged 2x2 per block;
         pingpong: merged 128x128 tasks with K step 32 / 64 as the two-group
-        ping-pong block.
+        ping-pong block; decode_norm: decode launches with the following `out = o / l`
+        launch folded in (the form a run uses when that launch follows).
         """
         src = ctypes.c_char_p()
         flags = ((1 if serial else 0) | (2 if merged else 0) | (4 if pingpong else 0) | (16 if row_loops else 0)
-                 | ((int(seq_mask) & 0xFF) << 8))
+                 | (32 if decode_norm else 0) | ((int(seq_mask) & 0xFF) << 8))
         if _lib.ptowsp_hip_precompile(self._h, int(index), flags, ctypes.byref(src)) != 0:
             raise RuntimeError(_error())
         return src.value.decode() if src.value else ""

@@ -177,6 +177,19 @@ def test_decode_family_page_sizes(page, family):
         assert ("vp_ %" in src) == (page > 16)
 
 
+def test_decode_precompile_folded_normalisation():
+    """precompile(decode_norm=True) emits the form a run uses when `out = o / l`
+    follows the decode launch: the completion writes out, and units without pages
+    are normalised from their accumulators."""
+    from pto_wsp._hip import NativeProgram
+
+    arrs = W.paged_decode_arrays([40, 300, 0, 17], 2, 4, 128)
+    prog = NativeProgram(workload_to_codegen_ir(W.rr4(W.paged_decode(arrs)), "d").module)
+    plain, folded = prog.precompile(0), prog.precompile(0, decode_norm=True)
+    assert "norm_ptr" not in plain and "::normalize(" not in plain
+    assert "norm_ptr" in folded and "::normalize(" in folded
+
+
 def _compile_err(w, match):
     with pytest.raises(CompileError, match=match):
         Program(w, "hip_gfx950", {})
