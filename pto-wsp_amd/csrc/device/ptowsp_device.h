@@ -1120,8 +1120,11 @@ struct DecodeWave {
     static_assert(G >= 1 && G <= 16 && (D == 64 || D == 128 || D == 256) && G * D <= 1024, "decode shape");
     static constexpr int NS = D / 32;          // head-dim slices of the score MFMA
     static constexpr int DV = D / 16;          // head-dim columns per lane in p @ v
-    // Chunk partial layout: m[G], l[G], o[G][D].
-    static constexpr int kPartFloats = 2 * G + G * D;
+    // Partial layout: o[G][D] (head dims permuted, see store), then m[G] and
+    // l[G]; padded to 16 bytes so that every partial's o rows are 16-byte
+    // aligned.
+    static constexpr int kPartM = G * D;
+    static constexpr int kPartFloats = G * D + ((2 * G + 3) & ~3);
 
     struct Page {
         u32x4 k[NS];           // lane l: token l%16, head dims 32*j + 8*(l/16) .. +7
@@ -1291,22 +1294,30 @@ struct DecodeWave {
         for (int e = 0; e < DV; ++e) st.o[e] = f32x4v_t{0.0f, 0.0f, 0.0f, 0.0f};
     }
 
-    // Writes st as a partial (m[G], l[G], o[G][D]).  o is kept in lane
-    // order: head dim DV*n + e sits at position 16*e + n (part_dim maps
-    // back), so the 16 lanes of a row group write 64 contiguous bytes per
-    // (row, e).
+    // Writes st as a partial.  The stores carry sc1, the cache policy of the
+    // agent-scope atomic stores of the memory model (see coherent_store):
+    // they are written through to memory, where a wave of another XCD reads
+    // them.  o is stored 128 bits per lane: lane n's four head dims
+    // DV*n + 4c .. +3 of a row sit at positions 64c + 4n .. +3 (part_dim maps
+    // back), so the 16 lanes of a row group write 256 contiguous bytes per
+    // (row, c).
     __device__ static void store(const State& st, float* part) {
         const int lane = threadIdx.x & 63, t = lane & 15, grp = lane >> 4;
         if (grp == 0 && t < G) {
-            coherent_store(part + t, st.m);
-            coherent_store(part + G + t, st.l);
+            coherent_store(part + kPartM + t, st.m);
+            coherent_store(part + kPartM + G + t, st.l);
         }
+        const buf_rsrc rp = __builtin_amdgcn_make_buffer_rsrc(part, 0, -1, 0x00020000);
 #pragma unroll
         for (int j = 0; j < 4; ++j) {
             const int g = 4 * grp + j;
             if (g < G) {
 #pragma unroll
-                for (int e = 0; e < DV; ++e) coherent_store(part + 2 * G + g * D + 16 * e + t, st.o[e][j]);
+                for (int c = 0; c < DV / 4; ++c) {
+                    const u32x4 w = {__float_as_uint(st.o[4 * c][j]), __float_as_uint(st.o[4 * c + 1][j]),
+                                     __float_as_uint(st.o[4 * c + 2][j]), __float_as_uint(st.o[4 * c + 3][j])};
+                    __builtin_amdgcn_raw_buffer_store_b128(w, rp, static_cast<u32>((g * D + 64 * c + 4 * t) * 4), 0, 16);
+                }
             }
         }
     }
@@ -1315,7 +1326,7 @@ struct DecodeWave {
 // Head dim held at position p of a partial's o row (see DecodeWave::store).
 template <int D>
 __device__ inline int part_dim(int p) {
-    return (D / 16) * (p & 15) + (p >> 4);
+    return (D / 16) * ((p & 63) >> 2) + 4 * (p >> 6) + (p & 3);
 }
 
 // Balanced split of a decode launch over the resident waves.  The units'
@@ -1616,10 +1627,10 @@ struct DecodeCombine {
                 const float* pc = part + (c + b) * pstride;
 #pragma unroll
                 for (int g = 0; g < G; ++g) {
-                    mc[b][g] = coherent_load(pc + g);
-                    lc[b][g] = coherent_load(pc + G + g);
+                    mc[b][g] = coherent_load(pc + G * D + g);
+                    lc[b][g] = coherent_load(pc + G * D + G + g);
 #pragma unroll
-                    for (int j = 0; j < DPL; ++j) oc[b][g][j] = coherent_load(pc + 2 * G + g * D + DPL * lane + j);
+                    for (int j = 0; j < DPL; ++j) oc[b][g][j] = coherent_load(pc + g * D + DPL * lane + j);
                 }
             }
 #pragma unroll
@@ -1630,10 +1641,10 @@ struct DecodeCombine {
             float mc[G], lc[G], oc[G][DPL];
 #pragma unroll
             for (int g = 0; g < G; ++g) {
-                mc[g] = coherent_load(pc + g);
-                lc[g] = coherent_load(pc + G + g);
+                mc[g] = coherent_load(pc + G * D + g);
+                lc[g] = coherent_load(pc + G * D + G + g);
 #pragma unroll
-                for (int j = 0; j < DPL; ++j) oc[g][j] = coherent_load(pc + 2 * G + g * D + DPL * lane + j);
+                for (int j = 0; j < DPL; ++j) oc[g][j] = coherent_load(pc + g * D + DPL * lane + j);
             }
             fold(mm, ll, oo, mc, lc, oc);
         }

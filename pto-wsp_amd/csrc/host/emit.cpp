@@ -992,7 +992,7 @@ EmittedKernel emit_decode(const Module& m, const KernelAnalysis& a, const Launch
     EmittedKernel ek;
     ek.threads = nt;
     ek.row_program = false;
-    ek.part_floats = 2 * d.g + d.g * d.d;
+    ek.part_floats = d.g * d.d + ((2 * d.g + 3) & ~3);  // DecodeWave::kPartFloats
     std::ostringstream o;
     o << "#include \"ptowsp_device.h\"\nusing namespace ptowsp;\n";
     o << "// decode program: kernel " << k.name << ", " << d.g << " query rows, head dim " << d.d << (d.f16 ? " f16" : " bf16")
@@ -1027,6 +1027,7 @@ EmittedKernel emit_decode(const Module& m, const KernelAnalysis& a, const Launch
     o << "  typedef " << tmpl << " DW;\n";
     o << "  static_assert(DecodeSplit::kMaxUnits == " << kDecodeMaxUnits << ", \"unit limit\");\n";
     o << "  static_assert(DecodeSplit::kUnitCost == " << kDecodeUnitCost << ", \"unit cost\");\n";
+    o << "  static_assert(DW::kPartFloats == " << ek.part_floats << ", \"partial size\");\n";
     o << "  __shared__ int pre[DecodeSplit::kMaxUnits + 1], cpre[DecodeSplit::kMaxUnits + 1];\n";
     o << "  __shared__ int wsum[" << nw << "], cwsum[" << nw << "];\n";
     o << "  const int tid = threadIdx.x, lane = tid & 63;\n";
