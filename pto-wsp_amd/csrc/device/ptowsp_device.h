@@ -1115,7 +1115,10 @@ __device__ inline void reset_count(int* cnt) {
     if ((threadIdx.x & 63) == 0) __hip_atomic_store(cnt, 0, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
 }
 
-template <int G, int D, bool F16, bool MASK>
+// H8: pages of 8 tokens, each folded as a 16-token step whose tokens 8-15
+// are read as zeros (their byte offsets lie beyond the buffer's record
+// limit of 8 token rows) and whose scores are -inf.
+template <int G, int D, bool F16, bool MASK, bool H8 = false>
 struct DecodeWave {
     static_assert(G >= 1 && G <= 16 && (D == 64 || D == 128 || D == 256) && G * D <= 1024, "decode shape");
     static constexpr int NS = D / 32;          // head-dim slices of the score MFMA
@@ -1137,7 +1140,8 @@ struct DecodeWave {
     // at t, four tokens per lane).
     struct Lanes {
         u32 k, v, m;
-        u32 vrow;  // bytes between consecutive V tokens
+        u32 vrow;    // bytes between consecutive V tokens
+        u32 kn, vn;  // H8: bytes of 8 K / V token rows (the record limits)
     };
     __device__ static Lanes lanes(i64 ks, i64 vs) {
         const int lane = threadIdx.x & 63, t = lane & 15, grp = lane >> 4;
@@ -1146,16 +1150,24 @@ struct DecodeWave {
         r.v = static_cast<u32>((4 * grp * vs + DV * t) * 2);
         r.m = static_cast<u32>(grp * 16);
         r.vrow = static_cast<u32>(vs * 2);
+        r.kn = static_cast<u32>(ks * 16);
+        r.vn = static_cast<u32>(vs * 16);
         return r;
     }
 
     // kp, vp, mp: wave-uniform page bases (buffer loads, streaming).  With
     // real false every load is out of range of its buffer (no records): it
     // reads no memory and returns zeros, and it still counts as a load.
+    // With H8 a real page's records end after its 8 token rows (token row
+    // stride >= head dim, so tokens 0-7 lie inside and 8-15 outside).
     __device__ static void load_page(Page& pg, const u16* kp, const u16* vp, const float* mp, const Lanes& ln, bool real) {
-        const int nrec = __builtin_amdgcn_readfirstlane(real ? -1 : 0);  // real is wave-uniform
-        const buf_rsrc rk = __builtin_amdgcn_make_buffer_rsrc(const_cast<u16*>(kp), 0, nrec, 0x00020000);
-        const buf_rsrc rv = __builtin_amdgcn_make_buffer_rsrc(const_cast<u16*>(vp), 0, nrec, 0x00020000);
+        // real and the limits are wave-uniform
+        const int nrec = __builtin_amdgcn_readfirstlane(real ? -1 : 0);
+        const int nk = H8 ? __builtin_amdgcn_readfirstlane(real ? static_cast<int>(ln.kn) : 0) : nrec;
+        const int nv = H8 ? __builtin_amdgcn_readfirstlane(real ? static_cast<int>(ln.vn) : 0) : nrec;
+        const int nm = H8 ? __builtin_amdgcn_readfirstlane(real ? 32 : 0) : nrec;
+        const buf_rsrc rk = __builtin_amdgcn_make_buffer_rsrc(const_cast<u16*>(kp), 0, nk, 0x00020000);
+        const buf_rsrc rv = __builtin_amdgcn_make_buffer_rsrc(const_cast<u16*>(vp), 0, nv, 0x00020000);
 #pragma unroll
         for (int j = 0; j < NS; ++j)
             pg.k[j] = __builtin_bit_cast(u32x4, __builtin_amdgcn_raw_buffer_load_b128(rk, ln.k + 64 * j, 0, 2));
@@ -1176,7 +1188,7 @@ struct DecodeWave {
             }
         }
         if constexpr (MASK) {
-            const buf_rsrc rm = __builtin_amdgcn_make_buffer_rsrc(const_cast<float*>(mp), 0, nrec, 0x00020000);
+            const buf_rsrc rm = __builtin_amdgcn_make_buffer_rsrc(const_cast<float*>(mp), 0, nm, 0x00020000);
             const u32x4 mk = __builtin_bit_cast(u32x4, __builtin_amdgcn_raw_buffer_load_b128(rm, ln.m, 0, 2));
             pg.mask[0] = __uint_as_float(mk.x);
             pg.mask[1] = __uint_as_float(mk.y);
@@ -1228,6 +1240,7 @@ struct DecodeWave {
         for (int i = 0; i < 4; ++i) {
             sc[i] = acc[i] * scale;
             if constexpr (MASK) sc[i] = sc[i] - pg.mask[i];
+            if constexpr (H8) sc[i] = grp < 2 ? sc[i] : -__builtin_inff();  // tokens 8-15: no token
         }
         // Online softmax of query row l%16 (rows >= G are q = 0 rows whose
         // results are never stored; p @ v keeps MFMA rows apart).

@@ -353,11 +353,12 @@ DecodeInfo classify_decode(const KernelDef& k, const KernelAnalysis& a) {
         const ValueInfo* mk = vi(mask_p);
         if (mk->dtype != DType::F32 || mk->rows != 1 || mk->cols != PG) return info;
     }
-    // Device template shapes: pages of 16, 32, 64 or 128 tokens (folded as 16-token
-    // sub-pages), up to 16 query rows, head dim 64 / 128 / 256, at most 64 partial
-    // outputs per lane (G * D / 16).
-    if ((PG != 16 && PG != 32 && PG != 64 && PG != 128) || G < 1 || G > 16 || (D != 64 && D != 128 && D != 256) ||
-        G * D > 1024)
+    // Device template shapes: pages of 8, 16, 32, 64 or 128 tokens (folded as 16-token
+    // steps: larger pages as 16-token sub-pages, 8-token pages as half-filled steps),
+    // up to 16 query rows, head dim 64 / 128 / 256, at most 64 partial outputs per lane
+    // (G * D / 16).
+    if ((PG != 8 && PG != 16 && PG != 32 && PG != 64 && PG != 128) || G < 1 || G > 16 ||
+        (D != 64 && D != 128 && D != 256) || G * D > 1024)
         return info;
     info.ok = true;
     info.q = a.tensor_ordinal[pq];

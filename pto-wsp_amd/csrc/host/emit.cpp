@@ -983,7 +983,8 @@ EmittedKernel emit_decode(const Module& m, const KernelAnalysis& a, const Launch
     for (int p = 1; p < ntens; ++p) first_term[p] = first_term[p - 1] + spec.indirect_count[p - 1];
     auto nterms = [&](int p) { return spec.indirect_count[p]; };
     const std::string tmpl = "DecodeWave<" + std::to_string(d.g) + ", " + std::to_string(d.d) + ", " +
-                             (d.f16 ? "true" : "false") + ", " + (d.mask >= 0 ? "true" : "false") + ">";
+                             (d.f16 ? "true" : "false") + ", " + (d.mask >= 0 ? "true" : "false") + ", " +
+                             (d.pg == 8 ? "true" : "false") + ">";
     std::ostringstream scale;
     scale.precision(9);
     scale << std::scientific << d.scale << "f";
@@ -1056,7 +1057,7 @@ EmittedKernel emit_decode(const Module& m, const KernelAnalysis& a, const Launch
     o << "        if (npg > maxp) { npg = maxp; if (blockIdx.x == 0) *A.err = 3; }\n";
     // Pages of more than 16 tokens are folded as 16-token sub-pages: the
     // prefixes, the split and the stream count sub-pages.
-    o << "        n_[i] = static_cast<int>(npg) * " << d.pg / 16 << ";\n";
+    o << "        n_[i] = static_cast<int>(npg) * " << std::max(1, d.pg / 16) << ";\n";
     o << "        run += n_[i];\n";
     o << "        crun += DecodeSplit::cost(n_[i]);\n";
     o << "      }\n";
@@ -1121,7 +1122,7 @@ EmittedKernel emit_decode(const Module& m, const KernelAnalysis& a, const Launch
     // of the K^T and mask tiles, s3 of the V tile).  The 16-token tile that
     // is loaded is bounds-checked; an out-of-range one raises the error flag
     // and reads the tensor's first tile instead.
-    const int sub = d.pg / 16;
+    const int sub = std::max(1, d.pg / 16), tok = std::min(16, d.pg);
     o << "  auto f_page = [&](i64 g, PageOffs& po) {\n";
     o << "    const int uu = DecodeSplit::unit_of(pre, U, g);\n";
     o << "    i64 vars[" << nvars << "];\n";
@@ -1140,9 +1141,9 @@ EmittedKernel emit_decode(const Module& m, const KernelAnalysis& a, const Launch
           << "] >= A.span[" << p << "]) { *A.err = 2; o_ = 0; }\n";
         o << "      po." << field << " = o_; }\n";
     };
-    checked(d.kt, d.d, 16, "k", "A.s4[" + std::to_string(d.kt) + "]");
-    checked(d.v, 16, d.d, "v", "A.s3[" + std::to_string(d.v) + "]");
-    if (d.mask >= 0) checked(d.mask, 1, 16, "m", "A.s4[" + std::to_string(d.mask) + "]");
+    checked(d.kt, d.d, tok, "k", "A.s4[" + std::to_string(d.kt) + "]");
+    checked(d.v, tok, d.d, "v", "A.s3[" + std::to_string(d.v) + "]");
+    if (d.mask >= 0) checked(d.mask, 1, tok, "m", "A.s4[" + std::to_string(d.mask) + "]");
     else o << "    po.m = 0;\n";
     o << "  };\n";
     o << "  auto f_bases = [&](const PageOffs& po, const u16*& kp, const u16*& vp, const float*& mp) {\n";

@@ -3,8 +3,9 @@
 Each seed draws the query rows per KV head (1..16), the head dim (64, 128,
 256, with rows x dim <= 1024), the KV heads, 1..24 sequences whose lengths
 mix empty, sub-page, exact-page and multi-thousand-token sequences, the page
-size (16, 32, 64: the streaming decode family, which folds pages of more
-than 16 tokens as 16-token sub-pages; 8: the tile program), the mask, and
+size (8, 16, 32, 64: the streaming decode family, which folds pages of more
+than 16 tokens as 16-token sub-pages and 8-token pages as half-filled
+16-token steps), the mask, and
 the input dtype (bf16 / f16).  The GPU accumulators and output must equal
 the oracle's within rtol 2e-5 (with an atol of 2e-5 of each tensor's largest
 magnitude: both fold the pages in fp32, split differently), sequences with
@@ -47,7 +48,7 @@ def test_random_decode_matches_oracle(gpu, seed):
     dt = W.F16 if c["f16"] else W.BF16
     prog = W.paged_decode(ga, masked=c["masked"], dtype=dt).compile(target="hip_gfx950")
     # (a [1, page] mask with as many query rows as page tokens is a row broadcast, see below)
-    want_family = "tile_program" if c["page"] == 8 or (c["masked"] and c["group"] == c["page"]) else "decode"
+    want_family = "tile_program" if c["masked"] and c["group"] == c["page"] else "decode"
     assert prog._native.kernel_family("decode_page") == want_family
     prog.execute()
     prog.synchronize()

@@ -514,9 +514,23 @@ def test_paged_decode_f16_and_unmasked(gpu):
     assert _rel_fro(ga["out"], W.paged_decode_ref(ga)) <= 1e-5
 
 
+def test_paged_decode_8_token_pages(gpu):
+    """8-token pages run on the decode family as half-filled 16-token steps: the
+    loads of tokens 8-15 read nothing and their scores are -inf."""
+    prog, ref, ga, ca = _decode_case([37, 8, 61, 1, 300, 16], 2, 4, 64, page=8, seed=3)
+    assert prog._native.kernel_family("decode_page") == "decode"
+    for k in ("m", "l", "o", "out"):
+        np.testing.assert_allclose(ga[k], ca[k], rtol=2e-5, atol=2e-5 * float(np.abs(ca[k]).max()), err_msg=k)
+    assert _rel_fro(ga["out"], W.paged_decode_ref(ga)) <= 1e-5
+    assert prog.stats.total_cycles == ref.total_cycles and prog.stats.task_count == ref.task_count
+
+
 def test_paged_decode_tile_program_path(gpu):
-    """8-token pages are outside the decode template: the tile program runs the page loop in order."""
-    prog, ref, ga, ca = _decode_case([37, 8, 61], 2, 4, 64, page=8, seed=3)
+    """A [1, page] mask with as many query rows as page tokens also fits the scores as a
+    row broadcast, which the decode template does not take: the tile program runs the
+    page loop in order.  The lengths are whole pages, so the mask is zero and both
+    readings of it agree with attention over the valid tokens."""
+    prog, ref, ga, ca = _decode_case([40, 8, 64], 2, 8, 64, page=8, seed=3)
     assert prog._native.kernel_family("decode_page") == "tile_program"
     for k in ("m", "l", "o", "out"):
         np.testing.assert_allclose(ga[k], ca[k], rtol=1e-5, atol=1e-6, err_msg=k)

@@ -160,11 +160,12 @@ def test_family_selection():
 
 
 @pytest.mark.parametrize("page, family", [(16, "decode"), (32, "decode"), (64, "decode"), (128, "decode"),
-                                          (8, "tile_program"), (48, "tile_program")])
+                                          (8, "decode"), (48, "tile_program"), (4, "tile_program")])
 def test_decode_family_page_sizes(page, family):
-    """Pages of 16, 32, 64 or 128 tokens take the decode family (pages of more than 16
-    tokens are folded as 16-token sub-pages: each sub-page's offset is the page's plus
-    16 tokens times the token stride); other sizes stay on the tile program."""
+    """Pages of 8, 16, 32, 64 or 128 tokens take the decode family (pages of more than
+    16 tokens are folded as 16-token sub-pages: each sub-page's offset is the page's plus
+    16 tokens times the token stride; 8-token pages as 16-token steps whose upper half
+    reads nothing); other sizes stay on the tile program."""
     from pto_wsp._hip import NativeProgram
 
     arrs = W.paged_decode_arrays([40, 300, 0, 17], 2, 4, 128, page=page)
@@ -173,8 +174,9 @@ def test_decode_family_page_sizes(page, family):
     if family == "decode":
         src = prog.precompile(0)
         assert "decode program" in src
-        assert f"n_[i] = static_cast<int>(npg) * {page // 16};" in src  # sub-page counts in the prefixes
+        assert f"n_[i] = static_cast<int>(npg) * {max(1, page // 16)};" in src  # sub-page counts in the prefixes
         assert ("vp_ %" in src) == (page > 16)
+        assert (", true>" in src) == (page == 8)  # the half-page template
 
 
 def test_decode_precompile_folded_normalisation():
