@@ -523,7 +523,7 @@ CASES = {
     "softmax3_overlap": lambda: Softmax3Case("softmax3_overlap", (8, 4096, 256), 0),
     # Not BASELINE configs: the C5 decode with 32- and 64-token pages (the same
     # lengths and heads; the decode family folds them as 16-token sub-pages)
-    # and with 8-token pages (folded as half-filled 16-token steps).
+    # and with 8-token pages (folded two to a 16-token step).
     "paged_decode_page32": lambda: DecodeCase("paged_decode_page32", 64, 32, 8, 128, 512, 8192, 0, None, page=32),
     "paged_decode_page64": lambda: DecodeCase("paged_decode_page64", 64, 32, 8, 128, 512, 8192, 0, None, page=64),
     "paged_decode_page8": lambda: DecodeCase("paged_decode_page8", 64, 32, 8, 128, 512, 8192, 0, None, page=8),

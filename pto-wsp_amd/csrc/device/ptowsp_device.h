@@ -1115,14 +1115,14 @@ __device__ inline void reset_count(int* cnt) {
     if ((threadIdx.x & 63) == 0) __hip_atomic_store(cnt, 0, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
 }
 
-// H8: pages of 8 tokens, each folded as a 16-token step whose tokens 8-15
-// are read as zeros (their byte offsets lie beyond the buffer's record
-// limit of 8 token rows) and whose scores are -inf.
+// H8: pages of 8 tokens, folded two to a 16-token step: page a supplies
+// tokens 0-7, page b tokens 8-15 (see load_pair).
 template <int G, int D, bool F16, bool MASK, bool H8 = false>
 struct DecodeWave {
     static_assert(G >= 1 && G <= 16 && (D == 64 || D == 128 || D == 256) && G * D <= 1024, "decode shape");
     static constexpr int NS = D / 32;          // head-dim slices of the score MFMA
     static constexpr int DV = D / 16;          // head-dim columns per lane in p @ v
+    static constexpr int kHalves = H8 ? 2 : 1;  // pages per 16-token step
     // Partial layout: o[G][D] (head dims permuted, see store), then m[G] and
     // l[G]; padded to 16 bytes so that every partial's o rows are 16-byte
     // aligned.
@@ -1133,41 +1133,77 @@ struct DecodeWave {
         u32x4 k[NS];           // lane l: token l%16, head dims 32*j + 8*(l/16) .. +7
         u32 v[4][DV / 2];      // lane l: tokens 4*(l/16) + i, head dims DV*(l%16) .. +DV-1
         float mask[4];         // lane l: tokens 4*(l/16) .. +3
+        float hneg;            // H8: added to the scores of tokens 8-15 (0, or -inf without page b)
     };
 
     // Per-lane byte offsets within a page, fixed for a launch: K (token t at
     // t*ks elements, head dims contiguous), V (token t at t*vs), mask (token t
-    // at t, four tokens per lane).
+    // at t, four tokens per lane).  With H8 tokens 8-15 are tokens 0-7 of the
+    // second page.
     struct Lanes {
         u32 k, v, m;
         u32 vrow;    // bytes between consecutive V tokens
-        u32 kn, vn;  // H8: bytes of 8 K / V token rows (the record limits)
     };
     __device__ static Lanes lanes(i64 ks, i64 vs) {
         const int lane = threadIdx.x & 63, t = lane & 15, grp = lane >> 4;
+        const int tk = H8 ? (t & 7) : t, gv = H8 ? (grp & 1) : grp;
         Lanes r;
-        r.k = static_cast<u32>((t * ks + 8 * grp) * 2);
-        r.v = static_cast<u32>((4 * grp * vs + DV * t) * 2);
-        r.m = static_cast<u32>(grp * 16);
+        r.k = static_cast<u32>((tk * ks + 8 * grp) * 2);
+        r.v = static_cast<u32>((4 * gv * vs + DV * t) * 2);
+        r.m = static_cast<u32>(gv * 16);
         r.vrow = static_cast<u32>(vs * 2);
-        r.kn = static_cast<u32>(ks * 16);
-        r.vn = static_cast<u32>(vs * 16);
         return r;
+    }
+
+    // H8: one step of two 8-token pages.  Each lane reads from the page its
+    // tokens belong to (K: token l%16 < 8 from page a; V and mask: tokens
+    // 4*(l/16)..+3 < 8 from page a), through a per-lane address: nontemporal
+    // global loads, one instruction per register as for a 16-token page.
+    // Without a page b (a unit's odd last page) the b bases are a's again, so
+    // the lanes of tokens 8-15 re-read page a (no new lines), and hneg sets
+    // those tokens' scores to -inf.  Steps past the stream's end are loaded
+    // from the stream's last step in the same way and never folded.
+    __device__ static void load_pair(Page& pg, const u16* ka, const u16* va, const float* ma, const u16* kb, const u16* vb,
+                                     const float* mb, const Lanes& ln, bool two) {
+        const int lane = threadIdx.x & 63, t = lane & 15, grp = lane >> 4;
+        const char* kp = reinterpret_cast<const char*>(t < 8 ? ka : kb) + ln.k;
+#pragma unroll
+        for (int j = 0; j < NS; ++j) pg.k[j] = __builtin_nontemporal_load(reinterpret_cast<const u32x4*>(kp + 64 * j));
+        const char* vp = reinterpret_cast<const char*>(grp < 2 ? va : vb) + ln.v;
+#pragma unroll
+        for (int i = 0; i < 4; ++i) {
+            const char* vi = vp + static_cast<u64>(i * ln.vrow);
+            if constexpr (DV == 16) {
+                const u32x4 a = __builtin_nontemporal_load(reinterpret_cast<const u32x4*>(vi));
+                const u32x4 b = __builtin_nontemporal_load(reinterpret_cast<const u32x4*>(vi + 16));
+                pg.v[i][0] = a.x; pg.v[i][1] = a.y; pg.v[i][2] = a.z; pg.v[i][3] = a.w;
+                pg.v[i][4] = b.x; pg.v[i][5] = b.y; pg.v[i][6] = b.z; pg.v[i][7] = b.w;
+            } else if constexpr (DV == 8) {
+                const u32x4 a = __builtin_nontemporal_load(reinterpret_cast<const u32x4*>(vi));
+                pg.v[i][0] = a.x; pg.v[i][1] = a.y; pg.v[i][2] = a.z; pg.v[i][3] = a.w;
+            } else {
+                const u32x2 a = __builtin_nontemporal_load(reinterpret_cast<const u32x2*>(vi));
+                pg.v[i][0] = a.x; pg.v[i][1] = a.y;
+            }
+        }
+        if constexpr (MASK) {
+            const u32x4 mk = __builtin_nontemporal_load(
+                reinterpret_cast<const u32x4*>(reinterpret_cast<const char*>(grp < 2 ? ma : mb) + ln.m));
+            pg.mask[0] = __uint_as_float(mk.x);
+            pg.mask[1] = __uint_as_float(mk.y);
+            pg.mask[2] = __uint_as_float(mk.z);
+            pg.mask[3] = __uint_as_float(mk.w);
+        }
+        pg.hneg = two ? 0.0f : -__builtin_inff();
     }
 
     // kp, vp, mp: wave-uniform page bases (buffer loads, streaming).  With
     // real false every load is out of range of its buffer (no records): it
     // reads no memory and returns zeros, and it still counts as a load.
-    // With H8 a real page's records end after its 8 token rows (token row
-    // stride >= head dim, so tokens 0-7 lie inside and 8-15 outside).
     __device__ static void load_page(Page& pg, const u16* kp, const u16* vp, const float* mp, const Lanes& ln, bool real) {
-        // real and the limits are wave-uniform
-        const int nrec = __builtin_amdgcn_readfirstlane(real ? -1 : 0);
-        const int nk = H8 ? __builtin_amdgcn_readfirstlane(real ? static_cast<int>(ln.kn) : 0) : nrec;
-        const int nv = H8 ? __builtin_amdgcn_readfirstlane(real ? static_cast<int>(ln.vn) : 0) : nrec;
-        const int nm = H8 ? __builtin_amdgcn_readfirstlane(real ? 32 : 0) : nrec;
-        const buf_rsrc rk = __builtin_amdgcn_make_buffer_rsrc(const_cast<u16*>(kp), 0, nk, 0x00020000);
-        const buf_rsrc rv = __builtin_amdgcn_make_buffer_rsrc(const_cast<u16*>(vp), 0, nv, 0x00020000);
+        const int nrec = __builtin_amdgcn_readfirstlane(real ? -1 : 0);  // real is wave-uniform
+        const buf_rsrc rk = __builtin_amdgcn_make_buffer_rsrc(const_cast<u16*>(kp), 0, nrec, 0x00020000);
+        const buf_rsrc rv = __builtin_amdgcn_make_buffer_rsrc(const_cast<u16*>(vp), 0, nrec, 0x00020000);
 #pragma unroll
         for (int j = 0; j < NS; ++j)
             pg.k[j] = __builtin_bit_cast(u32x4, __builtin_amdgcn_raw_buffer_load_b128(rk, ln.k + 64 * j, 0, 2));
@@ -1188,7 +1224,7 @@ struct DecodeWave {
             }
         }
         if constexpr (MASK) {
-            const buf_rsrc rm = __builtin_amdgcn_make_buffer_rsrc(const_cast<float*>(mp), 0, nm, 0x00020000);
+            const buf_rsrc rm = __builtin_amdgcn_make_buffer_rsrc(const_cast<float*>(mp), 0, nrec, 0x00020000);
             const u32x4 mk = __builtin_bit_cast(u32x4, __builtin_amdgcn_raw_buffer_load_b128(rm, ln.m, 0, 2));
             pg.mask[0] = __uint_as_float(mk.x);
             pg.mask[1] = __uint_as_float(mk.y);
@@ -1240,7 +1276,11 @@ struct DecodeWave {
         for (int i = 0; i < 4; ++i) {
             sc[i] = acc[i] * scale;
             if constexpr (MASK) sc[i] = sc[i] - pg.mask[i];
-            if constexpr (H8) sc[i] = grp < 2 ? sc[i] : -__builtin_inff();  // tokens 8-15: no token
+        }
+        if constexpr (H8) {
+            const float hb = grp < 2 ? 0.0f : pg.hneg;
+#pragma unroll
+            for (int i = 0; i < 4; ++i) sc[i] += hb;
         }
         // Online softmax of query row l%16 (rows >= G are q = 0 rows whose
         // results are never stored; p @ v keeps MFMA rows apart).
@@ -1409,10 +1449,12 @@ __device__ inline DecodeFns<P, B, Q, S, C> decode_fns(P p, B b, Q q, S s, C c) {
 }
 
 // One decode wave's pages [s, b) of the launch (units laid end to end, see
-// DecodeSplit) folded as a single stream: the NB-page register ring keeps
-// loading across unit boundaries and across the 64-page runs of page-table
-// offsets (lane i of a run holds page r0+i's offsets; the next run is read
-// 64 pages ahead), so the wave never waits for a page table or q read.
+// DecodeSplit; a "page" here is one 16-token step) folded as a single
+// stream: the NB-page register ring keeps loading across unit boundaries and
+// across the 64-page runs of page-table offsets (lane i of a run holds page
+// r0+i's offsets; the next run is read 64 pages ahead; with two 8-token pages
+// per step, 32 steps of two pages each), so the wave never waits for a page
+// table or q read.
 //
 // At the end of a unit's pages in this wave the partial is stored and its
 // completion deferred: vector memory operations of a wave complete in issue
@@ -1422,7 +1464,9 @@ __device__ inline DecodeFns<P, B, Q, S, C> decode_fns(P p, B b, Q q, S s, C c) {
 // the unit's partials.  A second unit end while one is pending, and the end
 // of the stream, complete it at once (waiting for the stores).
 //
-// F provides: page(g, PageOffs&) per lane; bases(PageOffs, kp, vp, mp);
+// F provides: page(h, PageOffs&) per lane, h = the step's index times
+// DW::kHalves plus the page's half (k < 0 for a half the unit does not
+// have); bases(PageOffs, kp, vp, mp);
 // q(u) (q tile of unit u, or null when out of range); slot(u) (this wave's
 // partial of unit u); combine(u, parts, first_slot).
 template <class DW, int NB, bool ORDERED>
@@ -1494,24 +1538,27 @@ struct DecodeStream {
                                float scale, i64 ks, i64 vs, i64 qs) {
         const int lane = threadIdx.x & 63;
         const typename DW::Lanes ln = DW::lanes(ks, vs);
-        // Page-table runs.
+        // Page-table runs: lane i holds the offsets of page i%HS of step
+        // r0 + i/HS (f.page takes that half-step index, HS*step + half).
+        constexpr int HS = DW::kHalves, RL = 64 / HS;
+        auto run_of = [&](i64 g0, PageOffs& po) { f.page(HS * g0 + lane < HS * b ? HS * g0 + lane : HS * b - 1, po); };
         i64 r0 = s;
         PageOffs rc, rn;
-        f.page(s + lane < b ? s + lane : b - 1, rc);
+        run_of(s, rc);
         rn = rc;
-        // Page g's offsets are read from the current run only: the run moves
-        // on just before the first page past it is loaded, so the next run's
-        // registers are read 64 pages after their load was issued.  (A select
+        // Step g's offsets are read from the current run only: the run moves
+        // on just before the first step past it is loaded, so the next run's
+        // registers are read RL steps after their load was issued.  (A select
         // between the two runs here would make every page load wait for the
         // most recent page-table read, i.e. for the whole ring.)
         auto load = [&](typename DW::Page& pg, i64 g) {
             const bool real = g < b;
-            if (real && g - r0 == 64) {
-                r0 += 64;
+            if (real && g - r0 == RL) {
+                r0 += RL;
                 rc = rn;
-                if (r0 + 64 < b) f.page(r0 + 64 + lane < b ? r0 + 64 + lane : b - 1, rn);
+                if (r0 + RL < b) run_of(r0 + RL, rn);
             }
-            const int li = static_cast<int>((real ? g : b - 1) - r0);
+            const int li = HS * static_cast<int>((real ? g : b - 1) - r0);
             PageOffs po;
             po.k = readlane64(rc.k, li);
             po.v = readlane64(rc.v, li);
@@ -1519,19 +1566,33 @@ struct DecodeStream {
             const u16 *kp, *vp;
             const float* mp;
             f.bases(po, kp, vp, mp);
-            // Past the stream's end the ring is still filled (so that every
-            // step waits for the same number of loads) with loads that read
-            // nothing.  The lane offsets stay the same registers on every
-            // path: a lane-offset temporary could share registers with a
-            // page load in flight, and the wait for that write would drain
-            // the ring.
-            DW::load_page(pg, kp, vp, mp, ln, real);
+            if constexpr (HS == 2) {
+                // A step's second page (k < 0: the unit has no such page).
+                PageOffs p2;
+                p2.k = readlane64(rc.k, li + 1);
+                p2.v = readlane64(rc.v, li + 1);
+                p2.m = readlane64(rc.m, li + 1);
+                const bool two = p2.k >= 0;
+                if (!two) p2 = po;
+                const u16 *kp2, *vp2;
+                const float* mp2;
+                f.bases(p2, kp2, vp2, mp2);
+                DW::load_pair(pg, kp, vp, mp, kp2, vp2, mp2, ln, two);
+            } else {
+                // Past the stream's end the ring is still filled (so that
+                // every step waits for the same number of loads) with loads
+                // that read nothing.  The lane offsets stay the same
+                // registers on every path: a lane-offset temporary could
+                // share registers with a page load in flight, and the wait
+                // for that write would drain the ring.
+                DW::load_page(pg, kp, vp, mp, ln, real);
+            }
         };
         // The first pages go out before anything else is read.
         typename DW::Page pg[NB];
 #pragma unroll
         for (int i = 0; i < NB - 1; ++i) load(pg[i], s + i);
-        if (s + 64 < b) f.page(s + 64 + lane < b ? s + 64 + lane : b - 1, rn);
+        if (s + RL < b) run_of(s + RL, rn);
         // Unit state.
         int u = DecodeSplit::unit_of(pre, U, s);
         u = __builtin_amdgcn_readfirstlane(u);

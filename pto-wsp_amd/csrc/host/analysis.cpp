@@ -354,7 +354,7 @@ DecodeInfo classify_decode(const KernelDef& k, const KernelAnalysis& a) {
         if (mk->dtype != DType::F32 || mk->rows != 1 || mk->cols != PG) return info;
     }
     // Device template shapes: pages of 8, 16, 32, 64 or 128 tokens (folded as 16-token
-    // steps: larger pages as 16-token sub-pages, 8-token pages as half-filled steps),
+    // steps: larger pages as 16-token sub-pages, 8-token pages two to a step),
     // up to 16 query rows, head dim 64 / 128 / 256, at most 64 partial outputs per lane
     // (G * D / 16).
     if ((PG != 8 && PG != 16 && PG != 32 && PG != 64 && PG != 128) || G < 1 || G > 16 ||

@@ -1048,16 +1048,20 @@ EmittedKernel emit_decode(const Module& m, const KernelAnalysis& a, const Launch
     o << "      if (i < per && u0 + i < U) {\n";
     decode_vars("u0 + i", "        ");
     o << "        vars[" << ng << "] = 0;\n";
-    {
+    // The unit's page count (vars of the unit set, vars[ng] = 0).
+    auto npg_expr = [&](const std::string& ind) {
         const int term = spec.inner_dyn_term.empty() ? -1 : spec.inner_dyn_term[0];
-        if (term >= 0) o << "        i64 npg = indirect_index(A, " << term << ", vars, " << ng << ");\n";
-        else o << "        i64 npg = A.ext[" << ng << "];\n";
-    }
-    o << "        if (npg < 0) npg = 0;\n";
+        if (term >= 0) o << ind << "i64 npg = indirect_index(A, " << term << ", vars, " << ng << ");\n";
+        else o << ind << "i64 npg = A.ext[" << ng << "];\n";
+        o << ind << "if (npg < 0) npg = 0;\n";
+    };
+    npg_expr("        ");
     o << "        if (npg > maxp) { npg = maxp; if (blockIdx.x == 0) *A.err = 3; }\n";
-    // Pages of more than 16 tokens are folded as 16-token sub-pages: the
-    // prefixes, the split and the stream count sub-pages.
-    o << "        n_[i] = static_cast<int>(npg) * " << std::max(1, d.pg / 16) << ";\n";
+    // Pages of more than 16 tokens are folded as 16-token sub-pages, pages of
+    // 8 tokens two to a 16-token step: the prefixes, the split and the
+    // stream count steps.
+    if (d.pg == 8) o << "        n_[i] = static_cast<int>((npg + 1) / 2);\n";
+    else o << "        n_[i] = static_cast<int>(npg) * " << std::max(1, d.pg / 16) << ";\n";
     o << "        run += n_[i];\n";
     o << "        crun += DecodeSplit::cost(n_[i]);\n";
     o << "      }\n";
@@ -1119,15 +1123,29 @@ EmittedKernel emit_decode(const Module& m, const KernelAnalysis& a, const Launch
     // Offsets of global (sub-)page g (per lane): its unit, the page index
     // within the unit, the affine and page-table terms, and for pages of
     // more than 16 tokens the sub-page's first token (its token stride: s4
-    // of the K^T and mask tiles, s3 of the V tile).  The 16-token tile that
-    // is loaded is bounds-checked; an out-of-range one raises the error flag
-    // and reads the tensor's first tile instead.
+    // of the K^T and mask tiles, s3 of the V tile).  With 8-token pages the
+    // argument is a half-step index (two pages per step).  The 16-token
+    // (8-token) tile that is loaded is bounds-checked; an out-of-range one
+    // raises the error flag and reads the tensor's first tile instead.
     const int sub = std::max(1, d.pg / 16), tok = std::min(16, d.pg);
-    o << "  auto f_page = [&](i64 g, PageOffs& po) {\n";
+    o << "  auto f_page = [&](i64 h, PageOffs& po) {\n";
+    if (d.pg == 8) o << "    const i64 g = h >> 1;\n";
+    else o << "    const i64 g = h;\n";
     o << "    const int uu = DecodeSplit::unit_of(pre, U, g);\n";
     o << "    i64 vars[" << nvars << "];\n";
     decode_vars("uu", "    ");
-    if (sub == 1) {
+    if (d.pg == 8) {
+        // Half h&1 of step g is page 2*(g - pre[uu]) + (h&1) of the unit; a
+        // unit with an odd page count has no second page in its last step.
+        o << "    vars[" << ng << "] = 0;\n";
+        o << "    {\n";
+        npg_expr("      ");
+        o << "      if (npg > maxp) npg = maxp;\n";
+        o << "      vars[" << ng << "] = 2 * (g - pre[uu]) + (h & 1);\n";
+        o << "      if (vars[" << ng << "] >= npg) { po.k = -1; po.v = 0; po.m = 0; return; }\n";
+        o << "    }\n";
+        o << "    const i64 t0_ = 0;\n";
+    } else if (sub == 1) {
         o << "    vars[" << ng << "] = g - pre[uu];\n";
         o << "    const i64 t0_ = 0;\n";
     } else {

@@ -745,10 +745,6 @@ bool decode_allowed(const KernelAnalysis& a, const LaunchSpec& L, const LaunchAr
     if (A.s3[d.kt] != 1 || A.s4[d.kt] % 8 || !aligned(d.kt, 8, 2)) return false;
     if (A.s4[d.v] != 1 || A.s3[d.v] % dv || !aligned(d.v, dv, 2)) return false;
     if (d.mask >= 0 && (A.s4[d.mask] != 1 || !aligned(d.mask, 1, 4))) return false;
-    // 8-token pages fill half of a 16-token step: the loads of tokens 8-15
-    // fall outside a record limit of 8 token rows, which holds only the page
-    // when token rows do not overlap.
-    if (d.pg == 8 && (A.s4[d.kt] < d.d || A.s3[d.v] < d.d)) return false;
     // Page loads use 32-bit byte offsets from the page base.
     const int64_t lim = int64_t(1) << 30;
     if (A.s4[d.kt] >= lim / 16 || A.s3[d.v] >= lim / 16) return false;

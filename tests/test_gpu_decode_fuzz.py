@@ -4,8 +4,8 @@ Each seed draws the query rows per KV head (1..16), the head dim (64, 128,
 256, with rows x dim <= 1024), the KV heads, 1..24 sequences whose lengths
 mix empty, sub-page, exact-page and multi-thousand-token sequences, the page
 size (8, 16, 32, 64: the streaming decode family, which folds pages of more
-than 16 tokens as 16-token sub-pages and 8-token pages as half-filled
-16-token steps), the mask, and
+than 16 tokens as 16-token sub-pages and 8-token pages two to a 16-token
+step), the mask, and
 the input dtype (bf16 / f16).  The GPU accumulators and output must equal
 the oracle's within rtol 2e-5 (with an atol of 2e-5 of each tensor's largest
 magnitude: both fold the pages in fp32, split differently), sequences with

@@ -515,8 +515,10 @@ def test_paged_decode_f16_and_unmasked(gpu):
 
 
 def test_paged_decode_8_token_pages(gpu):
-    """8-token pages run on the decode family as half-filled 16-token steps: the
-    loads of tokens 8-15 read nothing and their scores are -inf."""
+    """8-token pages run on the decode family two to a 16-token step (tokens 8-15
+    from the step's second page); a unit with an odd page count ends on a step
+    without a second page, whose tokens 8-15 get -inf scores.  The lengths give
+    5, 1, 8, 1, 38 and 2 pages."""
     prog, ref, ga, ca = _decode_case([37, 8, 61, 1, 300, 16], 2, 4, 64, page=8, seed=3)
     assert prog._native.kernel_family("decode_page") == "decode"
     for k in ("m", "l", "o", "out"):

@@ -164,8 +164,8 @@ def test_family_selection():
 def test_decode_family_page_sizes(page, family):
     """Pages of 8, 16, 32, 64 or 128 tokens take the decode family (pages of more than
     16 tokens are folded as 16-token sub-pages: each sub-page's offset is the page's plus
-    16 tokens times the token stride; 8-token pages as 16-token steps whose upper half
-    reads nothing); other sizes stay on the tile program."""
+    16 tokens times the token stride; 8-token pages two to a 16-token step, with a
+    per-unit step count of ceil(pages / 2)); other sizes stay on the tile program."""
     from pto_wsp._hip import NativeProgram
 
     arrs = W.paged_decode_arrays([40, 300, 0, 17], 2, 4, 128, page=page)
@@ -174,9 +174,13 @@ def test_decode_family_page_sizes(page, family):
     if family == "decode":
         src = prog.precompile(0)
         assert "decode program" in src
-        assert f"n_[i] = static_cast<int>(npg) * {max(1, page // 16)};" in src  # sub-page counts in the prefixes
+        if page == 8:
+            assert "n_[i] = static_cast<int>((npg + 1) / 2);" in src  # step counts in the prefixes
+            assert "DecodeWave<4, 128, false, true, true>" in src      # the paired-page template
+        else:
+            assert f"n_[i] = static_cast<int>(npg) * {page // 16};" in src  # sub-page counts in the prefixes
+            assert "DecodeWave<4, 128, false, true, false>" in src
         assert ("vp_ %" in src) == (page > 16)
-        assert (", true>" in src) == (page == 8)  # the half-page template
 
 
 def test_decode_precompile_folded_normalisation():
