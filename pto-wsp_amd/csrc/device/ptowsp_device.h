@@ -1119,7 +1119,7 @@ __device__ inline void reset_count(int* cnt) {
 // tokens 0-7, page b tokens 8-15 (see load_pair).
 template <int G, int D, bool F16, bool MASK, bool H8 = false>
 struct DecodeWave {
-    static_assert(G >= 1 && G <= 16 && (D == 64 || D == 128 || D == 256) && G * D <= 1024, "decode shape");
+    static_assert(G >= 1 && G <= 16 && (D == 64 || D == 128 || D == 256), "decode shape");
     static constexpr int NS = D / 32;          // head-dim slices of the score MFMA
     static constexpr int DV = D / 16;          // head-dim columns per lane in p @ v
     static constexpr int kHalves = H8 ? 2 : 1;  // pages per 16-token step
@@ -1668,71 +1668,89 @@ template <int G, int D>
 struct DecodeCombine {
     static constexpr int DPL = D / 64;
     static constexpr int CB = 2;  // partials loaded together
-    __device__ static void fold(float (&mm)[G], float (&ll)[G], float (&oo)[G][DPL], const float* mc, const float* lc,
+    // Query rows folded per pass: R * DPL <= 16 accumulators per lane, so
+    // the combine (inlined where a unit completes, with the page ring in
+    // flight) needs the same registers for every G.
+    static constexpr int R = (16 / DPL < G) ? 16 / DPL : G;
+    __device__ static void fold(int g0, float (&mm)[R], float (&ll)[R], float (&oo)[R][DPL], const float* mc, const float* lc,
                                 const float (*oc)[DPL]) {
 #pragma unroll
-        for (int g = 0; g < G; ++g) {
-            const float mn = fmaxf(mm[g], mc[g]);
-            const float a = expf(mm[g] - mn), b = expf(mc[g] - mn);
-            ll[g] = ll[g] * a + lc[g] * b;
+        for (int r = 0; r < R; ++r) {
+            if (g0 + r < G) {
+                const float mn = fmaxf(mm[r], mc[r]);
+                const float a = expf(mm[r] - mn), b = expf(mc[r] - mn);
+                ll[r] = ll[r] * a + lc[r] * b;
 #pragma unroll
-            for (int j = 0; j < DPL; ++j) oo[g][j] = oo[g][j] * a + oc[g][j] * b;
-            mm[g] = mn;
+                for (int j = 0; j < DPL; ++j) oo[r][j] = oo[r][j] * a + oc[r][j] * b;
+                mm[r] = mn;
+            }
+        }
+    }
+    // Rows g0 .. g0+R-1 (those below G) of partial pc.
+    __device__ static void load_rows(int g0, const float* pc, float (&mc)[R], float (&lc)[R], float (&oc)[R][DPL]) {
+        const int lane = threadIdx.x & 63;
+#pragma unroll
+        for (int r = 0; r < R; ++r) {
+            const int g = g0 + r;
+            if (g < G) {
+                mc[r] = coherent_load(pc + G * D + g);
+                lc[r] = coherent_load(pc + G * D + G + g);
+#pragma unroll
+                for (int j = 0; j < DPL; ++j) oc[r][j] = coherent_load(pc + g * D + DPL * lane + j);
+            }
         }
     }
     // Folds nch partials (page order) into the unit's accumulators; with out
     // non-null also writes out = o / l (the normalisation launch folded in).
+    // Rows pass by pass; each row folds its partials in page order.
     __device__ static void run(i64 nch, const float* part, i64 pstride, float* m, i64 ms3, float* l, i64 ls3, float* o,
                                i64 os3, i64 os4, float* out, i64 us3, i64 us4) {
         const int lane = threadIdx.x & 63;
-        float mm[G], ll[G], oo[G][DPL];
 #pragma unroll
-        for (int g = 0; g < G; ++g) {
-            mm[g] = m[g * ms3];
-            ll[g] = l[g * ls3];
+        for (int g0 = 0; g0 < G; g0 += R) {
+            float mm[R], ll[R], oo[R][DPL];
 #pragma unroll
-            for (int j = 0; j < DPL; ++j) oo[g][j] = o[g * os3 + part_dim<D>(DPL * lane + j) * os4];
-        }
-        i64 c = 0;
-        for (; c + CB <= nch; c += CB) {
-            float mc[CB][G], lc[CB][G], oc[CB][G][DPL];
+            for (int r = 0; r < R; ++r) {
+                const int g = g0 + r;
+                mm[r] = 0.0f;
+                ll[r] = 0.0f;
 #pragma unroll
-            for (int b = 0; b < CB; ++b) {
-                const float* pc = part + (c + b) * pstride;
+                for (int j = 0; j < DPL; ++j) oo[r][j] = 0.0f;
+                if (g < G) {
+                    mm[r] = m[g * ms3];
+                    ll[r] = l[g * ls3];
 #pragma unroll
-                for (int g = 0; g < G; ++g) {
-                    mc[b][g] = coherent_load(pc + G * D + g);
-                    lc[b][g] = coherent_load(pc + G * D + G + g);
-#pragma unroll
-                    for (int j = 0; j < DPL; ++j) oc[b][g][j] = coherent_load(pc + g * D + DPL * lane + j);
+                    for (int j = 0; j < DPL; ++j) oo[r][j] = o[g * os3 + part_dim<D>(DPL * lane + j) * os4];
                 }
             }
+            i64 c = 0;
+            for (; c + CB <= nch; c += CB) {
+                float mc[CB][R], lc[CB][R], oc[CB][R][DPL];
 #pragma unroll
-            for (int b = 0; b < CB; ++b) fold(mm, ll, oo, mc[b], lc[b], oc[b]);
-        }
-        for (; c < nch; ++c) {
-            const float* pc = part + c * pstride;
-            float mc[G], lc[G], oc[G][DPL];
+                for (int b = 0; b < CB; ++b) load_rows(g0, part + (c + b) * pstride, mc[b], lc[b], oc[b]);
 #pragma unroll
-            for (int g = 0; g < G; ++g) {
-                mc[g] = coherent_load(pc + G * D + g);
-                lc[g] = coherent_load(pc + G * D + G + g);
-#pragma unroll
-                for (int j = 0; j < DPL; ++j) oc[g][j] = coherent_load(pc + g * D + DPL * lane + j);
+                for (int b = 0; b < CB; ++b) fold(g0, mm, ll, oo, mc[b], lc[b], oc[b]);
             }
-            fold(mm, ll, oo, mc, lc, oc);
-        }
-#pragma unroll
-        for (int g = 0; g < G; ++g) {
-            if (lane == 0) {
-                m[g * ms3] = mm[g];
-                l[g * ls3] = ll[g];
+            for (; c < nch; ++c) {
+                float mc[R], lc[R], oc[R][DPL];
+                load_rows(g0, part + c * pstride, mc, lc, oc);
+                fold(g0, mm, ll, oo, mc, lc, oc);
             }
 #pragma unroll
-            for (int j = 0; j < DPL; ++j) o[g * os3 + part_dim<D>(DPL * lane + j) * os4] = oo[g][j];
-            if (out) {
+            for (int r = 0; r < R; ++r) {
+                const int g = g0 + r;
+                if (g < G) {
+                    if (lane == 0) {
+                        m[g * ms3] = mm[r];
+                        l[g * ls3] = ll[r];
+                    }
 #pragma unroll
-                for (int j = 0; j < DPL; ++j) out[g * us3 + part_dim<D>(DPL * lane + j) * us4] = oo[g][j] / ll[g];
+                    for (int j = 0; j < DPL; ++j) o[g * os3 + part_dim<D>(DPL * lane + j) * os4] = oo[r][j];
+                    if (out) {
+#pragma unroll
+                        for (int j = 0; j < DPL; ++j) out[g * us3 + part_dim<D>(DPL * lane + j) * us4] = oo[r][j] / ll[r];
+                    }
+                }
             }
         }
     }

@@ -355,10 +355,9 @@ DecodeInfo classify_decode(const KernelDef& k, const KernelAnalysis& a) {
     }
     // Device template shapes: pages of 8, 16, 32, 64 or 128 tokens (folded as 16-token
     // steps: larger pages as 16-token sub-pages, 8-token pages two to a step),
-    // up to 16 query rows, head dim 64 / 128 / 256, at most 64 partial outputs per lane
-    // (G * D / 16).
+    // up to 16 query rows (one MFMA row block), head dim 64 / 128 / 256.
     if ((PG != 8 && PG != 16 && PG != 32 && PG != 64 && PG != 128) || G < 1 || G > 16 ||
-        (D != 64 && D != 128 && D != 256) || G * D > 1024)
+        (D != 64 && D != 128 && D != 256))
         return info;
     info.ok = true;
     info.q = a.tensor_ordinal[pq];

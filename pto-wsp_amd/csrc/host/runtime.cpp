@@ -457,13 +457,20 @@ struct Tuning {
     int row_up = 2;
     bool nontemporal = true;
     bool gemm_pingpong = true;
-    int decode_ring = 4;
+    int decode_ring = 0;  // 0: decode_ring_for(head dim)
     int decode_waves = 4;
     bool decode_ordered = false;
     bool serial_groups = true;  // overlapping grids run as parallel groups of in-order tasks
     int tile_threads = 256;     // threads of a tile-program workgroup
     bool row_loops = true;      // row programs over in-kernel loops
 };
+
+// Page ring depth of the decode family: 32 KiB of K and V in flight per
+// wave at head dim 128 (4 steps of 16 tokens).  At head dim 256 a step is
+// twice the registers, and a 4-step ring spills to scratch (0.75 ms against
+// 0.41 ms with 2 steps on the C5 shape with head dim 256); 2 steps keep the
+// same bytes in flight.
+int decode_ring_for(int head_dim) { return head_dim >= 256 ? 2 : 4; }
 
 const Tuning& tuning() {
     static const Tuning t = [] {
@@ -998,7 +1005,7 @@ BuiltLaunch build_launch(RunEnv& E, const LaunchSpec& L) {
     }
     B.spec.decode = decode_allowed(a, L, A, B.spec, ng);
     B.spec.row_loops = tuning().row_loops && row_loops_allowed(a, L, A, B.spec, ng, nvars);
-    B.spec.decode_ring = tuning().decode_ring;
+    B.spec.decode_ring = tuning().decode_ring ? tuning().decode_ring : decode_ring_for(a.decode.d);
     B.spec.decode_waves = tuning().decode_waves;
     B.spec.decode_ordered = tuning().decode_ordered;
     B.spec.vec_width = a.family == Family::RowProgram ? pick_vec_width(a, A, nvars) : 1;
@@ -1713,7 +1720,7 @@ int ptowsp_hip_precompile(ptowsp_program* P, int index, int flags, const char** 
             spec.nontemporal = tuning().nontemporal;
             spec.gemm = a.family == Family::Gemm && !spec.serial;
             spec.decode = a.family == Family::Decode && !spec.serial && L.inner.size() == 1;
-            spec.decode_ring = tuning().decode_ring;
+            spec.decode_ring = tuning().decode_ring ? tuning().decode_ring : decode_ring_for(a.decode.d);
             spec.decode_waves = tuning().decode_waves;
             spec.decode_ordered = tuning().decode_ordered;
             spec.decode_norm = spec.decode && (flags & 32) != 0;

@@ -450,6 +450,22 @@ def test_paged_decode_family(gpu, lengths, hkv, group, d):
     assert prog.stats.total_cycles == ref.total_cycles and prog.stats.task_count == ref.task_count
 
 
+@pytest.mark.parametrize("lengths,hkv,group,d,page", [
+    ([300, 77, 1, 33], 2, 16, 128, 32),          # 16 query rows at head dim 128 (a 2-pass combine)
+    ([129, 40, 700], 2, 8, 256, 16),              # 8 rows at head dim 256 (2-step page ring)
+    ([513, 64, 5], 1, 16, 256, 64),               # 16 rows at head dim 256 (4 passes of 4 rows)
+])
+def test_paged_decode_wide_units(gpu, lengths, hkv, group, d, page):
+    """Units of more than 1024 accumulators (query rows x head dim) on the decode
+    family: the completing wave folds the partials a few rows per pass."""
+    prog, ref, ga, ca = _decode_case(lengths, hkv, group, d, page=page, seed=len(lengths) + group)
+    assert prog._native.kernel_family("decode_page") == "decode"
+    for k in ("m", "l", "o", "out"):
+        np.testing.assert_allclose(ga[k], ca[k], rtol=2e-5, atol=2e-5 * float(np.abs(ca[k]).max()), err_msg=k)
+    assert _rel_fro(ga["out"], W.paged_decode_ref(ga)) <= 1e-5
+    assert prog.stats.total_cycles == ref.total_cycles and prog.stats.task_count == ref.task_count
+
+
 def test_paged_decode_long_streams(gpu):
     """Thousands of pages: every wave folds a long stream of pages that crosses
     unit and page-table-run boundaries, mixing long units (split over several
