@@ -1664,14 +1664,15 @@ struct DecodeStream {
     }
 };
 
-template <int G, int D>
+template <int G, int D, int ACC = 16>
 struct DecodeCombine {
     static constexpr int DPL = D / 64;
     static constexpr int CB = 2;  // partials loaded together
-    // Query rows folded per pass: R * DPL <= 16 accumulators per lane, so
+    // Query rows folded per pass: R * DPL <= ACC accumulators per lane, so
     // the combine (inlined where a unit completes, with the page ring in
     // flight) needs the same registers for every G.
-    static constexpr int R = (16 / DPL < G) ? 16 / DPL : G;
+    static_assert(ACC >= DPL, "combine pass width");
+    static constexpr int R = (ACC / DPL < G) ? ACC / DPL : G;
     __device__ static void fold(int g0, float (&mm)[R], float (&ll)[R], float (&oo)[R][DPL], const float* mc, const float* lc,
                                 const float (*oc)[DPL]) {
 #pragma unroll

@@ -1195,7 +1195,9 @@ EmittedKernel emit_decode(const Module& m, const KernelAnalysis& a, const Launch
         o << "    if (!bad_acc) { if (!norm_check(vars)) bad_acc = true; else out_ = norm_ptr(vars); }\n";
     }
     o << "    if (!bad_acc)\n";
-    o << "      DecodeCombine<" << d.g << ", " << d.d << ">::run(parts, partials + first * DW::kPartFloats, DW::kPartFloats, "
+    // Accumulators per lane of one combine pass: half as many with two waves
+    // per SIMD (half the registers per wave).
+    o << "      DecodeCombine<" << d.g << ", " << d.d << ", " << (nw == 8 ? 8 : 16) << ">::run(parts, partials + first * DW::kPartFloats, DW::kPartFloats, "
       << ptr(d.m, "float*", 4) << ", A.s3[" << d.m << "], " << ptr(d.l, "float*", 4) << ", A.s3[" << d.l << "], "
       << ptr(d.o, "float*", 4) << ", A.s3[" << d.o << "], A.s4[" << d.o << "], "
       << (spec.decode_norm ? "out_, A.s3[" + std::to_string(ntens + 1) + "], A.s4[" + std::to_string(ntens + 1) + "]"
@@ -1220,7 +1222,7 @@ EmittedKernel emit_decode(const Module& m, const KernelAnalysis& a, const Launch
         unit_check(d.l, d.g, 1, "bad_acc");
         unit_check(d.o, d.g, d.d, "bad_acc");
         o << "    if (bad_acc || !norm_check(vars)) continue;\n";
-        o << "    DecodeCombine<" << d.g << ", " << d.d << ">::normalize(" << ptr(d.o, "const float*", 4) << ", A.s3[" << d.o
+        o << "    DecodeCombine<" << d.g << ", " << d.d << ", " << (nw == 8 ? 8 : 16) << ">::normalize(" << ptr(d.o, "const float*", 4) << ", A.s3[" << d.o
           << "], A.s4[" << d.o << "], " << ptr(d.l, "const float*", 4) << ", A.s3[" << d.l << "], norm_ptr(vars), A.s3["
           << q << "], A.s4[" << q << "]);\n";
         o << "  }\n";
