@@ -529,13 +529,14 @@ CASES = {
     "paged_decode_page8": lambda: DecodeCase("paged_decode_page8", 64, 32, 8, 128, 512, 8192, 0, None, page=8),
     # Not BASELINE configs: the C5 lengths and KV heads with other query-row
     # counts and head dims (head dim 64 with 8 rows, head dim 256 with 4
-    # rows, 16 rows at head dim 128 with 32-token pages).
+    # rows, 16 rows at head dim 128 with 32-token pages, 32 rows at 128).
     "paged_decode_d64": lambda: DecodeCase("paged_decode_d64", 64, 64, 8, 64, 512, 8192, 0, None),
     "paged_decode_d256": lambda: DecodeCase("paged_decode_d256", 64, 32, 8, 256, 512, 8192, 0, None),
     "paged_decode_g16": lambda: DecodeCase("paged_decode_g16", 64, 128, 8, 128, 512, 8192, 0, None, page=32),
+    "paged_decode_g32": lambda: DecodeCase("paged_decode_g32", 64, 256, 8, 128, 512, 8192, 0, None),
 }
 EXTRA = ("copy_calib", "softmax3", "softmax3_overlap", "paged_decode_page32", "paged_decode_page64", "paged_decode_page8",
-         "paged_decode_d64", "paged_decode_d256", "paged_decode_g16")
+         "paged_decode_d64", "paged_decode_d256", "paged_decode_g16", "paged_decode_g32")
 
 
 def load_traffic(name):

@@ -1119,9 +1119,11 @@ __device__ inline void reset_count(int* cnt) {
 // tokens 0-7, page b tokens 8-15 (see load_pair).
 template <int G, int D, bool F16, bool MASK, bool H8 = false>
 struct DecodeWave {
-    static_assert(G >= 1 && G <= 16 && (D == 64 || D == 128 || D == 256), "decode shape");
+    static_assert(G >= 1 && G <= 48 && (D == 64 || D == 128 || D == 256), "decode shape");
     static constexpr int NS = D / 32;          // head-dim slices of the score MFMA
     static constexpr int DV = D / 16;          // head-dim columns per lane in p @ v
+    static constexpr int RB = (G + 15) / 16;   // blocks of 16 query rows (one MFMA row block each)
+    static constexpr int NQ = RB * NS;         // q registers (u32x4) per lane
     static constexpr int kHalves = H8 ? 2 : 1;  // pages per 16-token step
     // Partial layout: o[G][D] (head dims permuted, see store), then m[G] and
     // l[G]; padded to 16 bytes so that every partial's o rows are 16-byte
@@ -1234,8 +1236,8 @@ struct DecodeWave {
     }
 
     struct State {
-        float m, l;            // query row l%16, replicated over its 4 lanes
-        f32x4v_t o[DV];        // o[e][j]: query row 4*(l/16) + j, head dim DV*(l%16) + e
+        float m[RB], l[RB];    // query row 16*rb + l%16, replicated over its 4 lanes
+        f32x4v_t o[RB][DV];    // o[rb][e][j]: query row 16*rb + 4*(l/16) + j, head dim DV*(l%16) + e
     };
 
     typedef float f32x2_t __attribute__((ext_vector_type(2)));
@@ -1267,33 +1269,45 @@ struct DecodeWave {
     __device__ static void step(State& st, const Page& pg, const u32x4* qa, float scale) {
         const int lane = threadIdx.x & 63, t = lane & 15, grp = lane >> 4;
         // Scores S^T: A = the K page, B = q^T; lane l holds tokens 4*(l/16) + i
-        // of query row l%16.
-        f32x4v_t acc = {0.0f, 0.0f, 0.0f, 0.0f};
+        // of query row 16*rb + l%16.  The page registers serve every row block.
+        f32x4v_t acc[RB];
 #pragma unroll
-        for (int j = 0; j < NS; ++j) acc = mfma_16x16x32<F16>(pg.k[j], qa[j], acc);
-        float sc[4];
+        for (int rb = 0; rb < RB; ++rb) {
+            acc[rb] = f32x4v_t{0.0f, 0.0f, 0.0f, 0.0f};
 #pragma unroll
-        for (int i = 0; i < 4; ++i) {
-            sc[i] = acc[i] * scale;
-            if constexpr (MASK) sc[i] = sc[i] - pg.mask[i];
+            for (int j = 0; j < NS; ++j) acc[rb] = mfma_16x16x32<F16>(pg.k[j], qa[rb * NS + j], acc[rb]);
         }
-        if constexpr (H8) {
-            const float hb = grp < 2 ? 0.0f : pg.hneg;
-#pragma unroll
-            for (int i = 0; i < 4; ++i) sc[i] += hb;
-        }
-        // Online softmax of query row l%16 (rows >= G are q = 0 rows whose
-        // results are never stored; p @ v keeps MFMA rows apart).
+        float hb = 0.0f;
+        if constexpr (H8) hb = grp < 2 ? 0.0f : pg.hneg;
+        // Online softmax of query row 16*rb + l%16 (rows >= G are q = 0 rows
+        // whose results are never stored; p @ v keeps MFMA rows apart).  The
+        // row blocks' softmax chains are independent and sit in one basic
+        // block, ahead of the rescale branches, so that they interleave.
         auto fmax_ = [](float x, float y) { return fmaxf(x, y); };
         auto fadd_ = [](float x, float y) { return x + y; };
-        const float mx = cross4_reduce(fmaxf(fmaxf(sc[0], sc[1]), fmaxf(sc[2], sc[3])), fmax_);
-        const float mn = fmaxf(st.m, mx);
-        const float a = expf(st.m - mn);
-        f32x4v_t pr;
+        float a[RB];
+        u32x2 ph[RB], pl[RB];
+        bool rescale[RB];
 #pragma unroll
-        for (int i = 0; i < 4; ++i) pr[i] = expf(sc[i] - mn);
-        st.l = st.l * a + cross4_reduce((pr[0] + pr[1]) + (pr[2] + pr[3]), fadd_);
-        st.m = mn;
+        for (int rb = 0; rb < RB; ++rb) {
+            float sc[4];
+#pragma unroll
+            for (int i = 0; i < 4; ++i) {
+                sc[i] = acc[rb][i] * scale;
+                if constexpr (MASK) sc[i] = sc[i] - pg.mask[i];
+                if constexpr (H8) sc[i] += hb;
+            }
+            const float mx = cross4_reduce(fmaxf(fmaxf(sc[0], sc[1]), fmaxf(sc[2], sc[3])), fmax_);
+            const float mn = fmaxf(st.m[rb], mx);
+            a[rb] = expf(st.m[rb] - mn);
+            f32x4v_t pr;
+#pragma unroll
+            for (int i = 0; i < 4; ++i) pr[i] = expf(sc[i] - mn);
+            st.l[rb] = st.l[rb] * a[rb] + cross4_reduce((pr[0] + pr[1]) + (pr[2] + pr[3]), fadd_);
+            st.m[rb] = mn;
+            rescale[rb] = __builtin_amdgcn_ballot_w64(16 * rb + t < G && a[rb] != 1.0f) != 0;
+            split4(pr, ph[rb], pl[rb]);
+        }
         // o <- o * a + p @ v on the matrix cores: v_mfma_f32_16x16x16 with
         // M = query rows, K = the page's 16 tokens, N = 16 head dims.  p is
         // fp32 and enters as hi + lo (split4), two products per MFMA step;
@@ -1304,47 +1318,57 @@ struct DecodeWave {
         // and accumulates o rows 4*(l/16)..+3.  Once the running maxima
         // settle, a == 1 for every row and o * a == o exactly, so the rescale
         // is skipped for the whole wave.
-        const bool rescale = __builtin_amdgcn_ballot_w64(t < G && a != 1.0f) != 0;
-        u32x2 ph, pl;
-        split4(pr, ph, pl);
-        if (rescale) {
-            // A real branch (the empty asm keeps it from being turned into
-            // selects): the multiply is rare, and o stays in the matrix
-            // cores' accumulator registers otherwise.  o row 4*(l/16) + j
-            // takes the factor of query row 4*(l/16) + j, held by lane
-            // 4*(l/16) + j.
-            asm volatile("");
-            f32x4v_t a4;
 #pragma unroll
-            for (int j = 0; j < 4; ++j) a4[j] = __int_as_float(__builtin_amdgcn_ds_bpermute((4 * grp + j) * 4, __float_as_int(a)));
+        for (int rb = 0; rb < RB; ++rb) {
+            if (rescale[rb]) {
+                // A real branch (the empty asm keeps it from being turned into
+                // selects): the multiply is rare, and o stays in the matrix
+                // cores' accumulator registers otherwise.  o row 4*(l/16) + j
+                // takes the factor of query row 4*(l/16) + j, held by lane
+                // 4*(l/16) + j.
+                asm volatile("");
+                f32x4v_t a4;
 #pragma unroll
-            for (int e = 0; e < DV; ++e) st.o[e] = st.o[e] * a4;
+                for (int j = 0; j < 4; ++j) a4[j] = __int_as_float(__builtin_amdgcn_ds_bpermute((4 * grp + j) * 4, __float_as_int(a[rb])));
+#pragma unroll
+                for (int e = 0; e < DV; ++e) st.o[rb][e] = st.o[rb][e] * a4;
+            }
         }
 #pragma unroll
         for (int e = 0; e < DV; ++e) {
             const u32 sel = (e & 1) ? 0x07060302u : 0x05040100u;
             const u32x2 bv = {__builtin_amdgcn_perm(pg.v[1][e >> 1], pg.v[0][e >> 1], sel),
                               __builtin_amdgcn_perm(pg.v[3][e >> 1], pg.v[2][e >> 1], sel)};
-            st.o[e] = mfma16(ph, bv, st.o[e]);
-            st.o[e] = mfma16(pl, bv, st.o[e]);
+#pragma unroll
+            for (int rb = 0; rb < RB; ++rb) {
+                st.o[rb][e] = mfma16(ph[rb], bv, st.o[rb][e]);
+                st.o[rb][e] = mfma16(pl[rb], bv, st.o[rb][e]);
+            }
         }
     }
 
-    // q rows as the score MFMA's B operand (rows >= G are zero).
-    __device__ static void load_q(u32x4 (&qa)[NS], const u16* q, i64 qs) {
+    // q rows as the score MFMA's B operand, row block rb in qa[rb*NS ..]
+    // (rows >= G are zero).
+    __device__ static void load_q(u32x4 (&qa)[NQ], const u16* q, i64 qs) {
         const int lane = threadIdx.x & 63, t = lane & 15, grp = lane >> 4;
 #pragma unroll
-        for (int j = 0; j < NS; ++j) {
-            qa[j] = u32x4{0u, 0u, 0u, 0u};
-            if (t < G) qa[j] = *reinterpret_cast<const u32x4*>(q + t * qs + 32 * j + 8 * grp);
+        for (int rb = 0; rb < RB; ++rb) {
+#pragma unroll
+            for (int j = 0; j < NS; ++j) {
+                qa[rb * NS + j] = u32x4{0u, 0u, 0u, 0u};
+                if (16 * rb + t < G) qa[rb * NS + j] = *reinterpret_cast<const u32x4*>(q + (16 * rb + t) * qs + 32 * j + 8 * grp);
+            }
         }
     }
 
     __device__ static void init(State& st) {
-        st.m = -__builtin_inff();
-        st.l = 0.0f;
 #pragma unroll
-        for (int e = 0; e < DV; ++e) st.o[e] = f32x4v_t{0.0f, 0.0f, 0.0f, 0.0f};
+        for (int rb = 0; rb < RB; ++rb) {
+            st.m[rb] = -__builtin_inff();
+            st.l[rb] = 0.0f;
+#pragma unroll
+            for (int e = 0; e < DV; ++e) st.o[rb][e] = f32x4v_t{0.0f, 0.0f, 0.0f, 0.0f};
+        }
     }
 
     // Writes st as a partial.  The stores carry sc1, the cache policy of the
@@ -1356,20 +1380,23 @@ struct DecodeWave {
     // (row, c).
     __device__ static void store(const State& st, float* part) {
         const int lane = threadIdx.x & 63, t = lane & 15, grp = lane >> 4;
-        if (grp == 0 && t < G) {
-            coherent_store(part + kPartM + t, st.m);
-            coherent_store(part + kPartM + G + t, st.l);
-        }
         const buf_rsrc rp = __builtin_amdgcn_make_buffer_rsrc(part, 0, -1, 0x00020000);
 #pragma unroll
-        for (int j = 0; j < 4; ++j) {
-            const int g = 4 * grp + j;
-            if (g < G) {
+        for (int rb = 0; rb < RB; ++rb) {
+            if (grp == 0 && 16 * rb + t < G) {
+                coherent_store(part + kPartM + 16 * rb + t, st.m[rb]);
+                coherent_store(part + kPartM + G + 16 * rb + t, st.l[rb]);
+            }
 #pragma unroll
-                for (int c = 0; c < DV / 4; ++c) {
-                    const u32x4 w = {__float_as_uint(st.o[4 * c][j]), __float_as_uint(st.o[4 * c + 1][j]),
-                                     __float_as_uint(st.o[4 * c + 2][j]), __float_as_uint(st.o[4 * c + 3][j])};
-                    __builtin_amdgcn_raw_buffer_store_b128(w, rp, static_cast<u32>((g * D + 64 * c + 4 * t) * 4), 0, 16);
+            for (int j = 0; j < 4; ++j) {
+                const int g = 16 * rb + 4 * grp + j;
+                if (g < G) {
+#pragma unroll
+                    for (int c = 0; c < DV / 4; ++c) {
+                        const u32x4 w = {__float_as_uint(st.o[rb][4 * c][j]), __float_as_uint(st.o[rb][4 * c + 1][j]),
+                                         __float_as_uint(st.o[rb][4 * c + 2][j]), __float_as_uint(st.o[rb][4 * c + 3][j])};
+                        __builtin_amdgcn_raw_buffer_store_b128(w, rp, static_cast<u32>((g * D + 64 * c + 4 * t) * 4), 0, 16);
+                    }
                 }
             }
         }
@@ -1600,16 +1627,16 @@ struct DecodeStream {
         if (eu > b) eu = b;
         typename DW::State st;
         DW::init(st);
-        u32x4 qa[DW::NS], qn[DW::NS];
+        u32x4 qa[DW::NQ], qn[DW::NQ];
         // A q tile out of range (error already flagged) folds with q = 0;
         // every step runs, so that its page waits order the partial stores.
-        auto get_q = [&](u32x4 (&dst)[DW::NS], int unit) {
+        auto get_q = [&](u32x4 (&dst)[DW::NQ], int unit) {
             const u16* qp = f.q(unit);
             if (qp) {
                 DW::load_q(dst, qp, qs);
             } else {
 #pragma unroll
-                for (int j = 0; j < DW::NS; ++j) dst[j] = u32x4{0u, 0u, 0u, 0u};
+                for (int j = 0; j < DW::NQ; ++j) dst[j] = u32x4{0u, 0u, 0u, 0u};
             }
         };
         get_q(qa, u);
@@ -1653,7 +1680,7 @@ struct DecodeStream {
                     if (eu > b) eu = b;
                     DW::init(st);
 #pragma unroll
-                    for (int j = 0; j < DW::NS; ++j) qa[j] = qn[j];
+                    for (int j = 0; j < DW::NQ; ++j) qa[j] = qn[j];
                     if (eu < b) {
                         un = next_unit(pre, u);
                         get_q(qn, un);

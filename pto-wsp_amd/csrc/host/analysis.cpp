@@ -355,8 +355,11 @@ DecodeInfo classify_decode(const KernelDef& k, const KernelAnalysis& a) {
     }
     // Device template shapes: pages of 8, 16, 32, 64 or 128 tokens (folded as 16-token
     // steps: larger pages as 16-token sub-pages, 8-token pages two to a step),
-    // up to 16 query rows (one MFMA row block), head dim 64 / 128 / 256.
-    if ((PG != 8 && PG != 16 && PG != 32 && PG != 64 && PG != 128) || G < 1 || G > 16 ||
+    // head dim 64 / 128 / 256, query rows in blocks of 16 (one MFMA row block
+    // each) up to what the wave's registers hold beside its page ring: 48
+    // rows at head dim 64 or 128, 16 at 256.
+    const int max_rows = D == 256 ? 16 : 48;
+    if ((PG != 8 && PG != 16 && PG != 32 && PG != 64 && PG != 128) || G < 1 || G > max_rows ||
         (D != 64 && D != 128 && D != 256))
         return info;
     info.ok = true;

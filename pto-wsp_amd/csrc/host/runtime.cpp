@@ -470,11 +470,18 @@ struct Tuning {
 // twice the registers, and a 4-step ring spills to scratch (0.75 ms against
 // 0.41 ms with 2 steps on the C5 shape with head dim 256); 2 steps keep the
 // same bytes in flight.
-int decode_ring_for(int head_dim) { return head_dim >= 256 ? 2 : head_dim <= 64 ? 3 : 4; }
+// More than 16 query rows add a block of accumulators and q registers per
+// 16 rows: 33-48 rows at head dim 128 leave room for 2 steps.
+int decode_ring_for(int head_dim, int rows) {
+    if (head_dim >= 256) return 2;
+    if (head_dim <= 64) return rows <= 16 ? 3 : 4;
+    return rows <= 32 ? 4 : 2;
+}
 // Waves per decode block (per CU).  At head dim 64 a step is 4 KiB of K and
 // V, and one wave per SIMD cannot cover the fold's latency chain with it;
-// two waves per SIMD (3-step rings, half the registers each) can.
-int decode_waves_for(int head_dim) { return head_dim <= 64 ? 8 : 4; }
+// two waves per SIMD (3-step rings, half the registers each) can, up to 16
+// query rows.
+int decode_waves_for(int head_dim, int rows) { return head_dim <= 64 && rows <= 16 ? 8 : 4; }
 
 const Tuning& tuning() {
     static const Tuning t = [] {
@@ -1009,8 +1016,8 @@ BuiltLaunch build_launch(RunEnv& E, const LaunchSpec& L) {
     }
     B.spec.decode = decode_allowed(a, L, A, B.spec, ng);
     B.spec.row_loops = tuning().row_loops && row_loops_allowed(a, L, A, B.spec, ng, nvars);
-    B.spec.decode_ring = tuning().decode_ring ? tuning().decode_ring : decode_ring_for(a.decode.d);
-    B.spec.decode_waves = tuning().decode_waves ? tuning().decode_waves : decode_waves_for(a.decode.d);
+    B.spec.decode_ring = tuning().decode_ring ? tuning().decode_ring : decode_ring_for(a.decode.d, a.decode.g);
+    B.spec.decode_waves = tuning().decode_waves ? tuning().decode_waves : decode_waves_for(a.decode.d, a.decode.g);
     B.spec.decode_ordered = tuning().decode_ordered;
     B.spec.vec_width = a.family == Family::RowProgram ? pick_vec_width(a, A, nvars) : 1;
     B.spec.threads = tuning().tile_threads;
@@ -1724,8 +1731,8 @@ int ptowsp_hip_precompile(ptowsp_program* P, int index, int flags, const char** 
             spec.nontemporal = tuning().nontemporal;
             spec.gemm = a.family == Family::Gemm && !spec.serial;
             spec.decode = a.family == Family::Decode && !spec.serial && L.inner.size() == 1;
-            spec.decode_ring = tuning().decode_ring ? tuning().decode_ring : decode_ring_for(a.decode.d);
-            spec.decode_waves = tuning().decode_waves ? tuning().decode_waves : decode_waves_for(a.decode.d);
+            spec.decode_ring = tuning().decode_ring ? tuning().decode_ring : decode_ring_for(a.decode.d, a.decode.g);
+            spec.decode_waves = tuning().decode_waves ? tuning().decode_waves : decode_waves_for(a.decode.d, a.decode.g);
             spec.decode_ordered = tuning().decode_ordered;
             spec.decode_norm = spec.decode && (flags & 32) != 0;
             spec.indirect_count.assign(L.targs.size(), 0);

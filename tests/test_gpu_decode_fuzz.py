@@ -1,7 +1,7 @@
 """Random paged-decode launches against the oracle.
 
-Each seed draws the query rows per KV head (1..16), the head dim (64, 128,
-256), the KV heads, 1..24 sequences whose lengths
+Each seed draws the query rows per KV head (1..16, or 17..48 at head dim 64
+and 128 for a fifth of the seeds), the head dim (64, 128, 256), the KV heads, 1..24 sequences whose lengths
 mix empty, sub-page, exact-page and multi-thousand-token sequences, the page
 size (8, 16, 32, 64: the streaming decode family, which folds pages of more
 than 16 tokens as 16-token sub-pages and 8-token pages two to a 16-token
@@ -25,6 +25,8 @@ pytestmark = pytest.mark.gpu
 def _case(seed):
     rng = np.random.default_rng(seed)
     group, d = int(rng.integers(1, 17)), int(rng.choice([64, 128, 256]))
+    if d < 256 and rng.random() < 0.2:
+        group = int(rng.integers(17, 49))  # 2 or 3 blocks of 16 query rows
     page = int(rng.choice([8, 16, 16, 16, 32, 32, 64]))
     n = int(rng.integers(1, 25))
     kinds = rng.integers(0, 4, n)

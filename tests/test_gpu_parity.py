@@ -454,10 +454,15 @@ def test_paged_decode_family(gpu, lengths, hkv, group, d):
     ([300, 77, 1, 33], 2, 16, 128, 32),          # 16 query rows at head dim 128 (a 2-pass combine)
     ([129, 40, 700], 2, 8, 256, 16),              # 8 rows at head dim 256 (2-step page ring)
     ([513, 64, 5], 1, 16, 256, 64),               # 16 rows at head dim 256 (4 passes of 4 rows)
+    ([300, 77, 1, 33], 1, 32, 128, 16),           # two 16-row blocks per step
+    ([129, 40, 700], 2, 48, 128, 8),              # three row blocks, 8-token pages, 2-step ring
+    ([513, 64, 5], 2, 24, 64, 16),                # a half-filled second row block at head dim 64
+    ([200, 17, 1000], 1, 48, 64, 32),             # three row blocks at head dim 64
 ])
 def test_paged_decode_wide_units(gpu, lengths, hkv, group, d, page):
     """Units of more than 1024 accumulators (query rows x head dim) on the decode
-    family: the completing wave folds the partials a few rows per pass."""
+    family: the completing wave folds the partials a few rows per pass; more than
+    16 query rows fold as 16-row blocks that share each step's page registers."""
     prog, ref, ga, ca = _decode_case(lengths, hkv, group, d, page=page, seed=len(lengths) + group)
     assert prog._native.kernel_family("decode_page") == "decode"
     for k in ("m", "l", "o", "out"):

@@ -183,6 +183,20 @@ def test_decode_family_page_sizes(page, family):
         assert ("vp_ %" in src) == (page > 16)
 
 
+@pytest.mark.parametrize("group, d, family", [(48, 128, "decode"), (49, 128, "tile_program"), (48, 64, "decode"),
+                                           (16, 256, "decode"), (17, 256, "tile_program"), (32, 128, "decode")])
+def test_decode_family_query_rows(group, d, family):
+    """Up to 48 query rows per KV head at head dims 64 and 128 (blocks of 16 rows that
+    share each step's pages), 16 at head dim 256; wider units stay on the tile program."""
+    from pto_wsp._hip import NativeProgram
+
+    arrs = W.paged_decode_arrays([40, 300], 1, group, d, page=64)
+    prog = NativeProgram(workload_to_codegen_ir(W.rr4(W.paged_decode(arrs)), "d").module)
+    assert prog.kernel_family("decode_page") == family
+    if family == "decode":
+        assert f"DecodeWave<{group}, {d}, false, true, false>" in prog.precompile(0)
+
+
 def test_decode_precompile_folded_normalisation():
     """precompile(decode_norm=True) emits the form a run uses when `out = o / l`
     follows the decode launch: the completion writes out, and units without pages
