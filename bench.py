@@ -29,6 +29,7 @@ for _p in (os.path.join(ROOT, "pto-wsp_amd"), ROOT):
 
 HBM_PEAK_GBS = 8000.0          # MI355X HBM3E
 BF16_PEAK_TFLOPS = 2500.0      # MI355X dense bf16 MFMA
+F32_PEAK_TFLOPS = 157.3        # MI355X dense fp32 MFMA
 METRIC = "GB/s & TFLOP/s as % of MI355X roofline per config, 1 GPU, vs cpu_sim wall"
 HEADLINE = "rmsnorm_bw"
 
@@ -83,11 +84,12 @@ def row_workload(kind, X, Y):
     return rr4(wl())
 
 
-def bgemm_workload(A, Bm, C, tm=128, tn=128, tk=64):
-    """examples/bgemm pattern: C[b] += A[b] @ B[b] with a P.seq K loop and an InOut fp32 tile."""
+def bgemm_workload(A, Bm, C, tm=128, tn=128, tk=64, f32_inputs=False):
+    """examples/bgemm pattern: C[b] += A[b] @ B[b] with a P.seq K loop and an InOut fp32 tile
+    (bf16 A / B, or f32 with f32_inputs)."""
     from pto_wsp import DType, Dense, In, InOut, P, Tensor, Tile, kernel, pto, workload
 
-    bf16, f32 = DType.BF16, DType.F32
+    bf16, f32 = (DType.F32 if f32_inputs else DType.BF16), DType.F32
     nb, M, K = tuple(A.shape)
     N = Bm.shape[2]
 
@@ -451,32 +453,35 @@ class RowCase:
 
 
 class GemmCase:
-    unit, bound, dtype = "TFLOP/s", "mfma", "bf16"
+    unit, bound = "TFLOP/s", "mfma"
 
-    def __init__(self, name, nb, m, n, k, seed, baseline_config):
+    def __init__(self, name, nb, m, n, k, seed, baseline_config, f32_inputs=False):
         self.name, self.nb, self.m, self.n, self.k, self.seed = name, nb, m, n, k, seed
         self.baseline_config = baseline_config
         self.shape = (nb, m, k)
+        self.f32_inputs = f32_inputs
+        self.dtype = "f32" if f32_inputs else "bf16"
 
     def setup(self, dev):
         import torch
 
         g = torch.Generator(device=dev)
         g.manual_seed(self.seed)
-        self.a = (torch.rand((self.nb, self.m, self.k), generator=g, device=dev) * 2 - 1).to(torch.bfloat16)
-        self.b = (torch.rand((self.nb, self.k, self.n), generator=g, device=dev) * 2 - 1).to(torch.bfloat16)
+        dt = torch.float32 if self.f32_inputs else torch.bfloat16
+        self.a = (torch.rand((self.nb, self.m, self.k), generator=g, device=dev) * 2 - 1).to(dt)
+        self.b = (torch.rand((self.nb, self.k, self.n), generator=g, device=dev) * 2 - 1).to(dt)
         self.c = torch.zeros((self.nb, self.m, self.n), device=dev, dtype=torch.float32)
-        self.prog = bgemm_workload(self.a, self.b, self.c).compile(target="hip_gfx950")
+        self.prog = bgemm_workload(self.a, self.b, self.c, f32_inputs=self.f32_inputs).compile(target="hip_gfx950")
         self.work = 2.0 * self.nb * self.m * self.n * self.k  # FLOP per step
 
     def peak(self):
-        return BF16_PEAK_TFLOPS
+        return F32_PEAK_TFLOPS if self.f32_inputs else BF16_PEAK_TFLOPS
 
     def rate(self, seconds):
         return self.work / seconds / 1e12
 
     def describe(self):
-        return (f"{self.name}: C[b] += A[b] @ B[b], A,B[{self.nb},{self.m},{self.k}] bf16 U(-1,1), C fp32, "
+        return (f"{self.name}: C[b] += A[b] @ B[b], A,B[{self.nb},{self.m},{self.k}] {self.dtype} U(-1,1), C fp32, "
                 "tiles 128x128 K-step 64, P(batch) x P(m_tiles) x P(n_tiles) x P.seq(k)")
 
     def cpu(self, budget_s):
@@ -488,11 +493,14 @@ class GemmCase:
         del budget_s
         import torch
 
-        a0 = self.a[:1, :256].contiguous().view(torch.int16).cpu().numpy().view(np.uint16)
-        b0 = self.b[:1].contiguous().view(torch.int16).cpu().numpy().view(np.uint16)
+        if self.f32_inputs:
+            a0, b0 = self.a[:1, :256].contiguous().cpu().numpy(), self.b[:1].contiguous().cpu().numpy()
+        else:
+            a0 = self.a[:1, :256].contiguous().view(torch.int16).cpu().numpy().view(np.uint16)
+            b0 = self.b[:1].contiguous().view(torch.int16).cpu().numpy().view(np.uint16)
         c0 = np.zeros((1, 256, self.n), np.float32)
         t0 = time.perf_counter()
-        run_workload(bgemm_workload(a0, b0, c0))
+        run_workload(bgemm_workload(a0, b0, c0, f32_inputs=self.f32_inputs))
         sec = time.perf_counter() - t0
         flop = 2.0 * 256 * self.n * self.k
         # GPU result for the same tiles, from a fresh C = 0 run.
@@ -534,9 +542,12 @@ CASES = {
     "paged_decode_d256": lambda: DecodeCase("paged_decode_d256", 64, 32, 8, 256, 512, 8192, 0, None),
     "paged_decode_g16": lambda: DecodeCase("paged_decode_g16", 64, 128, 8, 128, 512, 8192, 0, None, page=32),
     "paged_decode_g32": lambda: DecodeCase("paged_decode_g32", 64, 256, 8, 128, 512, 8192, 0, None),
+    # Not a BASELINE config: the C4 GEMM with f32 A and B (the reference's own
+    # matmul dtype), on the f32 MFMA block.
+    "bgemm_f32": lambda: GemmCase("bgemm_f32", 64, 2048, 2048, 2048, 0, None, f32_inputs=True),
 }
 EXTRA = ("copy_calib", "softmax3", "softmax3_overlap", "paged_decode_page32", "paged_decode_page64", "paged_decode_page8",
-         "paged_decode_d64", "paged_decode_d256", "paged_decode_g16", "paged_decode_g32")
+         "paged_decode_d64", "paged_decode_d256", "paged_decode_g16", "paged_decode_g32", "bgemm_f32")
 
 
 def load_traffic(name):

@@ -362,6 +362,7 @@ typedef short s16x4 __attribute__((ext_vector_type(4)));
 typedef __bf16 bf16x8 __attribute__((ext_vector_type(8)));
 typedef _Float16 f16x8 __attribute__((ext_vector_type(8)));
 typedef float f32x16 __attribute__((ext_vector_type(16)));
+typedef float f32x4v_t __attribute__((ext_vector_type(4)));
 typedef __amdgpu_buffer_rsrc_t buf_rsrc;
 
 template <bool F16>
@@ -620,6 +621,142 @@ struct GemmBlock {
             mma(acc, lds + static_cast<int>(st & (NS - 1)) * STAGE);
         }
         c_out<ACC>(acc, rc, ldc);
+    }
+};
+
+// ---------------------------------------------------------------------------
+// f32 GEMM block: f32 A and B on v_mfma_f32_32x32x2_f32
+// ---------------------------------------------------------------------------
+//
+// The block structure of GemmBlock (NS-stage LDS ring filled by direct
+// buffer->LDS loads, waves WM x WN over the C block, 32x32 accumulators in
+// the same layout, so the C epilogue is GemmBlock's) with 4-byte elements.
+// A stage holds A as [BM][BK] and B as [BK][BN], row-major, in 16-byte
+// chunks: A's chunks XOR-swizzled by row as in GemmBlock (every lane of a
+// half-wave reads the same chunk of 32 rows), B's 128-byte halves swapped on
+// rows whose bit 2 is set (the two half-waves read rows k and k+4 of the
+// same columns).
+//
+// v_mfma_f32_32x32x2_f32 takes one A and one B value per lane: lane l
+// supplies A[i = l%32][k = l/32] and B[k = l/32][j = l%32].  The K order of
+// a product is free, so for the 8 columns kk..kk+7 half-wave h reads
+// A[m][kk+4h .. +3] as one 16-byte chunk, and MFMA q (0..3) pairs column
+// kk+q (half 0) with kk+4+q (half 1).
+template <int BM, int BN, int BK, int WM, int WN, int NS = 2, int KSPLIT = 1>
+struct GemmF32 {
+    static constexpr int NW = WM * WN, NT = 64 * NW;
+    static constexpr int TM = BM / WM, TN = BN / WN, FI = TM / 32, FJ = TN / 32;
+    static constexpr int CH = BK / 4;                  // 16-byte chunks per A row
+    static constexpr int RPL = CH >= 8 ? 1 : 8 / CH;   // A rows per 128-byte LDS line
+    static constexpr int SWM = (CH < 8 ? CH : 8) - 1;
+    static constexpr int ARPB = 1024 / (4 * BK);       // A rows per 1 KiB load
+    static constexpr int BCPR = BN / 4;                // 16-byte chunks per B row
+    static constexpr int BRPB = 1024 / (4 * BN);       // B rows per 1 KiB load
+    static constexpr int ABLK = BM * BK * 4 / 1024, BBLK = BK * BN * 4 / 1024;
+    static constexpr int AQ = (ABLK + NW - 1) / NW, BQ = (BBLK + NW - 1) / NW;
+    static constexpr int ASZ = BM * BK, STAGE = ASZ + BK * BN;  // floats
+    static constexpr int kLdsElems = NS * STAGE * 2;            // 16-bit units (the kernel's LDS array)
+    static_assert(NS == 2, "two-stage ring");
+    static_assert(TM % 32 == 0 && TN % 32 == 0 && (BK == 16 || BK == 32), "f32 GEMM block shape");
+    static_assert(BN >= 64 && BN <= 256 && (BM * BK * 4) % 1024 == 0 && (BK * BN * 4) % 1024 == 0, "f32 GEMM block shape");
+    typedef GemmBlock<BM, BN, 16, WM, WN, false> Out;  // the C epilogue (same accumulator layout)
+    typedef typename Out::Acc Acc;
+
+    struct Offs {
+        int a[AQ];
+        int b[BQ];
+    };
+    __device__ static int swa(int m) { return ((m / RPL) ^ (m >> 3)) & SWM; }
+    __device__ static int swb(int k) { return ((k >> 2) & 1) << 3; }
+
+    // Per-lane byte offsets, from the block's A / B origin at the first K
+    // step, of the chunks this wave moves (lda / ldb: row pitch in elements).
+    __device__ static void offsets(Offs& o, int lda, int ldb) {
+        const int lane = threadIdx.x & 63, w = wave_index();
+#pragma unroll
+        for (int q = 0; q < AQ; ++q) {
+            const int m = (w * AQ + q) * ARPB + lane / CH, p = lane % CH;
+            o.a[q] = (m * lda + ((p ^ swa(m)) << 2)) * 4;
+        }
+#pragma unroll
+        for (int q = 0; q < BQ; ++q) {
+            const int k = (w * BQ + q) * BRPB + lane / BCPR, p = lane % BCPR;
+            o.b[q] = (k * ldb + ((p ^ swb(k)) << 2)) * 4;
+        }
+    }
+
+    __device__ static void load(float* stage, const Offs& o, u32x4 ra, int soa, u32x4 rb, int sob) {
+        const int w = wave_index();
+        const u32 base = lds_address(stage);
+#pragma unroll
+        for (int q = 0; q < AQ; ++q)
+            if (AQ * NW == ABLK || w * AQ + q < ABLK) dma16(ra, o.a[q], soa, base + (w * AQ + q) * 1024);
+#pragma unroll
+        for (int q = 0; q < BQ; ++q)
+            if (BQ * NW == BBLK || w * BQ + q < BBLK) dma16(rb, o.b[q], sob, base + ASZ * 4 + (w * BQ + q) * 1024);
+    }
+
+    __device__ static void mma(Acc& acc, const float* stage) {
+        const int lane = threadIdx.x & 63, wave = wave_index();
+        const int wm = wave / WN, wn = wave % WN;
+        const int r = lane & 31, h = lane >> 5;
+        const float* as = stage + (wm * TM + r) * BK;
+        const float* bs = stage + ASZ;
+#pragma unroll
+        for (int kk = 0; kk < BK; kk += 8) {
+            f32x4v_t af[FI];
+#pragma unroll
+            for (int i = 0; i < FI; ++i)
+                af[i] = *reinterpret_cast<const f32x4v_t*>(as + i * 32 * BK + ((((kk >> 2) + h) ^ swa(wm * TM + i * 32 + r)) << 2));
+#pragma unroll
+            for (int q = 0; q < 4; ++q) {
+                const int k = kk + 4 * h + q;
+                float bf[FJ];
+#pragma unroll
+                for (int j = 0; j < FJ; ++j) {
+                    const int n = wn * TN + j * 32 + r;
+                    bf[j] = bs[k * BN + ((((n >> 2) ^ swb(k)) << 2) | (n & 3))];
+                }
+#pragma unroll
+                for (int i = 0; i < FI; ++i)
+#pragma unroll
+                    for (int j = 0; j < FJ; ++j) acc.v[i][j] = __builtin_amdgcn_mfma_f32_32x32x2f32(af[i][q], bf[j], acc.v[i][j], 0, 0, 0);
+            }
+        }
+    }
+
+    // Task K steps it0 .. iters-1, as (iters-it0)*KSPLIT LDS stages (see
+    // GemmBlock::run); pa / pb point at f32 data.
+    template <bool ACC, class Off>
+    __device__ static void run(u16* lds, const u16* pa, int lda, const u16* pb, int ldb, float* pc, int ldc, i64 it0,
+                               i64 iters, Off off) {
+        float* ring = reinterpret_cast<float*>(lds);
+        const u32x4 ra = buffer_words(pa), rb = buffer_words(pb);
+        const buf_rsrc rc = __builtin_amdgcn_make_buffer_rsrc(pc, 0, -1, 0x00020000);
+        Offs o;
+        offsets(o, lda, ldb);
+        Acc acc;
+#pragma unroll
+        for (int i = 0; i < FI; ++i)
+#pragma unroll
+            for (int j = 0; j < FJ; ++j) acc.v[i][j] = f32x16{};
+        const i64 nst = (iters - it0) * KSPLIT;
+        auto issue = [&](i64 st) {
+            int soa, sob;
+            off(it0 + st / KSPLIT, soa, sob);
+            const int hs = static_cast<int>(st % KSPLIT);
+            load(ring + static_cast<int>(st & 1) * STAGE, o, ra, soa + hs * BK * 4, rb, sob + hs * BK * ldb * 4);
+        };
+        wait_vmcnt<0>();
+        __syncthreads();  // the previous block's last stage reads are done
+        if (nst > 0) issue(0);
+        for (i64 st = 0; st < nst; ++st) {
+            wait_vmcnt<0>();
+            __syncthreads();
+            if (st + 1 < nst) issue(st + 1);
+            mma(acc, ring + static_cast<int>(st & 1) * STAGE);
+        }
+        Out::template c_out<ACC>(acc, rc, ldc);
     }
 };
 
@@ -1065,7 +1202,6 @@ struct GemmPingPong {
 //    16-bit parts), lane l supplying tokens 4*(l/16)..+3 of every page for
 //    head dims (D/16)*(l%16)+e and accumulating query rows 4*(l/16)..+3.
 
-typedef float f32x4v_t __attribute__((ext_vector_type(4)));
 
 template <bool F16>
 __device__ inline f32x4v_t mfma_16x16x32(u32x4 a, u32x4 b, f32x4v_t c) {

@@ -160,14 +160,16 @@ GemmInfo classify_gemm(const KernelDef& k, const KernelAnalysis& a) {
     const ValueInfo* va = a.by_id[k.params[pa].id];
     const ValueInfo* vb = a.by_id[k.params[pb].id];
     const ValueInfo* vc = a.by_id[k.params[pc].id];
-    if (va->dtype != vb->dtype || (va->dtype != DType::BF16 && va->dtype != DType::F16)) return g;
+    if (va->dtype != vb->dtype || (va->dtype != DType::BF16 && va->dtype != DType::F16 && va->dtype != DType::F32)) return g;
     if (vc->dtype != DType::F32) return g;
     const int M = va->rows, K = va->cols, N = vb->cols;
+    const bool f32 = va->dtype == DType::F32;
     // MFMA block shapes: 64..256 rows / columns, K step a power of two in 16..128,
-    // two LDS stages of A and B within 160 KiB.
+    // two LDS stages of A and B within 160 KiB (f32: stages of at most 32 K
+    // columns, gemm_stage_k).
     if (M % 64 || N % 64 || M > 256 || N > 256) return g;
     if (K != 16 && K != 32 && K != 64 && K != 128) return g;
-    if (2 * (M + N) * K * 2 > 160 * 1024) return g;
+    if (2 * (M + N) * gemm_stage_k(K, f32) * (f32 ? 4 : 2) > 160 * 1024) return g;
     g.ok = true;
     g.a = a.tensor_ordinal[pa];
     g.b = a.tensor_ordinal[pb];
@@ -176,6 +178,7 @@ GemmInfo classify_gemm(const KernelDef& k, const KernelAnalysis& a) {
     g.n = N;
     g.k = K;
     g.f16 = va->dtype == DType::F16;
+    g.f32 = f32;
     return g;
 }
 

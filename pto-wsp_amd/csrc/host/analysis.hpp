@@ -22,11 +22,17 @@ enum class RowClass { None, Full, RowVec, RowVecT, ColVec, ColVecT, Scalar };
 
 // A kernel of the form  acc = matmul(a, b); [out = add(c, acc);] store(c, out|acc)
 // with bf16/f16 a, b and an fp32 c: runs on MFMA with the accumulator on chip.
+// K columns per LDS stage of a GEMM block: the task's K step; f32 A / B
+// stages hold at most 32 columns (a task step of 64 or 128 is split over 2
+// or 4 stages).
+inline int gemm_stage_k(int k, bool f32) { return f32 && k > 32 ? 32 : k; }
+
 struct GemmInfo {
     bool ok = false;
     int a = -1, b = -1, c = -1;  // tensor ordinals
     int m = 0, n = 0, k = 0;
     bool f16 = false;
+    bool f32 = false;            // f32 A and B (v_mfma_f32_32x32x2_f32)
     bool accumulate = false;     // c + a@b (InOut accumulator) instead of a@b
 };
 

@@ -877,16 +877,19 @@ EmittedKernel emit_gemm(const Module& m, const KernelAnalysis& a, const LaunchSp
     // One LDS stage per task K step, two stages (a 4-stage ring of 32-wide
     // stages measured slower on 256x256 blocks: twice the barriers).
     const int wm = gemm_waves_m(), wn = gemm_waves_n(bn);
-    const int bk = g.k, ns = 2, ksplit = 1;
+    // f32 A / B: stages of at most 32 K columns (GemmF32), a task K step
+    // split over ksplit stages; element size es bytes.
+    const int bk = gemm_stage_k(g.k, g.f32), ns = 2, ksplit = g.k / bk, es = g.f32 ? 4 : 2;
     // Ping-pong block: 256x256, K step 32 / 64, row pitches checked on the host.
-    const bool pp = spec.gemm_pingpong && bm == 256 && bn == 256 && (bk == 64 || bk == 32);
+    const bool pp = !g.f32 && spec.gemm_pingpong && bm == 256 && bn == 256 && (bk == 64 || bk == 32);
     EmittedKernel ek;
     ek.threads = 64 * wm * wn;
     ek.row_program = false;
     ek.tasks_per_block = fm * fn;
     std::ostringstream o;
     o << "#include \"ptowsp_device.h\"\nusing namespace ptowsp;\n";
-    o << "// gemm program: kernel " << k.name << ", task tile " << g.m << "x" << g.n << "x" << g.k << (g.f16 ? " f16" : " bf16")
+    o << "// gemm program: kernel " << k.name << ", task tile " << g.m << "x" << g.n << "x" << g.k
+      << (g.f32 ? " f32" : g.f16 ? " f16" : " bf16")
       << (g.accumulate ? ", accumulate" : "") << "; block " << bm << "x" << bn << " (" << fm * fn << " tasks)"
       << (pp ? ", ping-pong" : "") << "\n";
     ek.entry = entry_name("gemm", k);
@@ -894,6 +897,9 @@ EmittedKernel emit_gemm(const Module& m, const KernelAnalysis& a, const LaunchSp
       << ek.entry << "(const LaunchArgs A) {\n";
     if (pp)
         o << "  typedef GemmPingPong<" << bk << ", " << (g.f16 ? "true" : "false") << "> GB;\n";
+    else if (g.f32)
+        o << "  typedef GemmF32<" << bm << ", " << bn << ", " << bk << ", " << wm << ", " << wn << ", " << ns << ", " << ksplit
+          << "> GB;\n";
     else
         o << "  typedef GemmBlock<" << bm << ", " << bn << ", " << bk << ", " << wm << ", " << wn << ", "
           << (g.f16 ? "true" : "false") << ", " << ns << ", " << ksplit << "> GB;\n";
@@ -916,16 +922,18 @@ EmittedKernel emit_gemm(const Module& m, const KernelAnalysis& a, const LaunchSp
     for (int i = 0; i < ni; ++i) o << "    iters *= A.ext[" << ng + i << "];\n";
     o << "    if (iters <= 0) return;\n";
     for (int i = 0; i < ni; ++i) o << "    vars[" << ng + i << "] = 0;\n";
-    o << "    const u16* pa = reinterpret_cast<const u16*>(A.base[" << g.a << "] + (" << offset_expr(g.a, nvars, 0, 0) << ") * 2);\n";
-    o << "    const u16* pb = reinterpret_cast<const u16*>(A.base[" << g.b << "] + (" << offset_expr(g.b, nvars, 0, 0) << ") * 2);\n";
+    o << "    const u16* pa = reinterpret_cast<const u16*>(A.base[" << g.a << "] + (" << offset_expr(g.a, nvars, 0, 0) << ") * " << es
+      << ");\n";
+    o << "    const u16* pb = reinterpret_cast<const u16*>(A.base[" << g.b << "] + (" << offset_expr(g.b, nvars, 0, 0) << ") * " << es
+      << ");\n";
     // The output view does not move with the in-kernel loops (checked on the host).
     o << "    float* pc = reinterpret_cast<float*>(A.base[" << g.c << "] + (" << offset_expr(g.c, nvars, 0, 0) << ") * 4);\n";
     // Byte offsets of in-kernel iteration `it` from iteration 0 (mixed radix over the inner loops).
     if (ni == 1) {
         // One in-kernel loop: 32-bit byte steps (the host bounds every
         // offset below 2^31).
-        o << "    const int da_ = static_cast<int>(A.coef[" << g.a << "][" << ng << "] * 2), db_ = static_cast<int>(A.coef[" << g.b
-          << "][" << ng << "] * 2);\n";
+        o << "    const int da_ = static_cast<int>(A.coef[" << g.a << "][" << ng << "] * " << es << "), db_ = static_cast<int>(A.coef["
+          << g.b << "][" << ng << "] * " << es << ");\n";
         o << "    auto off = [=](i64 it, int& soa, int& sob) { soa = static_cast<int>(it) * da_; sob = static_cast<int>(it) * db_; };\n";
     } else {
         o << "    auto off = [&](i64 it, int& soa, int& sob) {\n";
@@ -935,7 +943,7 @@ EmittedKernel emit_gemm(const Module& m, const KernelAnalysis& a, const LaunchSp
             o << "      { const i64 x = it % A.ext[" << v << "]; it /= A.ext[" << v << "]; oa += A.coef[" << g.a << "][" << v
               << "] * x; ob += A.coef[" << g.b << "][" << v << "] * x; }\n";
         }
-        o << "      soa = static_cast<int>(oa * 2); sob = static_cast<int>(ob * 2);\n";
+        o << "      soa = static_cast<int>(oa * " << es << "); sob = static_cast<int>(ob * " << es << ");\n";
         o << "    };\n";
     }
     if (pp) {
@@ -954,7 +962,7 @@ EmittedKernel emit_gemm(const Module& m, const KernelAnalysis& a, const LaunchSp
       << (g.accumulate ? "0" : "iters - 1") << ", iters, off" << (pp ? ", pfa_row, pfb_row" : "") << ");\n";
     o << "  }\n}\n";
     ek.source = o.str();
-    ek.lds_bytes = pp ? static_cast<size_t>((bk == 64 ? 2 : 4) * 512 * bk * 2 + 256) : static_cast<size_t>(ns * (bm + bn) * bk * 2);
+    ek.lds_bytes = pp ? static_cast<size_t>((bk == 64 ? 2 : 4) * 512 * bk * 2 + 256) : static_cast<size_t>(ns * (bm + bn) * bk * es);
     return ek;
 }
 

@@ -613,12 +613,14 @@ bool gemm_allowed(const KernelAnalysis& a, const LaunchSpec& L, const LaunchArgs
     for (int t : spec.inner_dyn_term)
         if (t >= 0) return false;
     const GemmInfo& g = a.gemm;
+    // Element size of A / B, and elements per 16-byte chunk of the direct loads.
+    const int64_t es = g.f32 ? 4 : 2, epc = 16 / es;
     if (A.s4[g.a] != 1 || A.s4[g.b] != 1 || A.s4[g.c] != 1) return false;
     if (reinterpret_cast<uintptr_t>(A.base[g.a]) % 16 || reinterpret_cast<uintptr_t>(A.base[g.b]) % 16) return false;
     if (reinterpret_cast<uintptr_t>(A.base[g.c]) % 4) return false;
-    if (A.s3[g.a] % 8 || A.s3[g.b] % 8) return false;
+    if (A.s3[g.a] % epc || A.s3[g.b] % epc) return false;
     for (int v = 0; v < nvars; ++v) {
-        if (A.coef[g.a][v] % 8 || A.coef[g.b][v] % 8) return false;
+        if (A.coef[g.a][v] % epc || A.coef[g.b][v] % epc) return false;
         if (v >= ng && A.coef[g.c][v] != 0) return false;
         if (v >= ng && (A.coef[g.a][v] < 0 || A.coef[g.b][v] < 0)) return false;
     }
@@ -633,7 +635,9 @@ bool gemm_allowed(const KernelAnalysis& a, const LaunchSpec& L, const LaunchArgs
         else if (spec.gemm_vn < 0 && A.coef[g.b][v] == N && A.coef[g.c][v] == N && A.coef[g.a][v] == 0)
             spec.gemm_vn = v;
     }
-    auto lds_fits = [&](int64_t bm, int64_t bn) { return bm <= 256 && bn <= 256 && 2 * (bm + bn) * g.k * 2 <= 160 * 1024; };
+    auto lds_fits = [&](int64_t bm, int64_t bn) {
+        return bm <= 256 && bn <= 256 && 2 * (bm + bn) * gemm_stage_k(g.k, g.f32) * es <= 160 * 1024;
+    };
     if (spec.gemm_vm >= 0 && spec.gemm_vn >= 0 && !lds_fits(2 * M, 2 * N)) spec.gemm_vm = -1;
     if (spec.gemm_vm >= 0 && !lds_fits(2 * M, spec.gemm_vn >= 0 ? 2 * N : N)) spec.gemm_vm = -1;
     if (spec.gemm_vn >= 0 && !lds_fits(spec.gemm_vm >= 0 ? 2 * M : M, 2 * N)) spec.gemm_vn = -1;
@@ -646,10 +650,10 @@ bool gemm_allowed(const KernelAnalysis& a, const LaunchSpec& L, const LaunchArgs
     }
     const int64_t lim = int64_t(1) << 31;
     if (A.s3[g.a] >= lim || A.s3[g.b] >= lim || A.s3[g.c] >= lim) return false;
-    if (((bm - 1) * A.s3[g.a] + g.k) * 2 + ka * 2 >= lim) return false;
-    if (((g.k - 1) * A.s3[g.b] + bn) * 2 + kb * 2 >= lim) return false;
+    if (((bm - 1) * A.s3[g.a] + g.k) * es + ka * es >= lim) return false;
+    if (((g.k - 1) * A.s3[g.b] + bn) * es + kb * es >= lim) return false;
     if (((bm - 1) * A.s3[g.c] + bn) * 4 >= lim) return false;
-    spec.gemm_pingpong = tuning().gemm_pingpong && bm == 256 && bn == 256 && (g.k == 64 || g.k == 32) &&
+    spec.gemm_pingpong = tuning().gemm_pingpong && !g.f32 && bm == 256 && bn == 256 && (g.k == 64 || g.k == 32) &&
                          A.s3[g.a] % 64 == 0 && A.s3[g.b] % 64 == 0;
     return true;
 }

@@ -3,7 +3,8 @@
 Each seed draws a task tile (tm, tn in {64, 128, 256}, tk in {16, 32, 64,
 128}, within the LDS budget of the GEMM family), a batch, tile counts along
 M, N and K (odd counts leave the 2x2 block merge half used or off), the
-input dtype (f16 / bf16), the InOut accumulate form or the plain store, the
+input dtype (f16 / bf16, or f32 for about a third of the seeds: the f32
+block on v_mfma_f32_32x32x2_f32), the InOut accumulate form or the plain store, the
 order of the m and n loops, and seeded inputs with a random initial C.  The
 GPU result must equal the oracle's within a relative Frobenius error of 1e-5
 (both accumulate exact products in fp32, in different orders), with equal
@@ -27,14 +28,16 @@ def _case(seed):
         tk = int(rng.choice([16, 32, 64, 128]))
         if 2 * (tm + tn) * tk * 2 <= 160 * 1024:
             break
-    return dict(tm=tm, tn=tn, tk=tk, B=int(rng.integers(1, 3)), mt=int(rng.integers(1, 5)), nt=int(rng.integers(1, 5)),
-                kt=int(rng.integers(1, 6)), f16=bool(rng.random() < 0.5), plain=bool(rng.random() < 0.25),
-                n_outer=bool(rng.random() < 0.3))
+    c = dict(tm=tm, tn=tn, tk=tk, B=int(rng.integers(1, 3)), mt=int(rng.integers(1, 5)), nt=int(rng.integers(1, 5)),
+             kt=int(rng.integers(1, 6)), f16=bool(rng.random() < 0.5), plain=bool(rng.random() < 0.25),
+             n_outer=bool(rng.random() < 0.3))
+    c["f32"] = bool(rng.random() < 0.35)
+    return c
 
 
 def _workload(c, arrs):
     tm, tn, tk = c["tm"], c["tn"], c["tk"]
-    dt = W.F16 if c["f16"] else W.BF16
+    dt = W.F32 if c["f32"] else W.F16 if c["f16"] else W.BF16
     a, b_, cc = arrs["a"], arrs["b"], arrs["c"]
     B, M, K = a.shape
     N = b_.shape[2]
@@ -72,7 +75,9 @@ def test_random_gemm_matches_oracle(gpu, seed):
     M, N, K = c["tm"] * c["mt"], c["tn"] * c["nt"], c["tk"] * c["kt"]
     a = rng.uniform(-1, 1, (c["B"], M, K)).astype(np.float32)
     b = rng.uniform(-1, 1, (c["B"], K, N)).astype(np.float32)
-    if c["f16"]:
+    if c["f32"]:
+        a16, b16 = a, b
+    elif c["f16"]:
         a16, b16 = a.astype(np.float16), b.astype(np.float16)
     else:
         a16, b16 = W.bf16_round(a), W.bf16_round(b)
@@ -80,6 +85,7 @@ def test_random_gemm_matches_oracle(gpu, seed):
     ga = {"a": a16.copy(), "b": b16.copy(), "c": c0.copy()}
     ca = {"a": a16.copy(), "b": b16.copy(), "c": c0.copy()}
     prog = W.rr4(_workload(c, ga)).compile(target="hip_gfx950")
+    assert prog._native.kernel_family("gemm_tile") == "gemm"
     prog.execute()
     prog.synchronize()
     ref = run_workload(W.rr4(_workload(c, ca)))

@@ -407,6 +407,37 @@ def test_bgemm_plain_store_keeps_last_k_step(gpu):
     assert _rel_fro(ga["c"][0], last) <= 1e-5
 
 
+@pytest.mark.parametrize("shape,tiles,plain", [
+    ((2, 256, 256, 512), (128, 128, 64), False),   # merged 256x256 blocks, K step 64 as two 32-column stages
+    ((1, 384, 384, 256), (128, 128, 128), False),  # odd tile counts (no merge), K step 128 as four stages
+    ((3, 256, 192, 96), (64, 64, 32), False),      # rows and columns merged into 128x128 blocks
+    ((1, 128, 256, 64), (128, 64, 16), True),      # plain store (last K step), K step 16
+    ((1, 128, 128, 64), (64, 64, 8), False),       # K step 8: below the MFMA block, tile program
+])
+def test_bgemm_f32_mfma(gpu, shape, tiles, plain):
+    """f32 x f32 -> f32 tiles (the reference's validated_matmul form) on the f32 MFMA
+    block, against the oracle and float64 (MFMA sums the same exact products in
+    another order: relative Frobenius 1e-5, the examples' rtol)."""
+    nb, m, n, k = shape
+    tm, tn, tk = tiles
+    rng = np.random.default_rng(13)
+    a = rng.uniform(-1, 1, (nb, m, k)).astype(np.float32)
+    b = rng.uniform(-1, 1, (nb, k, n)).astype(np.float32)
+    c0 = rng.standard_normal((nb, m, n)).astype(np.float32)
+    ga = {"a": a, "b": b, "c": c0.copy()}
+    ca = {"a": a.copy(), "b": b.copy(), "c": c0.copy()}
+    prog = run_hip(W.bgemm(ga, tm, tn, tk, W.F32, plain=plain))
+    ref = run_workload(W.bgemm(ca, tm, tn, tk, W.F32, plain=plain))
+    assert prog._native.kernel_family("gemm_tile") == ("tile_program" if tk < 16 else "gemm")
+    assert _rel_fro(ga["c"], ca["c"]) <= 1e-5
+    if plain:
+        exact = a[:, :, k - tk:].astype(np.float64) @ b[:, k - tk:, :].astype(np.float64)
+    else:
+        exact = c0.astype(np.float64) + a.astype(np.float64) @ b.astype(np.float64)
+    assert _rel_fro(ga["c"], exact) <= 1e-5
+    assert prog.stats.total_cycles == ref.total_cycles
+
+
 def test_bgemm_f16_mfma_device_tensors(gpu):
     import torch
 
