@@ -761,6 +761,53 @@ struct GemmF32 {
 };
 
 // ---------------------------------------------------------------------------
+// Matmul op of a tile program on the matrix cores
+// ---------------------------------------------------------------------------
+//
+// c[M][N] = a @ b for fp32 tile values (a(i, q), b(q, j): the operand
+// elements, from an LDS tile or a global param), M and N multiples of 32,
+// K even and at most 32 or a multiple of 32, on v_mfma_f32_32x32x2_f32.
+// Wave w of NT/64 computes the 32x32 output blocks w, w + NW, ...  Lane l
+// supplies A[i0 + l%32][q + l/32] and B[q + l/32][j0 + l%32]; an LDS tile
+// of A is row-major with a row pitch of K floats, so the 32 rows one MFMA
+// reads at one column would share a bank.  Each 32-column slice of the
+// block's 32 A rows is therefore copied first into the wave's scratch with
+// a row pitch of 33 floats (32 distinct banks per column).  Products are
+// exact in the MFMA; the sum runs in its order, not the scalar loop's.
+constexpr int kTileMmaPitch = 33;
+__device__ inline void wave_lds_barrier() {
+    __builtin_amdgcn_fence(__ATOMIC_RELEASE, "wavefront");
+    __builtin_amdgcn_wave_barrier();
+    __builtin_amdgcn_fence(__ATOMIC_ACQUIRE, "wavefront");
+}
+template <int M, int K, int N, int NT, class FA, class FB>
+__device__ inline void tile_mma(FA a, FB b, float* c, float* scratch) {
+    static_assert(M % 32 == 0 && N % 32 == 0 && K % 2 == 0 && (K <= 32 || K % 32 == 0) && NT % 64 == 0, "tile_mma shape");
+    constexpr int NW = NT / 64, BJ = N / 32, NB = (M / 32) * BJ, KC = K < 32 ? K : 32;
+    const int lane = threadIdx.x & 63, w = threadIdx.x >> 6, r = lane & 31, h = lane >> 5;
+    float* s = scratch + w * 32 * kTileMmaPitch;
+    for (int blk = w; blk < NB; blk += NW) {
+        const int i0 = (blk / BJ) * 32, j0 = (blk % BJ) * 32;
+        f32x16 acc = {};
+        for (int k0 = 0; k0 < K; k0 += KC) {
+            // Lanes exchange the slice through LDS, whose operations a wave
+            // performs in order; the wave barriers (wave-scope fences around
+            // the wave barrier) keep the compiler from moving the copy across
+            // the previous slice's reads or this slice's.
+            wave_lds_barrier();
+#pragma unroll
+            for (int e = lane; e < 32 * KC; e += 64) s[(e / KC) * kTileMmaPitch + e % KC] = a(i0 + e / KC, k0 + e % KC);
+            wave_lds_barrier();
+#pragma unroll 8
+            for (int q = 0; q < KC; q += 2)
+                acc = __builtin_amdgcn_mfma_f32_32x32x2f32(s[r * kTileMmaPitch + q + h], b(k0 + q + h, j0 + r), acc, 0, 0, 0);
+        }
+#pragma unroll
+        for (int e = 0; e < 16; ++e) c[(i0 + 8 * (e >> 2) + 4 * h + (e & 3)) * N + j0 + r] = acc[e];
+    }
+}
+
+// ---------------------------------------------------------------------------
 // Ping-pong GEMM block: 256x256 C block, 8 waves in two groups of four
 // ---------------------------------------------------------------------------
 //

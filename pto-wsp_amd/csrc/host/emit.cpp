@@ -17,6 +17,10 @@ namespace ptowsp {
 
 namespace {
 
+// Row pitch (floats) of tile_mma's per-wave operand scratch
+// (kTileMmaPitch in ptowsp_device.h).
+constexpr int kTileMmaPitchHost = 33;
+
 std::string flt(double v) {
     char buf[64];
     std::snprintf(buf, sizeof buf, "%.17g", v);
@@ -558,6 +562,22 @@ EmittedKernel emit_tile(const Module& m, const KernelAnalysis& a, const LaunchSp
     size_t lds = pool;
     for (const auto& p : k.params)
         if (staged_id(p.id)) lds += static_cast<size_t>(SB) * a.by_id[p.id]->rows * a.by_id[p.id]->cols * (is_int_v(p.id) ? 8 : 4);
+    // Matmul ops of MFMA shape run on the matrix cores (tile_mma), with a
+    // 32-row operand scratch per wave, when that scratch fits beside the tiles.
+    auto mma_shape = [&](const OpInfo& op) {
+        if (op.kind != OpKind::Matmul || op.result <= 0) return false;
+        const ValueInfo* av = a.by_id[op.operands[0]];
+        const ValueInfo* bv = a.by_id[op.operands[1]];
+        const int M = av->rows, K = av->cols, N = bv->cols;
+        return !is_int_v(op.result) && !is_int_v(op.operands[0]) && !is_int_v(op.operands[1]) && M % 32 == 0 &&
+               N % 32 == 0 && K % 2 == 0 && (K <= 32 || K % 32 == 0) && spec.threads % 64 == 0;
+    };
+    const size_t mma_scratch = static_cast<size_t>(spec.threads / 64) * 32 * kTileMmaPitchHost * 4;
+    bool use_mma = false;
+    if (spec.tile_mma)
+        for (const auto& op : k.ops) use_mma = use_mma || mma_shape(op);
+    if (use_mma && lds + mma_scratch > 160 * 1024) use_mma = false;
+    if (use_mma) lds += mma_scratch;
     if (lds > 160 * 1024)
         throw CompileError("kernel " + k.name + ": tiles need " + std::to_string(lds) +
                            " bytes of LDS, more than the 160 KiB of a gfx950 workgroup");
@@ -575,6 +595,7 @@ EmittedKernel emit_tile(const Module& m, const KernelAnalysis& a, const LaunchSp
     o << "extern \"C\" __global__ void __launch_bounds__(" << spec.threads << ") " << ek.entry << "(const LaunchArgs A) {\n";
     o << "  constexpr int NT = " << spec.threads << ";\n";
     if (pool > 0) o << "  __shared__ __attribute__((aligned(16))) char pool_[" << pool << "];\n";
+    if (use_mma) o << "  __shared__ __attribute__((aligned(16))) float mma_scratch_[" << mma_scratch / 4 << "];\n";
     for (int id : lds_vals) {
         const char* ty = is_int_v(id) ? "i64" : "float";
         o << "  " << ty << "* const L" << id << " = reinterpret_cast<" << ty << "*>(pool_ + " << lds_off[id] << ");\n";
@@ -748,6 +769,14 @@ EmittedKernel emit_tile(const Module& m, const KernelAnalysis& a, const LaunchSp
                                std::to_string(p) + "] + (i64)(" + c + ") * A.s4[" + std::to_string(p) + "])";
                     return "L" + std::to_string(v->id) + "[(" + r + ") * " + std::to_string(ld) + " + (" + c + ")]";
                 };
+                if (use_mma && mma_shape(op)) {
+                    o << ind << "{\n";
+                    o << ind << "  auto fa_ = [&](int i, int q) -> float { return " << elem(av, "i", "q", K) << "; };\n";
+                    o << ind << "  auto fb_ = [&](int q, int jj) -> float { return " << elem(bv, "q", "jj", N) << "; };\n";
+                    o << ind << "  tile_mma<" << M << ", " << K << ", " << N << ", NT>(fa_, fb_, L" << res->id << ", mma_scratch_);\n";
+                    o << ind << "}\n";
+                    break;
+                }
                 o << ind << "for (int e = threadIdx.x; e < " << M * N << "; e += NT) {\n";
                 o << ind << "  const int i = e / " << N << ", jj = e % " << N << ";\n";
                 o << ind << "  float acc = 0.0f;\n";

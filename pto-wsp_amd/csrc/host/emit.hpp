@@ -33,6 +33,9 @@ struct EmitSpec {
     // (streaming) global accesses for full-row tiles.
     int row_up = 8;
     bool nontemporal = false;
+    // Tile programs: matmul ops of MFMA shape (M, N multiples of 32) on the
+    // matrix cores (tile_mma) instead of the scalar loop.
+    bool tile_mma = true;
     // GEMM family on MFMA (only when strides and alignment allow it).
     bool gemm = false;
     // GEMM: grid variables whose neighbouring tasks are merged into one

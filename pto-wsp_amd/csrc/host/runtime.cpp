@@ -463,6 +463,7 @@ struct Tuning {
     bool serial_groups = true;  // overlapping grids run as parallel groups of in-order tasks
     int tile_threads = 256;     // threads of a tile-program workgroup
     bool row_loops = true;      // row programs over in-kernel loops
+    bool tile_mma = true;       // tile-program matmuls of MFMA shape on the matrix cores
 };
 
 // Page ring depth of the decode family: 32 KiB of K and V in flight per
@@ -494,6 +495,7 @@ const Tuning& tuning() {
         if (const char* s = std::getenv("PTOWSP_DECODE_ORDERED")) v.decode_ordered = std::atoi(s) != 0;
         if (const char* s = std::getenv("PTOWSP_SERIAL_GROUPS")) v.serial_groups = std::atoi(s) != 0;
         if (const char* s = std::getenv("PTOWSP_ROW_LOOPS")) v.row_loops = std::atoi(s) != 0;
+        if (const char* s = std::getenv("PTOWSP_TILE_MMA")) v.tile_mma = std::atoi(s) != 0;
         if (const char* s = std::getenv("PTOWSP_TILE_THREADS")) {
             const int t = std::atoi(s);
             v.tile_threads = t == 64 || t == 128 || t == 256 || t == 512 ? t : 256;
@@ -1025,6 +1027,7 @@ BuiltLaunch build_launch(RunEnv& E, const LaunchSpec& L) {
     B.spec.decode_ordered = tuning().decode_ordered;
     B.spec.vec_width = a.family == Family::RowProgram ? pick_vec_width(a, A, nvars) : 1;
     B.spec.threads = tuning().tile_threads;
+    B.spec.tile_mma = tuning().tile_mma;
     if (P->ka[L.kernel].family == Family::Custom) {
         custom_axis_args(E, L, A);
         B.spec.gemm = B.spec.decode = B.spec.gemm_pingpong = false;
@@ -1038,7 +1041,7 @@ std::string spec_key(const EmitSpec& s) {
     o << "vw" << s.vec_width << (s.serial ? ";serial" + std::to_string(s.seq_mask) : "") << (s.task_list ? ";tl" : "") << ";up" << s.row_up << (s.nontemporal ? ";nt" : "")
       << (s.row_loops ? ";rl" : "") << (s.gemm ? ";gemm" : "") << ";m" << s.gemm_vm << ";n" << s.gemm_vn << (s.gemm_pingpong ? ";pp" : "")
       << (s.decode ? ";dec" : "")
-      << (s.decode_norm ? ";norm" : "") << ";t" << s.threads << ";r" << s.decode_ring << ";w" << s.decode_waves << (s.decode_ordered ? ";ord" : "")
+      << (s.decode_norm ? ";norm" : "") << (s.tile_mma ? ";mma" : "") << ";t" << s.threads << ";r" << s.decode_ring << ";w" << s.decode_waves << (s.decode_ordered ? ";ord" : "")
       << ";i";
     for (int c : s.indirect_count) o << c << ",";
     o << ";d";

@@ -130,6 +130,68 @@ def test_example_tiled_attention(gpu):
     assert prog.stats.total_cycles == ref.total_cycles == 1680
 
 
+def _has_tile_mma(prog):
+    return "tile_mma<" in prog._native.precompile(0)
+
+
+def test_tiled_attention_mfma_tiles(gpu):
+    """examples/attention with 64-token tiles and head dim 64: both matmuls of the fused
+    tile (q @ k_t and softmax(s) @ v) run on the matrix cores inside the tile program."""
+    rng = np.random.default_rng(3)
+    q, k, v = (rng.standard_normal((1, 2, 128, 64), dtype=np.float32) for _ in range(3))
+    ga, ca = W.attention_arrays(q, k, v, 64), W.attention_arrays(q, k, v, 64)
+    prog = run_hip(W.rr4(W.tiled_attention(ga, 64)))
+    ref = run_workload(W.rr4(W.tiled_attention(ca, 64)))
+    assert prog._native.kernel_family("attention_tile") == "tile_program" and _has_tile_mma(prog)
+    assert _rel_fro(ga["o"], ca["o"]) <= 1e-5
+    q64, k64, v64 = (x.astype(np.float64).reshape(1, 2, 2, 64, 64) for x in (q, k, v))
+    s = q64 @ k64.transpose(0, 1, 2, 4, 3) / 8.0
+    w = np.exp(s - s.max(-1, keepdims=True))
+    exact = ((w / w.sum(-1, keepdims=True)) @ v64).reshape(1, 2, 128, 64)
+    assert _rel_fro(ga["o"], exact) <= 1e-5
+    assert prog.stats.total_cycles == ref.total_cycles
+
+
+def test_llama_block_mfma_tiles(gpu):
+    """examples/llama with 64-token tiles, d = 64 and a 128-wide MLP: the attention and
+    ReLU-MLP tiles' four matmuls (K = 64 and 128) run on the matrix cores."""
+    rng = np.random.default_rng(4)
+    x = rng.standard_normal((256, 64), dtype=np.float32)
+    w1 = (rng.standard_normal((64, 128)) / 8).astype(np.float32)
+    w2 = (rng.standard_normal((128, 64)) / 11).astype(np.float32)
+    out, ref_out = np.zeros_like(x), np.zeros_like(x)
+    prog = run_hip(W.llama_block(x, w1, w2, out, 64, 1e-6))
+    ref = run_workload(W.llama_block(x, w1, w2, ref_out, 64, 1e-6))
+    assert _has_tile_mma(prog)
+    assert _rel_fro(out, ref_out) <= 1e-5
+    assert _rel_fro(out, W.llama_block_ref(x, w1, w2, 64, 1e-6)) <= 1e-5
+    assert prog.stats.total_cycles == ref.total_cycles
+
+
+@pytest.mark.parametrize("m,k,n", [(32, 16, 32), (32, 64, 96), (96, 32, 32), (32, 48, 32)])
+def test_tile_program_matmul_shapes(gpu, m, k, n):
+    """Matmul tiles below the GEMM family (M or N not a multiple of 64) on the tile
+    program: M, N multiples of 32 with K <= 32 or a multiple of 32 take the matrix cores,
+    K = 48 the scalar loop (bit for bit the oracle's)."""
+    rng = np.random.default_rng(m + k + n)
+    a = rng.uniform(-1, 1, (3, 1, m, k)).astype(np.float32)
+    b = rng.uniform(-1, 1, (3, 1, k, n)).astype(np.float32)
+    ga = {"a": a, "b": b, "c": np.zeros((3, 1, m, n), np.float32)}
+    ca = {k_: v.copy() for k_, v in ga.items()}
+    prog = run_hip(W.rr4(W.matmul_tile(ga, m, k, n), 1024))
+    ref = run_workload(W.rr4(W.matmul_tile(ca, m, k, n), 1024))
+    assert prog._native.kernel_family("mm") == "tile_program"
+    mma = k % 2 == 0 and (k <= 32 or k % 32 == 0)
+    assert _has_tile_mma(prog) == mma
+    if mma:
+        assert _rel_fro(ga["c"], ca["c"]) <= 1e-5
+    else:
+        np.testing.assert_array_equal(ga["c"], ca["c"])
+    exact = a.astype(np.float64) @ b.astype(np.float64)
+    assert _rel_fro(ga["c"], exact) <= 1e-5
+    assert prog.stats.total_cycles == ref.total_cycles
+
+
 def test_validated_matmul_and_exact_2x2(gpu):
     a = np.array([[[[1.0, 2.0], [3.0, 4.0]]]], np.float32)
     b = np.array([[[[5.0, 6.0], [7.0, 8.0]]]], np.float32)

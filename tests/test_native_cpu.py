@@ -197,6 +197,22 @@ def test_decode_family_query_rows(group, d, family):
         assert f"DecodeWave<{group}, {d}, false, true, false>" in prog.precompile(0)
 
 
+def test_tile_program_matmul_on_matrix_cores():
+    """A fused tile with matmuls of MFMA shape (the attention example at 64-token tiles)
+    stays a tile program whose matmuls call tile_mma; 8-token tiles keep the scalar loop."""
+    from pto_wsp._hip import NativeProgram
+
+    for ts, want in ((64, 2), (8, 0)):
+        q = np.zeros((1, 2, 128, 64), np.float32)
+        arrs = W.attention_arrays(q, q, q, ts)
+        prog = NativeProgram(workload_to_codegen_ir(W.tiled_attention(arrs, ts), "a").module)
+        src = prog.precompile(0)
+        assert prog.kernel_family("attention_tile") == "tile_program"
+        assert src.count("tile_mma<") == want
+        if want:
+            assert "tile_mma<64, 64, 64, NT>" in src and "mma_scratch_[" in src
+
+
 def test_decode_precompile_folded_normalisation():
     """precompile(decode_norm=True) emits the form a run uses when `out = o / l`
     follows the decode launch: the completion writes out, and units without pages
