@@ -134,7 +134,8 @@ def decode_workload(t, page=16):
 
     from pto_wsp import DType, Dense, DenseDyn, In, InOut, Out, P, Tensor, Tile, kernel, pto, workload
 
-    bf16, f32, i32 = DType.BF16, DType.F32, DType.I32
+    f32, i32 = DType.F32, DType.I32
+    bf16 = DType.F32 if str(t["q"].dtype) in ("torch.float32", "float32") else DType.BF16  # q / K / V dtype
     B, Hkv, G, D = tuple(t["q"].shape)
     max_pages = t["page_table"].shape[1]
     sc = 1.0 / math.sqrt(D)
@@ -302,10 +303,12 @@ class Softmax3Case:
 class DecodeCase:
     unit, bound, dtype = "GB/s", "hbm", "bf16"
 
-    def __init__(self, name, batch, hq, hkv, d, lmin, lmax, seed, baseline_config, page=16):
+    def __init__(self, name, batch, hq, hkv, d, lmin, lmax, seed, baseline_config, page=16, f32_inputs=False):
         self.name, self.batch, self.hq, self.hkv, self.d = name, batch, hq, hkv, d
         self.lmin, self.lmax, self.seed, self.page = lmin, lmax, seed, page
         self.baseline_config = baseline_config
+        self.f32_inputs = f32_inputs
+        self.dtype = "f32" if f32_inputs else "bf16"
 
     def setup(self, dev):
         import numpy as np
@@ -329,9 +332,10 @@ class DecodeCase:
         g = torch.Generator(device=dev)
         g.manual_seed(self.seed)
         shape_kv = (total, self.hkv, page, self.d)
-        t = {"q": torch.randn((B, self.hkv, G, self.d), generator=g, device=dev, dtype=torch.bfloat16),
-             "k_cache": torch.randn(shape_kv, generator=g, device=dev, dtype=torch.bfloat16),
-             "v_cache": torch.randn(shape_kv, generator=g, device=dev, dtype=torch.bfloat16),
+        dt = torch.float32 if self.f32_inputs else torch.bfloat16
+        t = {"q": torch.randn((B, self.hkv, G, self.d), generator=g, device=dev, dtype=dt),
+             "k_cache": torch.randn(shape_kv, generator=g, device=dev, dtype=dt),
+             "v_cache": torch.randn(shape_kv, generator=g, device=dev, dtype=dt),
              "page_table": torch.from_numpy(pt).to(dev), "npages": torch.from_numpy(npages.astype(np.int32)).to(dev),
              "mask": torch.from_numpy(mask).to(dev),
              "m": torch.full((B, self.hkv, G, 1), float("-inf"), device=dev),
@@ -340,8 +344,9 @@ class DecodeCase:
         self.t = t
         self.prog = decode_workload(t, page).compile(target="hip_gfx950")
         ntok = int(self.lengths.sum())
-        # Algorithmic bytes: K and V of the valid tokens, q (bf16), out (f32), the page table entries used.
-        self.work = ntok * self.hkv * self.d * 2 * 2 + B * self.hq * self.d * 2 + B * self.hq * self.d * 4 + 4 * total
+        # Algorithmic bytes: K and V of the valid tokens, q (bf16 / f32), out (f32), the page table entries used.
+        es = 4 if self.f32_inputs else 2
+        self.work = ntok * self.hkv * self.d * es * 2 + B * self.hq * self.d * es + B * self.hq * self.d * 4 + 4 * total
 
     def before_step(self):
         self.t["m"].fill_(float("-inf"))
@@ -356,7 +361,7 @@ class DecodeCase:
 
     def describe(self):
         return (f"{self.name}: paged GQA decode, batch {self.batch}, {self.hq} query / {self.hkv} KV heads, head dim "
-                f"{self.d}, bf16 Q/K/V N(0,1), lengths U[{self.lmin},{self.lmax}] (sum {int(self.lengths.sum())}), "
+                f"{self.d}, {self.dtype} Q/K/V N(0,1), lengths U[{self.lmin},{self.lmax}] (sum {int(self.lengths.sum())}), "
                 f"{self.page}-token pages, permuted page table; P(batch) x P(kv_head) x P.seq(DenseDyn(pages)) "
                 "+ normalize")
 
@@ -372,7 +377,10 @@ class DecodeCase:
         self.before_step()
         self.prog.execute()
         self.prog.synchronize()
-        u16 = lambda x: x.contiguous().view(torch.int16).cpu().numpy().view(np.uint16)
+        if self.f32_inputs:
+            u16 = lambda x: x.contiguous().cpu().numpy()  # f32 inputs pass through as they are
+        else:
+            u16 = lambda x: x.contiguous().view(torch.int16).cpu().numpy().view(np.uint16)
         h = {"q": u16(self.t["q"][:nb]), "k_cache": u16(self.t["k_cache"]), "v_cache": u16(self.t["v_cache"]),
              "page_table": self.t["page_table"][:nb].cpu().numpy(), "npages": self.t["npages"][:nb].cpu().numpy(),
              "mask": self.t["mask"][:nb].cpu().numpy()}
@@ -542,12 +550,14 @@ CASES = {
     "paged_decode_d256": lambda: DecodeCase("paged_decode_d256", 64, 32, 8, 256, 512, 8192, 0, None),
     "paged_decode_g16": lambda: DecodeCase("paged_decode_g16", 64, 128, 8, 128, 512, 8192, 0, None, page=32),
     "paged_decode_g32": lambda: DecodeCase("paged_decode_g32", 64, 256, 8, 128, 512, 8192, 0, None),
+    # Not a BASELINE config: the C5 decode with f32 q / K / V.
+    "paged_decode_f32": lambda: DecodeCase("paged_decode_f32", 64, 32, 8, 128, 512, 8192, 0, None, f32_inputs=True),
     # Not a BASELINE config: the C4 GEMM with f32 A and B (the reference's own
     # matmul dtype), on the f32 MFMA block.
     "bgemm_f32": lambda: GemmCase("bgemm_f32", 64, 2048, 2048, 2048, 0, None, f32_inputs=True),
 }
 EXTRA = ("copy_calib", "softmax3", "softmax3_overlap", "paged_decode_page32", "paged_decode_page64", "paged_decode_page8",
-         "paged_decode_d64", "paged_decode_d256", "paged_decode_g16", "paged_decode_g32", "bgemm_f32")
+         "paged_decode_d64", "paged_decode_d256", "paged_decode_g16", "paged_decode_g32", "paged_decode_f32", "bgemm_f32")
 
 
 def load_traffic(name):

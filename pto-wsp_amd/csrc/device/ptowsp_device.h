@@ -1300,11 +1300,19 @@ __device__ inline void reset_count(int* cnt) {
 
 // H8: pages of 8 tokens, folded two to a 16-token step: page a supplies
 // tokens 0-7, page b tokens 8-15 (see load_pair).
-template <int G, int D, bool F16, bool MASK, bool H8 = false>
+// F32: f32 q, K and V (the reference's own dtype): scores on
+// v_mfma_f32_16x16x4_f32 with lane l holding head dims (D/4)*(l/16) .. +D/4-1
+// of its token (the K order of a product is free), p @ v on the same MFMA
+// with p as it is (no hi / lo split); F16 is then unused.
+template <int G, int D, bool F16, bool MASK, bool H8 = false, bool F32 = false>
 struct DecodeWave {
     static_assert(G >= 1 && G <= 48 && (D == 64 || D == 128 || D == 256), "decode shape");
-    static constexpr int NS = D / 32;          // head-dim slices of the score MFMA
+    static_assert(!F32 || (G <= 16 && D <= 128), "f32 decode shape");
+    static constexpr int ES = F32 ? 4 : 2;     // element bytes of q, K, V
+    static constexpr int NS = D * ES / 64;     // u32x4 of K per lane (bf16 / f16: head-dim slices of the score MFMA)
     static constexpr int DV = D / 16;          // head-dim columns per lane in p @ v
+    static constexpr int VW = DV * ES / 4;     // u32 of V per lane and token
+    static constexpr int KC = F32 ? 16 : 64;   // bytes between a lane's K chunks
     static constexpr int RB = (G + 15) / 16;   // blocks of 16 query rows (one MFMA row block each)
     static constexpr int NQ = RB * NS;         // q registers (u32x4) per lane
     static constexpr int kHalves = H8 ? 2 : 1;  // pages per 16-token step
@@ -1315,8 +1323,8 @@ struct DecodeWave {
     static constexpr int kPartFloats = G * D + ((2 * G + 3) & ~3);
 
     struct Page {
-        u32x4 k[NS];           // lane l: token l%16, head dims 32*j + 8*(l/16) .. +7
-        u32 v[4][DV / 2];      // lane l: tokens 4*(l/16) + i, head dims DV*(l%16) .. +DV-1
+        u32x4 k[NS];           // lane l: token l%16, head dims 32*j + 8*(l/16) .. +7 (F32: (D/4)*(l/16) + 4*j .. +3)
+        u32 v[4][VW];          // lane l: tokens 4*(l/16) + i, head dims DV*(l%16) .. +DV-1
         float mask[4];         // lane l: tokens 4*(l/16) .. +3
         float hneg;            // H8: added to the scores of tokens 8-15 (0, or -inf without page b)
     };
@@ -1333,10 +1341,10 @@ struct DecodeWave {
         const int lane = threadIdx.x & 63, t = lane & 15, grp = lane >> 4;
         const int tk = H8 ? (t & 7) : t, gv = H8 ? (grp & 1) : grp;
         Lanes r;
-        r.k = static_cast<u32>((tk * ks + 8 * grp) * 2);
-        r.v = static_cast<u32>((4 * gv * vs + DV * t) * 2);
+        r.k = static_cast<u32>((tk * ks + (F32 ? D / 4 : 8) * grp) * ES);
+        r.v = static_cast<u32>((4 * gv * vs + DV * t) * ES);
         r.m = static_cast<u32>(gv * 16);
-        r.vrow = static_cast<u32>(vs * 2);
+        r.vrow = static_cast<u32>(vs * ES);
         return r;
     }
 
@@ -1353,17 +1361,17 @@ struct DecodeWave {
         const int lane = threadIdx.x & 63, t = lane & 15, grp = lane >> 4;
         const char* kp = reinterpret_cast<const char*>(t < 8 ? ka : kb) + ln.k;
 #pragma unroll
-        for (int j = 0; j < NS; ++j) pg.k[j] = __builtin_nontemporal_load(reinterpret_cast<const u32x4*>(kp + 64 * j));
+        for (int j = 0; j < NS; ++j) pg.k[j] = __builtin_nontemporal_load(reinterpret_cast<const u32x4*>(kp + KC * j));
         const char* vp = reinterpret_cast<const char*>(grp < 2 ? va : vb) + ln.v;
 #pragma unroll
         for (int i = 0; i < 4; ++i) {
             const char* vi = vp + static_cast<u64>(i * ln.vrow);
-            if constexpr (DV == 16) {
+            if constexpr (VW == 8) {
                 const u32x4 a = __builtin_nontemporal_load(reinterpret_cast<const u32x4*>(vi));
                 const u32x4 b = __builtin_nontemporal_load(reinterpret_cast<const u32x4*>(vi + 16));
                 pg.v[i][0] = a.x; pg.v[i][1] = a.y; pg.v[i][2] = a.z; pg.v[i][3] = a.w;
                 pg.v[i][4] = b.x; pg.v[i][5] = b.y; pg.v[i][6] = b.z; pg.v[i][7] = b.w;
-            } else if constexpr (DV == 8) {
+            } else if constexpr (VW == 4) {
                 const u32x4 a = __builtin_nontemporal_load(reinterpret_cast<const u32x4*>(vi));
                 pg.v[i][0] = a.x; pg.v[i][1] = a.y; pg.v[i][2] = a.z; pg.v[i][3] = a.w;
             } else {
@@ -1391,16 +1399,16 @@ struct DecodeWave {
         const buf_rsrc rv = __builtin_amdgcn_make_buffer_rsrc(const_cast<u16*>(vp), 0, nrec, 0x00020000);
 #pragma unroll
         for (int j = 0; j < NS; ++j)
-            pg.k[j] = __builtin_bit_cast(u32x4, __builtin_amdgcn_raw_buffer_load_b128(rk, ln.k + 64 * j, 0, 2));
+            pg.k[j] = __builtin_bit_cast(u32x4, __builtin_amdgcn_raw_buffer_load_b128(rk, ln.k + KC * j, 0, 2));
 #pragma unroll
         for (int i = 0; i < 4; ++i) {
             const u32 so = i * ln.vrow;
-            if constexpr (DV == 16) {
+            if constexpr (VW == 8) {
                 const u32x4 a = __builtin_bit_cast(u32x4, __builtin_amdgcn_raw_buffer_load_b128(rv, ln.v, so, 2));
                 const u32x4 b = __builtin_bit_cast(u32x4, __builtin_amdgcn_raw_buffer_load_b128(rv, ln.v + 16, so, 2));
                 pg.v[i][0] = a.x; pg.v[i][1] = a.y; pg.v[i][2] = a.z; pg.v[i][3] = a.w;
                 pg.v[i][4] = b.x; pg.v[i][5] = b.y; pg.v[i][6] = b.z; pg.v[i][7] = b.w;
-            } else if constexpr (DV == 8) {
+            } else if constexpr (VW == 4) {
                 const u32x4 a = __builtin_bit_cast(u32x4, __builtin_amdgcn_raw_buffer_load_b128(rv, ln.v, so, 2));
                 pg.v[i][0] = a.x; pg.v[i][1] = a.y; pg.v[i][2] = a.z; pg.v[i][3] = a.w;
             } else {
@@ -1457,8 +1465,19 @@ struct DecodeWave {
 #pragma unroll
         for (int rb = 0; rb < RB; ++rb) {
             acc[rb] = f32x4v_t{0.0f, 0.0f, 0.0f, 0.0f};
+            if constexpr (F32) {
+                // MFMA (j, x) pairs head dim (D/4)*g + 4*j + x of lane group g
+                // of K and q.
 #pragma unroll
-            for (int j = 0; j < NS; ++j) acc[rb] = mfma_16x16x32<F16>(pg.k[j], qa[rb * NS + j], acc[rb]);
+                for (int j = 0; j < NS; ++j)
+#pragma unroll
+                    for (int x = 0; x < 4; ++x)
+                        acc[rb] = __builtin_amdgcn_mfma_f32_16x16x4f32(__uint_as_float(pg.k[j][x]), __uint_as_float(qa[rb * NS + j][x]),
+                                                                     acc[rb], 0, 0, 0);
+            } else {
+#pragma unroll
+                for (int j = 0; j < NS; ++j) acc[rb] = mfma_16x16x32<F16>(pg.k[j], qa[rb * NS + j], acc[rb]);
+            }
         }
         float hb = 0.0f;
         if constexpr (H8) hb = grp < 2 ? 0.0f : pg.hneg;
@@ -1470,6 +1489,7 @@ struct DecodeWave {
         auto fadd_ = [](float x, float y) { return x + y; };
         float a[RB];
         u32x2 ph[RB], pl[RB];
+        f32x4v_t pf[RB];
         bool rescale[RB];
 #pragma unroll
         for (int rb = 0; rb < RB; ++rb) {
@@ -1489,7 +1509,8 @@ struct DecodeWave {
             st.l[rb] = st.l[rb] * a[rb] + cross4_reduce((pr[0] + pr[1]) + (pr[2] + pr[3]), fadd_);
             st.m[rb] = mn;
             rescale[rb] = __builtin_amdgcn_ballot_w64(16 * rb + t < G && a[rb] != 1.0f) != 0;
-            split4(pr, ph[rb], pl[rb]);
+            if constexpr (F32) pf[rb] = pr;
+            else split4(pr, ph[rb], pl[rb]);
         }
         // o <- o * a + p @ v on the matrix cores: v_mfma_f32_16x16x16 with
         // M = query rows, K = the page's 16 tokens, N = 16 head dims.  p is
@@ -1517,15 +1538,27 @@ struct DecodeWave {
                 for (int e = 0; e < DV; ++e) st.o[rb][e] = st.o[rb][e] * a4;
             }
         }
+        if constexpr (F32) {
+            // MFMA i pairs token 4*g + i of lane group g: the lane's own score
+            // pf[i] and V value pg.v[i][e].
 #pragma unroll
-        for (int e = 0; e < DV; ++e) {
-            const u32 sel = (e & 1) ? 0x07060302u : 0x05040100u;
-            const u32x2 bv = {__builtin_amdgcn_perm(pg.v[1][e >> 1], pg.v[0][e >> 1], sel),
-                              __builtin_amdgcn_perm(pg.v[3][e >> 1], pg.v[2][e >> 1], sel)};
+            for (int e = 0; e < DV; ++e)
 #pragma unroll
-            for (int rb = 0; rb < RB; ++rb) {
-                st.o[rb][e] = mfma16(ph[rb], bv, st.o[rb][e]);
-                st.o[rb][e] = mfma16(pl[rb], bv, st.o[rb][e]);
+                for (int rb = 0; rb < RB; ++rb)
+#pragma unroll
+                    for (int i = 0; i < 4; ++i)
+                        st.o[rb][e] = __builtin_amdgcn_mfma_f32_16x16x4f32(pf[rb][i], __uint_as_float(pg.v[i][e]), st.o[rb][e], 0, 0, 0);
+        } else {
+#pragma unroll
+            for (int e = 0; e < DV; ++e) {
+                const u32 sel = (e & 1) ? 0x07060302u : 0x05040100u;
+                const u32x2 bv = {__builtin_amdgcn_perm(pg.v[1][e >> 1], pg.v[0][e >> 1], sel),
+                                  __builtin_amdgcn_perm(pg.v[3][e >> 1], pg.v[2][e >> 1], sel)};
+#pragma unroll
+                for (int rb = 0; rb < RB; ++rb) {
+                    st.o[rb][e] = mfma16(ph[rb], bv, st.o[rb][e]);
+                    st.o[rb][e] = mfma16(pl[rb], bv, st.o[rb][e]);
+                }
             }
         }
     }
@@ -1534,12 +1567,14 @@ struct DecodeWave {
     // (rows >= G are zero).
     __device__ static void load_q(u32x4 (&qa)[NQ], const u16* q, i64 qs) {
         const int lane = threadIdx.x & 63, t = lane & 15, grp = lane >> 4;
+        const char* qb = reinterpret_cast<const char*>(q);
 #pragma unroll
         for (int rb = 0; rb < RB; ++rb) {
 #pragma unroll
             for (int j = 0; j < NS; ++j) {
                 qa[rb * NS + j] = u32x4{0u, 0u, 0u, 0u};
-                if (16 * rb + t < G) qa[rb * NS + j] = *reinterpret_cast<const u32x4*>(q + (16 * rb + t) * qs + 32 * j + 8 * grp);
+                const i64 e = (16 * rb + t) * qs + (F32 ? (D / 4) * grp + 4 * j : 32 * j + 8 * grp);
+                if (16 * rb + t < G) qa[rb * NS + j] = *reinterpret_cast<const u32x4*>(qb + e * ES);
             }
         }
     }

@@ -347,7 +347,10 @@ DecodeInfo classify_decode(const KernelDef& k, const KernelAnalysis& a) {
     auto vi = [&](int pidx) { return a.by_id[k.params[pidx].id]; };
     const ValueInfo *q = vi(pq), *kt = vi(pkt), *v = vi(pv_p), *m = vi(pm), *l = vi(pl), *o = vi(po);
     const int G = q->rows, D = q->cols, PG = kt->cols;
-    if (q->dtype != kt->dtype || q->dtype != v->dtype || (q->dtype != DType::BF16 && q->dtype != DType::F16)) return info;
+    if (q->dtype != kt->dtype || q->dtype != v->dtype ||
+        (q->dtype != DType::BF16 && q->dtype != DType::F16 && q->dtype != DType::F32))
+        return info;
+    const bool f32 = q->dtype == DType::F32;
     if (m->dtype != DType::F32 || l->dtype != DType::F32 || o->dtype != DType::F32) return info;
     if (kt->rows != D || v->rows != PG || v->cols != D || m->rows != G || m->cols != 1 || l->rows != G || l->cols != 1 ||
         o->rows != G || o->cols != D)
@@ -360,12 +363,14 @@ DecodeInfo classify_decode(const KernelDef& k, const KernelAnalysis& a) {
     // steps: larger pages as 16-token sub-pages, 8-token pages two to a step),
     // head dim 64 / 128 / 256, query rows in blocks of 16 (one MFMA row block
     // each) up to what the wave's registers hold beside its page ring: 48
-    // rows at head dim 64 or 128, 16 at 256.
-    const int max_rows = D == 256 ? 16 : 48;
+    // rows at head dim 64 or 128, 16 at 256; f32 pages (twice the registers)
+    // up to 16 rows and head dim 128.
+    const int max_rows = f32 || D == 256 ? 16 : 48;
     if ((PG != 8 && PG != 16 && PG != 32 && PG != 64 && PG != 128) || G < 1 || G > max_rows ||
-        (D != 64 && D != 128 && D != 256))
+        (D != 64 && D != 128 && D != 256) || (f32 && D > 128))
         return info;
     info.ok = true;
+    info.f32 = f32;
     info.q = a.tensor_ordinal[pq];
     info.kt = a.tensor_ordinal[pkt];
     info.v = a.tensor_ordinal[pv_p];

@@ -46,6 +46,7 @@ struct DecodeInfo {
     int m = -1, l = -1, o = -1;              // accumulators (InOut)
     int g = 0, d = 0, pg = 0;                // query rows, head dim, tokens per page
     bool f16 = false;                        // q / k / v are f16 (else bf16)
+    bool f32 = false;                        // q / k / v are f32
     float scale = 1.0f;                      // score scale (a Constant)
 };
 

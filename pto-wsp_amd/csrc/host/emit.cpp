@@ -1021,7 +1021,8 @@ EmittedKernel emit_decode(const Module& m, const KernelAnalysis& a, const Launch
     auto nterms = [&](int p) { return spec.indirect_count[p]; };
     const std::string tmpl = "DecodeWave<" + std::to_string(d.g) + ", " + std::to_string(d.d) + ", " +
                              (d.f16 ? "true" : "false") + ", " + (d.mask >= 0 ? "true" : "false") + ", " +
-                             (d.pg == 8 ? "true" : "false") + ">";
+                             (d.pg == 8 ? "true" : "false") + (d.f32 ? ", true" : "") + ">";
+    const int es = d.f32 ? 4 : 2;  // bytes per q / K / V element
     std::ostringstream scale;
     scale.precision(9);
     scale << std::scientific << d.scale << "f";
@@ -1033,7 +1034,8 @@ EmittedKernel emit_decode(const Module& m, const KernelAnalysis& a, const Launch
     ek.part_floats = d.g * d.d + ((2 * d.g + 3) & ~3);  // DecodeWave::kPartFloats
     std::ostringstream o;
     o << "#include \"ptowsp_device.h\"\nusing namespace ptowsp;\n";
-    o << "// decode program: kernel " << k.name << ", " << d.g << " query rows, head dim " << d.d << (d.f16 ? " f16" : " bf16")
+    o << "// decode program: kernel " << k.name << ", " << d.g << " query rows, head dim " << d.d
+      << (d.f32 ? " f32" : d.f16 ? " f16" : " bf16")
       << (d.mask >= 0 ? ", masked" : "") << ", pages balanced over the resident waves\n";
     // Grid variables of a unit.  Units number at most kDecodeMaxUnits, so
     // every grid extent and unit index fits 32-bit unsigned arithmetic.
@@ -1202,8 +1204,8 @@ EmittedKernel emit_decode(const Module& m, const KernelAnalysis& a, const Launch
     else o << "    po.m = 0;\n";
     o << "  };\n";
     o << "  auto f_bases = [&](const PageOffs& po, const u16*& kp, const u16*& vp, const float*& mp) {\n";
-    o << "    kp = reinterpret_cast<const u16*>(A.base[" << d.kt << "] + po.k * 2);\n";
-    o << "    vp = reinterpret_cast<const u16*>(A.base[" << d.v << "] + po.v * 2);\n";
+    o << "    kp = reinterpret_cast<const u16*>(A.base[" << d.kt << "] + po.k * " << es << ");\n";
+    o << "    vp = reinterpret_cast<const u16*>(A.base[" << d.v << "] + po.v * " << es << ");\n";
     if (d.mask >= 0) o << "    mp = reinterpret_cast<const float*>(A.base[" << d.mask << "] + po.m * 4);\n";
     else o << "    mp = nullptr;\n";
     o << "  };\n";
@@ -1214,7 +1216,7 @@ EmittedKernel emit_decode(const Module& m, const KernelAnalysis& a, const Launch
     o << "    vars[" << ng << "] = 0;\n";
     o << "    bool bad = false;\n";
     unit_check(d.q, d.g, d.d, "bad");
-    o << "    return bad ? nullptr : " << ptr(d.q, "const u16*", 2) << ";\n";
+    o << "    return bad ? nullptr : " << ptr(d.q, "const u16*", es) << ";\n";
     o << "  };\n";
     o << "  auto f_slot = [&](int u) { return partials + ((i64)u + w) * DW::kPartFloats; };\n";
     // Folds unit u's partials (slots first .. first+parts-1, in page order)

@@ -473,7 +473,8 @@ struct Tuning {
 // same bytes in flight.
 // More than 16 query rows add a block of accumulators and q registers per
 // 16 rows: 33-48 rows at head dim 128 leave room for 2 steps.
-int decode_ring_for(int head_dim, int rows) {
+int decode_ring_for(int head_dim, int rows, bool f32) {
+    if (f32) return head_dim >= 128 ? 3 : 4;  // 0.654 against 0.750 ms with 2 steps at head dim 128
     if (head_dim >= 256) return 2;
     if (head_dim <= 64) return rows <= 16 ? 3 : 4;
     return rows <= 32 ? 4 : 2;
@@ -482,7 +483,7 @@ int decode_ring_for(int head_dim, int rows) {
 // V, and one wave per SIMD cannot cover the fold's latency chain with it;
 // two waves per SIMD (3-step rings, half the registers each) can, up to 16
 // query rows.
-int decode_waves_for(int head_dim, int rows) { return head_dim <= 64 && rows <= 16 ? 8 : 4; }
+int decode_waves_for(int head_dim, int rows, bool f32) { return !f32 && head_dim <= 64 && rows <= 16 ? 8 : 4; }
 
 const Tuning& tuning() {
     static const Tuning t = [] {
@@ -764,14 +765,17 @@ bool decode_allowed(const KernelAnalysis& a, const LaunchSpec& L, const LaunchAr
     for (int p : {d.q, d.m, d.l, d.o}) {
         if (spec.indirect_count[p] != 0 || A.coef[p][ng] != 0) return false;
     }
-    const int dv = std::min(d.d / 16, 8);  // V loads: 8 (d 64) or 16 bytes per lane and token
-    if (A.s4[d.q] != 1 || A.s3[d.q] % 8 || !aligned(d.q, 8, 2)) return false;
-    if (A.s3[d.kt] != 1 || A.s4[d.kt] % 8 || !aligned(d.kt, 8, 2)) return false;
-    if (A.s4[d.v] != 1 || A.s3[d.v] % dv || !aligned(d.v, dv, 2)) return false;
+    // 16-byte q and K loads; V loads of 8 (bf16 / f16 at d 64) or 16 bytes
+    // per lane and token.
+    const int es = d.f32 ? 4 : 2, e16 = 16 / es;
+    const int dv = std::min(d.d / 16, e16);
+    if (A.s4[d.q] != 1 || A.s3[d.q] % e16 || !aligned(d.q, e16, es)) return false;
+    if (A.s3[d.kt] != 1 || A.s4[d.kt] % e16 || !aligned(d.kt, e16, es)) return false;
+    if (A.s4[d.v] != 1 || A.s3[d.v] % dv || !aligned(d.v, dv, es)) return false;
     if (d.mask >= 0 && (A.s4[d.mask] != 1 || !aligned(d.mask, 1, 4))) return false;
     // Page loads use 32-bit byte offsets from the page base.
     const int64_t lim = int64_t(1) << 30;
-    if (A.s4[d.kt] >= lim / 16 || A.s3[d.v] >= lim / 16) return false;
+    if (A.s4[d.kt] >= lim / (8 * es) || A.s3[d.v] >= lim / (8 * es)) return false;
     std::set<int> tids;
     for (int p : {d.q, d.kt, d.v, d.m, d.l, d.o}) tids.insert(L.targs[p]->tid);
     if (d.mask >= 0) tids.insert(L.targs[d.mask]->tid);
@@ -1022,8 +1026,8 @@ BuiltLaunch build_launch(RunEnv& E, const LaunchSpec& L) {
     }
     B.spec.decode = decode_allowed(a, L, A, B.spec, ng);
     B.spec.row_loops = tuning().row_loops && row_loops_allowed(a, L, A, B.spec, ng, nvars);
-    B.spec.decode_ring = tuning().decode_ring ? tuning().decode_ring : decode_ring_for(a.decode.d, a.decode.g);
-    B.spec.decode_waves = tuning().decode_waves ? tuning().decode_waves : decode_waves_for(a.decode.d, a.decode.g);
+    B.spec.decode_ring = tuning().decode_ring ? tuning().decode_ring : decode_ring_for(a.decode.d, a.decode.g, a.decode.f32);
+    B.spec.decode_waves = tuning().decode_waves ? tuning().decode_waves : decode_waves_for(a.decode.d, a.decode.g, a.decode.f32);
     B.spec.decode_ordered = tuning().decode_ordered;
     B.spec.vec_width = a.family == Family::RowProgram ? pick_vec_width(a, A, nvars) : 1;
     B.spec.threads = tuning().tile_threads;
@@ -1738,8 +1742,8 @@ int ptowsp_hip_precompile(ptowsp_program* P, int index, int flags, const char** 
             spec.nontemporal = tuning().nontemporal;
             spec.gemm = a.family == Family::Gemm && !spec.serial;
             spec.decode = a.family == Family::Decode && !spec.serial && L.inner.size() == 1;
-            spec.decode_ring = tuning().decode_ring ? tuning().decode_ring : decode_ring_for(a.decode.d, a.decode.g);
-            spec.decode_waves = tuning().decode_waves ? tuning().decode_waves : decode_waves_for(a.decode.d, a.decode.g);
+            spec.decode_ring = tuning().decode_ring ? tuning().decode_ring : decode_ring_for(a.decode.d, a.decode.g, a.decode.f32);
+            spec.decode_waves = tuning().decode_waves ? tuning().decode_waves : decode_waves_for(a.decode.d, a.decode.g, a.decode.f32);
             spec.decode_ordered = tuning().decode_ordered;
             spec.decode_norm = spec.decode && (flags & 32) != 0;
             spec.indirect_count.assign(L.targs.size(), 0);

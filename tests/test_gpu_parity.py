@@ -518,10 +518,10 @@ def test_bgemm_f16_mfma_device_tensors(gpu):
 
 
 # ---------------------------------------------------------------- paged GQA decode
-def _decode_case(lengths, hkv, group, d, page=16, seed=0, masked=True, f16=False):
-    ga = W.paged_decode_arrays(lengths, hkv, group, d, page=page, seed=seed, f16=f16)
+def _decode_case(lengths, hkv, group, d, page=16, seed=0, masked=True, f16=False, f32=False):
+    ga = W.paged_decode_arrays(lengths, hkv, group, d, page=page, seed=seed, f16=f16, f32=f32)
     ca = {k: v.copy() for k, v in ga.items()}
-    dt = W.F16 if f16 else W.BF16
+    dt = W.F32 if f32 else W.F16 if f16 else W.BF16
     prog = run_hip(W.paged_decode(ga, masked=masked, dtype=dt))
     ref = run_workload(W.paged_decode(ca, masked=masked, dtype=dt))
     return prog, ref, ga, ca
@@ -561,6 +561,27 @@ def test_paged_decode_wide_units(gpu, lengths, hkv, group, d, page):
     for k in ("m", "l", "o", "out"):
         np.testing.assert_allclose(ga[k], ca[k], rtol=2e-5, atol=2e-5 * float(np.abs(ca[k]).max()), err_msg=k)
     assert _rel_fro(ga["out"], W.paged_decode_ref(ga)) <= 1e-5
+    assert prog.stats.total_cycles == ref.total_cycles and prog.stats.task_count == ref.task_count
+
+
+@pytest.mark.parametrize("lengths,hkv,group,d,page,masked", [
+    ([37, 16, 200, 1, 256, 513], 2, 4, 128, 16, True),   # partial, exact, single-token and multi-page sequences
+    ([300, 77, 0], 1, 8, 64, 32, True),                   # head dim 64, sub-pages, an empty sequence
+    ([129, 40, 700], 2, 16, 128, 8, True),                # 16 rows, 8-token pages two to a step
+    ([64, 160, 32], 2, 1, 128, 16, False),                # unmasked, one query row
+])
+def test_paged_decode_f32(gpu, lengths, hkv, group, d, page, masked):
+    """f32 q / K / V (the reference's own dtype) on the decode family: scores and p @ v on
+    v_mfma_f32_16x16x4_f32, against the oracle and float64 attention."""
+    prog, ref, ga, ca = _decode_case(lengths, hkv, group, d, page=page, seed=len(lengths) + d, masked=masked, f32=True)
+    assert prog._native.kernel_family("decode_page") == "decode"
+    for k in ("m", "l", "o", "out"):
+        fin = np.isfinite(ca[k])
+        assert np.array_equal(fin, np.isfinite(ga[k])), k
+        np.testing.assert_allclose(ga[k][fin], ca[k][fin], rtol=2e-5, atol=2e-5 * float(np.abs(ca[k][fin]).max()), err_msg=k)
+    live = np.asarray(lengths) > 0
+    if masked or all(n % page == 0 for n in lengths):
+        assert _rel_fro(ga["out"][live], W.paged_decode_ref(ga)[live]) <= 1e-5
     assert prog.stats.total_cycles == ref.total_cycles and prog.stats.task_count == ref.task_count
 
 

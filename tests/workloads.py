@@ -319,9 +319,9 @@ def paged_decode(arrs: dict, scale: float | None = None, masked: bool = True, dt
 
 
 def paged_decode_arrays(lengths, hkv: int, group: int, d: int, page: int = 16, seed: int = 0,
-                        spare_pages: int = 3, f16: bool = False) -> dict:
-    """Seeded numpy inputs: bf16 q / K / V ~ N(0,1); page table = a random permutation of the
-    physical pages (plus a few never-referenced spares)."""
+                        spare_pages: int = 3, f16: bool = False, f32: bool = False) -> dict:
+    """Seeded numpy inputs: bf16 (f16, f32) q / K / V ~ N(0,1); page table = a random permutation
+    of the physical pages (plus a few never-referenced spares)."""
     rng = np.random.default_rng(seed)
     lengths = np.asarray(lengths, np.int64)
     B = len(lengths)
@@ -338,7 +338,9 @@ def paged_decode_arrays(lengths, hkv: int, group: int, d: int, page: int = 16, s
         off += n
         t = np.arange(max_pages * page).reshape(max_pages, page)
         mask[b, :, 0, :] = np.where(t < lengths[b], 0.0, 1e30)
-    if f16:
+    if f32:
+        bf = lambda shape: rng.standard_normal(shape).astype(np.float32)
+    elif f16:
         bf = lambda shape: rng.standard_normal(shape).astype(np.float16)
     else:
         bf = lambda shape: bf16_round(rng.standard_normal(shape).astype(np.float32))
@@ -385,7 +387,8 @@ def paged_decode_torch(dev, batch: int, hq: int, hkv: int, d: int, lmin: int, lm
 
 def paged_decode_ref(arrs: dict) -> np.ndarray:
     """float64 softmax(q k^T / sqrt(d)) v over each sequence's valid tokens."""
-    up = (lambda x: x.astype(np.float64)) if arrs["q"].dtype == np.float16 else (lambda x: bf16_to_f32(x).astype(np.float64))
+    up = ((lambda x: x.astype(np.float64)) if arrs["q"].dtype in (np.float16, np.float32)
+          else (lambda x: bf16_to_f32(x).astype(np.float64)))
     q, kc, vc = up(arrs["q"]), up(arrs["k_cache"]), up(arrs["v_cache"])
     B, Hkv, G, D = q.shape
     page = kc.shape[2]
