@@ -203,3 +203,64 @@ def test_paged_decode_32_token_pages_full(gpu):
         del k, v, s, ref, got
     del t
     torch.cuda.empty_cache()
+
+
+def test_config3_bgemm_f32_full(gpu):
+    """The C4 shape with f32 A and B (the f32 MFMA block): every batch against float64,
+    per element within K * 2^-24 * (|A| |B|) and per batch at rel-Frobenius 1e-5."""
+    import torch
+
+    dev = torch.device("cuda:0")
+    g = torch.Generator(device=dev)
+    g.manual_seed(1)
+    a = torch.rand((64, 2048, 2048), generator=g, device=dev) * 2 - 1
+    b = torch.rand((64, 2048, 2048), generator=g, device=dev) * 2 - 1
+    c = torch.zeros((64, 2048, 2048), device=dev, dtype=torch.float32)
+    prog = W.rr4(W.bgemm({"a": a, "b": b, "c": c}, 128, 128, 64, W.F32)).compile(target="hip_gfx950")
+    assert prog._native.kernel_family("gemm_tile") == "gemm"
+    prog.execute()
+    prog.synchronize()
+    gamma = 2048 * 2.0 ** -24
+    for bi in range(64):
+        a64, b64 = a[bi].double(), b[bi].double()
+        ref = a64 @ b64
+        err = (c[bi].double() - ref).abs()
+        bound = gamma * (a64.abs() @ b64.abs())
+        assert bool((err <= bound).all()), (bi, float((err / bound.clamp_min(1e-300)).max()))
+        assert float((c[bi].double() - ref).norm() / ref.norm()) <= 1e-5, bi
+        del a64, b64, ref, err, bound
+    # Oracle on a slice: batch 0, m-tiles 0-1, all n, all k.
+    c0 = np.zeros((1, 256, 2048), np.float32)
+    run_workload(W.bgemm({"a": a[:1, :256].cpu().numpy(), "b": b[:1].cpu().numpy(), "c": c0}, 128, 128, 64, W.F32))
+    got = c[0, :256].cpu().numpy()
+    assert float(np.linalg.norm(got - c0[0]) / np.linalg.norm(c0[0])) <= 1e-5
+    del a, b, c
+    torch.cuda.empty_cache()
+
+
+def test_config4_paged_decode_f32_full(gpu):
+    """The C5 shape with f32 q / K / V: every sequence and KV head against float64
+    attention, rel-Frobenius <= 1e-5 per (sequence, KV head)."""
+    import torch
+
+    dev = torch.device("cuda:0")
+    t = W.paged_decode_torch(dev, 64, 32, 8, 128, 512, 8192, seed=2, f32=True)
+    prog = W.rr4(W.paged_decode(t, dtype=W.F32)).compile(target="hip_gfx950")
+    assert prog._native.kernel_family("decode_page") == "decode"
+    prog.execute()
+    prog.synchronize()
+    lengths, out = t["lengths"], t["out"]
+    npg = (lengths + 15) // 16
+    for b in range(64):
+        L, n = int(lengths[b]), int(npg[b])
+        pages = t["page_table"][b, :n].long()
+        k = t["k_cache"][pages].double().permute(1, 0, 2, 3).reshape(8, n * 16, 128)[:, :L]
+        v = t["v_cache"][pages].double().permute(1, 0, 2, 3).reshape(8, n * 16, 128)[:, :L]
+        s = torch.matmul(t["q"][b].double(), k.transpose(1, 2).contiguous()) / (128 ** 0.5)
+        ref = torch.matmul(torch.softmax(s, dim=-1), v)
+        got = out[b].double()
+        for g in range(8):
+            assert float((got[g] - ref[g]).norm() / ref[g].norm()) <= 1e-5, (b, g)
+        del k, v, s, ref, got
+    del t
+    torch.cuda.empty_cache()

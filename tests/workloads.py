@@ -352,9 +352,9 @@ def paged_decode_arrays(lengths, hkv: int, group: int, d: int, page: int = 16, s
 
 
 def paged_decode_torch(dev, batch: int, hq: int, hkv: int, d: int, lmin: int, lmax: int, seed: int = 0,
-                       page: int = 16) -> dict:
+                       page: int = 16, f32: bool = False) -> dict:
     """Config-5 sized inputs on the device: lengths ~ U[lmin, lmax] and a permuted page
-    table from numpy (seeded), bf16 q / K / V ~ N(0,1) from torch's device RNG."""
+    table from numpy (seeded), bf16 (f32) q / K / V ~ N(0,1) from torch's device RNG."""
     import torch
 
     rng = np.random.default_rng(seed)
@@ -375,9 +375,10 @@ def paged_decode_torch(dev, batch: int, hq: int, hkv: int, d: int, lmin: int, lm
     g = torch.Generator(device=dev)
     g.manual_seed(seed)
     kv = (total, hkv, page, d)
-    return {"q": torch.randn((batch, hkv, G, d), generator=g, device=dev, dtype=torch.bfloat16),
-            "k_cache": torch.randn(kv, generator=g, device=dev, dtype=torch.bfloat16),
-            "v_cache": torch.randn(kv, generator=g, device=dev, dtype=torch.bfloat16),
+    dt = torch.float32 if f32 else torch.bfloat16
+    return {"q": torch.randn((batch, hkv, G, d), generator=g, device=dev, dtype=dt),
+            "k_cache": torch.randn(kv, generator=g, device=dev, dtype=dt),
+            "v_cache": torch.randn(kv, generator=g, device=dev, dtype=dt),
             "page_table": torch.from_numpy(pt).to(dev), "npages": torch.from_numpy(npages.astype(np.int32)).to(dev),
             "mask": torch.from_numpy(mask).to(dev),
             "m": torch.full((batch, hkv, G, 1), float("-inf"), device=dev),
