@@ -543,25 +543,46 @@ EmittedKernel emit_tile(const Module& m, const KernelAnalysis& a, const LaunchSp
             }
     }
     auto tile_bytes = [&](int id) { return static_cast<size_t>(a.by_id[id]->rows) * a.by_id[id]->cols * (is_int_v(id) ? 8 : 4); };
-    std::vector<int> order(lds_vals.begin(), lds_vals.end());
-    std::stable_sort(order.begin(), order.end(), [&](int x, int y) { return tile_bytes(x) > tile_bytes(y); });
-    std::map<int, size_t> lds_off;
-    size_t pool = 0;
-    for (int id : order) {
-        const size_t sz = (tile_bytes(id) + 15) & ~static_cast<size_t>(15);
-        std::vector<std::pair<size_t, size_t>> busy;
-        for (const auto& [q, off] : lds_off)
-            if (life[q].first <= life[id].second && life[id].first <= life[q].second) busy.push_back({off, off + ((tile_bytes(q) + 15) & ~static_cast<size_t>(15))});
-        std::sort(busy.begin(), busy.end());
-        size_t off = 0;
-        for (const auto& [lo, hi] : busy)
-            if (off + sz > lo && off < hi) off = hi;
-        lds_off[id] = off;
-        pool = std::max(pool, off + sz);
-    }
-    size_t lds = pool;
+    // First-fit placement of a set of tiles by lifetime (largest first).
+    auto place = [&](const std::vector<int>& ids, std::map<int, size_t>& offs) {
+        std::vector<int> order(ids);
+        std::stable_sort(order.begin(), order.end(), [&](int x, int y) { return tile_bytes(x) > tile_bytes(y); });
+        size_t top = 0;
+        for (int id : order) {
+            const size_t sz = (tile_bytes(id) + 15) & ~static_cast<size_t>(15);
+            std::vector<std::pair<size_t, size_t>> busy;
+            for (const auto& [q, off] : offs)
+                if (life[q].first <= life[id].second && life[id].first <= life[q].second)
+                    busy.push_back({off, off + ((tile_bytes(q) + 15) & ~static_cast<size_t>(15))});
+            std::sort(busy.begin(), busy.end());
+            size_t off = 0;
+            for (const auto& [lo, hi] : busy)
+                if (off + sz > lo && off < hi) off = hi;
+            offs[id] = off;
+            top = std::max(top, off + sz);
+        }
+        return top;
+    };
+    size_t staged_bytes = 0;
     for (const auto& p : k.params)
-        if (staged_id(p.id)) lds += static_cast<size_t>(SB) * a.by_id[p.id]->rows * a.by_id[p.id]->cols * (is_int_v(p.id) ? 8 : 4);
+        if (staged_id(p.id)) staged_bytes += static_cast<size_t>(SB) * a.by_id[p.id]->rows * a.by_id[p.id]->cols * (is_int_v(p.id) ? 8 : 4);
+    // Tiles that do not fit in LDS go to a per-workgroup global scratch
+    // (largest first, until the rest fits beside the staged params).
+    std::vector<int> in_lds(lds_vals.begin(), lds_vals.end()), in_glob;
+    std::map<int, size_t> lds_off, glob_off;
+    size_t pool = place(in_lds, lds_off);
+    while (pool + staged_bytes > 160 * 1024 && !in_lds.empty()) {
+        auto big = std::max_element(in_lds.begin(), in_lds.end(), [&](int x, int y) { return tile_bytes(x) < tile_bytes(y); });
+        in_glob.push_back(*big);
+        in_lds.erase(big);
+        lds_off.clear();
+        pool = place(in_lds, lds_off);
+    }
+    const size_t gpool = in_glob.empty() ? 0 : place(in_glob, glob_off);
+    const bool glob_tiles = gpool > 0 && ntens < kMaxParams;
+    if (gpool > 0 && !glob_tiles)
+        throw CompileError("kernel " + k.name + ": tiles exceed the 160 KiB of LDS and the launch has no argument slot left for global tiles");
+    size_t lds = pool + staged_bytes;
     // Matmul ops of MFMA shape run on the matrix cores (tile_mma), with a
     // 32-row operand scratch per wave, when that scratch fits beside the tiles.
     auto mma_shape = [&](const OpInfo& op) {
@@ -586,6 +607,7 @@ EmittedKernel emit_tile(const Module& m, const KernelAnalysis& a, const LaunchSp
     ek.row_program = false;
     ek.threads = spec.threads;
     ek.lds_bytes = lds;
+    ek.gtile_bytes = glob_tiles ? gpool : 0;
     std::ostringstream o;
     o << "#include \"ptowsp_device.h\"\nusing namespace ptowsp;\n";
     o << "// tile program: kernel " << k.name;
@@ -596,9 +618,15 @@ EmittedKernel emit_tile(const Module& m, const KernelAnalysis& a, const LaunchSp
     o << "  constexpr int NT = " << spec.threads << ";\n";
     if (pool > 0) o << "  __shared__ __attribute__((aligned(16))) char pool_[" << pool << "];\n";
     if (use_mma) o << "  __shared__ __attribute__((aligned(16))) float mma_scratch_[" << mma_scratch / 4 << "];\n";
+    // Global tiles: workgroup blockIdx.x's region of base[ntens]; the
+    // workgroup barriers between ops order these accesses as they do LDS.
+    if (glob_tiles) o << "  char* const gtile_ = A.base[" << ntens << "] + (i64)blockIdx.x * " << gpool << ";\n";
     for (int id : lds_vals) {
         const char* ty = is_int_v(id) ? "i64" : "float";
-        o << "  " << ty << "* const L" << id << " = reinterpret_cast<" << ty << "*>(pool_ + " << lds_off[id] << ");\n";
+        if (glob_off.count(id))
+            o << "  " << ty << "* const L" << id << " = reinterpret_cast<" << ty << "*>(gtile_ + " << glob_off[id] << ");\n";
+        else
+            o << "  " << ty << "* const L" << id << " = reinterpret_cast<" << ty << "*>(pool_ + " << lds_off[id] << ");\n";
     }
     for (const auto& p : k.params)
         if (staged_id(p.id)) {

@@ -77,6 +77,10 @@ struct EmittedKernel {
     int tasks_per_block = 1;    // GEMM: tasks merged into one workgroup
     int part_floats = 0;        // decode: floats per partial (m, l, o of one unit)
     size_t lds_bytes = 0;
+    // Tile programs: bytes of global scratch per workgroup for the tiles that
+    // do not fit in LDS (base[ntens] of the launch; the grid is capped so
+    // that blocks x gtile_bytes stays bounded).
+    size_t gtile_bytes = 0;
 };
 
 EmittedKernel emit_launch(const Module& m, const KernelAnalysis& a, const LaunchSpec& L, const EmitSpec& spec);

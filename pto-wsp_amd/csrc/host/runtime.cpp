@@ -105,6 +105,8 @@ struct ptowsp_program {
     std::string precompiled_source;
     void* scratch = nullptr;  // decode: unit counters and partials
     size_t scratch_bytes = 0;
+    void* gtile = nullptr;    // tile programs: tiles beyond LDS, one region per workgroup
+    size_t gtile_bytes = 0;
     // Task lists of masked launches: pinned host chunks copied into device
     // chunks on the launch stream; reused from the start at every run (the
     // previous run has been synchronized by then).
@@ -143,6 +145,7 @@ struct ptowsp_program {
         }
         if (slot_stage) (void)hipHostFree(slot_stage);
         if (scratch) (void)hipFree(scratch);
+        if (gtile) (void)hipFree(gtile);
         for (void* b : stage_buf)
             if (b) (void)hipFree(b);
         if (h_err) (void)hipHostFree(h_err);
@@ -224,6 +227,10 @@ struct RunEnv {
     char* nscratch = nullptr;
     size_t nscratch_limit = 0;
 };
+
+// Workgroups of a tile-program launch whose tiles exceed LDS (each has its
+// own region of global tile scratch).
+constexpr int64_t kGlobalTileBlocks = 1024;
 
 // Device time starts at the program's first kernel: host work that precedes
 // it (building launch arguments, compiling) is not counted.
@@ -1211,6 +1218,30 @@ void enqueue_built(RunEnv& E, int li, BuiltLaunch& B, hipStream_t stream, uint64
         blocks = std::min<int64_t>(blocks, int64_t(1) << 20);
     }
     blocks = std::max<int64_t>(1, blocks);
+    if (ek.gtile_bytes > 0) {
+        // Tiles beyond LDS live in global scratch, one region per workgroup;
+        // the kernel walks its tasks grid-stride, so the grid is capped (four
+        // workgroups per CU of the MI355X).
+        blocks = std::min<int64_t>(blocks, kGlobalTileBlocks);
+        const int ntens = static_cast<int>(P->ka[L.kernel].tensor_param_index.size());
+        const size_t need = static_cast<size_t>(blocks) * ek.gtile_bytes;
+        if (E.nscratch)
+            throw std::runtime_error("ptowsp_hip_launch_noalloc: launch " + std::to_string(li) +
+                                     " keeps tiles beyond LDS in global scratch, which this entry point does not provide");
+        if (need > P->gtile_bytes) {
+            // Earlier launches of this run may still use the smaller region.
+            if (P->gtile) {
+                check(hipDeviceSynchronize(), "hipDeviceSynchronize");
+                check(hipFree(P->gtile), "hipFree(tile scratch)");
+            }
+            P->gtile = nullptr;
+            P->gtile_bytes = 0;
+            check(hipMalloc(&P->gtile, need), "hipMalloc(tile scratch)");
+            P->gtile_bytes = need;
+        }
+        B.args.base[ntens] = static_cast<char*>(P->gtile);
+        B.args.span[ntens] = static_cast<int64_t>(need / sizeof(float));
+    }
     void* params[] = {&B.args};
     launch_kernel(E, jk->function, blocks, ek.threads, 0, stream, params, "hipModuleLaunchKernel");
     ++launches;

@@ -152,6 +152,24 @@ def test_tiled_attention_mfma_tiles(gpu):
     assert prog.stats.total_cycles == ref.total_cycles
 
 
+def test_tiled_attention_tiles_beyond_lds(gpu):
+    """256-token attention tiles (scores 256 x 256 f32 = 256 KiB): the tiles that do not
+    fit in LDS live in a per-workgroup global scratch; results as the oracle's."""
+    rng = np.random.default_rng(5)
+    q, k, v = (rng.standard_normal((1, 2, 512, 64), dtype=np.float32) for _ in range(3))
+    ga, ca = W.attention_arrays(q, k, v, 256), W.attention_arrays(q, k, v, 256)
+    prog = run_hip(W.rr4(W.tiled_attention(ga, 256)))
+    ref = run_workload(W.rr4(W.tiled_attention(ca, 256)))
+    assert "gtile_" in prog._native.precompile(0)
+    assert _rel_fro(ga["o"], ca["o"]) <= 1e-5
+    q64, k64, v64 = (x.astype(np.float64).reshape(1, 2, 2, 256, 64) for x in (q, k, v))
+    s = q64 @ k64.transpose(0, 1, 2, 4, 3) / 8.0
+    w = np.exp(s - s.max(-1, keepdims=True))
+    exact = ((w / w.sum(-1, keepdims=True)) @ v64).reshape(1, 2, 512, 64)
+    assert _rel_fro(ga["o"], exact) <= 1e-5
+    assert prog.stats.total_cycles == ref.total_cycles
+
+
 def test_llama_block_mfma_tiles(gpu):
     """examples/llama with 64-token tiles, d = 64 and a 128-wide MLP: the attention and
     ReLU-MLP tiles' four matmuls (K = 64 and 128) run on the matrix cores."""

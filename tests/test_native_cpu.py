@@ -213,6 +213,19 @@ def test_tile_program_matmul_on_matrix_cores():
             assert "tile_mma<64, 64, 64, NT>" in src and "mma_scratch_[" in src
 
 
+def test_tile_program_tiles_beyond_lds_go_to_global_scratch():
+    """A fused tile whose tiles exceed the 160 KiB of LDS (256-token attention: 256 x 256
+    f32 scores) keeps the largest ones in a per-workgroup global scratch instead of
+    failing to compile; 64-token tiles stay in LDS."""
+    from pto_wsp._hip import NativeProgram
+
+    for ts, glob in ((256, True), (64, False)):
+        q = np.zeros((1, 2, 512, 64), np.float32)
+        arrs = W.attention_arrays(q, q, q, ts)
+        src = NativeProgram(workload_to_codegen_ir(W.tiled_attention(arrs, ts), "a").module).precompile(0)
+        assert ("gtile_" in src) == glob
+
+
 def test_decode_precompile_folded_normalisation():
     """precompile(decode_norm=True) emits the form a run uses when `out = o / l`
     follows the decode launch: the completion writes out, and units without pages
