@@ -78,8 +78,9 @@ int ptowsp_hip_launch(ptowsp_program* prog, RuntimeContext* ctx, void* hip_strea
  * kernel was already built and loaded by an earlier ptowsp_hip_launch of
  * the same program (same bindings), which also resolves the device's
  * scratch and loads the kernel that clears it (without one on this device
- * the call is refused); no cpp_src kernels, slot loads or masked
- * (cond-on-grid) launches.  It is not made for HIP stream capture: it
+ * the call is refused); no cpp_src kernels, slot loads, masked
+ * (cond-on-grid) launches or tile programs whose tiles exceed LDS (those
+ * keep tiles in an allocated global scratch).  It is not made for HIP stream capture: it
  * records timing events and may read index tensors with synchronous
  * copies.  All no-allocation runs on one GPU share its scratch: runs that
  * overlap in time on one GPU race and must not be issued.  Finish with
