@@ -1,12 +1,13 @@
 """Random paged-decode launches against the oracle.
 
 Each seed draws the query rows per KV head (1..16, or 17..48 at head dim 64
-and 128 for a fifth of the seeds), the head dim (64, 128, 256), the KV heads, 1..24 sequences whose lengths
-mix empty, sub-page, exact-page and multi-thousand-token sequences, the page
-size (8, 16, 32, 64: the streaming decode family, which folds pages of more
-than 16 tokens as 16-token sub-pages and 8-token pages two to a 16-token
-step), the mask, and
-the input dtype (bf16 / f16).  The GPU accumulators and output must equal
+and 128 for a fifth of the seeds), the head dim (64, 128, 256), the KV
+heads, 1..24 sequences whose lengths mix empty, sub-page, exact-page and
+multi-thousand-token sequences, the page size (8, 16, 32, 64: the streaming
+decode family, which folds pages of more than 16 tokens as 16-token
+sub-pages and 8-token pages two to a 16-token step), the mask, and the
+input dtype (bf16 / f16, or f32 for a fifth of the seeds up to 16 rows and
+head dim 128).  The GPU accumulators and output must equal
 the oracle's within rtol 2e-5 (with an atol of 2e-5 of each tensor's largest
 magnitude: both fold the pages in fp32, split differently), sequences with
 pages must match float64 attention over their valid tokens when masked (and
@@ -34,17 +35,21 @@ def _case(seed):
                else int(rng.integers(page + 1, 3000)) for k in kinds]
     if max(lengths) == 0:
         lengths[0] = 5
-    return dict(lengths=lengths, hkv=int(rng.integers(1, 5)), group=group, d=d, page=page,
-                masked=bool(rng.random() < 0.8), f16=bool(rng.random() < 0.3))
+    c = dict(lengths=lengths, hkv=int(rng.integers(1, 5)), group=group, d=d, page=page,
+             masked=bool(rng.random() < 0.8), f16=bool(rng.random() < 0.3))
+    # f32 q / K / V for about a fifth of the seeds whose shape the f32 form takes
+    c["f32"] = bool(rng.random() < 0.2) and group <= 16 and d <= 128
+    return c
 
 
 @pytest.mark.parametrize("seed", range(24))
 def test_random_decode_matches_oracle(gpu, seed):
     c = _case(seed)
     print(c, flush=True)
-    ga = W.paged_decode_arrays(c["lengths"], c["hkv"], c["group"], c["d"], page=c["page"], seed=seed, f16=c["f16"])
+    ga = W.paged_decode_arrays(c["lengths"], c["hkv"], c["group"], c["d"], page=c["page"], seed=seed, f16=c["f16"],
+                               f32=c["f32"])
     ca = {k: v.copy() for k, v in ga.items()}
-    dt = W.F16 if c["f16"] else W.BF16
+    dt = W.F32 if c["f32"] else W.F16 if c["f16"] else W.BF16
     prog = W.paged_decode(ga, masked=c["masked"], dtype=dt).compile(target="hip_gfx950")
     # (a [1, page] mask with as many query rows as page tokens is a row broadcast, see below)
     want_family = "tile_program" if c["masked"] and c["group"] == c["page"] else "decode"
