@@ -84,12 +84,13 @@ def row_workload(kind, X, Y):
     return rr4(wl())
 
 
-def bgemm_workload(A, Bm, C, tm=128, tn=128, tk=64, f32_inputs=False):
+def bgemm_workload(A, Bm, C, tm=128, tn=128, tk=64, f32_inputs=False, f16_inputs=False):
     """examples/bgemm pattern: C[b] += A[b] @ B[b] with a P.seq K loop and an InOut fp32 tile
-    (bf16 A / B, or f32 with f32_inputs)."""
+    (bf16 A / B, or f32 / f16 with f32_inputs / f16_inputs)."""
     from pto_wsp import DType, Dense, In, InOut, P, Tensor, Tile, kernel, pto, workload
 
-    bf16, f32 = (DType.F32 if f32_inputs else DType.BF16), DType.F32
+    bf16 = DType.F32 if f32_inputs else DType.F16 if f16_inputs else DType.BF16  # A / B dtype
+    f32 = DType.F32
     nb, M, K = tuple(A.shape)
     N = Bm.shape[2]
 
@@ -463,23 +464,27 @@ class RowCase:
 class GemmCase:
     unit, bound = "TFLOP/s", "mfma"
 
-    def __init__(self, name, nb, m, n, k, seed, baseline_config, f32_inputs=False):
+    def __init__(self, name, nb, m, n, k, seed, baseline_config, f32_inputs=False, tile=(128, 128, 64), dtype="bf16"):
         self.name, self.nb, self.m, self.n, self.k, self.seed = name, nb, m, n, k, seed
         self.baseline_config = baseline_config
         self.shape = (nb, m, k)
         self.f32_inputs = f32_inputs
-        self.dtype = "f32" if f32_inputs else "bf16"
+        self.tile = tile
+        self.in_dtype = "f32" if f32_inputs else dtype
+        self.dtype = self.in_dtype
 
     def setup(self, dev):
         import torch
 
         g = torch.Generator(device=dev)
         g.manual_seed(self.seed)
-        dt = torch.float32 if self.f32_inputs else torch.bfloat16
+        dt = {"f32": torch.float32, "f16": torch.float16, "bf16": torch.bfloat16}[self.in_dtype]
         self.a = (torch.rand((self.nb, self.m, self.k), generator=g, device=dev) * 2 - 1).to(dt)
         self.b = (torch.rand((self.nb, self.k, self.n), generator=g, device=dev) * 2 - 1).to(dt)
         self.c = torch.zeros((self.nb, self.m, self.n), device=dev, dtype=torch.float32)
-        self.prog = bgemm_workload(self.a, self.b, self.c, f32_inputs=self.f32_inputs).compile(target="hip_gfx950")
+        tm, tn, tk = self.tile
+        self.prog = bgemm_workload(self.a, self.b, self.c, tm, tn, tk, f32_inputs=self.f32_inputs,
+                                   f16_inputs=self.in_dtype == "f16").compile(target="hip_gfx950")
         self.work = 2.0 * self.nb * self.m * self.n * self.k  # FLOP per step
 
     def peak(self):
@@ -489,8 +494,9 @@ class GemmCase:
         return self.work / seconds / 1e12
 
     def describe(self):
+        tm, tn, tk = self.tile
         return (f"{self.name}: C[b] += A[b] @ B[b], A,B[{self.nb},{self.m},{self.k}] {self.dtype} U(-1,1), C fp32, "
-                "tiles 128x128 K-step 64, P(batch) x P(m_tiles) x P(n_tiles) x P.seq(k)")
+                f"tiles {tm}x{tn} K-step {tk}, P(batch) x P(m_tiles) x P(n_tiles) x P.seq(k)")
 
     def cpu(self, budget_s):
         """Oracle on a bounded sample: batch 0, the first 2 m-tiles (all n, all k), from C = 0."""
@@ -501,14 +507,15 @@ class GemmCase:
         del budget_s
         import torch
 
-        if self.f32_inputs:
+        if self.in_dtype in ("f32", "f16"):
             a0, b0 = self.a[:1, :256].contiguous().cpu().numpy(), self.b[:1].contiguous().cpu().numpy()
         else:
             a0 = self.a[:1, :256].contiguous().view(torch.int16).cpu().numpy().view(np.uint16)
             b0 = self.b[:1].contiguous().view(torch.int16).cpu().numpy().view(np.uint16)
         c0 = np.zeros((1, 256, self.n), np.float32)
+        tm, tn, tk = self.tile
         t0 = time.perf_counter()
-        run_workload(bgemm_workload(a0, b0, c0, f32_inputs=self.f32_inputs))
+        run_workload(bgemm_workload(a0, b0, c0, tm, tn, tk, f32_inputs=self.f32_inputs, f16_inputs=self.in_dtype == "f16"))
         sec = time.perf_counter() - t0
         flop = 2.0 * 256 * self.n * self.k
         # GPU result for the same tiles, from a fresh C = 0 run.
@@ -555,9 +562,14 @@ CASES = {
     # Not a BASELINE config: the C4 GEMM with f32 A and B (the reference's own
     # matmul dtype), on the f32 MFMA block.
     "bgemm_f32": lambda: GemmCase("bgemm_f32", 64, 2048, 2048, 2048, 0, None, f32_inputs=True),
+    # Not a BASELINE config: the reference bgemm example's own pattern (16x16x16
+    # f16 tiles) at the C4 shape; the host merges 16 x 16 tasks per block and
+    # 4 K steps per LDS stage.
+    "bgemm_tile16": lambda: GemmCase("bgemm_tile16", 64, 2048, 2048, 2048, 0, None, tile=(16, 16, 16), dtype="f16"),
 }
 EXTRA = ("copy_calib", "softmax3", "softmax3_overlap", "paged_decode_page32", "paged_decode_page64", "paged_decode_page8",
-         "paged_decode_d64", "paged_decode_d256", "paged_decode_g16", "paged_decode_g32", "paged_decode_f32", "bgemm_f32")
+         "paged_decode_d64", "paged_decode_d256", "paged_decode_g16", "paged_decode_g32", "paged_decode_f32", "bgemm_f32",
+         "bgemm_tile16")
 
 
 def load_traffic(name):

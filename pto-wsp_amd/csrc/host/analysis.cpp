@@ -164,10 +164,11 @@ GemmInfo classify_gemm(const KernelDef& k, const KernelAnalysis& a) {
     if (vc->dtype != DType::F32) return g;
     const int M = va->rows, K = va->cols, N = vb->cols;
     const bool f32 = va->dtype == DType::F32;
-    // MFMA block shapes: 64..256 rows / columns, K step a power of two in 16..128,
-    // two LDS stages of A and B within 160 KiB (f32: stages of at most 32 K
-    // columns, gemm_stage_k).
-    if (M % 64 || N % 64 || M > 256 || N > 256) return g;
+    // Task tiles of 16..256 rows / columns (multiples of 16; the host merges
+    // neighbouring tasks into blocks of 64..256, or runs the tile program when
+    // it cannot), K step a power of two in 16..128, two LDS stages of A and B
+    // within 160 KiB (f32: stages of at most 32 K columns, gemm_stage_k).
+    if (M % 16 || N % 16 || M > 256 || N > 256) return g;
     if (K != 16 && K != 32 && K != 64 && K != 128) return g;
     if (2 * (M + N) * gemm_stage_k(K, f32) * (f32 ? 4 : 2) > 160 * 1024) return g;
     g.ok = true;

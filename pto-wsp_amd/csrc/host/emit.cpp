@@ -929,14 +929,16 @@ EmittedKernel emit_gemm(const Module& m, const KernelAnalysis& a, const LaunchSp
     const GemmInfo& g = a.gemm;
     const int ng = static_cast<int>(L.grid.size()), ni = static_cast<int>(L.inner.size());
     const int nvars = ng + ni;
-    const int fm = spec.gemm_vm >= 0 ? 2 : 1, fn = spec.gemm_vn >= 0 ? 2 : 1;
+    const int fm = spec.gemm_vm >= 0 ? spec.gemm_fm : 1, fn = spec.gemm_vn >= 0 ? spec.gemm_fn : 1;
     const int bm = g.m * fm, bn = g.n * fn;
-    // One LDS stage per task K step, two stages (a 4-stage ring of 32-wide
+    // One LDS stage per kf task K steps (kf consecutive steps are adjacent
+    // columns of A and rows of B), two stages (a 4-stage ring of 32-wide
     // stages measured slower on 256x256 blocks: twice the barriers).
     const int wm = gemm_waves_m(), wn = gemm_waves_n(bn);
-    // f32 A / B: stages of at most 32 K columns (GemmF32), a task K step
-    // split over ksplit stages; element size es bytes.
-    const int bk = gemm_stage_k(g.k, g.f32), ns = 2, ksplit = g.k / bk, es = g.f32 ? 4 : 2;
+    const int kf = ni == 1 ? spec.gemm_kf : 1, kstep = g.k * kf;
+    // f32 A / B: stages of at most 32 K columns (GemmF32), a K step split
+    // over ksplit stages; element size es bytes.
+    const int bk = gemm_stage_k(kstep, g.f32), ns = 2, ksplit = kstep / bk, es = g.f32 ? 4 : 2;
     // Ping-pong block: 256x256, K step 32 / 64, row pitches checked on the host.
     const bool pp = !g.f32 && spec.gemm_pingpong && bm == 256 && bn == 256 && (bk == 64 || bk == 32);
     EmittedKernel ek;
@@ -948,6 +950,7 @@ EmittedKernel emit_gemm(const Module& m, const KernelAnalysis& a, const LaunchSp
     o << "// gemm program: kernel " << k.name << ", task tile " << g.m << "x" << g.n << "x" << g.k
       << (g.f32 ? " f32" : g.f16 ? " f16" : " bf16")
       << (g.accumulate ? ", accumulate" : "") << "; block " << bm << "x" << bn << " (" << fm * fn << " tasks)"
+      << (kf > 1 ? "; " + std::to_string(kf) + " K steps per stage" : "")
       << (pp ? ", ping-pong" : "") << "\n";
     ek.entry = entry_name("gemm", k);
     o << "extern \"C\" __global__ void __launch_bounds__(" << ek.threads << ") "
@@ -977,6 +980,9 @@ EmittedKernel emit_gemm(const Module& m, const KernelAnalysis& a, const LaunchSp
     }
     o << "    i64 iters = 1;\n";
     for (int i = 0; i < ni; ++i) o << "    iters *= A.ext[" << ng + i << "];\n";
+    // Merged K steps: iterations count stages of kf task steps (the host has
+    // checked that kf divides the loop).
+    if (kf > 1) o << "    iters /= " << kf << ";\n";
     o << "    if (iters <= 0) return;\n";
     for (int i = 0; i < ni; ++i) o << "    vars[" << ng + i << "] = 0;\n";
     o << "    const u16* pa = reinterpret_cast<const u16*>(A.base[" << g.a << "] + (" << offset_expr(g.a, nvars, 0, 0) << ") * " << es
@@ -989,8 +995,8 @@ EmittedKernel emit_gemm(const Module& m, const KernelAnalysis& a, const LaunchSp
     if (ni == 1) {
         // One in-kernel loop: 32-bit byte steps (the host bounds every
         // offset below 2^31).
-        o << "    const int da_ = static_cast<int>(A.coef[" << g.a << "][" << ng << "] * " << es << "), db_ = static_cast<int>(A.coef["
-          << g.b << "][" << ng << "] * " << es << ");\n";
+        o << "    const int da_ = static_cast<int>(A.coef[" << g.a << "][" << ng << "] * " << es * kf << "), db_ = static_cast<int>(A.coef["
+          << g.b << "][" << ng << "] * " << es * kf << ");\n";
         o << "    auto off = [=](i64 it, int& soa, int& sob) { soa = static_cast<int>(it) * da_; sob = static_cast<int>(it) * db_; };\n";
     } else {
         o << "    auto off = [&](i64 it, int& soa, int& sob) {\n";

@@ -41,6 +41,10 @@ struct EmitSpec {
     // GEMM: grid variables whose neighbouring tasks are merged into one
     // workgroup block (factor 2 along rows / columns of C), or -1.
     int gemm_vm = -1, gemm_vn = -1;
+    // GEMM: tasks per block along those variables (powers of two), and task
+    // K steps per LDS stage (consecutive steps whose A columns and B rows
+    // are adjacent, in the accumulate form).
+    int gemm_fm = 1, gemm_fn = 1, gemm_kf = 1;
     // GEMM: 256x256 blocks with K step 32 or 64 and A / B row pitches that
     // are multiples of 64 elements run as a two-group ping-pong block.
     bool gemm_pingpong = false;

@@ -616,6 +616,7 @@ uint32_t grid_write_hazard(const KernelAnalysis& a, const LaunchSpec& L, const L
 // direct buffer->LDS loads of the GEMM block.
 bool gemm_allowed(const KernelAnalysis& a, const LaunchSpec& L, const LaunchArgs& A, EmitSpec& spec, int ng, int nvars) {
     spec.gemm_vm = spec.gemm_vn = -1;
+    spec.gemm_fm = spec.gemm_fn = spec.gemm_kf = 1;
     spec.gemm_pingpong = false;
     if (a.family != Family::Gemm || spec.serial) return false;
     for (int c : spec.indirect_count)
@@ -638,20 +639,46 @@ bool gemm_allowed(const KernelAnalysis& a, const LaunchSpec& L, const LaunchArgs
     if (L.targs[g.a]->tid == tc || L.targs[g.b]->tid == tc) return false;
     // Merge candidates: rows of C move with A's rows, columns with B's.
     const int64_t M = g.m, N = g.n;
+    int vm = -1, vn = -1;
     for (int v = 0; v < ng; ++v) {
         if (A.ext[v] <= 0 || A.ext[v] % 2) continue;
-        if (spec.gemm_vm < 0 && A.coef[g.a][v] == M * A.s3[g.a] && A.coef[g.c][v] == M * A.s3[g.c] && A.coef[g.b][v] == 0)
-            spec.gemm_vm = v;
-        else if (spec.gemm_vn < 0 && A.coef[g.b][v] == N && A.coef[g.c][v] == N && A.coef[g.a][v] == 0)
-            spec.gemm_vn = v;
+        if (vm < 0 && A.coef[g.a][v] == M * A.s3[g.a] && A.coef[g.c][v] == M * A.s3[g.c] && A.coef[g.b][v] == 0)
+            vm = v;
+        else if (vn < 0 && A.coef[g.b][v] == N && A.coef[g.c][v] == N && A.coef[g.a][v] == 0)
+            vn = v;
     }
+    // Task K steps per LDS stage: in the accumulate form with one in-kernel
+    // loop whose consecutive steps are adjacent A columns and B rows, steps
+    // are merged up to 64 columns per stage (32 for f32), dividing the loop.
+    int64_t kf = 1;
+    if (g.accumulate && nvars == ng + 1) {
+        const int v = ng;
+        const int64_t kmax = g.f32 ? 32 : 64;
+        if (A.coef[g.a][v] == g.k && A.coef[g.b][v] == g.k * A.s3[g.b])
+            while (g.k * kf * 2 <= kmax && A.ext[v] % (kf * 2) == 0) kf *= 2;
+    }
+    const int64_t bk = g.k * kf;
     auto lds_fits = [&](int64_t bm, int64_t bn) {
-        return bm <= 256 && bn <= 256 && 2 * (bm + bn) * gemm_stage_k(g.k, g.f32) * es <= 160 * 1024;
+        return bm <= 256 && bn <= 256 && 2 * (bm + bn) * gemm_stage_k(static_cast<int>(bk), g.f32) * es <= 160 * 1024;
     };
-    if (spec.gemm_vm >= 0 && spec.gemm_vn >= 0 && !lds_fits(2 * M, 2 * N)) spec.gemm_vm = -1;
-    if (spec.gemm_vm >= 0 && !lds_fits(2 * M, spec.gemm_vn >= 0 ? 2 * N : N)) spec.gemm_vm = -1;
-    if (spec.gemm_vn >= 0 && !lds_fits(spec.gemm_vm >= 0 ? 2 * M : M, 2 * N)) spec.gemm_vn = -1;
-    const int64_t bm = M * (spec.gemm_vm >= 0 ? 2 : 1), bn = N * (spec.gemm_vn >= 0 ? 2 : 1);
+    // Tasks per block: powers of two along the merge variables (dividing
+    // their extents), growing the smaller side first, up to 256 x 256.
+    int64_t fm = 1, fn = 1;
+    for (;;) {
+        const bool gm = vm >= 0 && M * fm * 2 <= 256 && A.ext[vm] % (fm * 2) == 0 && lds_fits(M * fm * 2, N * fn);
+        const bool gn = vn >= 0 && N * fn * 2 <= 256 && A.ext[vn] % (fn * 2) == 0 && lds_fits(M * fm, N * fn * 2);
+        if (gm && (M * fm <= N * fn || !gn)) fm *= 2;
+        else if (gn) fn *= 2;
+        else break;
+    }
+    const int64_t bm = M * fm, bn = N * fn;
+    // Blocks below the MFMA block shape (64 rows / columns) stay on the tile program.
+    if (bm % 64 || bn % 64 || !lds_fits(bm, bn)) return false;
+    spec.gemm_vm = fm > 1 ? vm : -1;
+    spec.gemm_vn = fn > 1 ? vn : -1;
+    spec.gemm_fm = static_cast<int>(fm);
+    spec.gemm_fn = static_cast<int>(fn);
+    spec.gemm_kf = static_cast<int>(kf);
     // Buffer offsets (32-bit) from a block's step-0 origins.
     int64_t ka = 0, kb = 0;
     for (int v = ng; v < nvars; ++v) {
@@ -661,9 +688,9 @@ bool gemm_allowed(const KernelAnalysis& a, const LaunchSpec& L, const LaunchArgs
     const int64_t lim = int64_t(1) << 31;
     if (A.s3[g.a] >= lim || A.s3[g.b] >= lim || A.s3[g.c] >= lim) return false;
     if (((bm - 1) * A.s3[g.a] + g.k) * es + ka * es >= lim) return false;
-    if (((g.k - 1) * A.s3[g.b] + bn) * es + kb * es >= lim) return false;
+    if (((bk - 1) * A.s3[g.b] + bn) * es + kb * es >= lim) return false;
     if (((bm - 1) * A.s3[g.c] + bn) * 4 >= lim) return false;
-    spec.gemm_pingpong = tuning().gemm_pingpong && !g.f32 && bm == 256 && bn == 256 && (g.k == 64 || g.k == 32) &&
+    spec.gemm_pingpong = tuning().gemm_pingpong && !g.f32 && bm == 256 && bn == 256 && (bk == 64 || bk == 32) &&
                          A.s3[g.a] % 64 == 0 && A.s3[g.b] % 64 == 0;
     return true;
 }
@@ -826,6 +853,7 @@ void apply_masks(RunEnv& E, const LaunchSpec& L, BuiltLaunch& B) {
     B.spec.gemm = false;
     B.spec.gemm_pingpong = false;
     B.spec.gemm_vm = B.spec.gemm_vn = -1;
+    B.spec.gemm_fm = B.spec.gemm_fn = B.spec.gemm_kf = 1;
     B.spec.decode = false;
 }
 
@@ -1029,6 +1057,7 @@ BuiltLaunch build_launch(RunEnv& E, const LaunchSpec& L) {
     B.spec.gemm = gemm_allowed(a, L, A, B.spec, ng, nvars);
     if (!B.spec.gemm) {
         B.spec.gemm_vm = B.spec.gemm_vn = -1;
+        B.spec.gemm_fm = B.spec.gemm_fn = B.spec.gemm_kf = 1;
         B.spec.gemm_pingpong = false;
     }
     B.spec.decode = decode_allowed(a, L, A, B.spec, ng);
@@ -1050,7 +1079,8 @@ BuiltLaunch build_launch(RunEnv& E, const LaunchSpec& L) {
 std::string spec_key(const EmitSpec& s) {
     std::ostringstream o;
     o << "vw" << s.vec_width << (s.serial ? ";serial" + std::to_string(s.seq_mask) : "") << (s.task_list ? ";tl" : "") << ";up" << s.row_up << (s.nontemporal ? ";nt" : "")
-      << (s.row_loops ? ";rl" : "") << (s.gemm ? ";gemm" : "") << ";m" << s.gemm_vm << ";n" << s.gemm_vn << (s.gemm_pingpong ? ";pp" : "")
+      << (s.row_loops ? ";rl" : "") << (s.gemm ? ";gemm" : "") << ";m" << s.gemm_vm << ";n" << s.gemm_vn << ";f" << s.gemm_fm << "x" << s.gemm_fn << "x" << s.gemm_kf
+      << (s.gemm_pingpong ? ";pp" : "")
       << (s.decode ? ";dec" : "")
       << (s.decode_norm ? ";norm" : "") << (s.tile_mma ? ";mma" : "") << ";t" << s.threads << ";r" << s.decode_ring << ";w" << s.decode_waves << (s.decode_ordered ? ";ord" : "")
       << ";i";
@@ -1802,7 +1832,14 @@ int ptowsp_hip_precompile(ptowsp_program* P, int index, int flags, const char** 
                 2 * (2 * a.gemm.m + 2 * a.gemm.n) * a.gemm.k * 2 <= 160 * 1024) {
                 spec.gemm_vm = ng - 2;
                 spec.gemm_vn = ng - 1;
+                spec.gemm_fm = spec.gemm_fn = 2;
                 spec.gemm_pingpong = (flags & 4) && a.gemm.m == 128 && a.gemm.n == 128 && (a.gemm.k == 64 || a.gemm.k == 32);
+            }
+            // Blocks below the MFMA block shape: the tile program.
+            if (spec.gemm && ((a.gemm.m * spec.gemm_fm) % 64 || (a.gemm.n * spec.gemm_fn) % 64)) {
+                spec.gemm = spec.gemm_pingpong = false;
+                spec.gemm_vm = spec.gemm_vn = -1;
+                spec.gemm_fm = spec.gemm_fn = 1;
             }
             const EmittedKernel& ek = emitted_for(P, static_cast<int>(li), spec);
             (void)jit_compile(ek.source);

@@ -88,6 +88,9 @@ def test_example_softmax_three_phase(gpu):
 
 
 def test_example_bgemm_f16(gpu):
+    """examples/bgemm at its own size (16x16x16 f16 tiles, one 64x64 batch): the 4x4 tasks
+    of C merge into one 64x64 MFMA block and the four K steps into one 64-column stage.
+    The MFMA sums the same exact f16 products as the oracle in another order."""
     rng = np.random.default_rng(0)
     a = rng.standard_normal((1, 64, 64), dtype=np.float32).astype(np.float16)
     b = rng.standard_normal((1, 64, 64), dtype=np.float32).astype(np.float16)
@@ -95,8 +98,39 @@ def test_example_bgemm_f16(gpu):
     ca = {"a": a.copy(), "b": b.copy(), "c": np.zeros((1, 64, 64), np.float32)}
     prog = run_hip(W.rr4(W.bgemm(ga)))
     run_workload(W.rr4(W.bgemm(ca)))
-    np.testing.assert_array_equal(ga["c"], ca["c"])
+    assert prog._native.kernel_family("gemm_tile") == "gemm"
+    assert _rel_fro(ga["c"], ca["c"]) <= 1e-5
+    assert _rel_fro(ga["c"], a[0].astype(np.float64) @ b[0].astype(np.float64)) <= 1e-5
     assert prog.stats.total_cycles == 275968
+
+
+@pytest.mark.parametrize("shape,tile,dt", [
+    ((2, 512, 512, 512), 16, "f16"),    # the bgemm example's tiles at scale: 16x16 tasks, 4 K steps per stage
+    ((1, 256, 384, 256), 32, "bf16"),   # 32-wide tasks: 8 x 4 per 256 x 128 block (12 along N)
+    ((2, 512, 256, 256), 16, "f32"),    # f32 16x16 tiles: stages of two K steps
+    ((1, 96, 160, 64), 16, "f16"),      # extents that do not merge to 64: the tile program
+])
+def test_bgemm_small_tiles_merged(gpu, shape, tile, dt):
+    """Task tiles below the MFMA block (the reference's bgemm pattern) merged into
+    64..256 blocks and K-merged stages, against the oracle and float64."""
+    nb, m, n, k = shape
+    rng = np.random.default_rng(m + n + k)
+    a32 = rng.uniform(-1, 1, (nb, m, k)).astype(np.float32)
+    b32 = rng.uniform(-1, 1, (nb, k, n)).astype(np.float32)
+    if dt == "f16":
+        a, b, wdt, up = a32.astype(np.float16), b32.astype(np.float16), W.F16, lambda x: x.astype(np.float64)
+    elif dt == "bf16":
+        a, b, wdt, up = W.bf16_round(a32), W.bf16_round(b32), W.BF16, lambda x: W.bf16_to_f32(x).astype(np.float64)
+    else:
+        a, b, wdt, up = a32, b32, W.F32, lambda x: x.astype(np.float64)
+    c0 = rng.standard_normal((nb, m, n)).astype(np.float32)
+    ga = {"a": a.copy(), "b": b.copy(), "c": c0.copy()}
+    ca = {"a": a.copy(), "b": b.copy(), "c": c0.copy()}
+    prog = run_hip(W.rr4(W.bgemm(ga, tile, tile, tile, wdt)))
+    ref = run_workload(W.rr4(W.bgemm(ca, tile, tile, tile, wdt)))
+    assert _rel_fro(ga["c"], ca["c"]) <= 1e-5
+    assert _rel_fro(ga["c"], c0.astype(np.float64) + up(a) @ up(b)) <= 1e-5
+    assert prog.stats.total_cycles == ref.total_cycles
 
 
 def test_example_decode_attention(gpu):
@@ -198,7 +232,7 @@ def test_tile_program_matmul_shapes(gpu, m, k, n):
     ca = {k_: v.copy() for k_, v in ga.items()}
     prog = run_hip(W.rr4(W.matmul_tile(ga, m, k, n), 1024))
     ref = run_workload(W.rr4(W.matmul_tile(ca, m, k, n), 1024))
-    assert prog._native.kernel_family("mm") == "tile_program"
+    assert "tile program" in prog._native.precompile(0)  # no merge candidates: below the MFMA block
     mma = k % 2 == 0 and (k <= 32 or k % 32 == 0)
     assert _has_tile_mma(prog) == mma
     if mma:

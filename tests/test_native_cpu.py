@@ -142,7 +142,13 @@ def test_family_selection():
     assert prog.kernel_cycles("rmsnorm_tile") == 4 * 2048 + 3 * 16
     a = np.zeros((1, 64, 64), np.float16)
     prog = NativeProgram(workload_to_codegen_ir(W.bgemm({"a": a, "b": a, "c": np.zeros((1, 64, 64), np.float32)}), "g").module)
-    assert prog.kernel_family("gemm_tile") == "tile_program"  # 16x16 tiles: below the MFMA tile minimum
+    # 16x16 tiles (the reference's bgemm example): GEMM family; the host merges neighbouring
+    # tasks into MFMA blocks, and without merge candidates the launch is a tile program
+    assert prog.kernel_family("gemm_tile") == "gemm"
+    src = prog.precompile(0)
+    assert "tile program" in src and "gemm program" not in src
+    src = prog.precompile(0, merged=True)   # 2x2 tasks: 32x32, still below the MFMA block
+    assert "tile program" in src
     a = np.zeros((1, 256, 256), np.uint16)
     prog = NativeProgram(workload_to_codegen_ir(
         W.bgemm({"a": a, "b": a, "c": np.zeros((1, 256, 256), np.float32)}, 128, 128, 64, W.BF16), "g").module)
