@@ -166,11 +166,15 @@ GemmInfo classify_gemm(const KernelDef& k, const KernelAnalysis& a) {
     const bool f32 = va->dtype == DType::F32;
     // Task tiles of 16..256 rows / columns (multiples of 16; the host merges
     // neighbouring tasks into blocks of 64..256, or runs the tile program when
-    // it cannot), K step a power of two in 16..128, two LDS stages of A and B
-    // within 160 KiB (f32: stages of at most 32 K columns, gemm_stage_k).
-    if (M % 16 || N % 16 || M > 256 || N > 256) return g;
-    if (K != 16 && K != 32 && K != 64 && K != 128) return g;
-    if (2 * (M + N) * gemm_stage_k(K, f32) * (f32 ? 4 : 2) > 160 * 1024) return g;
+    // it cannot), or multiples of 256 up to 16384 (split into 256-wide
+    // blocks); K step a power of two in 16..128 or a multiple of 64 (f32: 32)
+    // up to 16384, taken in stages (gemm_stage_k); two LDS stages of A and B
+    // within 160 KiB.
+    auto dim_ok = [](int t) { return (t % 16 == 0 && t >= 16 && t <= 256) || (t % 256 == 0 && t <= 16384); };
+    if (!dim_ok(M) || !dim_ok(N)) return g;
+    const bool k_small = K == 16 || K == 32 || K == 64 || K == 128;
+    if (!k_small && (K % (f32 ? 32 : 64) || K > 16384)) return g;
+    if (2 * (gemm_block_dim(M) + gemm_block_dim(N)) * gemm_stage_k(K, f32) * (f32 ? 4 : 2) > 160 * 1024) return g;
     g.ok = true;
     g.a = a.tensor_ordinal[pa];
     g.b = a.tensor_ordinal[pb];

@@ -24,8 +24,11 @@ enum class RowClass { None, Full, RowVec, RowVecT, ColVec, ColVecT, Scalar };
 // with bf16/f16 a, b and an fp32 c: runs on MFMA with the accumulator on chip.
 // K columns per LDS stage of a GEMM block: the task's K step; f32 A / B
 // stages hold at most 32 columns (a task step of 64 or 128 is split over 2
-// or 4 stages).
-inline int gemm_stage_k(int k, bool f32) { return f32 && k > 32 ? 32 : k; }
+// or 4 stages), bf16 / f16 stages 64 once a step exceeds 128 columns.
+inline int gemm_stage_k(int k, bool f32) { return f32 ? (k > 32 ? 32 : k) : (k > 128 ? 64 : k); }
+// Rows / columns of a GEMM block for a task tile dimension: tiles above 256
+// (multiples of 256) are split into blocks of 256.
+inline int gemm_block_dim(int t) { return t > 256 ? 256 : t; }
 
 struct GemmInfo {
     bool ok = false;

@@ -930,7 +930,9 @@ EmittedKernel emit_gemm(const Module& m, const KernelAnalysis& a, const LaunchSp
     const int ng = static_cast<int>(L.grid.size()), ni = static_cast<int>(L.inner.size());
     const int nvars = ng + ni;
     const int fm = spec.gemm_vm >= 0 ? spec.gemm_fm : 1, fn = spec.gemm_vn >= 0 ? spec.gemm_fn : 1;
-    const int bm = g.m * fm, bn = g.n * fn;
+    // Task tiles above 256 rows / columns run as sm x sn blocks of 256.
+    const int sm = g.m > 256 ? g.m / 256 : 1, sn = g.n > 256 ? g.n / 256 : 1;
+    const int bm = gemm_block_dim(g.m) * fm, bn = gemm_block_dim(g.n) * fn;
     // One LDS stage per kf task K steps (kf consecutive steps are adjacent
     // columns of A and rows of B), two stages (a 4-stage ring of 32-wide
     // stages measured slower on 256x256 blocks: twice the barriers).
@@ -938,13 +940,18 @@ EmittedKernel emit_gemm(const Module& m, const KernelAnalysis& a, const LaunchSp
     const int kf = ni == 1 ? spec.gemm_kf : 1, kstep = g.k * kf;
     // f32 A / B: stages of at most 32 K columns (GemmF32), a K step split
     // over ksplit stages; element size es bytes.
-    const int bk = gemm_stage_k(kstep, g.f32), ns = 2, ksplit = kstep / bk, es = g.f32 ? 4 : 2;
+    const int bk = gemm_stage_k(kstep, g.f32), ns = 2, es = g.f32 ? 4 : 2;
+    // Stages per K step: GemmF32 takes them as its KSPLIT; the bf16 / f16
+    // blocks see each stage as one step of a stage-level offset function
+    // (sks stages per task step).
+    const int ksplit = g.f32 ? kstep / bk : 1, sks = g.f32 ? 1 : kstep / bk;
     // Ping-pong block: 256x256, K step 32 / 64, row pitches checked on the host.
     const bool pp = !g.f32 && spec.gemm_pingpong && bm == 256 && bn == 256 && (bk == 64 || bk == 32);
     EmittedKernel ek;
     ek.threads = 64 * wm * wn;
     ek.row_program = false;
     ek.tasks_per_block = fm * fn;
+    ek.blocks_per_task = sm * sn;
     std::ostringstream o;
     o << "#include \"ptowsp_device.h\"\nusing namespace ptowsp;\n";
     o << "// gemm program: kernel " << k.name << ", task tile " << g.m << "x" << g.n << "x" << g.k
@@ -967,9 +974,14 @@ EmittedKernel emit_gemm(const Module& m, const KernelAnalysis& a, const LaunchSp
     o << "  i64 vars[" << (nvars > 0 ? nvars : 1) << "];\n  (void)vars;\n";
     // One workgroup per block (the host launches every block): nothing of
     // the launch arguments stays live through the K loop.
-    o << "  const i64 nblk = A.ntasks / " << fm * fn << ";\n";
+    o << "  const i64 nblk = A.ntasks / " << fm * fn << " * " << sm * sn << ";\n";
     o << "  {\n    const i64 w = blockIdx.x;\n    if (w >= nblk) return;\n";
     o << "    i64 q_ = xcd_order(w, nblk);\n";
+    if (sm * sn > 1) {
+        // The block's 256 x 256 sub-tile of its task.
+        o << "    const i64 sn_ = q_ % " << sn << "; q_ /= " << sn << ";\n";
+        o << "    const i64 sm_ = q_ % " << sm << "; q_ /= " << sm << ";\n";
+    }
     // Decode the block index over the grid with the merged extents divided.
     for (int v = ng - 1; v >= 0; --v) {
         const int f = v == spec.gemm_vm ? fm : (v == spec.gemm_vn ? fn : 1);
@@ -991,6 +1003,11 @@ EmittedKernel emit_gemm(const Module& m, const KernelAnalysis& a, const LaunchSp
       << ");\n";
     // The output view does not move with the in-kernel loops (checked on the host).
     o << "    float* pc = reinterpret_cast<float*>(A.base[" << g.c << "] + (" << offset_expr(g.c, nvars, 0, 0) << ") * 4);\n";
+    if (sm * sn > 1) {
+        o << "    pa = reinterpret_cast<const u16*>(reinterpret_cast<const char*>(pa) + sm_ * 256 * A.s3[" << g.a << "] * " << es << ");\n";
+        o << "    pb = reinterpret_cast<const u16*>(reinterpret_cast<const char*>(pb) + sn_ * 256 * " << es << ");\n";
+        o << "    pc += sm_ * 256 * A.s3[" << g.c << "] + sn_ * 256;\n";
+    }
     // Byte offsets of in-kernel iteration `it` from iteration 0 (mixed radix over the inner loops).
     if (ni == 1) {
         // One in-kernel loop: 32-bit byte steps (the host bounds every
@@ -1009,6 +1026,15 @@ EmittedKernel emit_gemm(const Module& m, const KernelAnalysis& a, const LaunchSp
         o << "      soa = static_cast<int>(oa * " << es << "); sob = static_cast<int>(ob * " << es << ");\n";
         o << "    };\n";
     }
+    if (sks > 1) {
+        // Stage st: task step st / sks, columns (st % sks) * BK of it.
+        o << "    const i64 ldb_ = A.s3[" << g.b << "];\n";
+        o << "    auto offs = [=](i64 st, int& soa, int& sob) {\n";
+        o << "      off(st / " << sks << ", soa, sob);\n";
+        o << "      const int h_ = static_cast<int>(st % " << sks << ");\n";
+        o << "      soa += h_ * " << bk * es << "; sob += h_ * static_cast<int>(ldb_) * " << bk * es << ";\n";
+        o << "    };\n";
+    }
     if (pp) {
         // L2 touches: the blocks that share an A panel (same m block) split its
         // rows by their n block (8 x 32 rows); those that share a B panel
@@ -1020,9 +1046,11 @@ EmittedKernel emit_gemm(const Module& m, const KernelAnalysis& a, const LaunchSp
         else
             o << "    const int pfa_row = -1, pfb_row = -1;\n";
     }
+    const std::string its = sks > 1 ? "iters * " + std::to_string(sks) : "iters";
+    const std::string it0 = g.accumulate ? "0" : (sks > 1 ? "(iters - 1) * " + std::to_string(sks) : "iters - 1");
     o << "    GB::template run<" << (g.accumulate ? "true" : "false") << ">(lds, pa, static_cast<int>(A.s3[" << g.a
       << "]), pb, static_cast<int>(A.s3[" << g.b << "]), pc, static_cast<int>(A.s3[" << g.c << "]), "
-      << (g.accumulate ? "0" : "iters - 1") << ", iters, off" << (pp ? ", pfa_row, pfb_row" : "") << ");\n";
+      << it0 << ", " << its << ", " << (sks > 1 ? "offs" : "off") << (pp ? ", pfa_row, pfb_row" : "") << ");\n";
     o << "  }\n}\n";
     ek.source = o.str();
     ek.lds_bytes = pp ? static_cast<size_t>((bk == 64 ? 2 : 4) * 512 * bk * 2 + 256) : static_cast<size_t>(ns * (bm + bn) * bk * es);

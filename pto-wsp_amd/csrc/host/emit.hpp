@@ -79,6 +79,7 @@ struct EmittedKernel {
     int waves_per_block = 4;
     bool row_program = false;
     int tasks_per_block = 1;    // GEMM: tasks merged into one workgroup
+    int blocks_per_task = 1;    // GEMM: 256-wide blocks of a task tile above 256
     int part_floats = 0;        // decode: floats per partial (m, l, o of one unit)
     size_t lds_bytes = 0;
     // Tile programs: bytes of global scratch per workgroup for the tiles that

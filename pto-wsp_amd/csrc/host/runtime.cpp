@@ -663,15 +663,17 @@ bool gemm_allowed(const KernelAnalysis& a, const LaunchSpec& L, const LaunchArgs
     };
     // Tasks per block: powers of two along the merge variables (dividing
     // their extents), growing the smaller side first, up to 256 x 256.
+    // Tiles above 256 are split into 256-wide blocks instead.
+    const int64_t M0 = gemm_block_dim(static_cast<int>(M)), N0 = gemm_block_dim(static_cast<int>(N));
     int64_t fm = 1, fn = 1;
     for (;;) {
-        const bool gm = vm >= 0 && M * fm * 2 <= 256 && A.ext[vm] % (fm * 2) == 0 && lds_fits(M * fm * 2, N * fn);
-        const bool gn = vn >= 0 && N * fn * 2 <= 256 && A.ext[vn] % (fn * 2) == 0 && lds_fits(M * fm, N * fn * 2);
-        if (gm && (M * fm <= N * fn || !gn)) fm *= 2;
+        const bool gm = vm >= 0 && M0 * fm * 2 <= 256 && A.ext[vm] % (fm * 2) == 0 && lds_fits(M0 * fm * 2, N0 * fn);
+        const bool gn = vn >= 0 && N0 * fn * 2 <= 256 && A.ext[vn] % (fn * 2) == 0 && lds_fits(M0 * fm, N0 * fn * 2);
+        if (gm && (M0 * fm <= N0 * fn || !gn)) fm *= 2;
         else if (gn) fn *= 2;
         else break;
     }
-    const int64_t bm = M * fm, bn = N * fn;
+    const int64_t bm = M0 * fm, bn = N0 * fn;
     // Blocks below the MFMA block shape (64 rows / columns) stay on the tile program.
     if (bm % 64 || bn % 64 || !lds_fits(bm, bn)) return false;
     spec.gemm_vm = fm > 1 ? vm : -1;
@@ -1239,7 +1241,7 @@ void enqueue_built(RunEnv& E, int li, BuiltLaunch& B, hipStream_t stream, uint64
             for (size_t v = 0; v < L.grid.size(); ++v)
                 if (!((seq >> v) & 1u)) blocks *= std::max<int64_t>(1, B.args.ext[v]);
     } else {
-        blocks = B.ntasks / ek.tasks_per_block;
+        blocks = B.ntasks / ek.tasks_per_block * ek.blocks_per_task;
     }
     if (B.spec.gemm && !B.spec.serial) {
         // GEMM kernels run exactly one block per workgroup.

@@ -5,7 +5,10 @@ Each seed draws a task tile (tm, tn in {64, 128, 256}, tk in {16, 32, 64,
 M, N and K (odd counts leave the 2x2 block merge half used or off), the
 input dtype (f16 / bf16, or f32 for about a third of the seeds: the f32
 block on v_mfma_f32_32x32x2_f32), the InOut accumulate form or the plain store, the
-order of the m and n loops, and seeded inputs with a random initial C.  The
+order of the m and n loops, and seeded inputs with a random initial C (a
+second set of seeds draws tiles of 16 / 32, merged into MFMA blocks or run
+as tile programs, and of 512, split into 256-wide blocks, with K steps up to
+256).  The
 GPU result must equal the oracle's within a relative Frobenius error of 1e-5
 (both accumulate exact products in fp32, in different orders), with equal
 cycle counts.
@@ -86,6 +89,46 @@ def test_random_gemm_matches_oracle(gpu, seed):
     ca = {"a": a16.copy(), "b": b16.copy(), "c": c0.copy()}
     prog = W.rr4(_workload(c, ga)).compile(target="hip_gfx950")
     assert prog._native.kernel_family("gemm_tile") == "gemm"
+    prog.execute()
+    prog.synchronize()
+    ref = run_workload(W.rr4(_workload(c, ca)))
+    assert prog.stats.total_cycles == ref.total_cycles
+    err = np.linalg.norm(ga["c"] - ca["c"]) / np.linalg.norm(ca["c"])
+    assert err <= 1e-5, err
+
+
+def _case_tiles(seed):
+    """Task tiles below and above the MFMA block: 16 / 32 (merged into blocks, or the
+    tile program when the extents do not merge to 64) and 512 (split into 256-wide
+    blocks), with K steps up to 256 (taken in LDS stages)."""
+    rng = np.random.default_rng(1000 + seed)
+    tm, tn = int(rng.choice([16, 32, 64, 512])), int(rng.choice([16, 32, 128, 512]))
+    tk = int(rng.choice([16, 32, 64, 256]))
+    small = lambda t: int(rng.integers(1, 9)) if t <= 32 else (int(rng.integers(1, 3)) if t == 512 else int(rng.integers(1, 4)))
+    c = dict(tm=tm, tn=tn, tk=tk, B=1, mt=small(tm), nt=small(tn), kt=int(rng.integers(1, 4)), f16=bool(rng.random() < 0.5),
+             plain=bool(rng.random() < 0.25), n_outer=bool(rng.random() < 0.3))
+    c["f32"] = bool(rng.random() < 0.3)
+    return c
+
+
+@pytest.mark.parametrize("seed", range(12))
+def test_random_gemm_tile_sizes_match_oracle(gpu, seed):
+    c = _case_tiles(seed)
+    print(c, flush=True)
+    rng = np.random.default_rng(seed + 99)
+    M, N, K = c["tm"] * c["mt"], c["tn"] * c["nt"], c["tk"] * c["kt"]
+    a = rng.uniform(-1, 1, (c["B"], M, K)).astype(np.float32)
+    b = rng.uniform(-1, 1, (c["B"], K, N)).astype(np.float32)
+    if c["f32"]:
+        a16, b16 = a, b
+    elif c["f16"]:
+        a16, b16 = a.astype(np.float16), b.astype(np.float16)
+    else:
+        a16, b16 = W.bf16_round(a), W.bf16_round(b)
+    c0 = rng.uniform(-1, 1, (c["B"], M, N)).astype(np.float32)
+    ga = {"a": a16.copy(), "b": b16.copy(), "c": c0.copy()}
+    ca = {"a": a16.copy(), "b": b16.copy(), "c": c0.copy()}
+    prog = W.rr4(_workload(c, ga)).compile(target="hip_gfx950")
     prog.execute()
     prog.synchronize()
     ref = run_workload(W.rr4(_workload(c, ca)))

@@ -552,6 +552,52 @@ def test_bgemm_f32_mfma(gpu, shape, tiles, plain):
     assert prog.stats.total_cycles == ref.total_cycles
 
 
+@pytest.mark.parametrize("m,k,n,dt", [
+    (512, 512, 512, "f32"),     # 2 x 2 blocks of 256, 16 stages of 32 columns
+    (512, 1024, 256, "bf16"),   # 2 x 1 blocks, 16 stages of 64 (ping-pong)
+    (768, 192, 512, "f16"),     # 3 x 2 blocks, 3 stages of 64
+])
+def test_matmul_large_tiles(gpu, m, k, n, dt):
+    """The validated_matmul form (one task per batch, C[b] = A[b] @ B[b]) with tiles above
+    256 rows / columns and K above 128: each task runs as 256 x 256 blocks whose K loop
+    takes the task's K in LDS stages."""
+    rng = np.random.default_rng(m + k + n)
+    a32 = rng.uniform(-1, 1, (2, 1, m, k)).astype(np.float32)
+    b32 = rng.uniform(-1, 1, (2, 1, k, n)).astype(np.float32)
+    if dt == "f16":
+        a, b, wdt, up = a32.astype(np.float16), b32.astype(np.float16), W.F16, lambda x: x.astype(np.float64)
+    elif dt == "bf16":
+        a, b, wdt, up = W.bf16_round(a32), W.bf16_round(b32), W.BF16, lambda x: W.bf16_to_f32(x).astype(np.float64)
+    else:
+        a, b, wdt, up = a32, b32, W.F32, lambda x: x.astype(np.float64)
+    ga = {"a": a.copy(), "b": b.copy(), "c": np.zeros((2, 1, m, n), np.float32)}
+    ca = {k_: v.copy() for k_, v in ga.items()}
+    prog = run_hip(W.rr4(W.matmul_tile(ga, m, k, n, wdt), 1024))
+    ref = run_workload(W.rr4(W.matmul_tile(ca, m, k, n, wdt), 1024))
+    assert prog._native.kernel_family("mm") == "gemm" and "gemm program" in prog._native.precompile(0)
+    assert _rel_fro(ga["c"], ca["c"]) <= 1e-5
+    assert _rel_fro(ga["c"], up(a) @ up(b)) <= 1e-5
+    assert prog.stats.total_cycles == ref.total_cycles
+
+
+def test_bgemm_large_tiles_accumulate(gpu):
+    """512 x 512 task tiles with a K step of 256 over a P.seq loop of 3 steps (accumulate
+    form): 2 x 2 blocks per task, 4 stages per step, against the oracle and float64."""
+    rng = np.random.default_rng(21)
+    a = W.bf16_round(rng.uniform(-1, 1, (1, 1024, 768)).astype(np.float32))
+    b = W.bf16_round(rng.uniform(-1, 1, (1, 768, 512)).astype(np.float32))
+    c0 = rng.standard_normal((1, 1024, 512)).astype(np.float32)
+    ga = {"a": a.copy(), "b": b.copy(), "c": c0.copy()}
+    ca = {"a": a.copy(), "b": b.copy(), "c": c0.copy()}
+    prog = run_hip(W.bgemm(ga, 512, 512, 256, W.BF16))
+    ref = run_workload(W.bgemm(ca, 512, 512, 256, W.BF16))
+    assert prog._native.kernel_family("gemm_tile") == "gemm"
+    assert _rel_fro(ga["c"], ca["c"]) <= 1e-5
+    exact = c0.astype(np.float64) + W.bf16_to_f32(a).astype(np.float64) @ W.bf16_to_f32(b).astype(np.float64)
+    assert _rel_fro(ga["c"], exact) <= 1e-5
+    assert prog.stats.total_cycles == ref.total_cycles
+
+
 def test_bgemm_f16_mfma_device_tensors(gpu):
     import torch
 
