@@ -807,6 +807,33 @@ __device__ inline void tile_mma(FA a, FB b, float* c, float* scratch) {
     }
 }
 
+// The same for M and N multiples of 16 (K a multiple of 4, at most 32 or a
+// multiple of 32) on v_mfma_f32_16x16x4_f32: 16x16 output blocks, lane l
+// supplying A[i0 + l%16][q + l/16] (from the wave's scratch copy of the
+// block's 16 A rows) and B[q + l/16][j0 + l%16].
+template <int M, int K, int N, int NT, class FA, class FB>
+__device__ inline void tile_mma16(FA a, FB b, float* c, float* scratch) {
+    static_assert(M % 16 == 0 && N % 16 == 0 && K % 4 == 0 && (K <= 32 || K % 32 == 0) && NT % 64 == 0, "tile_mma16 shape");
+    constexpr int NW = NT / 64, BJ = N / 16, NB = (M / 16) * BJ, KC = K < 32 ? K : 32;
+    const int lane = threadIdx.x & 63, w = threadIdx.x >> 6, r = lane & 15, h = lane >> 4;
+    float* s = scratch + w * 32 * kTileMmaPitch;
+    for (int blk = w; blk < NB; blk += NW) {
+        const int i0 = (blk / BJ) * 16, j0 = (blk % BJ) * 16;
+        f32x4v_t acc = {0.0f, 0.0f, 0.0f, 0.0f};
+        for (int k0 = 0; k0 < K; k0 += KC) {
+            wave_lds_barrier();
+#pragma unroll
+            for (int e = lane; e < 16 * KC; e += 64) s[(e / KC) * kTileMmaPitch + e % KC] = a(i0 + e / KC, k0 + e % KC);
+            wave_lds_barrier();
+#pragma unroll 8
+            for (int q = 0; q < KC; q += 4)
+                acc = __builtin_amdgcn_mfma_f32_16x16x4f32(s[r * kTileMmaPitch + q + h], b(k0 + q + h, j0 + r), acc, 0, 0, 0);
+        }
+#pragma unroll
+        for (int e = 0; e < 4; ++e) c[(i0 + 4 * h + e) * N + j0 + r] = acc[e];
+    }
+}
+
 // ---------------------------------------------------------------------------
 // Ping-pong GEMM block: 256x256 C block, 8 waves in two groups of four
 // ---------------------------------------------------------------------------

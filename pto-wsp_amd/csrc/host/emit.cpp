@@ -585,14 +585,22 @@ EmittedKernel emit_tile(const Module& m, const KernelAnalysis& a, const LaunchSp
     size_t lds = pool + staged_bytes;
     // Matmul ops of MFMA shape run on the matrix cores (tile_mma), with a
     // 32-row operand scratch per wave, when that scratch fits beside the tiles.
-    auto mma_shape = [&](const OpInfo& op) {
-        if (op.kind != OpKind::Matmul || op.result <= 0) return false;
+    // 32: 32x32 blocks (M, N multiples of 32, K even); 16: 16x16 blocks (M, N
+    // multiples of 16, K a multiple of 4, at least 32^3 products); K at most
+    // 32 or a multiple of 32.
+    auto mma_kind = [&](const OpInfo& op) {
+        if (op.kind != OpKind::Matmul || op.result <= 0) return 0;
         const ValueInfo* av = a.by_id[op.operands[0]];
         const ValueInfo* bv = a.by_id[op.operands[1]];
         const int M = av->rows, K = av->cols, N = bv->cols;
-        return !is_int_v(op.result) && !is_int_v(op.operands[0]) && !is_int_v(op.operands[1]) && M % 32 == 0 &&
-               N % 32 == 0 && K % 2 == 0 && (K <= 32 || K % 32 == 0) && spec.threads % 64 == 0;
+        if (is_int_v(op.result) || is_int_v(op.operands[0]) || is_int_v(op.operands[1]) || spec.threads % 64 != 0) return 0;
+        if (K > 32 && K % 32 != 0) return 0;
+        if (M % 32 == 0 && N % 32 == 0 && K % 2 == 0) return 32;
+        // (smaller products keep the scalar loop, bit for bit the oracle's)
+        if (M % 16 == 0 && N % 16 == 0 && K % 4 == 0 && M * N * K >= 32 * 32 * 32) return 16;
+        return 0;
     };
+    auto mma_shape = [&](const OpInfo& op) { return mma_kind(op) != 0; };
     const size_t mma_scratch = static_cast<size_t>(spec.threads / 64) * 32 * kTileMmaPitchHost * 4;
     bool use_mma = false;
     if (spec.tile_mma)
@@ -801,7 +809,8 @@ EmittedKernel emit_tile(const Module& m, const KernelAnalysis& a, const LaunchSp
                     o << ind << "{\n";
                     o << ind << "  auto fa_ = [&](int i, int q) -> float { return " << elem(av, "i", "q", K) << "; };\n";
                     o << ind << "  auto fb_ = [&](int q, int jj) -> float { return " << elem(bv, "q", "jj", N) << "; };\n";
-                    o << ind << "  tile_mma<" << M << ", " << K << ", " << N << ", NT>(fa_, fb_, L" << res->id << ", mma_scratch_);\n";
+                    o << ind << "  tile_mma" << (mma_kind(op) == 16 ? "16" : "") << "<" << M << ", " << K << ", " << N
+                      << ", NT>(fa_, fb_, L" << res->id << ", mma_scratch_);\n";
                     o << ind << "}\n";
                     break;
                 }

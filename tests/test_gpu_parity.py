@@ -165,7 +165,8 @@ def test_example_tiled_attention(gpu):
 
 
 def _has_tile_mma(prog):
-    return "tile_mma<" in prog._native.precompile(0)
+    src = prog._native.precompile(0)
+    return "tile_mma<" in src or "tile_mma16<" in src
 
 
 def test_tiled_attention_mfma_tiles(gpu):
@@ -220,11 +221,12 @@ def test_llama_block_mfma_tiles(gpu):
     assert prog.stats.total_cycles == ref.total_cycles
 
 
-@pytest.mark.parametrize("m,k,n", [(32, 16, 32), (32, 64, 96), (96, 32, 32), (32, 48, 32)])
+@pytest.mark.parametrize("m,k,n", [(32, 16, 32), (32, 64, 96), (96, 32, 32), (32, 48, 32), (16, 64, 48), (48, 32, 80)])
 def test_tile_program_matmul_shapes(gpu, m, k, n):
-    """Matmul tiles below the GEMM family (M or N not a multiple of 64) on the tile
-    program: M, N multiples of 32 with K <= 32 or a multiple of 32 take the matrix cores,
-    K = 48 the scalar loop (bit for bit the oracle's)."""
+    """Matmul tiles below the GEMM family's blocks on the tile program: M, N multiples of
+    32 (or of 16, with at least 32^3 products) with K <= 32 or a multiple of 32 take the
+    matrix cores (32x32 or 16x16 MFMA blocks), K = 48 the scalar loop (bit for bit the
+    oracle's)."""
     rng = np.random.default_rng(m + k + n)
     a = rng.uniform(-1, 1, (3, 1, m, k)).astype(np.float32)
     b = rng.uniform(-1, 1, (3, 1, k, n)).astype(np.float32)
@@ -235,6 +237,8 @@ def test_tile_program_matmul_shapes(gpu, m, k, n):
     assert "tile program" in prog._native.precompile(0)  # no merge candidates: below the MFMA block
     mma = k % 2 == 0 and (k <= 32 or k % 32 == 0)
     assert _has_tile_mma(prog) == mma
+    if mma and (m % 32 or n % 32):
+        assert "tile_mma16<" in prog._native.precompile(0)
     if mma:
         assert _rel_fro(ga["c"], ca["c"]) <= 1e-5
     else:
