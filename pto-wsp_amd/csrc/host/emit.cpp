@@ -566,25 +566,6 @@ EmittedKernel emit_tile(const Module& m, const KernelAnalysis& a, const LaunchSp
     size_t staged_bytes = 0;
     for (const auto& p : k.params)
         if (staged_id(p.id)) staged_bytes += static_cast<size_t>(SB) * a.by_id[p.id]->rows * a.by_id[p.id]->cols * (is_int_v(p.id) ? 8 : 4);
-    // Tiles that do not fit in LDS go to a per-workgroup global scratch
-    // (largest first, until the rest fits beside the staged params).
-    std::vector<int> in_lds(lds_vals.begin(), lds_vals.end()), in_glob;
-    std::map<int, size_t> lds_off, glob_off;
-    size_t pool = place(in_lds, lds_off);
-    while (pool + staged_bytes > 160 * 1024 && !in_lds.empty()) {
-        auto big = std::max_element(in_lds.begin(), in_lds.end(), [&](int x, int y) { return tile_bytes(x) < tile_bytes(y); });
-        in_glob.push_back(*big);
-        in_lds.erase(big);
-        lds_off.clear();
-        pool = place(in_lds, lds_off);
-    }
-    const size_t gpool = in_glob.empty() ? 0 : place(in_glob, glob_off);
-    const bool glob_tiles = gpool > 0 && ntens < kMaxParams;
-    if (gpool > 0 && !glob_tiles)
-        throw CompileError("kernel " + k.name + ": tiles exceed the 160 KiB of LDS and the launch has no argument slot left for global tiles");
-    size_t lds = pool + staged_bytes;
-    // Matmul ops of MFMA shape run on the matrix cores (tile_mma), with a
-    // 32-row operand scratch per wave, when that scratch fits beside the tiles.
     // 32: 32x32 blocks (M, N multiples of 32, K even); 16: 16x16 blocks (M, N
     // multiples of 16, K a multiple of 4, at least 32^3 products); K at most
     // 32 or a multiple of 32.
@@ -602,9 +583,31 @@ EmittedKernel emit_tile(const Module& m, const KernelAnalysis& a, const LaunchSp
     };
     auto mma_shape = [&](const OpInfo& op) { return mma_kind(op) != 0; };
     const size_t mma_scratch = static_cast<size_t>(spec.threads / 64) * 32 * kTileMmaPitchHost * 4;
-    bool use_mma = false;
+    bool want_mma = false;
     if (spec.tile_mma)
-        for (const auto& op : k.ops) use_mma = use_mma || mma_shape(op);
+        for (const auto& op : k.ops) want_mma = want_mma || mma_shape(op);
+    // Tiles that do not fit in LDS go to a per-workgroup global scratch
+    // (largest first, until the rest fits beside the staged params and the
+    // matmul scratch).
+    std::vector<int> in_lds(lds_vals.begin(), lds_vals.end()), in_glob;
+    std::map<int, size_t> lds_off, glob_off;
+    size_t pool = place(in_lds, lds_off);
+    const size_t lds_budget = 160 * 1024 - (want_mma ? mma_scratch : 0);
+    while (pool + staged_bytes > lds_budget && !in_lds.empty()) {
+        auto big = std::max_element(in_lds.begin(), in_lds.end(), [&](int x, int y) { return tile_bytes(x) < tile_bytes(y); });
+        in_glob.push_back(*big);
+        in_lds.erase(big);
+        lds_off.clear();
+        pool = place(in_lds, lds_off);
+    }
+    const size_t gpool = in_glob.empty() ? 0 : place(in_glob, glob_off);
+    const bool glob_tiles = gpool > 0 && ntens < kMaxParams;
+    if (gpool > 0 && !glob_tiles)
+        throw CompileError("kernel " + k.name + ": tiles exceed the 160 KiB of LDS and the launch has no argument slot left for global tiles");
+    size_t lds = pool + staged_bytes;
+    // Matmul ops of MFMA shape run on the matrix cores (tile_mma), with a
+    // 32-row operand scratch per wave, when that scratch fits beside the tiles.
+    bool use_mma = want_mma;
     if (use_mma && lds + mma_scratch > 160 * 1024) use_mma = false;
     if (use_mma) lds += mma_scratch;
     if (lds > 160 * 1024)
