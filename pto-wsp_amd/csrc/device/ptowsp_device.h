@@ -1328,8 +1328,8 @@ __device__ inline void reset_count(int* cnt) {
 // H8: pages of 8 tokens, folded two to a 16-token step: page a supplies
 // tokens 0-7, page b tokens 8-15 (see load_pair).
 // F32: f32 q, K and V (the reference's own dtype): scores on
-// v_mfma_f32_16x16x4_f32 with lane l holding head dims (D/4)*(l/16) .. +D/4-1
-// of its token (the K order of a product is free), p @ v on the same MFMA
+// v_mfma_f32_16x16x4_f32 with lane l holding head dims 16*j + 4*(l/16) .. +3
+// of its token for j < D/16 (the K order of a product is free), p @ v on the same MFMA
 // with p as it is (no hi / lo split); F16 is then unused.
 template <int G, int D, bool F16, bool MASK, bool H8 = false, bool F32 = false>
 struct DecodeWave {
@@ -1339,7 +1339,7 @@ struct DecodeWave {
     static constexpr int NS = D * ES / 64;     // u32x4 of K per lane (bf16 / f16: head-dim slices of the score MFMA)
     static constexpr int DV = D / 16;          // head-dim columns per lane in p @ v
     static constexpr int VW = DV * ES / 4;     // u32 of V per lane and token
-    static constexpr int KC = F32 ? 16 : 64;   // bytes between a lane's K chunks
+    static constexpr int KC = 64;              // bytes between a lane's K chunks
     static constexpr int RB = (G + 15) / 16;   // blocks of 16 query rows (one MFMA row block each)
     static constexpr int NQ = RB * NS;         // q registers (u32x4) per lane
     static constexpr int kHalves = H8 ? 2 : 1;  // pages per 16-token step
@@ -1350,7 +1350,7 @@ struct DecodeWave {
     static constexpr int kPartFloats = G * D + ((2 * G + 3) & ~3);
 
     struct Page {
-        u32x4 k[NS];           // lane l: token l%16, head dims 32*j + 8*(l/16) .. +7 (F32: (D/4)*(l/16) + 4*j .. +3)
+        u32x4 k[NS];           // lane l: token l%16, head dims 32*j + 8*(l/16) .. +7 (F32: 16*j + 4*(l/16) .. +3)
         u32 v[4][VW];          // lane l: tokens 4*(l/16) + i, head dims DV*(l%16) .. +DV-1
         float mask[4];         // lane l: tokens 4*(l/16) .. +3
         float hneg;            // H8: added to the scores of tokens 8-15 (0, or -inf without page b)
@@ -1368,7 +1368,7 @@ struct DecodeWave {
         const int lane = threadIdx.x & 63, t = lane & 15, grp = lane >> 4;
         const int tk = H8 ? (t & 7) : t, gv = H8 ? (grp & 1) : grp;
         Lanes r;
-        r.k = static_cast<u32>((tk * ks + (F32 ? D / 4 : 8) * grp) * ES);
+        r.k = static_cast<u32>((tk * ks + (F32 ? 4 : 8) * grp) * ES);
         r.v = static_cast<u32>((4 * gv * vs + DV * t) * ES);
         r.m = static_cast<u32>(gv * 16);
         r.vrow = static_cast<u32>(vs * ES);
@@ -1493,8 +1493,9 @@ struct DecodeWave {
         for (int rb = 0; rb < RB; ++rb) {
             acc[rb] = f32x4v_t{0.0f, 0.0f, 0.0f, 0.0f};
             if constexpr (F32) {
-                // MFMA (j, x) pairs head dim (D/4)*g + 4*j + x of lane group g
-                // of K and q.
+                // MFMA (j, x) pairs head dim 16*j + 4*g + x of lane group g of
+                // K and q: a K load instruction covers 64 contiguous bytes of
+                // each token's row.
 #pragma unroll
                 for (int j = 0; j < NS; ++j)
 #pragma unroll
@@ -1600,7 +1601,7 @@ struct DecodeWave {
 #pragma unroll
             for (int j = 0; j < NS; ++j) {
                 qa[rb * NS + j] = u32x4{0u, 0u, 0u, 0u};
-                const i64 e = (16 * rb + t) * qs + (F32 ? (D / 4) * grp + 4 * j : 32 * j + 8 * grp);
+                const i64 e = (16 * rb + t) * qs + (F32 ? 16 * j + 4 * grp : 32 * j + 8 * grp);
                 if (16 * rb + t < G) qa[rb * NS + j] = *reinterpret_cast<const u32x4*>(qb + e * ES);
             }
         }
