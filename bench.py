@@ -559,6 +559,9 @@ CASES = {
     "paged_decode_g32": lambda: DecodeCase("paged_decode_g32", 64, 256, 8, 128, 512, 8192, 0, None),
     # Not a BASELINE config: the C5 decode with f32 q / K / V.
     "paged_decode_f32": lambda: DecodeCase("paged_decode_f32", 64, 32, 8, 128, 512, 8192, 0, None, f32_inputs=True),
+    "paged_decode_f32_g32": lambda: DecodeCase("paged_decode_f32_g32", 64, 256, 8, 128, 512, 8192, 0, None, f32_inputs=True),
+    "paged_decode_f32_d64_g48": lambda: DecodeCase("paged_decode_f32_d64_g48", 64, 384, 8, 64, 512, 8192, 0, None,
+                                                   f32_inputs=True),
     # Not a BASELINE config: the C4 GEMM with f32 A and B (the reference's own
     # matmul dtype), on the f32 MFMA block.
     "bgemm_f32": lambda: GemmCase("bgemm_f32", 64, 2048, 2048, 2048, 0, None, f32_inputs=True),
@@ -568,8 +571,8 @@ CASES = {
     "bgemm_tile16": lambda: GemmCase("bgemm_tile16", 64, 2048, 2048, 2048, 0, None, tile=(16, 16, 16), dtype="f16"),
 }
 EXTRA = ("copy_calib", "softmax3", "softmax3_overlap", "paged_decode_page32", "paged_decode_page64", "paged_decode_page8",
-         "paged_decode_d64", "paged_decode_d256", "paged_decode_g16", "paged_decode_g32", "paged_decode_f32", "bgemm_f32",
-         "bgemm_tile16")
+         "paged_decode_d64", "paged_decode_d256", "paged_decode_g16", "paged_decode_g32", "paged_decode_f32",
+         "paged_decode_f32_g32", "paged_decode_f32_d64_g48", "bgemm_f32", "bgemm_tile16")
 
 
 def load_traffic(name):

@@ -1334,7 +1334,7 @@ __device__ inline void reset_count(int* cnt) {
 template <int G, int D, bool F16, bool MASK, bool H8 = false, bool F32 = false>
 struct DecodeWave {
     static_assert(G >= 1 && G <= 48 && (D == 64 || D == 128 || D == 256), "decode shape");
-    static_assert(!F32 || (G <= 16 && D <= 128), "f32 decode shape");
+    static_assert(!F32 || D <= 128, "f32 decode shape");
     static constexpr int ES = F32 ? 4 : 2;     // element bytes of q, K, V
     static constexpr int NS = D * ES / 64;     // u32x4 of K per lane (bf16 / f16: head-dim slices of the score MFMA)
     static constexpr int DV = D / 16;          // head-dim columns per lane in p @ v
@@ -1343,6 +1343,10 @@ struct DecodeWave {
     static constexpr int RB = (G + 15) / 16;   // blocks of 16 query rows (one MFMA row block each)
     static constexpr int NQ = RB * NS;         // q registers (u32x4) per lane
     static constexpr int kHalves = H8 ? 2 : 1;  // pages per 16-token step
+    // The stream holds the next unit's q in registers ahead of its first
+    // page, except for f32 pages with more than 16 query rows, whose q
+    // (32 registers per 16 rows at head dim 128) would not fit beside them.
+    static constexpr bool kPrefetchQ = !(F32 && RB > 1);
     // Partial layout: o[G][D] (head dims permuted, see store), then m[G] and
     // l[G]; padded to 16 bytes so that every partial's o rows are 16-byte
     // aligned.
@@ -1891,7 +1895,7 @@ struct DecodeStream {
         // the compiler's wait counts drain the ring at every loop iteration.
         wait_vmcnt<0>();
         int un = u;
-        if (eu < b) {
+        if (DW::kPrefetchQ && eu < b) {
             un = next_unit(pre, u);
             get_q(qn, un);
         }
@@ -1921,15 +1925,26 @@ struct DecodeStream {
                         flush(pd, cnt, f);
                         return;
                     }
-                    u = un;
-                    eu = __builtin_amdgcn_readfirstlane(pre[u + 1]);
-                    if (eu > b) eu = b;
-                    DW::init(st);
+                    if constexpr (DW::kPrefetchQ) {
+                        u = un;
+                        eu = __builtin_amdgcn_readfirstlane(pre[u + 1]);
+                        if (eu > b) eu = b;
+                        DW::init(st);
 #pragma unroll
-                    for (int j = 0; j < DW::NQ; ++j) qa[j] = qn[j];
-                    if (eu < b) {
-                        un = next_unit(pre, u);
-                        get_q(qn, un);
+                        for (int j = 0; j < DW::NQ; ++j) qa[j] = qn[j];
+                        if (eu < b) {
+                            un = next_unit(pre, u);
+                            get_q(qn, un);
+                        }
+                    } else {
+                        // q is read here, behind the whole ring: the wait
+                        // keeps the load out of the loop's later wait counts.
+                        u = next_unit(pre, u);
+                        eu = __builtin_amdgcn_readfirstlane(pre[u + 1]);
+                        if (eu > b) eu = b;
+                        DW::init(st);
+                        get_q(qa, u);
+                        wait_vmcnt<0>();
                     }
                 }
             }

@@ -369,8 +369,8 @@ DecodeInfo classify_decode(const KernelDef& k, const KernelAnalysis& a) {
     // head dim 64 / 128 / 256, query rows in blocks of 16 (one MFMA row block
     // each) up to what the wave's registers hold beside its page ring: 48
     // rows at head dim 64 or 128, 16 at 256; f32 pages (twice the registers)
-    // up to 16 rows and head dim 128.
-    const int max_rows = f32 || D == 256 ? 16 : 48;
+    // up to head dim 128.
+    const int max_rows = D == 256 ? 16 : 48;
     if ((PG != 8 && PG != 16 && PG != 32 && PG != 64 && PG != 128) || G < 1 || G > max_rows ||
         (D != 64 && D != 128 && D != 256) || (f32 && D > 128))
         return info;

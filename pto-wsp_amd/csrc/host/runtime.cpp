@@ -479,9 +479,12 @@ struct Tuning {
 // 0.41 ms with 2 steps on the C5 shape with head dim 256); 2 steps keep the
 // same bytes in flight.
 // More than 16 query rows add a block of accumulators and q registers per
-// 16 rows: 33-48 rows at head dim 128 leave room for 2 steps.
+// 16 rows: 33-48 rows at head dim 128 leave room for 2 steps.  f32 pages
+// are twice the registers of bf16 ones: 2 steps at head dim 128 (0.406
+// against 0.409 ms with 3 on the C5 shape in f32), and beyond 16 rows; 4 at
+// head dim 64 up to 16 rows.
 int decode_ring_for(int head_dim, int rows, bool f32) {
-    if (f32) return head_dim >= 128 ? 3 : 4;  // 0.654 against 0.750 ms with 2 steps at head dim 128
+    if (f32) return rows > 16 || head_dim >= 128 ? 2 : 4;
     if (head_dim >= 256) return 2;
     if (head_dim <= 64) return rows <= 16 ? 3 : 4;
     return rows <= 32 ? 4 : 2;

@@ -671,6 +671,9 @@ def test_paged_decode_wide_units(gpu, lengths, hkv, group, d, page):
     ([300, 77, 0], 1, 8, 64, 32, True),                   # head dim 64, sub-pages, an empty sequence
     ([129, 40, 700], 2, 16, 128, 8, True),                # 16 rows, 8-token pages two to a step
     ([64, 160, 32], 2, 1, 128, 16, False),                # unmasked, one query row
+    ([400, 33, 1000], 1, 32, 128, 16, True),              # 32 rows: two row blocks, 2-step rings
+    ([250, 0, 1300, 16], 2, 48, 64, 32, True),            # 48 rows at head dim 64
+    ([90, 700], 1, 20, 128, 8, True),                     # 20 rows, 8-token pages
 ])
 def test_paged_decode_f32(gpu, lengths, hkv, group, d, page, masked):
     """f32 q / K / V (the reference's own dtype) on the decode family: scores and p @ v on

@@ -203,6 +203,23 @@ def test_decode_family_query_rows(group, d, family):
         assert f"DecodeWave<{group}, {d}, false, true, false>" in prog.precompile(0)
 
 
+@pytest.mark.parametrize("group, d, family, ring", [(4, 128, "decode", 2), (16, 64, "decode", 4), (32, 128, "decode", 2),
+                                                 (48, 64, "decode", 2), (49, 64, "tile_program", 0),
+                                                 (4, 256, "tile_program", 0)])
+def test_decode_family_f32(group, d, family, ring):
+    """f32 q / K / V take the decode family up to head dim 128 and 48 query rows, with
+    2-step page rings at head dim 128 or beyond 16 rows."""
+    from pto_wsp._hip import NativeProgram
+
+    arrs = W.paged_decode_arrays([40, 300], 1, group, d, page=64, f32=True)
+    prog = NativeProgram(workload_to_codegen_ir(W.rr4(W.paged_decode(arrs, dtype=W.F32)), "d").module)
+    assert prog.kernel_family("decode_page") == family
+    if family == "decode":
+        src = prog.precompile(0)
+        assert f"DecodeWave<{group}, {d}, false, true, false, true>" in src
+        assert f"DecodeStream<DW, {ring}, false>" in src
+
+
 def test_tile_program_matmul_on_matrix_cores():
     """A fused tile with matmuls of MFMA shape (the attention example at 64-token tiles)
     stays a tile program whose matmuls call tile_mma; 8-token tiles keep the scalar loop."""
