@@ -1344,9 +1344,10 @@ struct DecodeWave {
     static constexpr int NQ = RB * NS;         // q registers (u32x4) per lane
     static constexpr int kHalves = H8 ? 2 : 1;  // pages per 16-token step
     // The stream holds the next unit's q in registers ahead of its first
-    // page, except for f32 pages with more than 16 query rows, whose q
-    // (32 registers per 16 rows at head dim 128) would not fit beside them.
-    static constexpr bool kPrefetchQ = !(F32 && RB > 1);
+    // page, except with more than 16 query rows at head dim 128 or in f32:
+    // there a second q set (16 or 32 registers per 16 rows) costs the fold
+    // more than reading q behind a full wait at each unit start.
+    static constexpr bool kPrefetchQ = !(RB > 1 && (F32 || D >= 128));
     // Partial layout: o[G][D] (head dims permuted, see store), then m[G] and
     // l[G]; padded to 16 bytes so that every partial's o rows are 16-byte
     // aligned.
