@@ -562,6 +562,7 @@ CASES = {
     "paged_decode_f32_g32": lambda: DecodeCase("paged_decode_f32_g32", 64, 256, 8, 128, 512, 8192, 0, None, f32_inputs=True),
     "paged_decode_f32_d64_g48": lambda: DecodeCase("paged_decode_f32_d64_g48", 64, 384, 8, 64, 512, 8192, 0, None,
                                                    f32_inputs=True),
+    "paged_decode_f32_d256": lambda: DecodeCase("paged_decode_f32_d256", 64, 32, 8, 256, 512, 8192, 0, None, f32_inputs=True),
     # Not a BASELINE config: the C4 GEMM with f32 A and B (the reference's own
     # matmul dtype), on the f32 MFMA block.
     "bgemm_f32": lambda: GemmCase("bgemm_f32", 64, 2048, 2048, 2048, 0, None, f32_inputs=True),
@@ -572,7 +573,7 @@ CASES = {
 }
 EXTRA = ("copy_calib", "softmax3", "softmax3_overlap", "paged_decode_page32", "paged_decode_page64", "paged_decode_page8",
          "paged_decode_d64", "paged_decode_d256", "paged_decode_g16", "paged_decode_g32", "paged_decode_f32",
-         "paged_decode_f32_g32", "paged_decode_f32_d64_g48", "bgemm_f32", "bgemm_tile16")
+         "paged_decode_f32_g32", "paged_decode_f32_d64_g48", "paged_decode_f32_d256", "bgemm_f32", "bgemm_tile16")
 
 
 def load_traffic(name):

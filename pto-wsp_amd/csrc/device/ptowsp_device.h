@@ -1334,11 +1334,12 @@ __device__ inline void reset_count(int* cnt) {
 template <int G, int D, bool F16, bool MASK, bool H8 = false, bool F32 = false>
 struct DecodeWave {
     static_assert(G >= 1 && G <= 48 && (D == 64 || D == 128 || D == 256), "decode shape");
-    static_assert(!F32 || D <= 128, "f32 decode shape");
+    static_assert(!F32 || D <= 128 || G <= 16, "f32 decode shape");
     static constexpr int ES = F32 ? 4 : 2;     // element bytes of q, K, V
     static constexpr int NS = D * ES / 64;     // u32x4 of K per lane (bf16 / f16: head-dim slices of the score MFMA)
     static constexpr int DV = D / 16;          // head-dim columns per lane in p @ v
     static constexpr int VW = DV * ES / 4;     // u32 of V per lane and token
+    static_assert(VW == 2 || VW % 4 == 0, "V loads");
     static constexpr int KC = 64;              // bytes between a lane's K chunks
     static constexpr int RB = (G + 15) / 16;   // blocks of 16 query rows (one MFMA row block each)
     static constexpr int NQ = RB * NS;         // q registers (u32x4) per lane
@@ -1347,7 +1348,7 @@ struct DecodeWave {
     // page, except with more than 16 query rows at head dim 128 or in f32:
     // there a second q set (16 or 32 registers per 16 rows) costs the fold
     // more than reading q behind a full wait at each unit start.
-    static constexpr bool kPrefetchQ = !(RB > 1 && (F32 || D >= 128));
+    static constexpr bool kPrefetchQ = !((RB > 1 && (F32 || D >= 128)) || (F32 && D > 128));
     // Partial layout: o[G][D] (head dims permuted, see store), then m[G] and
     // l[G]; padded to 16 bytes so that every partial's o rows are 16-byte
     // aligned.
@@ -1398,14 +1399,12 @@ struct DecodeWave {
 #pragma unroll
         for (int i = 0; i < 4; ++i) {
             const char* vi = vp + static_cast<u64>(i * ln.vrow);
-            if constexpr (VW == 8) {
-                const u32x4 a = __builtin_nontemporal_load(reinterpret_cast<const u32x4*>(vi));
-                const u32x4 b = __builtin_nontemporal_load(reinterpret_cast<const u32x4*>(vi + 16));
-                pg.v[i][0] = a.x; pg.v[i][1] = a.y; pg.v[i][2] = a.z; pg.v[i][3] = a.w;
-                pg.v[i][4] = b.x; pg.v[i][5] = b.y; pg.v[i][6] = b.z; pg.v[i][7] = b.w;
-            } else if constexpr (VW == 4) {
-                const u32x4 a = __builtin_nontemporal_load(reinterpret_cast<const u32x4*>(vi));
-                pg.v[i][0] = a.x; pg.v[i][1] = a.y; pg.v[i][2] = a.z; pg.v[i][3] = a.w;
+            if constexpr (VW % 4 == 0) {
+#pragma unroll
+                for (int c = 0; c < VW / 4; ++c) {
+                    const u32x4 a = __builtin_nontemporal_load(reinterpret_cast<const u32x4*>(vi + 16 * c));
+                    pg.v[i][4 * c] = a.x; pg.v[i][4 * c + 1] = a.y; pg.v[i][4 * c + 2] = a.z; pg.v[i][4 * c + 3] = a.w;
+                }
             } else {
                 const u32x2 a = __builtin_nontemporal_load(reinterpret_cast<const u32x2*>(vi));
                 pg.v[i][0] = a.x; pg.v[i][1] = a.y;
@@ -1435,14 +1434,12 @@ struct DecodeWave {
 #pragma unroll
         for (int i = 0; i < 4; ++i) {
             const u32 so = i * ln.vrow;
-            if constexpr (VW == 8) {
-                const u32x4 a = __builtin_bit_cast(u32x4, __builtin_amdgcn_raw_buffer_load_b128(rv, ln.v, so, 2));
-                const u32x4 b = __builtin_bit_cast(u32x4, __builtin_amdgcn_raw_buffer_load_b128(rv, ln.v + 16, so, 2));
-                pg.v[i][0] = a.x; pg.v[i][1] = a.y; pg.v[i][2] = a.z; pg.v[i][3] = a.w;
-                pg.v[i][4] = b.x; pg.v[i][5] = b.y; pg.v[i][6] = b.z; pg.v[i][7] = b.w;
-            } else if constexpr (VW == 4) {
-                const u32x4 a = __builtin_bit_cast(u32x4, __builtin_amdgcn_raw_buffer_load_b128(rv, ln.v, so, 2));
-                pg.v[i][0] = a.x; pg.v[i][1] = a.y; pg.v[i][2] = a.z; pg.v[i][3] = a.w;
+            if constexpr (VW % 4 == 0) {
+#pragma unroll
+                for (int c = 0; c < VW / 4; ++c) {
+                    const u32x4 a = __builtin_bit_cast(u32x4, __builtin_amdgcn_raw_buffer_load_b128(rv, ln.v + 16 * c, so, 2));
+                    pg.v[i][4 * c] = a.x; pg.v[i][4 * c + 1] = a.y; pg.v[i][4 * c + 2] = a.z; pg.v[i][4 * c + 3] = a.w;
+                }
             } else {
                 const u32x2 a = __builtin_bit_cast(u32x2, __builtin_amdgcn_raw_buffer_load_b64(rv, ln.v, so, 2));
                 pg.v[i][0] = a.x; pg.v[i][1] = a.y;

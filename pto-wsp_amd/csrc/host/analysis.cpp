@@ -368,11 +368,11 @@ DecodeInfo classify_decode(const KernelDef& k, const KernelAnalysis& a) {
     // steps: larger pages as 16-token sub-pages, 8-token pages two to a step),
     // head dim 64 / 128 / 256, query rows in blocks of 16 (one MFMA row block
     // each) up to what the wave's registers hold beside its page ring: 48
-    // rows at head dim 64 or 128, 16 at 256; f32 pages (twice the registers)
-    // up to head dim 128.
+    // rows at head dim 64 or 128, 16 at 256, in every dtype (f32 pages are
+    // twice the registers and take 2-step rings from head dim 128).
     const int max_rows = D == 256 ? 16 : 48;
     if ((PG != 8 && PG != 16 && PG != 32 && PG != 64 && PG != 128) || G < 1 || G > max_rows ||
-        (D != 64 && D != 128 && D != 256) || (f32 && D > 128))
+        (D != 64 && D != 128 && D != 256))
         return info;
     info.ok = true;
     info.f32 = f32;

@@ -674,6 +674,8 @@ def test_paged_decode_wide_units(gpu, lengths, hkv, group, d, page):
     ([400, 33, 1000], 1, 32, 128, 16, True),              # 32 rows: two row blocks, 2-step rings
     ([250, 0, 1300, 16], 2, 48, 64, 32, True),            # 48 rows at head dim 64
     ([90, 700], 1, 20, 128, 8, True),                     # 20 rows, 8-token pages
+    ([333, 64, 1], 2, 8, 256, 32, True),                  # head dim 256
+    ([500, 17], 1, 16, 256, 16, False),                   # 16 rows at head dim 256, unmasked
 ])
 def test_paged_decode_f32(gpu, lengths, hkv, group, d, page, masked):
     """f32 q / K / V (the reference's own dtype) on the decode family: scores and p @ v on

@@ -205,10 +205,10 @@ def test_decode_family_query_rows(group, d, family):
 
 @pytest.mark.parametrize("group, d, family, ring", [(4, 128, "decode", 2), (16, 64, "decode", 4), (32, 128, "decode", 2),
                                                  (48, 64, "decode", 2), (49, 64, "tile_program", 0),
-                                                 (4, 256, "tile_program", 0)])
+                                                 (4, 256, "decode", 2), (17, 256, "tile_program", 0)])
 def test_decode_family_f32(group, d, family, ring):
-    """f32 q / K / V take the decode family up to head dim 128 and 48 query rows, with
-    2-step page rings at head dim 128 or beyond 16 rows."""
+    """f32 q / K / V take the decode family at the bf16 shapes (48 query rows at head dims
+    64 and 128, 16 at 256), with 2-step page rings from head dim 128 or beyond 16 rows."""
     from pto_wsp._hip import NativeProgram
 
     arrs = W.paged_decode_arrays([40, 300], 1, group, d, page=64, f32=True)
