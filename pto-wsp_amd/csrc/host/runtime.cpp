@@ -479,15 +479,16 @@ struct Tuning {
 // 0.41 ms with 2 steps on the C5 shape with head dim 256); 2 steps keep the
 // same bytes in flight.
 // More than 16 query rows add a block of accumulators and q registers per
-// 16 rows: 33-48 rows at head dim 128 leave room for 2 steps.  f32 pages
-// are twice the registers of bf16 ones: 2 steps at head dim 128 (0.406
-// against 0.409 ms with 3 on the C5 shape in f32), and beyond 16 rows; 4 at
-// head dim 64 up to 16 rows.
+// 16 rows, and the fold, not the page latency, bounds them: 2 steps (C5
+// lengths, one box: 32 rows at head dim 128 0.282 against 0.295 ms with 4,
+// 48 rows at head dim 64 0.289 against 0.299 ms).  f32 pages are twice the
+// registers of bf16 ones: 2 steps at head dim 128 (0.406 against 0.409 ms
+// with 3 on the C5 shape in f32); 4 at head dim 64 up to 16 rows.
 int decode_ring_for(int head_dim, int rows, bool f32) {
-    if (f32) return rows > 16 || head_dim >= 128 ? 2 : 4;
+    if (rows > 16) return 2;
+    if (f32) return head_dim >= 128 ? 2 : 4;
     if (head_dim >= 256) return 2;
-    if (head_dim <= 64) return rows <= 16 ? 3 : 4;
-    return rows <= 32 ? 4 : 2;
+    return head_dim <= 64 ? 3 : 4;
 }
 // Waves per decode block (per CU).  At head dim 64 a step is 4 KiB of K and
 // V, and one wave per SIMD cannot cover the fold's latency chain with it;
