@@ -483,12 +483,16 @@ struct Tuning {
 // lengths, one box: 32 rows at head dim 128 0.282 against 0.295 ms with 4,
 // 48 rows at head dim 64 0.289 against 0.299 ms).  f32 pages are twice the
 // registers of bf16 ones: 2 steps at head dim 128 (0.406 against 0.409 ms
-// with 3 on the C5 shape in f32); 4 at head dim 64 up to 16 rows.
+// with 3 on the C5 shape in f32); 4 at head dim 64 up to 16 rows.  bf16 /
+// f16 at head dim 128 (C5 lengths, rings of 2 / 3 / 4 steps, one box): 4
+// rows 0.204 / 0.205 / 0.202 ms, 8 rows 0.210 / 0.208 / 0.209, 12 rows
+// 0.218 / 0.218 / 0.219, 16 rows (32-token pages) 0.222 / 0.224 / 0.227.
 int decode_ring_for(int head_dim, int rows, bool f32) {
     if (rows > 16) return 2;
     if (f32) return head_dim >= 128 ? 2 : 4;
     if (head_dim >= 256) return 2;
-    return head_dim <= 64 ? 3 : 4;
+    if (head_dim <= 64) return 3;
+    return rows <= 4 ? 4 : rows <= 12 ? 3 : 2;
 }
 // Waves per decode block (per CU).  At head dim 64 a step is 4 KiB of K and
 // V, and one wave per SIMD cannot cover the fold's latency chain with it;
