@@ -1331,10 +1331,13 @@ __device__ inline void reset_count(int* cnt) {
 // v_mfma_f32_16x16x4_f32 with lane l holding head dims 16*j + 4*(l/16) .. +3
 // of its token for j < D/16 (the K order of a product is free), p @ v on the same MFMA
 // with p as it is (no hi / lo split); F16 is then unused.
-template <int G, int D, bool F16, bool MASK, bool H8 = false, bool F32 = false>
+// RM: the [1, 16] mask is a row broadcast (the reference's rule for a square
+// score tile): one value per query row, mask[r] for row r, G == 16.
+template <int G, int D, bool F16, bool MASK, bool H8 = false, bool F32 = false, bool RM = false>
 struct DecodeWave {
     static_assert(G >= 1 && G <= 48 && (D == 64 || D == 128 || D == 256), "decode shape");
     static_assert(!F32 || D <= 128 || G <= 16, "f32 decode shape");
+    static_assert(!RM || (G == 16 && MASK && !H8), "row-broadcast mask shape");
     static constexpr int ES = F32 ? 4 : 2;     // element bytes of q, K, V
     static constexpr int NS = D * ES / 64;     // u32x4 of K per lane (bf16 / f16: head-dim slices of the score MFMA)
     static constexpr int DV = D / 16;          // head-dim columns per lane in p @ v
@@ -1358,7 +1361,7 @@ struct DecodeWave {
     struct Page {
         u32x4 k[NS];           // lane l: token l%16, head dims 32*j + 8*(l/16) .. +7 (F32: 16*j + 4*(l/16) .. +3)
         u32 v[4][VW];          // lane l: tokens 4*(l/16) + i, head dims DV*(l%16) .. +DV-1
-        float mask[4];         // lane l: tokens 4*(l/16) .. +3
+        float mask[4];         // lane l: tokens 4*(l/16) .. +3 (RM: query row l%16's value, four times)
         float hneg;            // H8: added to the scores of tokens 8-15 (0, or -inf without page b)
     };
 
@@ -1376,7 +1379,7 @@ struct DecodeWave {
         Lanes r;
         r.k = static_cast<u32>((tk * ks + (F32 ? 4 : 8) * grp) * ES);
         r.v = static_cast<u32>((4 * gv * vs + DV * t) * ES);
-        r.m = static_cast<u32>(gv * 16);
+        r.m = static_cast<u32>(RM ? t * 4 : gv * 16);
         r.vrow = static_cast<u32>(vs * ES);
         return r;
     }
@@ -1445,7 +1448,15 @@ struct DecodeWave {
                 pg.v[i][0] = a.x; pg.v[i][1] = a.y;
             }
         }
-        if constexpr (MASK) {
+        if constexpr (MASK && RM) {
+            // The lane's query row's value, for all four of its tokens.
+            const buf_rsrc rm = __builtin_amdgcn_make_buffer_rsrc(const_cast<float*>(mp), 0, nrec, 0x00020000);
+            const float mk = __uint_as_float(__builtin_amdgcn_raw_buffer_load_b32(rm, ln.m, 0, 2));
+            pg.mask[0] = mk;
+            pg.mask[1] = mk;
+            pg.mask[2] = mk;
+            pg.mask[3] = mk;
+        } else if constexpr (MASK) {
             const buf_rsrc rm = __builtin_amdgcn_make_buffer_rsrc(const_cast<float*>(mp), 0, nrec, 0x00020000);
             const u32x4 mk = __builtin_bit_cast(u32x4, __builtin_amdgcn_raw_buffer_load_b128(rm, ln.m, 0, 2));
             pg.mask[0] = __uint_as_float(mk.x);

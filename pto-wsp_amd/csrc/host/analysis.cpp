@@ -277,16 +277,19 @@ DecodeInfo classify_decode(const KernelDef& k, const KernelAnalysis& a) {
     const int s_id = rowmax->operands[0];
     // s = mul(matmul(q, k_t), c) [- mask]
     int s2 = s_id, mask_p = -1;
+    bool row_mask = false;
     if (const OpInfo* sub = producer(s_id, OpKind::Sub)) {
         mask_p = param(sub->operands[1]);
         if (mask_p < 0) return info;
-        // The mask must apply one value per token: a column broadcast, or the same
-        // [1, PG] shape when there is one query row.  When the score tile is square
-        // the reference's rule makes a [1,R] operand a row broadcast
-        // (src/python/pto_codegen.cpp:1094-1105): not this pattern.
+        // The mask applies one value per token (a column broadcast, or the same
+        // [1, PG] shape when there is one query row).  When the score tile is
+        // square the reference's rule makes a [1,R] operand a row broadcast
+        // (src/python/pto_codegen.cpp:1094-1105): one value per query row,
+        // taken by the template for 16 rows and 16-token pages.
         const size_t oi = static_cast<size_t>(sub - k.ops.data());
         if (oi >= a.bin_mode.size()) return info;
-        if (a.bin_mode[oi] != BinMode::ColExpand && a.bin_mode[oi] != BinMode::Same) return info;
+        row_mask = a.bin_mode[oi] == BinMode::RowExpand;
+        if (a.bin_mode[oi] != BinMode::ColExpand && a.bin_mode[oi] != BinMode::Same && !row_mask) return info;
         s2 = sub->operands[0];
         used.insert(sub);
     }
@@ -363,6 +366,7 @@ DecodeInfo classify_decode(const KernelDef& k, const KernelAnalysis& a) {
     if (mask_p >= 0) {
         const ValueInfo* mk = vi(mask_p);
         if (mk->dtype != DType::F32 || mk->rows != 1 || mk->cols != PG) return info;
+        if (row_mask && (G != 16 || PG != 16)) return info;
     }
     // Device template shapes: pages of 8, 16, 32, 64 or 128 tokens (folded as 16-token
     // steps: larger pages as 16-token sub-pages, 8-token pages two to a step),
@@ -376,6 +380,7 @@ DecodeInfo classify_decode(const KernelDef& k, const KernelAnalysis& a) {
         return info;
     info.ok = true;
     info.f32 = f32;
+    info.row_mask = row_mask;
     info.q = a.tensor_ordinal[pq];
     info.kt = a.tensor_ordinal[pkt];
     info.v = a.tensor_ordinal[pv_p];

@@ -50,6 +50,7 @@ struct DecodeInfo {
     int g = 0, d = 0, pg = 0;                // query rows, head dim, tokens per page
     bool f16 = false;                        // q / k / v are f16 (else bf16)
     bool f32 = false;                        // q / k / v are f32
+    bool row_mask = false;                   // the [1, PG] mask is a row broadcast (G == PG == 16)
     float scale = 1.0f;                      // score scale (a Constant)
 };
 

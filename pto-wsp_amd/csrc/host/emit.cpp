@@ -1095,7 +1095,8 @@ EmittedKernel emit_decode(const Module& m, const KernelAnalysis& a, const Launch
     auto nterms = [&](int p) { return spec.indirect_count[p]; };
     const std::string tmpl = "DecodeWave<" + std::to_string(d.g) + ", " + std::to_string(d.d) + ", " +
                              (d.f16 ? "true" : "false") + ", " + (d.mask >= 0 ? "true" : "false") + ", " +
-                             (d.pg == 8 ? "true" : "false") + (d.f32 ? ", true" : "") + ">";
+                             (d.pg == 8 ? "true" : "false") + (d.f32 || d.row_mask ? (d.f32 ? ", true" : ", false") : "") +
+                             (d.row_mask ? ", true" : "") + ">";
     const int es = d.f32 ? 4 : 2;  // bytes per q / K / V element
     std::ostringstream scale;
     scale.precision(9);

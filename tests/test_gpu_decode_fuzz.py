@@ -50,8 +50,9 @@ def test_random_decode_matches_oracle(gpu, seed):
     ca = {k: v.copy() for k, v in ga.items()}
     dt = W.F32 if c["f32"] else W.F16 if c["f16"] else W.BF16
     prog = W.paged_decode(ga, masked=c["masked"], dtype=dt).compile(target="hip_gfx950")
-    # (a [1, page] mask with as many query rows as page tokens is a row broadcast, see below)
-    want_family = "tile_program" if c["masked"] and c["group"] == c["page"] else "decode"
+    # (a [1, page] mask with as many query rows as page tokens is a row broadcast, see
+    # below: the decode template takes it for 16 rows and 16-token pages)
+    want_family = "tile_program" if c["masked"] and c["group"] == c["page"] != 16 else "decode"
     assert prog._native.kernel_family("decode_page") == want_family
     prog.execute()
     prog.synchronize()

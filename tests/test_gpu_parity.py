@@ -736,16 +736,24 @@ def test_paged_decode_sixteen_rows(gpu):
     """16 query rows fill every MFMA column.  Unmasked it is the decode family; with
     the [1,16] mask on a square [16,16] score tile the reference's broadcast rule
     subtracts mask[row] (a row broadcast, src/python/pto_codegen.cpp:1094-1105),
-    so the launch stays a tile program and matches the oracle, not a token mask."""
+    which the decode template's row-mask form applies (each lane subtracts its
+    query row's value): the launch matches the oracle, not a token mask.  Rows
+    whose value is 1e30 end with uniform weights, as in the oracle."""
     prog, ref, ga, ca = _decode_case([96, 512, 16], 1, 16, 64, seed=3, masked=False)
     assert prog._native.kernel_family("decode_page") == "decode"
     for k in ("m", "l", "o", "out"):
         np.testing.assert_allclose(ga[k], ca[k], rtol=2e-5, atol=2e-5 * float(np.abs(ca[k]).max()), err_msg=k)
     assert _rel_fro(ga["out"], W.paged_decode_ref(ga)) <= 1e-5
-    prog, ref, ga, ca = _decode_case([90, 40], 1, 16, 64, seed=3, masked=True)
-    assert prog._native.kernel_family("decode_page") == "tile_program"
-    for k in ("m", "l", "o", "out"):
-        np.testing.assert_allclose(ga[k], ca[k], rtol=1e-5, atol=1e-5 * float(np.abs(ca[k]).max()), err_msg=k)
+    for lengths, hkv, d in (([90, 40], 1, 64), ([700, 5, 0, 260], 2, 128), ([33, 1500], 1, 256)):
+        prog, ref, ga, ca = _decode_case(lengths, hkv, 16, d, seed=3, masked=True)
+        assert prog._native.kernel_family("decode_page") == "decode"
+        assert "true, false, false, true>" in prog._native.precompile(0)  # the row-mask form
+        for k in ("m", "l", "o", "out"):
+            fin = np.isfinite(ca[k])
+            assert np.array_equal(fin, np.isfinite(ga[k])), k
+            np.testing.assert_allclose(ga[k][fin], ca[k][fin], rtol=2e-5, atol=2e-5 * float(np.abs(ca[k][fin]).max()),
+                                       err_msg=k)
+        assert prog.stats.total_cycles == ref.total_cycles and prog.stats.task_count == ref.task_count
 
 
 def test_paged_decode_f16_and_unmasked(gpu):
