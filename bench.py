@@ -557,6 +557,8 @@ CASES = {
     "paged_decode_d256": lambda: DecodeCase("paged_decode_d256", 64, 32, 8, 256, 512, 8192, 0, None),
     "paged_decode_g16": lambda: DecodeCase("paged_decode_g16", 64, 128, 8, 128, 512, 8192, 0, None, page=32),
     "paged_decode_g32": lambda: DecodeCase("paged_decode_g32", 64, 256, 8, 128, 512, 8192, 0, None),
+    # 16 rows with 16-token pages: the [1, 16] mask is a row broadcast there.
+    "paged_decode_g16_rowmask": lambda: DecodeCase("paged_decode_g16_rowmask", 64, 128, 8, 128, 512, 8192, 0, None),
     # Not a BASELINE config: the C5 decode with f32 q / K / V.
     "paged_decode_f32": lambda: DecodeCase("paged_decode_f32", 64, 32, 8, 128, 512, 8192, 0, None, f32_inputs=True),
     "paged_decode_f32_g32": lambda: DecodeCase("paged_decode_f32_g32", 64, 256, 8, 128, 512, 8192, 0, None, f32_inputs=True),
@@ -572,7 +574,8 @@ CASES = {
     "bgemm_tile16": lambda: GemmCase("bgemm_tile16", 64, 2048, 2048, 2048, 0, None, tile=(16, 16, 16), dtype="f16"),
 }
 EXTRA = ("copy_calib", "softmax3", "softmax3_overlap", "paged_decode_page32", "paged_decode_page64", "paged_decode_page8",
-         "paged_decode_d64", "paged_decode_d256", "paged_decode_g16", "paged_decode_g32", "paged_decode_f32",
+         "paged_decode_d64", "paged_decode_d256", "paged_decode_g16", "paged_decode_g32", "paged_decode_g16_rowmask",
+         "paged_decode_f32",
          "paged_decode_f32_g32", "paged_decode_f32_d64_g48", "paged_decode_f32_d256", "bgemm_f32", "bgemm_tile16")
 
 
